@@ -1,0 +1,167 @@
+/* libqutai_amd — MI355X (gfx950) GEMM hot path of Qutai behind a C ABI.
+ *
+ * Every entry point takes plain device pointers, element counts and dtype
+ * codes, enqueues its kernels on `stream` (NULL = the default stream, the
+ * only stream the reference uses: src/qutai/backends/cuda_runtime.py:326)
+ * and returns without synchronising.  Return value: QA_OK (0), a negative
+ * QA_E* code for invalid arguments, or a positive hipError_t from the launch.
+ *
+ * Device memory is owned by the caller (the Python runtime in
+ * qutai_amd/backends/amd_runtime.py allocates it through libamdhip64, as the
+ * reference allocates through the CUDA driver: cuda_runtime.py:184-228).
+ *
+ * dtype codes are the positions in the reference storage table
+ * (src/qutai/backends/cuda.py:17, `_TYPES`): float32 = 0, float64 = 1,
+ * int64 = 4, bfloat16 = 5.  bfloat16 data is raw 16-bit words.
+ */
+#ifndef QUTAI_AMD_H
+#define QUTAI_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QA_F32 0
+#define QA_F64 1
+#define QA_I64 4
+#define QA_BF16 5
+
+#define QA_OK 0
+#define QA_EINVAL (-1)     /* shapes, strides, dtypes or pointers rejected */
+#define QA_EWORKSPACE (-2) /* workspace missing or too small */
+
+/* Batched GEMM: for z in [0, batch)
+ *   out[z][m][n] (+)= sum_k A_z(m,k) * B_z(k,n)
+ *   A_z(m,k) = transpose_left  ? a[z*left_stride  + k*rows + m] : a[z*left_stride  + m*inner + k]
+ *   B_z(k,n) = transpose_right ? b[z*right_stride + n*inner + k] : b[z*right_stride + k*cols + n]
+ * out is [batch][rows][cols] contiguous.  A stride of 0 broadcasts one
+ * operand over the batch.  fp32 x fp32 runs on v_mfma_f32_32x32x2_f32; any
+ * bf16 operand, or bf16_compute != 0 (autocast), runs on
+ * v_mfma_f32_32x32x16_bf16 with fp32 accumulation, an fp32 operand being
+ * rounded to bf16 (nearest even) into `workspace` first; fp64 runs a SIMT
+ * kernel.  accumulate != 0 adds the old output before the single rounding
+ * to out_dtype.  inner == 0 writes zeros (or keeps out when accumulating).
+ * Replaces: `cuda.gemm` (src/qutai/backends/cuda.py:305-362) and the kernels
+ * gemm_tiled / gemm_register / gemm_bf16 / gemm_bf16_wide / gemm_bf16_long
+ * (src/qutai/backends/cuda/gemm.cu:35-223), whose common signature
+ * `(a, b, out, M, K, N, sa, sb, ta, tb, accumulate)` this mirrors. */
+int qutai_amd_gemm(const void* a, const void* b, void* out, int64_t rows, int64_t inner, int64_t cols,
+                   int64_t batch, int64_t left_stride, int64_t right_stride, int transpose_left,
+                   int transpose_right, int a_dtype, int b_dtype, int out_dtype, int accumulate,
+                   int bf16_compute, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Bytes of workspace qutai_amd_gemm needs for these arguments (0 when no
+ * operand has to be narrowed to bf16).  Helper of qutai_amd_gemm; the
+ * reference narrows inside its kernels (gemm.cu:21-24, 105-142). */
+size_t qutai_amd_gemm_workspace_size(int64_t rows, int64_t inner, int64_t cols, int64_t batch,
+                                     int64_t left_stride, int64_t right_stride, int a_dtype, int b_dtype,
+                                     int bf16_compute);
+
+/* Grouped GEMM for MoE experts: group g owns rows [offsets[g], offsets[g+1])
+ * of a (row-major, `inner` columns) and of out (row-major, `cols` columns);
+ *   out_g = a_g @ B_g   with B_g = b + g*expert_stride, stored [cols][inner]
+ *   when transpose_right (the lm weight layout (out, in)) else [inner][cols].
+ * `offsets` ([groups+1] int64) lives in device memory and is read by the
+ * kernel, so the host never waits for the per-expert counts; max_rows is an
+ * upper bound of offsets[groups] (rows * top_k).  dtype is QA_BF16 or QA_F32
+ * for both operands.  Replaces the per-expert loop of 3 `cuda_lm.gemm`
+ * launches per expert in SparseMoE (src/qutai/lm/layers.py:395-397,
+ * src/qutai/backends/cuda_lm.py:31-55) and the count download that sizes
+ * them (cuda_lm.py:432-434). */
+int qutai_amd_gemm_grouped(const void* a, const void* b, void* out, const int64_t* offsets, int groups,
+                           int64_t max_rows, int64_t inner, int64_t cols, int64_t expert_stride,
+                           int transpose_right, int dtype, int out_dtype, int accumulate, void* stream);
+
+/* Element-wise dtype conversion of n values (fp32/fp64/bf16 among each
+ * other; narrowing to bf16 rounds to nearest even).
+ * Replaces: `cast` (src/qutai/backends/cuda/tensor.cu:21-29) as driven by
+ * `cuda.from_storage` (src/qutai/backends/cuda.py:125-133). */
+int qutai_amd_cast(const void* src, void* dst, int64_t n, int src_dtype, int dst_dtype, void* stream);
+
+/* dst[0..n) = value (rounded to dtype; int64 takes the integer part).
+ * Replaces: `fill` / `fill_int` (src/qutai/backends/cuda/tensor.cu:11),
+ * driven by `cuda.full` (src/qutai/backends/cuda.py:116-122). */
+int qutai_amd_fill(void* dst, int64_t n, double value, int dtype, void* stream);
+
+/* out = left + right element-wise (fp32/fp64/bf16; computed in fp32 or fp64,
+ * one rounding).  Replaces the `binary` add of tensor.cu used by
+ * `cuda.add` for gradient accumulation (src/qutai/core/grad.py:60). */
+int qutai_amd_add(const void* left, const void* right, void* out, int64_t n, int dtype, void* stream);
+
+/* out[r][c] = x[r][c] + bias[c] (rows x cols; one rounding).  The bias add
+ * of nn.Linear (src/qutai/nn/layers.py:145-148, a broadcast `add`) and the
+ * broadcast of a scalar gradient (cols = 1). */
+int qutai_amd_add_rows(const void* x, const void* bias, void* out, int64_t rows, int64_t cols, int dtype,
+                       void* stream);
+
+/* out[g] = reduce over the middle axis of x viewed as [outer][count][inner]
+ * (sum).  Used to sum gradients over broadcast batch axes; replaces
+ * `cuda.unbroadcast` as called by src/qutai/core/operations/linalg.py:51,55. */
+int qutai_amd_sum_middle(const void* x, void* out, int64_t outer, int64_t count, int64_t inner, int dtype,
+                         void* stream);
+
+/* Swap the last two axes: out[z][c][r] = x[z][r][c].  Replaces the
+ * `broadcast`-kernel transpose of src/qutai/backends/cuda.py:255-262 on the
+ * non-gemm branch of the matmul gradient (linalg.py:48-55). */
+int qutai_amd_transpose_last2(const void* x, void* out, int64_t batch, int64_t rows, int64_t cols, int dtype,
+                              void* stream);
+
+/* Row softmax of (scale * x): rows x width, fp32 math, max subtracted.
+ * dtype QA_F32 or QA_BF16 (in and out); QA_F64 is computed in fp64.
+ * Replaces: `softmax_rows` / `softmax_forward`
+ * (src/qutai/backends/cuda/nn.cu:28-37, 67-76) driven by `cuda.softmax`
+ * (src/qutai/backends/cuda.py:464-472); scale folds the 1/sqrt(D) of
+ * src/qutai/nn/layers.py:336 into the same pass. */
+int qutai_amd_softmax_rows(const void* x, void* out, int64_t rows, int64_t width, double scale, int dtype,
+                           void* stream);
+
+/* out = silu(gate) * up element-wise (fp32 math, one rounding to dtype).
+ * Replaces `lm_silu` (src/qutai/backends/cuda/lm.cu:54) followed by the
+ * elementwise multiply of SwiGLU (src/qutai/lm/layers.py:310-311). */
+int qutai_amd_silu_mul(const void* gate, const void* up, void* out, int64_t n, int dtype, void* stream);
+
+/* MoE routing, forward.  scores: [rows][experts] fp32 router logits.
+ * Writes probs [rows][experts] (fp32 softmax), weights [rows][top_k] (fp32,
+ * renormalised over the selected experts), indices [rows][top_k] (int64;
+ * descending probability, lowest expert index first on ties), counts
+ * [experts], ids / slots [experts][capacity] (stable token-major lists per
+ * expert), locations [rows][top_k] (position inside the expert list),
+ * offsets [experts+1] (exclusive prefix sum of counts), order [rows*top_k]
+ * (ids concatenated expert-major: order[offsets[e]+i] = ids[e][i]),
+ * utilization [experts] (count / (rows*top_k)) and aux [1]
+ * (experts * sum_{r,e} probs*utilization / rows).  capacity = rows * top_k.
+ * Replaces `cuda_lm.routing` (src/qutai/backends/cuda_lm.py:368-449) and its
+ * kernels lm_route, lm_route_pack, lm_route_util, lm_route_aux
+ * (src/qutai/backends/cuda/lm.cu:345-387); selection follows the CPU
+ * oracle `cpu_lm.routing` (src/qutai/backends/cpu_lm.py:204-242). */
+int qutai_amd_route(const float* scores, float* probs, float* weights, int64_t* indices, int64_t* counts,
+                    int64_t* ids, int64_t* slots, int64_t* locations, int64_t* offsets, int64_t* order,
+                    float* utilization, float* aux, int64_t rows, int64_t experts, int64_t top_k,
+                    void* stream);
+
+/* out[r] = x[order[r]] for r in [0, count): gathers the token rows of all
+ * experts into one expert-major block (width values per row).  backward != 0
+ * scatters instead: out[order[r]] = x[r] (each token appears once per
+ * expert, so no accumulation is needed within one expert).
+ * Replaces `lm_route_gather` (src/qutai/backends/cuda/lm.cu:394-396) driven
+ * per expert by `cuda_lm.route_gather` (src/qutai/backends/cuda_lm.py:471-502). */
+int qutai_amd_route_gather(const void* x, const int64_t* order, void* out, int64_t count, int64_t width,
+                           int backward, int dtype, void* stream);
+
+/* Weighted combine: y[row] = sum_slot weights[row][slot] *
+ *   expert_out[offsets[indices[row][slot]] + locations[row][slot]]
+ * summed in fp32 in slot order with one rounding to dtype.
+ * Replaces `lm_pointer_table` + `lm_combine_all`
+ * (src/qutai/backends/cuda/lm.cu:400-416, src/qutai/backends/cuda_lm.py:505-541). */
+int qutai_amd_combine(const void* expert_out, const float* weights, const int64_t* indices,
+                      const int64_t* locations, const int64_t* offsets, void* y, int64_t rows, int64_t width,
+                      int64_t top_k, int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QUTAI_AMD_H */

@@ -1,0 +1,63 @@
+"""Reverse-mode graph: record and backward (src/qutai/core/grad.py:7-65)."""
+from __future__ import annotations
+
+from ..backends.device import get_backend
+from .context import is_recording
+
+
+def record(result, parents, rule=None):
+    """Keep the parents and the bound local backward rule on the result."""
+    result.requires_grad = is_recording() and any(parent.requires_grad for parent in parents)
+    if result.requires_grad:
+        result.parents = parents
+        result.backward_rule = rule
+    return result
+
+
+def _topological_order(output):
+    order, seen, pending = [], set(), [(output, False)]
+    while pending:
+        tensor, expanded = pending.pop()
+        if expanded:
+            order.append(tensor)
+        elif tensor not in seen:
+            seen.add(tensor)
+            if getattr(tensor, "_graph_released", False):
+                raise RuntimeError("graph already released; run forward again or retain the graph")
+            if tensor.parents and tensor.backward_rule is None:
+                raise NotImplementedError("graph contains an operation without a backward rule")
+            pending.append((tensor, True))
+            pending.extend((parent, False) for parent in tensor.parents if parent.requires_grad)
+    return order
+
+
+def backward(output, gradient, *, retain_graph=True, leaf_sink=None):
+    """Propagate ``gradient``; leaves go to ``leaf_sink`` (or a returned dict)."""
+    order = _topological_order(output)
+    gradients = {output: gradient}
+    leaves = {}
+    while order:
+        tensor = order.pop()
+        incoming = gradients.pop(tensor, None)
+        if incoming is None:
+            continue
+        rule = tensor.backward_rule
+        if rule is None:
+            if leaf_sink is None:
+                leaves[tensor] = incoming
+            else:
+                leaf_sink(tensor, incoming)
+            continue
+        contributions = rule(incoming)
+        parents = tensor.parents
+        if not retain_graph:
+            tensor.parents, tensor.backward_rule, tensor._graph_released = (), None, True
+        for parent, contribution in zip(parents, contributions, strict=True):
+            if parent.requires_grad and contribution is not None:
+                if leaf_sink is not None and parent.backward_rule is None:
+                    leaf_sink(parent, contribution)
+                elif parent in gradients:
+                    gradients[parent] = get_backend(contribution.device).add(gradients[parent], contribution)
+                else:
+                    gradients[parent] = contribution
+    return leaves

@@ -1,0 +1,54 @@
+// Shared device helpers for the gfx950 (CDNA4) kernels of libqutai_amd.
+//
+// Element codes follow the storage dtype table of the reference CUDA backend
+// (src/qutai/backends/cuda.py:17, `_TYPES` order: float32=0, float64=1,
+// complex64=2, complex128=3, int64=4, bfloat16=5), so a host that already
+// speaks those codes can pass them straight through the C ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qa {
+
+enum Dtype : int { F32 = 0, F64 = 1, I64 = 4, BF16 = 5 };
+
+typedef uint16_t bf16_t;  // raw bfloat16 bits in HBM
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(8 * sizeof(short)))) short i16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(short)))) short i16x4;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
+
+// bfloat16 -> float is exact: the 16 bits become the high half of an fp32.
+__device__ __forceinline__ float bf16_to_f32(bf16_t v) {
+  return __uint_as_float(((uint32_t)v) << 16);
+}
+
+// float -> bfloat16, round to nearest even; NaN stays a quiet NaN with its
+// sign and top payload bits.  Same bit rule as the reference host encoder
+// (src/qutai/backends/cuda.py:98-101) and __float2bfloat16_rn on device.
+__device__ __forceinline__ bf16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x40u);
+  return (bf16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+// Two floats -> two packed bfloat16 (low half = a).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  return (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
+}
+
+// MI355X has 8 XCDs, each with its own L2.  Consecutive workgroup ids are
+// dispatched round-robin over the XCDs, so id i runs on XCD i % 8.  This maps
+// the hardware id to a "logical" id such that each XCD receives one
+// contiguous range of logical ids (sizes differ by at most one); tiles that
+// are adjacent in logical order then share one L2.
+__device__ __forceinline__ int xcd_remap(int pid, int n) {
+  const int xcds = 8;
+  int xcd = pid % xcds, q = pid / xcds;
+  int per = n / xcds, rem = n % xcds;
+  return xcd < rem ? xcd * (per + 1) + q : rem * (per + 1) + (xcd - rem) * per + q;
+}
+
+}  // namespace qa

@@ -1,0 +1,244 @@
+// MoE routing, token gather and weighted combine for the grouped expert
+// GEMMs (C ABI).  Reference counterparts are cited per entry point in
+// include/qutai_amd.h.
+#include "common.h"
+#include "qutai_amd.h"
+
+using namespace qa;
+
+namespace {
+
+// One thread per token: fp32 softmax of the router logits, then top-k.
+// Selection compares the logits themselves: softmax is monotone, so the
+// order of the logits is the order of the probabilities, and comparing the
+// exact inputs keeps the chosen experts identical to a float64 softmax (the
+// CPU oracle, cpu_lm.py:204-216).  A strict '>' keeps the lowest expert
+// index among equal values, like the stable descending sort of the oracle.
+__global__ void route_select(const float* scores, float* probs, float* weights, int64_t* indices, int64_t rows,
+                             int64_t experts, int64_t top_k) {
+  int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  const float* s = scores + r * experts;
+  float peak = -INFINITY;
+  for (int64_t e = 0; e < experts; e++) peak = fmaxf(peak, s[e]);
+  float total = 0.f;
+  for (int64_t e = 0; e < experts; e++) total += expf(s[e] - peak);
+  for (int64_t e = 0; e < experts; e++) probs[r * experts + e] = expf(s[e] - peak) / total;
+  float chosen = 0.f;
+  for (int64_t slot = 0; slot < top_k; slot++) {
+    int64_t best = -1;
+    for (int64_t e = 0; e < experts; e++) {
+      bool used = false;
+      for (int64_t q = 0; q < slot; q++) used |= indices[r * top_k + q] == e;
+      if (!used && (best < 0 || s[e] > s[best])) best = e;
+    }
+    indices[r * top_k + slot] = best;
+    float p = probs[r * experts + best];
+    weights[r * top_k + slot] = p;
+    chosen += p;
+  }
+  for (int64_t slot = 0; slot < top_k; slot++) weights[r * top_k + slot] /= chosen;
+}
+
+// One workgroup per expert: stable compaction of the (token, slot)
+// assignments routed to it, in increasing assignment order.
+constexpr int PACK = 256;
+__global__ void __launch_bounds__(PACK) route_pack(const int64_t* indices, int64_t* counts, int64_t* ids,
+                                                   int64_t* slots, int64_t* locations, int64_t* offsets,
+                                                   int64_t* order, int64_t n, int64_t top_k, int64_t experts) {
+  __shared__ int64_t wave_count[PACK / 64];
+  __shared__ int64_t lower_total;
+  const int64_t e = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // pass 1: assignments to lower experts = start of this expert in `order`
+  int64_t lower = 0;
+  for (int64_t at = tid; at < n; at += PACK) lower += indices[at] < e;
+  for (int o = 32; o > 0; o >>= 1) lower += __shfl_xor(lower, o);
+  if (lane == 0) wave_count[wave] = lower;
+  __syncthreads();
+  if (tid == 0) {
+    int64_t t = 0;
+    for (int w = 0; w < PACK / 64; w++) t += wave_count[w];
+    lower_total = t;
+  }
+  __syncthreads();
+  const int64_t base = lower_total;
+  // pass 2: ordered compaction, 256 assignments per step
+  int64_t written = 0;
+  for (int64_t start = 0; start < n; start += PACK) {
+    int64_t at = start + tid;
+    bool sel = at < n && indices[at] == e;
+    uint64_t mask = __ballot(sel);
+    int64_t before_lane = __popcll(mask & ((1ull << lane) - 1ull));
+    __syncthreads();
+    if (lane == 0) wave_count[wave] = __popcll(mask);
+    __syncthreads();
+    int64_t before_wave = 0, step = 0;
+    for (int w = 0; w < PACK / 64; w++) {
+      if (w < wave) before_wave += wave_count[w];
+      step += wave_count[w];
+    }
+    if (sel) {
+      int64_t pos = written + before_wave + before_lane;
+      ids[e * n + pos] = at / top_k;
+      slots[e * n + pos] = at % top_k;
+      locations[at] = pos;
+      order[base + pos] = at / top_k;
+    }
+    written += step;
+  }
+  if (tid == 0) {
+    counts[e] = written;
+    offsets[e] = base;
+    if (e == experts - 1) offsets[experts] = n;
+  }
+}
+
+// utilization = count / (rows * top_k); aux = experts * sum(p * util) / rows.
+__global__ void __launch_bounds__(256) route_stats(const float* probs, const int64_t* counts, float* utilization,
+                                                   float* aux, int64_t rows, int64_t experts, int64_t n) {
+  __shared__ float red[4];
+  int tid = threadIdx.x;
+  for (int64_t e = tid; e < experts; e += 256) utilization[e] = (float)counts[e] / (float)n;
+  float total = 0.f;
+  for (int64_t i = tid; i < rows * experts; i += 256) total += probs[i] * ((float)counts[i % experts] / (float)n);
+  for (int o = 32; o > 0; o >>= 1) total += __shfl_xor(total, o);
+  if ((tid & 63) == 0) red[tid >> 6] = total;
+  __syncthreads();
+  if (tid == 0) aux[0] = (float)experts * (red[0] + red[1] + red[2] + red[3]) / (float)rows;
+}
+
+// Row gather / scatter in 16-byte pieces.
+__global__ void gather_rows16(const u32x4* x, const int64_t* order, u32x4* out, int64_t count, int64_t pieces,
+                              int backward) {
+  int64_t total = count * pieces;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    int64_t r = i / pieces, j = i % pieces;
+    int64_t src = order[r] * pieces + j;
+    if (backward) out[src] = x[i];
+    else out[i] = x[src];
+  }
+}
+template <class T>
+__global__ void gather_rows(const T* x, const int64_t* order, T* out, int64_t count, int64_t width, int backward) {
+  int64_t total = count * width;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    int64_t r = i / width, j = i % width;
+    int64_t src = order[r] * width + j;
+    if (backward) out[src] = x[i];
+    else out[i] = x[src];
+  }
+}
+
+// y[row] = sum over slots of w * expert row, fp32 sum in slot order.
+template <class T, int V>  // V values per thread
+__global__ void combine_kernel(const T* eo, const float* w, const int64_t* idx, const int64_t* loc,
+                               const int64_t* off, T* y, int64_t rows, int64_t width, int64_t top_k) {
+  int64_t per_row = width / V;
+  int64_t total = rows * per_row;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    int64_t row = i / per_row, j = (i % per_row) * V;
+    float acc[V];
+#pragma unroll
+    for (int v = 0; v < V; v++) acc[v] = 0.f;
+    for (int64_t s = 0; s < top_k; s++) {
+      int64_t at = row * top_k + s;
+      float f = w[at];
+      const T* src = eo + (off[idx[at]] + loc[at]) * width + j;
+#pragma unroll
+      for (int v = 0; v < V; v++) {
+        float x;
+        if constexpr (sizeof(T) == 2) x = bf16_to_f32(src[v]);
+        else x = (float)src[v];
+        acc[v] += f * x;
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < V; v++) {
+      if constexpr (sizeof(T) == 2) y[row * width + j + v] = f32_to_bf16(acc[v]);
+      else y[row * width + j + v] = acc[v];
+    }
+  }
+}
+
+unsigned blocks_for(int64_t n) {
+  int64_t b = (n + 255) / 256;
+  return (unsigned)(b < 1 ? 1 : b > 1048576 ? 1048576 : b);
+}
+
+}  // namespace
+
+extern "C" {
+
+int qutai_amd_route(const float* scores, float* probs, float* weights, int64_t* indices, int64_t* counts,
+                    int64_t* ids, int64_t* slots, int64_t* locations, int64_t* offsets, int64_t* order,
+                    float* utilization, float* aux, int64_t rows, int64_t experts, int64_t top_k, void* stream) {
+  if (rows < 0 || experts <= 0 || top_k <= 0 || top_k > experts) return QA_EINVAL;
+  hipStream_t s = (hipStream_t)stream;
+  int64_t n = rows * top_k;
+  if (experts > 0x7fffffff) return QA_EINVAL;
+  if (rows > 0)
+    hipLaunchKernelGGL(route_select, dim3(blocks_for(rows)), dim3(256), 0, s, scores, probs, weights, indices, rows,
+                       experts, top_k);
+  hipLaunchKernelGGL(route_pack, dim3((unsigned)experts), dim3(PACK), 0, s, indices, counts, ids, slots, locations,
+                     offsets, order, n, top_k, experts);
+  if (rows > 0)
+    hipLaunchKernelGGL(route_stats, dim3(1), dim3(256), 0, s, probs, counts, utilization, aux, rows, experts, n);
+  return (int)hipGetLastError();
+}
+
+int qutai_amd_route_gather(const void* x, const int64_t* order, void* out, int64_t count, int64_t width,
+                           int backward, int dtype, void* stream) {
+  if (count < 0 || width < 0) return QA_EINVAL;
+  if (dtype != F32 && dtype != BF16 && dtype != F64) return QA_EINVAL;
+  if (count * width == 0) return QA_OK;
+  hipStream_t s = (hipStream_t)stream;
+  int64_t es = dtype == BF16 ? 2 : dtype == F64 ? 8 : 4;
+  bool vec = (width * es) % 16 == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)out % 16 == 0;
+  if (vec) {
+    int64_t pieces = width * es / 16;
+    hipLaunchKernelGGL(gather_rows16, dim3(blocks_for(count * pieces)), dim3(256), 0, s, (const u32x4*)x, order,
+                       (u32x4*)out, count, pieces, backward);
+  } else if (dtype == BF16) {
+    hipLaunchKernelGGL(gather_rows<bf16_t>, dim3(blocks_for(count * width)), dim3(256), 0, s, (const bf16_t*)x,
+                       order, (bf16_t*)out, count, width, backward);
+  } else if (dtype == F32) {
+    hipLaunchKernelGGL(gather_rows<float>, dim3(blocks_for(count * width)), dim3(256), 0, s, (const float*)x, order,
+                       (float*)out, count, width, backward);
+  } else {
+    hipLaunchKernelGGL(gather_rows<double>, dim3(blocks_for(count * width)), dim3(256), 0, s, (const double*)x,
+                       order, (double*)out, count, width, backward);
+  }
+  return (int)hipGetLastError();
+}
+
+int qutai_amd_combine(const void* expert_out, const float* weights, const int64_t* indices,
+                      const int64_t* locations, const int64_t* offsets, void* y, int64_t rows, int64_t width,
+                      int64_t top_k, int dtype, void* stream) {
+  if (rows < 0 || width < 0 || top_k <= 0) return QA_EINVAL;
+  if (dtype != F32 && dtype != BF16) return QA_EINVAL;
+  if (rows * width == 0) return QA_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == BF16) {
+    if (width % 8 == 0)
+      hipLaunchKernelGGL((combine_kernel<bf16_t, 8>), dim3(blocks_for(rows * width / 8)), dim3(256), 0, s,
+                         (const bf16_t*)expert_out, weights, indices, locations, offsets, (bf16_t*)y, rows, width,
+                         top_k);
+    else
+      hipLaunchKernelGGL((combine_kernel<bf16_t, 1>), dim3(blocks_for(rows * width)), dim3(256), 0, s,
+                         (const bf16_t*)expert_out, weights, indices, locations, offsets, (bf16_t*)y, rows, width,
+                         top_k);
+  } else {
+    if (width % 4 == 0)
+      hipLaunchKernelGGL((combine_kernel<float, 4>), dim3(blocks_for(rows * width / 4)), dim3(256), 0, s,
+                         (const float*)expert_out, weights, indices, locations, offsets, (float*)y, rows, width,
+                         top_k);
+    else
+      hipLaunchKernelGGL((combine_kernel<float, 1>), dim3(blocks_for(rows * width)), dim3(256), 0, s,
+                         (const float*)expert_out, weights, indices, locations, offsets, (float*)y, rows, width,
+                         top_k);
+  }
+  return (int)hipGetLastError();
+}
+
+}  // extern "C"

@@ -1,0 +1,342 @@
+// Element-wise and row kernels around the GEMM path (C ABI): dtype casts,
+// fills, adds, batch reductions, last-two-axes transpose, row softmax and
+// SwiGLU's silu(gate) * up.  Reference counterparts are cited per entry
+// point in include/qutai_amd.h.
+#include "common.h"
+#include "qutai_amd.h"
+
+using namespace qa;
+
+namespace {
+
+constexpr int THREADS = 256;
+
+unsigned grid_for(int64_t n, int64_t per_thread = 1) {
+  int64_t blocks = (n + THREADS * per_thread - 1) / (THREADS * per_thread);
+  return (unsigned)(blocks < 1 ? 1 : blocks > 1048576 ? 1048576 : blocks);
+}
+
+__device__ __forceinline__ double load_any(const void* p, int64_t i, int dtype) {
+  switch (dtype) {
+    case F32: return ((const float*)p)[i];
+    case F64: return ((const double*)p)[i];
+    case BF16: return bf16_to_f32(((const bf16_t*)p)[i]);
+    default: return (double)((const int64_t*)p)[i];
+  }
+}
+
+// Conversion with the reference cast semantics (tensor.cu:21-29): the value
+// goes through double; bf16 is produced from its fp32 rounding.
+__global__ void cast_kernel(const void* src, void* dst, int64_t n, int s, int d) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    double v = load_any(src, i, s);
+    switch (d) {
+      case F32: ((float*)dst)[i] = (float)v; break;
+      case F64: ((double*)dst)[i] = v; break;
+      case BF16: ((bf16_t*)dst)[i] = f32_to_bf16((float)v); break;
+      default: ((int64_t*)dst)[i] = (int64_t)v; break;
+    }
+  }
+}
+
+__global__ void fill_kernel(void* dst, int64_t n, double value, int d) {
+  float f = (float)value;
+  bf16_t h = f32_to_bf16(f);
+  int64_t iv = (int64_t)value;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    switch (d) {
+      case F32: ((float*)dst)[i] = f; break;
+      case F64: ((double*)dst)[i] = value; break;
+      case BF16: ((bf16_t*)dst)[i] = h; break;
+      default: ((int64_t*)dst)[i] = iv; break;
+    }
+  }
+}
+
+__global__ void add_kernel(const void* a, const void* b, void* out, int64_t n, int d) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    if (d == F64) {
+      ((double*)out)[i] = ((const double*)a)[i] + ((const double*)b)[i];
+    } else if (d == F32) {
+      ((float*)out)[i] = ((const float*)a)[i] + ((const float*)b)[i];
+    } else {
+      float v = bf16_to_f32(((const bf16_t*)a)[i]) + bf16_to_f32(((const bf16_t*)b)[i]);
+      ((bf16_t*)out)[i] = f32_to_bf16(v);
+    }
+  }
+}
+
+__global__ void sum_middle_kernel(const void* x, void* out, int64_t outer, int64_t count, int64_t inner, int d) {
+  int64_t n = outer * inner;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    int64_t o = i / inner, j = i % inner;
+    if (d == F64) {
+      double s = 0;
+      for (int64_t c = 0; c < count; c++) s += ((const double*)x)[(o * count + c) * inner + j];
+      ((double*)out)[i] = s;
+    } else {
+      float s = 0;
+      for (int64_t c = 0; c < count; c++) s += (float)load_any(x, (o * count + c) * inner + j, d);
+      if (d == F32) ((float*)out)[i] = s;
+      else ((bf16_t*)out)[i] = f32_to_bf16(s);
+    }
+  }
+}
+
+// 32x32 tiles through LDS so both the read and the write are coalesced.
+template <class T>
+__global__ void transpose_kernel(const T* x, T* out, int64_t rows, int64_t cols, int64_t tiles_r, int64_t tiles_c) {
+  __shared__ T tile[32][33];
+  int64_t id = blockIdx.x;
+  int64_t z = id / (tiles_r * tiles_c), t = id % (tiles_r * tiles_c);
+  int64_t r0 = (t / tiles_c) * 32, c0 = (t % tiles_c) * 32;
+  x += z * rows * cols;
+  out += z * rows * cols;
+  int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+  for (int j = ty; j < 32; j += 8) {
+    int64_t r = r0 + j, c = c0 + tx;
+    if (r < rows && c < cols) tile[j][tx] = x[r * cols + c];
+  }
+  __syncthreads();
+  for (int j = ty; j < 32; j += 8) {
+    int64_t c = c0 + j, r = r0 + tx;
+    if (r < rows && c < cols) out[c * rows + r] = tile[tx][j];
+  }
+}
+
+// Row softmax, one workgroup per row.  Three passes over the row (max,
+// sum of exp, write) with the row kept in registers when it fits, so HBM
+// sees one read and one write of the row.
+template <class T, int PER>  // PER values per thread held in registers
+__global__ void __launch_bounds__(THREADS) softmax_rows_kernel(const T* x, T* out, int64_t rows, int64_t width,
+                                                               float scale) {
+  __shared__ float red[THREADS / 64];
+  int64_t row = blockIdx.x;
+  if (row >= rows) return;
+  const T* xr = x + row * width;
+  T* yr = out + row * width;
+  int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float v[PER];
+  float peak = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < PER; j++) {
+    int64_t at = tid + (int64_t)j * THREADS;
+    float f = -INFINITY;
+    if (at < width) {
+      if constexpr (sizeof(T) == 2) f = bf16_to_f32(xr[at]) * scale;
+      else f = (float)xr[at] * scale;
+    }
+    v[j] = f;
+    peak = fmaxf(peak, f);
+  }
+  for (int64_t at = tid + (int64_t)PER * THREADS; at < width; at += THREADS) {
+    float f;
+    if constexpr (sizeof(T) == 2) f = bf16_to_f32(xr[at]) * scale;
+    else f = (float)xr[at] * scale;
+    peak = fmaxf(peak, f);
+  }
+  for (int o = 32; o > 0; o >>= 1) peak = fmaxf(peak, __shfl_xor(peak, o));
+  if (lane == 0) red[wave] = peak;
+  __syncthreads();
+  peak = red[0];
+  for (int w = 1; w < THREADS / 64; w++) peak = fmaxf(peak, red[w]);
+  __syncthreads();
+  float total = 0.f;
+#pragma unroll
+  for (int j = 0; j < PER; j++) {
+    v[j] = __expf(v[j] - peak);
+    total += (tid + (int64_t)j * THREADS < width) ? v[j] : 0.f;
+  }
+  for (int64_t at = tid + (int64_t)PER * THREADS; at < width; at += THREADS) {
+    float f;
+    if constexpr (sizeof(T) == 2) f = bf16_to_f32(xr[at]) * scale;
+    else f = (float)xr[at] * scale;
+    total += __expf(f - peak);
+  }
+  for (int o = 32; o > 0; o >>= 1) total += __shfl_xor(total, o);
+  if (lane == 0) red[wave] = total;
+  __syncthreads();
+  total = 0.f;
+  for (int w = 0; w < THREADS / 64; w++) total += red[w];
+  float inv = 1.0f / total;
+#pragma unroll
+  for (int j = 0; j < PER; j++) {
+    int64_t at = tid + (int64_t)j * THREADS;
+    if (at < width) {
+      if constexpr (sizeof(T) == 2) yr[at] = f32_to_bf16(v[j] * inv);
+      else yr[at] = v[j] * inv;
+    }
+  }
+  for (int64_t at = tid + (int64_t)PER * THREADS; at < width; at += THREADS) {
+    float f;
+    if constexpr (sizeof(T) == 2) {
+      f = bf16_to_f32(xr[at]) * scale;
+      yr[at] = f32_to_bf16(__expf(f - peak) * inv);
+    } else {
+      f = (float)xr[at] * scale;
+      yr[at] = __expf(f - peak) * inv;
+    }
+  }
+}
+
+__global__ void softmax_rows_f64(const double* x, double* out, int64_t rows, int64_t width, double scale) {
+  __shared__ double red[THREADS];
+  int64_t row = blockIdx.x;
+  const double* xr = x + row * width;
+  double* yr = out + row * width;
+  int tid = threadIdx.x;
+  double peak = -INFINITY;
+  for (int64_t at = tid; at < width; at += THREADS) peak = fmax(peak, xr[at] * scale);
+  red[tid] = peak;
+  __syncthreads();
+  for (int s = THREADS / 2; s; s >>= 1) {
+    if (tid < s) red[tid] = fmax(red[tid], red[tid + s]);
+    __syncthreads();
+  }
+  peak = red[0];
+  __syncthreads();
+  double total = 0;
+  for (int64_t at = tid; at < width; at += THREADS) total += exp(xr[at] * scale - peak);
+  red[tid] = total;
+  __syncthreads();
+  for (int s = THREADS / 2; s; s >>= 1) {
+    if (tid < s) red[tid] += red[tid + s];
+    __syncthreads();
+  }
+  total = red[0];
+  for (int64_t at = tid; at < width; at += THREADS) yr[at] = exp(xr[at] * scale - peak) / total;
+}
+
+// silu as in lm_silu (lm.cu:54): s = v >= 0 ? 1/(1+e^-v) : e^v/(1+e^v).
+// With bf16 storage the silu output is itself a bf16 tensor before the
+// multiply (two roundings), as in the unfused SwiGLU of the reference.
+__device__ __forceinline__ float silu_f(float v) {
+  float s = v >= 0.f ? 1.f / (1.f + expf(-v)) : expf(v) / (1.f + expf(v));
+  return v * s;
+}
+__global__ void silu_mul_kernel(const void* g, const void* u, void* out, int64_t n, int d) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    if (d == BF16) {
+      float s = bf16_to_f32(f32_to_bf16(silu_f(bf16_to_f32(((const bf16_t*)g)[i]))));
+      ((bf16_t*)out)[i] = f32_to_bf16(s * bf16_to_f32(((const bf16_t*)u)[i]));
+    } else if (d == F32) {
+      ((float*)out)[i] = silu_f(((const float*)g)[i]) * ((const float*)u)[i];
+    } else {
+      double v = ((const double*)g)[i];
+      double s = v >= 0 ? 1.0 / (1.0 + exp(-v)) : exp(v) / (1.0 + exp(v));
+      ((double*)out)[i] = (v * s) * ((const double*)u)[i];
+    }
+  }
+}
+
+__global__ void add_rows_kernel(const void* x, const void* bias, void* out, int64_t rows, int64_t cols, int d) {
+  int64_t n = rows * cols;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    int64_t c = i % cols;
+    if (d == F64) {
+      ((double*)out)[i] = ((const double*)x)[i] + ((const double*)bias)[c];
+    } else if (d == F32) {
+      ((float*)out)[i] = ((const float*)x)[i] + ((const float*)bias)[c];
+    } else {
+      float v = bf16_to_f32(((const bf16_t*)x)[i]) + bf16_to_f32(((const bf16_t*)bias)[c]);
+      ((bf16_t*)out)[i] = f32_to_bf16(v);
+    }
+  }
+}
+
+bool float_dtype(int d) { return d == F32 || d == F64 || d == BF16; }
+
+}  // namespace
+
+extern "C" {
+
+int qutai_amd_cast(const void* src, void* dst, int64_t n, int src_dtype, int dst_dtype, void* stream) {
+  if (n < 0) return QA_EINVAL;
+  for (int d : {src_dtype, dst_dtype})
+    if (!float_dtype(d) && d != I64) return QA_EINVAL;
+  if (n == 0) return QA_OK;
+  hipLaunchKernelGGL(cast_kernel, dim3(grid_for(n)), dim3(THREADS), 0, (hipStream_t)stream, src, dst, n, src_dtype,
+                     dst_dtype);
+  return (int)hipGetLastError();
+}
+
+int qutai_amd_fill(void* dst, int64_t n, double value, int dtype, void* stream) {
+  if (n < 0 || (!float_dtype(dtype) && dtype != I64)) return QA_EINVAL;
+  if (n == 0) return QA_OK;
+  hipLaunchKernelGGL(fill_kernel, dim3(grid_for(n)), dim3(THREADS), 0, (hipStream_t)stream, dst, n, value, dtype);
+  return (int)hipGetLastError();
+}
+
+int qutai_amd_add(const void* left, const void* right, void* out, int64_t n, int dtype, void* stream) {
+  if (n < 0 || !float_dtype(dtype)) return QA_EINVAL;
+  if (n == 0) return QA_OK;
+  hipLaunchKernelGGL(add_kernel, dim3(grid_for(n)), dim3(THREADS), 0, (hipStream_t)stream, left, right, out, n,
+                     dtype);
+  return (int)hipGetLastError();
+}
+
+int qutai_amd_add_rows(const void* x, const void* bias, void* out, int64_t rows, int64_t cols, int dtype,
+                       void* stream) {
+  if (rows < 0 || cols < 0 || !float_dtype(dtype)) return QA_EINVAL;
+  if (rows * cols == 0) return QA_OK;
+  hipLaunchKernelGGL(add_rows_kernel, dim3(grid_for(rows * cols)), dim3(THREADS), 0, (hipStream_t)stream, x, bias,
+                     out, rows, cols, dtype);
+  return (int)hipGetLastError();
+}
+
+int qutai_amd_sum_middle(const void* x, void* out, int64_t outer, int64_t count, int64_t inner, int dtype,
+                         void* stream) {
+  if (outer < 0 || count < 0 || inner < 0 || !float_dtype(dtype)) return QA_EINVAL;
+  if (outer * inner == 0) return QA_OK;
+  hipLaunchKernelGGL(sum_middle_kernel, dim3(grid_for(outer * inner)), dim3(THREADS), 0, (hipStream_t)stream, x,
+                     out, outer, count, inner, dtype);
+  return (int)hipGetLastError();
+}
+
+int qutai_amd_transpose_last2(const void* x, void* out, int64_t batch, int64_t rows, int64_t cols, int dtype,
+                              void* stream) {
+  if (batch < 0 || rows < 0 || cols < 0 || !float_dtype(dtype)) return QA_EINVAL;
+  if (batch * rows * cols == 0) return QA_OK;
+  int64_t tr = (rows + 31) / 32, tc = (cols + 31) / 32;
+  int64_t blocks = batch * tr * tc;
+  if (blocks > 0x7fffffff) return QA_EINVAL;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == F64)
+    hipLaunchKernelGGL(transpose_kernel<double>, dim3((unsigned)blocks), dim3(256), 0, s, (const double*)x,
+                       (double*)out, rows, cols, tr, tc);
+  else if (dtype == F32)
+    hipLaunchKernelGGL(transpose_kernel<float>, dim3((unsigned)blocks), dim3(256), 0, s, (const float*)x,
+                       (float*)out, rows, cols, tr, tc);
+  else
+    hipLaunchKernelGGL(transpose_kernel<bf16_t>, dim3((unsigned)blocks), dim3(256), 0, s, (const bf16_t*)x,
+                       (bf16_t*)out, rows, cols, tr, tc);
+  return (int)hipGetLastError();
+}
+
+int qutai_amd_softmax_rows(const void* x, void* out, int64_t rows, int64_t width, double scale, int dtype,
+                           void* stream) {
+  if (rows < 0 || width < 0 || !float_dtype(dtype)) return QA_EINVAL;
+  if (rows == 0 || width == 0) return QA_OK;
+  if (rows > 0x7fffffff) return QA_EINVAL;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == F64)
+    hipLaunchKernelGGL(softmax_rows_f64, dim3((unsigned)rows), dim3(THREADS), 0, s, (const double*)x, (double*)out,
+                       rows, width, scale);
+  else if (dtype == F32)
+    hipLaunchKernelGGL((softmax_rows_kernel<float, 8>), dim3((unsigned)rows), dim3(THREADS), 0, s, (const float*)x,
+                       (float*)out, rows, width, (float)scale);
+  else
+    hipLaunchKernelGGL((softmax_rows_kernel<bf16_t, 8>), dim3((unsigned)rows), dim3(THREADS), 0, s,
+                       (const bf16_t*)x, (bf16_t*)out, rows, width, (float)scale);
+  return (int)hipGetLastError();
+}
+
+int qutai_amd_silu_mul(const void* gate, const void* up, void* out, int64_t n, int dtype, void* stream) {
+  if (n < 0 || !float_dtype(dtype)) return QA_EINVAL;
+  if (n == 0) return QA_OK;
+  hipLaunchKernelGGL(silu_mul_kernel, dim3(grid_for(n)), dim3(THREADS), 0, (hipStream_t)stream, gate, up, out, n,
+                     dtype);
+  return (int)hipGetLastError();
+}
+
+}  // extern "C"
