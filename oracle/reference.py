@@ -1,0 +1,261 @@
+"""TEST INFRASTRUCTURE ONLY — CPU parity oracle for the MI355X GEMM path.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` may import this module, and only as the checker (or, for the
+baseline, as the timed CPU restatement).  The product (``qutai_amd``) never
+imports it and has no CPU fallback.
+
+Contents
+  * pure-Python restatements of the reference CPU path, each citing the
+    reference file:line it follows: ``matmul`` (cpu.py:140-163), ``gemm``
+    (cpu_lm.py:11-42), ``softmax`` (cpu.py:250-260 with ``_axis_indices``
+    cpu.py:231-237), ``silu`` (cpu_lm.py:107-111), ``routing``
+    (cpu_lm.py:204-242), ``route_gather`` (cpu_lm.py:279-283), ``combine``
+    (cpu_lm.py:294-303), ``bf16`` (the RNE encoder of cuda.py:98-101 /
+    tests/test_bfloat16_storage.py:10-16);
+  * ``gemm_f64``: the same float64 sequential-k GEMM compiled from
+    ``oracle/gemm_f64.c`` (bit-identical to ``gemm``; used at sizes the
+    Python loop cannot finish);
+  * numpy helpers for bf16 rounding of whole arrays.
+
+How each function is pinned (tests/test_oracle.py): reference-test golden
+vectors and closed forms, agreement of the two independent GEMM
+restatements (Python loop vs C) bit for bit, numpy cross-checks within
+tolerance, brute-force routing invariants.  No function is left unpinned.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import struct
+import subprocess
+from math import exp, fsum, prod
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIBRARY = HERE / "_build" / "liboracle.so"
+
+
+# ---- pure-Python restatements ------------------------------------------------
+
+def bf16(value: float) -> float:
+    """fp32 -> bfloat16 -> fp32, round to nearest even (cuda.py:98-101)."""
+    bits = struct.unpack("<I", struct.pack("<f", value))[0]
+    if bits & 0x7FFFFFFF > 0x7F800000:
+        bits = (bits >> 16) | 0x40
+    else:
+        bits = (bits + 0x7FFF + ((bits >> 16) & 1)) >> 16
+    return struct.unpack("<f", struct.pack("<I", bits << 16))[0]
+
+
+def _broadcast_shape(left, right):
+    result = []
+    for i in range(max(len(left), len(right))):
+        a = left[-1 - i] if i < len(left) else 1
+        b = right[-1 - i] if i < len(right) else 1
+        if a != b and 1 not in (a, b):
+            raise ValueError(f"shapes {left} and {right} cannot be broadcast")
+        result.append(max(a, b) if 1 in (a, b) else a)
+    return tuple(reversed(result))
+
+
+def _strides(shape):
+    return tuple(prod(shape[axis + 1:]) for axis in range(len(shape)))
+
+
+def matmul(left, right, left_shape, right_shape) -> list[float]:
+    """cpu.matmul (src/qutai/backends/cpu.py:140-163): vectors promoted,
+    batch axes broadcast, float64 sum with k = 0..K-1 in order."""
+    if len(left_shape) == 1:
+        left_shape = (1, *left_shape)
+    if len(right_shape) == 1:
+        right_shape = (*right_shape, 1)
+    batches = _broadcast_shape(left_shape[:-2], right_shape[:-2])
+    left_shape = (1,) * (len(batches) + 2 - len(left_shape)) + tuple(left_shape)
+    right_shape = (1,) * (len(batches) + 2 - len(right_shape)) + tuple(right_shape)
+    left_steps, right_steps = _strides(left_shape), _strides(right_shape)
+    rows, inner = left_shape[-2:]
+    columns = right_shape[-1]
+    result = [0.0] * (prod(batches) * rows * columns)
+    from itertools import product as coordinates
+    for batch, coordinate in enumerate(coordinates(*(range(size) for size in batches))):
+        left_start = right_start = 0
+        for axis, position in enumerate(coordinate):
+            if left_shape[axis] != 1:
+                left_start += position * left_steps[axis]
+            if right_shape[axis] != 1:
+                right_start += position * right_steps[axis]
+        for row in range(rows):
+            for column in range(columns):
+                total = 0.0
+                for k in range(inner):
+                    total += left[left_start + row * inner + k] * right[right_start + k * columns + column]
+                result[(batch * rows + row) * columns + column] = total
+    return result
+
+
+def gemm(a, b, rows, inner, cols, *, transpose_left=False, transpose_right=False, out=None, accumulate=False):
+    """cpu_lm.gemm (src/qutai/backends/cpu_lm.py:11-42)."""
+    if accumulate and out is None:
+        raise ValueError("accumulate needs out")
+    result = list(out) if out is not None else [0.0] * (rows * cols)
+    for i in range(rows):
+        for j in range(cols):
+            value = 0.0
+            for k in range(inner):
+                value += (a[k * rows + i if transpose_left else i * inner + k]
+                          * b[j * inner + k if transpose_right else k * cols + j])
+            result[i * cols + j] = value + result[i * cols + j] if accumulate else value
+    return result
+
+
+def _axis_indices(shape, axis):
+    """cpu._axis_indices (src/qutai/backends/cpu.py:231-237)."""
+    axis %= len(shape)
+    step = prod(shape[axis + 1:])
+    width = shape[axis] * step
+    return (range(outer * width + offset, (outer + 1) * width + offset, step)
+            for outer in range(prod(shape[:axis])) for offset in range(step))
+
+
+def softmax(values, shape, axis) -> list[float]:
+    """cpu.softmax (src/qutai/backends/cpu.py:250-260): subtract the group
+    maximum, exponentiate, divide by the fsum."""
+    result = [0.0] * len(values)
+    for indices in _axis_indices(shape, axis):
+        items = [values[index] for index in indices]
+        peak = max(items)
+        weights = [exp(value - peak) for value in items]
+        total = fsum(weights)
+        for index, weight in zip(indices, weights):
+            result[index] = weight / total
+    return result
+
+
+def silu(values) -> list[float]:
+    """cpu_lm.silu (src/qutai/backends/cpu_lm.py:107-111)."""
+    return [x * (1 / (1 + exp(-x)) if x >= 0 else exp(x) / (1 + exp(x))) for x in values]
+
+
+def routing(scores, rows, experts, top_k) -> dict:
+    """cpu_lm.routing (src/qutai/backends/cpu_lm.py:204-242): float64 softmax
+    of the scores, experts sorted by descending probability (stable: lower
+    index first on ties), weights renormalised over the top_k, per-expert
+    (token, slot) lists in token order, utilization and the aux loss."""
+    probs = softmax(scores, (rows, experts), 1)
+    weights = [0.0] * (rows * top_k)
+    indices = [0] * (rows * top_k)
+    token_ids = [[] for _ in range(experts)]
+    slot_ids = [[] for _ in range(experts)]
+    for row in range(rows):
+        selected = sorted(range(experts), key=lambda e: probs[row * experts + e], reverse=True)[:top_k]
+        total = sum(probs[row * experts + e] for e in selected)
+        for slot, e in enumerate(selected):
+            indices[row * top_k + slot] = e
+            weights[row * top_k + slot] = probs[row * experts + e] / total
+            token_ids[e].append(row)
+            slot_ids[e].append(slot)
+    counts = tuple(map(len, token_ids))
+    utilization = [c / (rows * top_k) for c in counts]
+    aux = experts * sum(utilization[e] * sum(probs[row * experts + e] for row in range(rows)) / rows
+                        for e in range(experts))
+    return dict(probs=probs, weights=weights, indices=indices, counts=counts, ids=token_ids, slots=slot_ids,
+                utilization=utilization, aux=aux, rows=rows, experts=experts, top_k=top_k)
+
+
+def route_gather(values, route, expert, width) -> list[float]:
+    """cpu_lm.route_gather (src/qutai/backends/cpu_lm.py:279-283)."""
+    return [values[row * width + j] for row in route["ids"][expert] for j in range(width)]
+
+
+def combine(outputs, weights, route, width) -> list[float]:
+    """cpu_lm.combine (src/qutai/backends/cpu_lm.py:294-303): expert-major
+    weighted scatter-add."""
+    result = [0.0] * (route["rows"] * width)
+    for expert, values in outputs:
+        for i, (row, slot) in enumerate(zip(route["ids"][expert], route["slots"][expert])):
+            factor = weights[row * route["top_k"] + slot]
+            for j in range(width):
+                result[row * width + j] += factor * values[i * width + j]
+    return result
+
+
+# ---- compiled float64 GEMM -----------------------------------------------------
+
+_lib = None
+
+
+def build() -> Path:
+    """Compile oracle/gemm_f64.c (gcc, -ffp-contract=off) into oracle/_build."""
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIBRARY
+
+
+def _library():
+    global _lib
+    if _lib is None:
+        if not LIBRARY.exists():
+            build()
+        lib = ctypes.CDLL(str(LIBRARY))
+        lib.oracle_gemm_f64.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int64] * 3 + [ctypes.c_int] * 3 + [
+            ctypes.c_void_p, ctypes.c_int64, ctypes.c_int]
+        lib.oracle_gemm_f64.restype = ctypes.c_int
+        lib.oracle_bf16_round.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
+        lib.oracle_bf16_round.restype = None
+        _lib = lib
+    return _lib
+
+
+def gemm_f64(a, b, rows, inner, cols, *, transpose_left=False, transpose_right=False, row_list=None, out=None,
+             accumulate=False, threads=None) -> np.ndarray:
+    """Compiled restatement of ``gemm`` (bit-identical).  ``a``/``b`` are
+    float64 arrays in the reference layouts; ``row_list`` restricts the
+    output to those rows (result shape [len(row_list), cols])."""
+    a = np.ascontiguousarray(a, dtype=np.float64).ravel()
+    b = np.ascontiguousarray(b, dtype=np.float64).ravel()
+    if a.size < rows * inner or b.size < inner * cols:
+        raise ValueError("operand too small")
+    selected = None if row_list is None else np.ascontiguousarray(row_list, dtype=np.int64)
+    n = rows if selected is None else selected.size
+    result = np.zeros((n, cols)) if out is None else np.array(out, dtype=np.float64).reshape(n, cols)
+    threads = threads or min(16, os.cpu_count() or 1)
+    status = _library().oracle_gemm_f64(
+        a.ctypes.data, b.ctypes.data, result.ctypes.data, rows, inner, cols, int(transpose_left),
+        int(transpose_right), int(accumulate), None if selected is None else selected.ctypes.data, n, threads)
+    if status:
+        raise MemoryError("oracle allocation failed")
+    return result
+
+
+def bf16_round_c(x: np.ndarray) -> np.ndarray:
+    """C restatement of the RNE encoder; returns the bf16 words."""
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    y = np.empty(x.size, dtype=np.uint16)
+    _library().oracle_bf16_round(x.ctypes.data, y.ctypes.data, x.size)
+    return y
+
+
+def bf16_words(x: np.ndarray) -> np.ndarray:
+    """numpy restatement of the RNE encoder (fp32 -> bf16 words)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    rounded = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    return np.where(nan, (u >> 16) | 0x40, rounded).astype(np.uint16)
+
+
+def bf16_values(words: np.ndarray) -> np.ndarray:
+    """bf16 words -> fp32 values (exact)."""
+    return (np.asarray(words, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def bf16_round_array(x: np.ndarray) -> np.ndarray:
+    return bf16_values(bf16_words(x)).reshape(np.shape(x))
+
+
+def rel_frobenius(got, ref) -> float:
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    denominator = np.linalg.norm(ref)
+    return float(np.linalg.norm(got - ref) / denominator) if denominator else float(np.linalg.norm(got - ref))

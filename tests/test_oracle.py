@@ -1,0 +1,237 @@
+"""Pins the CPU oracle before it is trusted as the parity reference.
+
+Each oracle function is checked against the reference's own known-answer
+tests (golden vectors, cited per test), against what mathematics fixes
+(closed forms, invariants), and against an independent restatement (the
+Python loop vs the compiled C loop, bit for bit; numpy within tolerance),
+chosen so that a dropped term, a swapped index or a transposed operand
+fails at least one check.
+"""
+import math
+import random
+
+import numpy as np
+import pytest
+
+from oracle import reference as ora
+
+
+# ---- GEMM / matmul --------------------------------------------------------------
+
+def test_matmul_golden_vectors_from_reference_tests():
+    # tests/test_batched_matmul.py:28-37
+    assert ora.matmul([1, 2, 3], [4, 5, 6], (3,), (3,)) == [32]
+    assert ora.matmul([1, 2], [3, 4, 5, 6, 7, 8], (2,), (2, 3)) == [15, 18, 21]
+    assert ora.matmul([1, 2, 3, 4], [5, 6], (2, 2), (2,)) == [17, 39]
+    # tests/test_batched_matmul.py:39-42
+    matrices = [1, 2, 3, 4, 5, 6, 7, 8]
+    assert ora.matmul([1, 2], matrices, (2,), (2, 2, 2)) == [7, 10, 19, 22]
+    assert ora.matmul(matrices, [1, 2], (2, 2, 2), (2,)) == [5, 11, 17, 23]
+    # tests/test_gemm_precision.py:86-90: left broadcast over a batch of 2
+    assert ora.matmul([1, 2, 3, 4, 5, 6], [1, 2, 3, 4, 5, 6, 6, 5, 4, 3, 2, 1], (2, 3), (2, 3, 2)) == [
+        22, 28, 49, 64, 20, 14, 56, 41]
+
+
+def test_matmul_batch_broadcast_does_not_mix_matrices():
+    # tests/test_batched_matmul.py:44-53, brute force over both broadcast axes
+    left = list(range(1, 13))
+    right = list(range(1, 19))
+    a = np.array(left, dtype=float).reshape(2, 1, 2, 3)
+    b = np.array(right, dtype=float).reshape(1, 3, 3, 2)
+    expected = [sum(a[g][0][r][k] * b[0][z][k][c] for k in range(3))
+                for g in range(2) for z in range(3) for r in range(2) for c in range(2)]
+    assert ora.matmul(left, right, (2, 1, 2, 3), (1, 3, 3, 2)) == expected
+
+
+def test_accumulation_order_is_sequential_k():
+    # tests/test_batched_matmul.py:105-106: (1e16 + 1) - 1e16 == 0 only in order
+    assert ora.matmul([1e16, 1, -1e16], [1, 1, 1], (1, 3), (3, 1)) == [0.0]
+    out = ora.gemm_f64(np.array([1e16, 1, -1e16]), np.array([1.0, 1, 1]), 1, 3, 1)
+    assert out.tolist() == [[0.0]]
+
+
+def test_linear_known_answers_through_matmul():
+    # tests/test_layers.py:23-33: X @ W + b with W stored (in, out)
+    w = [1, 2, 3, 4, 5, 6]
+    x = [1, 2, -1, 0]
+    y = ora.matmul(x, w, (2, 2), (2, 3))
+    bias = [0.5, -0.5, 1]
+    assert [v + bias[i % 3] for i, v in enumerate(y)] == [9.5, 11.5, 16, -0.5, -2.5, -2]
+    # tests/test_layers.py:35-43: gradients of sum(X @ W + b)
+    ones = [1.0] * 4
+    dx = ora.gemm(ones, [1, 2, 3, 4], 2, 2, 2, transpose_right=True)
+    dw = ora.gemm([1, 2, 3, 4], ones, 2, 2, 2, transpose_left=True)
+    assert dx == [3, 7, 3, 7]
+    assert dw == [4, 4, 6, 6]
+
+
+def test_gemm_transposes_follow_the_reference_index_maps():
+    rng = random.Random(11)
+    m, k, n = 3, 4, 5
+    a = [rng.uniform(-1, 1) for _ in range(m * k)]
+    b = [rng.uniform(-1, 1) for _ in range(k * n)]
+    A, B = np.array(a).reshape(m, k), np.array(b).reshape(k, n)
+    for ta in (False, True):
+        for tb in (False, True):
+            a_in = (A.T if ta else A).ravel().tolist()
+            b_in = (B.T if tb else B).ravel().tolist()
+            got = ora.gemm(a_in, b_in, m, k, n, transpose_left=ta, transpose_right=tb)
+            assert np.allclose(np.array(got).reshape(m, n), A @ B, rtol=1e-13, atol=1e-13)
+
+
+def test_python_and_compiled_gemm_agree_bit_for_bit():
+    rng = np.random.default_rng(5)
+    for (m, k, n) in [(7, 13, 5), (16, 64, 9), (1, 1, 1), (3, 0, 2)]:
+        for ta in (False, True):
+            for tb in (False, True):
+                a = rng.standard_normal(m * k)
+                b = rng.standard_normal(k * n)
+                old = rng.standard_normal(m * n)
+                for accumulate in (False, True):
+                    py = ora.gemm(a.tolist(), b.tolist(), m, k, n, transpose_left=ta, transpose_right=tb,
+                                  out=old.tolist() if accumulate else None, accumulate=accumulate)
+                    c = ora.gemm_f64(a, b, m, k, n, transpose_left=ta, transpose_right=tb,
+                                     out=old if accumulate else None, accumulate=accumulate)
+                    assert c.ravel().tolist() == py
+
+
+def test_compiled_gemm_row_subset_and_threads_do_not_change_bits():
+    rng = np.random.default_rng(6)
+    m, k, n = 37, 300, 23
+    a, b = rng.standard_normal(m * k), rng.standard_normal(k * n)
+    full = ora.gemm_f64(a, b, m, k, n, threads=1)
+    rows = [0, 5, 36, 17]
+    part = ora.gemm_f64(a, b, m, k, n, row_list=rows, threads=3)
+    assert np.array_equal(part, full[rows])
+    assert np.array_equal(ora.gemm_f64(a, b, m, k, n, threads=7), full)
+    assert np.allclose(full, a.reshape(m, k) @ b.reshape(k, n), rtol=1e-12, atol=1e-12)
+
+
+def test_long_reduction_closed_form():
+    # tests/test_gemm_precision.py:191-206 in miniature: 0.5 * -0.25 summed k times
+    k = 8193
+    out = ora.gemm_f64(np.full(2 * k, 0.5), np.full(k * 3, -0.25), 2, k, 3, out=np.full(6, 0.25), accumulate=True)
+    assert (out == -k * 0.125 + 0.25).all()
+
+
+# ---- bf16 ---------------------------------------------------------------------
+
+def test_bf16_rounding_golden_values():
+    # tests/test_bfloat16_storage.py:20-24 inputs; the expected values follow
+    # from round-to-nearest-even: 1 + 2^-8 is a tie between 1 and 1 + 2^-7
+    # (even mantissa 1), 1 + 3*2^-8 a tie between 1 + 2^-7 and 1 + 2^-6.
+    assert ora.bf16(1.00390625) == 1.0
+    assert ora.bf16(1.01171875) == 1.015625
+    assert ora.bf16(0.0) == 0.0 and math.copysign(1, ora.bf16(-0.0)) == -1
+    assert ora.bf16(-2.71828) == -2.71875
+    assert ora.bf16(1e30) == 202 * 2.0 ** 92  # 1e30 = 201.93 ulps of 2^92 -> 202
+    assert ora.bf16(math.inf) == math.inf and ora.bf16(-math.inf) == -math.inf
+    assert math.isnan(ora.bf16(math.nan))
+    # tests/test_gemm_precision.py:99-112 autocast values
+    assert [ora.bf16(x) for x in (0.1, 0.2, 0.3, 0.4)] == [0.10009765625, 0.2001953125, 0.30078125, 0.400390625]
+
+
+def test_bf16_three_restatements_agree():
+    rng = np.random.default_rng(7)
+    x = np.concatenate([rng.standard_normal(4000) * 10.0 ** rng.integers(-30, 30, 4000),
+                        np.array([0, -0.0, np.inf, -np.inf, np.nan, 1.00390625, 1.01171875], np.float32)])
+    x = x.astype(np.float32)
+    words_np = ora.bf16_words(x)
+    words_c = ora.bf16_round_c(x)
+    assert np.array_equal(words_np, words_c)
+    py = [ora.bf16(float(v)) for v in x]
+    vals = ora.bf16_values(words_np)
+    for got, want in zip(vals.tolist(), py):
+        assert (math.isnan(got) and math.isnan(want)) or got == want
+    # every rounded value is within half a bf16 ulp (2^-8 relative) of its input
+    finite = np.isfinite(x) & (x != 0)
+    rel = np.abs(vals[finite].astype(np.float64) - x[finite]) / np.abs(x[finite].astype(np.float64))
+    assert rel.max() <= 2.0 ** -8
+
+
+# ---- softmax / silu -------------------------------------------------------------
+
+def test_softmax_known_answer_and_invariants():
+    # tests/test_attention.py:10-22: scores [1/sqrt2, 0] -> e^(1/sqrt2)/(e^(1/sqrt2)+1)
+    p = math.exp(1 / math.sqrt(2)) / (math.exp(1 / math.sqrt(2)) + 1)
+    got = ora.softmax([1 / math.sqrt(2), 0.0, 0.0, 1 / math.sqrt(2)], (2, 2), 1)
+    assert got == pytest.approx([p, 1 - p, 1 - p, p], rel=1e-15)
+    rng = random.Random(3)
+    row = [rng.gauss(0, 3) for _ in range(50)]
+    out = ora.softmax(row, (1, 50), 1)
+    assert math.fsum(out) == pytest.approx(1.0, abs=1e-15)
+    shifted = ora.softmax([v + 1000 for v in row], (1, 50), 1)
+    assert shifted == pytest.approx(out, rel=1e-12)
+    # axis other than the last walks the strided groups
+    two = ora.softmax([0.0, 1.0, 2.0, 3.0], (2, 2), 0)
+    q = 1 / (1 + math.exp(2))
+    assert two == pytest.approx([q, q, 1 - q, 1 - q], rel=1e-15)
+
+
+def test_silu_closed_forms():
+    xs = [-30.0, -2.0, -0.5, 0.0, 0.5, 2.0, 30.0]
+    ys = ora.silu(xs)
+    assert ys[3] == 0.0
+    for x, y in zip(xs, ys):
+        assert y == pytest.approx(x / (1 + math.exp(-x)), rel=1e-14)
+    # silu(x) - silu(-x) = x
+    for x in (0.3, 1.7, 5.0):
+        a, b = ora.silu([x, -x])
+        assert a - b == pytest.approx(x, rel=1e-14)
+
+
+# ---- routing / gather / combine --------------------------------------------------
+
+def test_routing_golden_vector():
+    # tests/test_lm_moe.py:65-71
+    route = ora.routing([3.0, 2.0, -1.0, -1.0, 2.0, 3.0], 2, 3, 2)
+    assert route["indices"] == [0, 1, 2, 1]
+    assert route["counts"] == (1, 2, 1)
+    assert sum(route["weights"][:2]) == pytest.approx(1)
+    assert sum(route["weights"][2:]) == pytest.approx(1)
+    assert route["ids"] == [[0], [0, 1], [1]]
+    assert route["slots"] == [[0], [1, 1], [0]]
+
+
+def test_routing_brute_force_invariants():
+    # the 517 x 5 x 3 case of tests/test_lm_moe.py:140-147, checked against a
+    # direct brute-force definition of each output
+    rows, experts, top_k = 517, 5, 3
+    scores = [((row * 37 + expert * 11) % 101) / 13 for row in range(rows) for expert in range(experts)]
+    route = ora.routing(scores, rows, experts, top_k)
+    for row in range(rows):
+        s = scores[row * experts:(row + 1) * experts]
+        # lexicographic (value desc, index asc) order = stable descending sort
+        order = sorted(range(experts), key=lambda e: (-s[e], e))[:top_k]
+        assert route["indices"][row * top_k:(row + 1) * top_k] == order
+        w = route["weights"][row * top_k:(row + 1) * top_k]
+        assert math.fsum(w) == pytest.approx(1, abs=1e-15)
+        assert w == sorted(w, reverse=True)
+    for e in range(experts):
+        pairs = [(r, slot) for r in range(rows) for slot in range(top_k) if route["indices"][r * top_k + slot] == e]
+        assert route["ids"][e] == [r for r, _ in pairs]
+        assert route["slots"][e] == [slot for _, slot in pairs]
+    assert sum(route["counts"]) == rows * top_k
+    util = route["utilization"]
+    probs = route["probs"]
+    aux = experts * math.fsum(util[e] * math.fsum(probs[r * experts + e] for r in range(rows)) / rows
+                              for e in range(experts))
+    assert route["aux"] == pytest.approx(aux, rel=1e-12)
+
+
+def test_gather_and_combine_round_trip():
+    rng = random.Random(9)
+    rows, experts, top_k, width = 11, 4, 2, 3
+    scores = [rng.gauss(0, 1) for _ in range(rows * experts)]
+    route = ora.routing(scores, rows, experts, top_k)
+    x = [rng.gauss(0, 1) for _ in range(rows * width)]
+    outputs = [(e, ora.route_gather(x, route, e, width)) for e in range(experts) if route["counts"][e]]
+    for e, values in outputs:
+        for i, row in enumerate(route["ids"][e]):
+            assert values[i * width:(i + 1) * width] == x[row * width:(row + 1) * width]
+    # identity experts: combine returns x scaled by the weight sum (= 1)
+    y = ora.combine(outputs, route["weights"], route, width)
+    assert y == pytest.approx(x, rel=1e-12, abs=1e-12)
+    # a single unit weight reproduces the expert rows exactly
+    one = dict(route, top_k=1, ids=[[0, 2]], slots=[[0, 0]], rows=3)
+    assert ora.combine([(0, [1.0, 2.0, 3.0, 4.0])], [1.0, 0.0, 1.0], one, 2) == [1.0, 2.0, 0.0, 0.0, 3.0, 4.0]
