@@ -1,0 +1,273 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X GEMM hot path (BASELINE.json metric).
+
+Step = one bf16-storage 4096^3 GEMM (fp32 accumulation, fp32 output) through
+the amd backend's ``gemm`` (the largest single-GPU
+config the headline is quoted on).  W untimed warm-up steps, then K steps
+timed with HIP events on the default stream (the stream every kernel runs
+on) between two device synchronisations.  The JSON line also carries the
+other configs (fp32 4096^3, the ragged shape, attention bmm, dense Linear
+fwd/bwd, MoE grouped experts) measured the same way, the roofline of the
+dominant kernel and the CPU baseline (the pure-Python float64 restatement
+of the reference CPU GEMM, timed on a bounded sample on this host).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only NAME]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+from array import array
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "TFLOP/s + % MFMA peak: fp32/bf16 GEMM 4096^3, attention bmm, MoE grouped GEMM"
+PEAK = {"bf16": 2516.6, "fp32": 157.3}  # dense MFMA TFLOP/s of MI355X (AMD spec)
+HBM_PEAK = 8000.0  # GB/s
+
+
+def upload(x, dtype):
+    from qutai_amd.backends import amd
+
+    return amd.storage(array("f", np.ascontiguousarray(x, dtype=np.float32).tobytes()), dtype=dtype)
+
+
+class Timer:
+    """HIP events on the default stream around a block of launches."""
+
+    def __init__(self, runtime):
+        self.runtime = runtime
+        self.start, self.end = runtime.event(), runtime.event()
+
+    def time(self, fn, steps, warmup):
+        for _ in range(warmup):
+            fn()
+        self.runtime.synchronize()
+        wall = time.perf_counter()
+        self.runtime.record(self.start)
+        for _ in range(steps):
+            fn()
+        self.runtime.record(self.end)
+        self.runtime.synchronize()
+        wall = time.perf_counter() - wall
+        return self.runtime.elapsed_ms(self.start, self.end) / steps, wall * 1e3 / steps
+
+
+# ---- workloads -----------------------------------------------------------------
+
+def gemm_square(dtype, n=4096, seed=1):
+    from qutai_amd.backends import amd
+
+    rng = np.random.default_rng(seed)
+    a = upload(rng.standard_normal(n * n) * n ** -0.5, dtype)
+    b = upload(rng.standard_normal(n * n) * n ** -0.5, dtype)
+    out = amd.full(n * n, 0.0, dtype="float32")
+    flops = 2.0 * n ** 3
+    return (lambda: amd.gemm(a, b, n, n, n, out=out)), flops, {"M": n, "N": n, "K": n, "storage": dtype,
+                                                               "layout": "row-major A@B (NN)", "out": "float32"}
+
+
+def gemm_ragged(dtype, seed=1):
+    from qutai_amd.backends import amd
+
+    m, n, k = 4095, 4097, 1000
+    rng = np.random.default_rng(seed)
+    a = upload(rng.standard_normal(m * k) * k ** -0.5, dtype)
+    b = upload(rng.standard_normal(k * n) * k ** -0.5, dtype)
+    out = amd.full(m * n, 0.0, dtype="float32")
+    return (lambda: amd.gemm(a, b, m, k, n, out=out)), 2.0 * m * n * k, {"M": m, "N": n, "K": k, "storage": dtype}
+
+
+def attention_bmm(seed=2):
+    """S = Q K^T (NT, batched 128), P = softmax(S / 8) rows, O = P V (NN)."""
+    from qutai_amd.backends import amd
+
+    b, h, t, d = 8, 16, 2048, 64
+    rng = np.random.default_rng(seed)
+    q = upload(rng.standard_normal(b * h * t * d), "bfloat16")
+    k = upload(rng.standard_normal(b * h * t * d), "bfloat16")
+    v = upload(rng.standard_normal(b * h * t * d), "bfloat16")
+    s = amd.full(b * h * t * t, 0.0, dtype="bfloat16")
+    o = amd.full(b * h * t * d, 0.0, dtype="bfloat16")
+
+    def step():
+        amd.gemm(q, k, t, d, t, batch=b * h, transpose_right=True, out_dtype="bfloat16", out=s)
+        p = amd.softmax(s, (b * h * t, t), -1, scale=d ** -0.5)
+        amd.gemm(p, v, t, t, d, batch=b * h, out_dtype="bfloat16", out=o)
+
+    return step, 2 * 2.0 * b * h * t * t * d, {"batch": b, "heads": h, "seq": t, "head_dim": d, "storage": "bfloat16"}
+
+
+def dense_linear(seed=3):
+    """SwiGLU projections of a 4096-token batch: Y = X W^T, dX = dY W, dW = dY^T X (x3)."""
+    from qutai_amd.backends import amd
+
+    tokens, width, hidden = 4096, 2048, 5632
+    rng = np.random.default_rng(seed)
+    x = upload(rng.standard_normal(tokens * width), "bfloat16")
+    w_in = [upload(rng.standard_normal(hidden * width) * 0.02, "bfloat16") for _ in range(2)]
+    w_down = upload(rng.standard_normal(width * hidden) * 0.02, "bfloat16")
+    g_hidden = upload(rng.standard_normal(tokens * hidden), "bfloat16")
+    h_act = upload(rng.standard_normal(tokens * hidden), "bfloat16")
+    g_out = upload(rng.standard_normal(tokens * width), "bfloat16")
+
+    def step():
+        for w in w_in:  # gate / up: X [T,d] W^T [h,d]
+            amd.gemm(x, w, tokens, width, hidden, transpose_right=True, out_dtype="bfloat16")
+            amd.gemm(g_hidden, w, tokens, hidden, width, out_dtype="bfloat16")
+            amd.gemm(g_hidden, x, hidden, tokens, width, transpose_left=True, out_dtype="bfloat16")
+        amd.gemm(h_act, w_down, tokens, hidden, width, transpose_right=True, out_dtype="bfloat16")
+        amd.gemm(g_out, w_down, tokens, width, hidden, out_dtype="bfloat16")
+        amd.gemm(g_out, h_act, width, tokens, hidden, transpose_left=True, out_dtype="bfloat16")
+
+    return step, 9 * 2.0 * tokens * width * hidden, {"tokens": tokens, "d_model": width, "ffn": hidden,
+                                                      "storage": "bfloat16", "gemms": 9}
+
+
+def moe_experts(seed=4):
+    """Routing + gather + grouped gate/up/down + SiLU*up + combine (forward)."""
+    from qutai_amd.backends import amd
+    from qutai_amd.backends import amd_lm
+
+    tokens, width, experts, hidden, top_k = 8192, 2048, 8, 1408, 2
+    rng = np.random.default_rng(seed)
+    x = upload(rng.standard_normal(tokens * width), "bfloat16")
+    logits = upload(rng.standard_normal(tokens * experts), "float32")
+    w_gate = upload(rng.standard_normal(experts * hidden * width) * 0.02, "bfloat16")
+    w_up = upload(rng.standard_normal(experts * hidden * width) * 0.02, "bfloat16")
+    w_down = upload(rng.standard_normal(experts * width * hidden) * 0.02, "bfloat16")
+
+    def step():
+        route = amd_lm.routing(logits, tokens, experts, top_k, download_counts=False)
+        amd_lm.moe_experts_forward(x, route, w_gate, w_up, w_down, width, hidden)
+
+    flops = 2.0 * tokens * top_k * 3 * width * hidden
+    return step, flops, {"tokens": tokens, "d_model": width, "experts": experts, "top_k": top_k,
+                         "hidden": hidden, "storage": "bfloat16"}
+
+
+WORKLOADS = {
+    "gemm_bf16_4096": (lambda: gemm_square("bfloat16"), "bf16"),
+    "gemm_fp32_4096": (lambda: gemm_square("float32"), "fp32"),
+    "gemm_bf16_ragged": (lambda: gemm_ragged("bfloat16"), "bf16"),
+    "gemm_fp32_ragged": (lambda: gemm_ragged("float32"), "fp32"),
+    "attention_bmm": (attention_bmm, "bf16"),
+    "dense_linear_fwd_bwd": (dense_linear, "bf16"),
+    "moe_grouped": (moe_experts, "bf16"),
+}
+HEADLINE = "gemm_bf16_4096"
+
+
+def traffic_from_profiles(name):
+    """HBM bytes per launch of the headline kernel, from the committed
+    rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, copy-kernel scaled)."""
+    path = ROOT / "profiles" / f"{name}_traffic.md"
+    if not path.exists():
+        return None
+    match = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", path.read_text())
+    return float(match.group(1)) if match else None
+
+
+def cpu_baseline(seconds_target=15.0):
+    """Pure-Python float64 restatement of the reference CPU GEMM
+    (src/qutai/backends/cpu.py:152-162) on the first rows of the 4096^3
+    product, one core; scaled to TFLOP/s by the FLOPs of the sample."""
+    from oracle import reference as ora
+
+    n = 4096
+    rng = np.random.default_rng(1)
+    a = (rng.standard_normal(n * n) * n ** -0.5).astype(np.float32).astype(np.float64)
+    b = (rng.standard_normal(n * n) * n ** -0.5).astype(np.float32).astype(np.float64)
+    left_rows = a.reshape(n, n)
+    right = b.tolist()
+    rows = 1
+    elapsed = 0.0
+    done_rows = 0
+    while elapsed < seconds_target and done_rows < 64:
+        sample = left_rows[done_rows:done_rows + rows].ravel().tolist()
+        start = time.perf_counter()
+        ora.matmul(sample, right, (rows, n), (n, n))
+        elapsed += time.perf_counter() - start
+        done_rows += rows
+    flops = 2.0 * done_rows * n * n
+    return {"value": flops / elapsed / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"first {done_rows} rows of C = A@B, 4096^3 float64 (cpu.matmul restated, oracle/reference.py),"
+                      f" {flops / 1e9:.2f} GFLOP in {elapsed:.1f} s on 1 of {os.cpu_count()} host cores"}
+
+
+def main():
+    parser = argparse.ArgumentParser()
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--only", default=None, help="run one workload")
+    parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = parser.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the GEMM path is single-device (see DESIGN.md for how it would shard)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    from qutai_amd.backends import amd
+
+    runtime = amd.get_runtime()
+    timer = Timer(runtime)
+    names = [args.only] if args.only else list(WORKLOADS)
+    results = {}
+    for name in names:
+        make, kind = WORKLOADS[name]
+        try:
+            fn, flops, config = make()
+        except (AttributeError, ImportError, NotImplementedError) as error:
+            results[name] = {"error": f"not available: {error}"}
+            continue
+        steps = args.steps if name == HEADLINE else max(3, args.steps // 2)
+        ms, wall_ms = timer.time(fn, steps, args.warmup)
+        tflops = flops / (ms * 1e-3) / 1e12
+        results[name] = {"ms": round(ms, 4), "wall_ms": round(wall_ms, 4), "tflops": round(tflops, 1),
+                         "peak_frac": round(tflops / PEAK[kind], 4), "dtype": kind, **config}
+        print(f"# {name}: {ms * 1e3:.1f} us/step  {tflops:.1f} TFLOP/s  ({100 * tflops / PEAK[kind]:.1f}% of "
+              f"{kind} peak)", file=sys.stderr, flush=True)
+        del fn
+    head = results.get(HEADLINE, {})
+    ms = head.get("ms")
+    value = head.get("tflops")
+    traffic = traffic_from_profiles(HEADLINE)
+    line = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (numpy PCG64 draws, N(0,1)*K^-1/2, seed 1); inputs resident in HBM",
+        "config": {"workload": HEADLINE, "M": 4096, "N": 4096, "K": 4096, "storage": "bfloat16",
+                   "accumulate": "float32", "out": "float32", "layout": "row-major A@B"},
+        "roofline": None,
+        "results": results,
+    }
+    if value is not None:
+        line["roofline"] = {"bound": "mfma", "achieved": value, "peak": PEAK["bf16"], "unit": "TFLOP/s",
+                            "frac": round(value / PEAK["bf16"], 4), "traffic": traffic,
+                            "kernel": "gemm_entry<GemmKernel<bf16,NN,256x256>>",
+                            "algorithmic_flops_per_launch": 2 * 4096 ** 3}
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -123,6 +123,13 @@ int qutai_amd_softmax_rows(const void* x, void* out, int64_t rows, int64_t width
  * elementwise multiply of SwiGLU (src/qutai/lm/layers.py:310-311). */
 int qutai_amd_silu_mul(const void* gate, const void* up, void* out, int64_t n, int dtype, void* stream);
 
+/* Gradients of out = silu(gate) * up: dgate = dy * up * s * (1 + gate (1 - s))
+ * and dup = dy * silu(gate), s = sigmoid(gate).  Replaces the backward of
+ * `lm_silu` (src/qutai/backends/cuda/lm.cu:54, backward branch) and of the
+ * elementwise multiply in SwiGLU (src/qutai/lm/layers.py:310-311). */
+int qutai_amd_silu_mul_backward(const void* dy, const void* gate, const void* up, void* dgate, void* dup, int64_t n,
+                                int dtype, void* stream);
+
 /* MoE routing, forward.  scores: [rows][experts] fp32 router logits.
  * Writes probs [rows][experts] (fp32 softmax), weights [rows][top_k] (fp32,
  * renormalised over the selected experts), indices [rows][top_k] (int64;

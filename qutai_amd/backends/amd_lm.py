@@ -1,0 +1,187 @@
+"""Decoder-LM kernels of the amd device (sibling of src/qutai/backends/cuda_lm.py).
+
+Same names and argument meaning as the reference LM backend for the
+contraction path: ``gemm`` (cuda_lm.py:31-55), ``routing`` (:368-449),
+``route_gather`` / ``route_gather_backward`` (:471-502), ``combine`` /
+``combine_backward`` (:505-581), ``silu`` products, ``take``.  Additions that
+the MI355X design needs: ``route_gather_all`` and ``combine_all`` (one launch
+for every expert), ``grouped_gemm`` and ``moe_experts_forward`` (the expert
+projections as grouped GEMMs whose per-expert row ranges stay in device
+memory, so no host synchronisation sizes them).
+"""
+from __future__ import annotations
+
+from array import array
+from random import Random
+
+from . import amd
+from .amd import AMDStorage, code
+from .amd_runtime import get_runtime
+
+
+def normal(size, mean=0.0, std=1.0, *, seed=None, dtype="float32"):
+    """Host-drawn N(mean, std) values (Random(seed).gauss, as the CPU path
+    draws them: src/qutai/backends/cpu_lm.py:6-8), uploaded once."""
+    random = Random(seed)
+    return amd.storage(array("f", (random.gauss(mean, std) for _ in range(size))), dtype=dtype)
+
+
+def gemm(a, b, rows, inner, cols, *, transpose_left=False, transpose_right=False, out_dtype=None, out=None,
+         accumulate=False):
+    """LM GEMM without batch/strides (src/qutai/backends/cuda_lm.py:31-55)."""
+    return amd.gemm(a, b, rows, inner, cols, transpose_left=transpose_left, transpose_right=transpose_right,
+                    out_dtype=out_dtype, out=out, accumulate=accumulate)
+
+
+def take(values, start, size):
+    return amd.take(values, start, size)
+
+
+def silu_mul(gate: AMDStorage, up: AMDStorage) -> AMDStorage:
+    """silu(gate) * up with the reference's per-op rounding."""
+    if (gate.dtype, gate.size) != (up.dtype, up.size):
+        raise ValueError("silu_mul needs operands of equal dtype and size")
+    out = AMDStorage(gate.size, gate.dtype)
+    if gate.size:
+        out.runtime.call("qutai_amd_silu_mul", gate.ptr, up.ptr, out.ptr, gate.size, code(gate.dtype))
+    return out
+
+
+def silu_mul_backward(gradient, gate, up):
+    dgate, dup = AMDStorage(gate.size, gate.dtype), AMDStorage(up.size, up.dtype)
+    if gate.size:
+        dgate.runtime.call("qutai_amd_silu_mul_backward", gradient.ptr, gate.ptr, up.ptr, dgate.ptr, dup.ptr,
+                           gate.size, code(gate.dtype))
+    return dgate, dup
+
+
+def routing(scores, rows, experts, top_k, *, download_counts=True):
+    """Router softmax, top-k selection and stable per-expert packing.
+
+    Returns the dict of ``cuda_lm.routing`` (cuda_lm.py:436-449): probs,
+    weights, indices, counts, ids, slots, locations, utilization, aux, rows,
+    experts, top_k, capacity; plus ``offsets`` ([experts+1], device) and
+    ``order`` (token ids expert-major, device) used by the one-launch gather
+    and the grouped GEMMs.  ``counts`` is a host tuple (one device read, as
+    in the reference) unless ``download_counts`` is False.
+    """
+    if scores.dtype == "bfloat16":
+        scores = amd.from_storage(scores, dtype="float32")
+    if scores.dtype != "float32":
+        raise ValueError("amd routing takes float32 or bfloat16 router scores")
+    if experts <= 0 or not 0 < top_k <= experts or scores.size != rows * experts:
+        raise ValueError("routing needs 0 < top_k <= experts and rows * experts scores")
+    capacity = rows * top_k
+    probs = AMDStorage(rows * experts, "float32")
+    weights = AMDStorage(capacity, "float32")
+    indices = AMDStorage(capacity, "int64")
+    counts = AMDStorage(experts, "int64")
+    ids = AMDStorage(experts * capacity, "int64")
+    slots = AMDStorage(experts * capacity, "int64")
+    locations = AMDStorage(capacity, "int64")
+    offsets = AMDStorage(experts + 1, "int64")
+    order = AMDStorage(capacity, "int64")
+    utilization = AMDStorage(experts, "float32")
+    aux = AMDStorage(1, "float32")
+    runtime = get_runtime()
+    runtime.call("qutai_amd_route", scores.ptr, probs.ptr, weights.ptr, indices.ptr, counts.ptr, ids.ptr, slots.ptr,
+                 locations.ptr, offsets.ptr, order.ptr, utilization.ptr, aux.ptr, rows, experts, top_k)
+    host_counts = tuple(counts.to_array().tolist()) if download_counts else None
+    return dict(probs=probs, weights=weights, indices=indices, counts=host_counts, count_buffer=counts, ids=ids,
+                slots=slots, locations=locations, offsets=offsets, order=order, utilization=utilization, aux=aux,
+                rows=rows, experts=experts, top_k=top_k, capacity=capacity)
+
+
+def _host_offsets(route):
+    counts = route["counts"]
+    if counts is None:
+        raise ValueError("per-expert calls need the host counts (routing(..., download_counts=True))")
+    starts = [0]
+    for count in counts:
+        starts.append(starts[-1] + count)
+    return starts
+
+
+def route_gather(values, route, expert, width):
+    """Rows of one expert, in token order (cuda_lm.py:471-485)."""
+    start = _host_offsets(route)[expert]
+    count = route["counts"][expert]
+    result = AMDStorage(count * width, values.dtype)
+    if count * width:
+        result.runtime.call("qutai_amd_route_gather", values.ptr, route["order"].ptr + 8 * start, result.ptr, count,
+                            width, 0, code(values.dtype))
+    return result
+
+
+def route_gather_backward(gradient, route, expert, width):
+    """Scatter one expert's row gradients back to token rows (cuda_lm.py:488-502)."""
+    start = _host_offsets(route)[expert]
+    count = route["counts"][expert]
+    result = amd.full(route["rows"] * width, 0.0, dtype=gradient.dtype)
+    if count * width:
+        result.runtime.call("qutai_amd_route_gather", gradient.ptr, route["order"].ptr + 8 * start, result.ptr,
+                            count, width, 1, code(gradient.dtype))
+    return result
+
+
+def route_gather_all(values, route, width):
+    """All experts' token rows in one expert-major block [rows*top_k, width]."""
+    total = route["capacity"]
+    result = AMDStorage(total * width, values.dtype)
+    if total * width:
+        result.runtime.call("qutai_amd_route_gather", values.ptr, route["order"].ptr, result.ptr, total, width, 0,
+                            code(values.dtype))
+    return result
+
+
+def combine_all(expert_rows, route, width):
+    """y[row] = sum_slot weight * expert output row, from the expert-major
+    block produced by the grouped GEMMs (one launch, fp32 sum, one rounding)."""
+    result = AMDStorage(route["rows"] * width, expert_rows.dtype)
+    if result.size:
+        result.runtime.call("qutai_amd_combine", expert_rows.ptr, route["weights"].ptr, route["indices"].ptr,
+                            route["locations"].ptr, route["offsets"].ptr, result.ptr, route["rows"], width,
+                            route["top_k"], code(expert_rows.dtype))
+    return result
+
+
+def combine(outputs, weights, route, width):
+    """Reference-shaped combine over a list of (expert, rows) outputs
+    (cuda_lm.py:505-541): the rows are laid out expert-major and combined
+    in one launch."""
+    if weights is not route["weights"]:
+        route = dict(route, weights=weights)
+    dtype = outputs[0][1].dtype if outputs else "float32"
+    block = AMDStorage(route["capacity"] * width, dtype)
+    starts = _host_offsets(route)
+    item = 2 if dtype == "bfloat16" else 4
+    for expert, values in outputs:
+        if values.size:
+            block.runtime.copy(block.ptr + starts[expert] * width * item, values.ptr, values.nbytes)
+    return combine_all(block, route, width)
+
+
+def grouped_gemm(rows_block, weight_stack, route, inner, cols, *, out_dtype="bfloat16"):
+    """out[offsets[e]:offsets[e+1]] = rows_block[offsets[e]:offsets[e+1]] @ W_e^T
+    with W_e = weight_stack[e] stored (cols, inner), for every expert in one
+    launch; the row ranges are read on the device."""
+    experts = route["experts"]
+    if weight_stack.size != experts * cols * inner or rows_block.dtype != weight_stack.dtype:
+        raise ValueError("grouped_gemm needs [experts][cols][inner] weights of the rows' dtype")
+    out = AMDStorage(route["capacity"] * cols, out_dtype)
+    if out.size:
+        out.runtime.call("qutai_amd_gemm_grouped", rows_block.ptr, weight_stack.ptr, out.ptr, route["offsets"].ptr,
+                         experts, route["capacity"], inner, cols, cols * inner, 1, code(rows_block.dtype),
+                         code(out_dtype), 0, mfma=True)
+    return out
+
+
+def moe_experts_forward(x, route, w_gate, w_up, w_down, width, hidden):
+    """Expert SwiGLU for every routed (token, slot): gather, grouped gate/up,
+    silu(gate) * up, grouped down, weighted combine (lm/layers.py:395-399)."""
+    rows = route_gather_all(x, route, width)
+    gate = grouped_gemm(rows, w_gate, route, width, hidden, out_dtype=x.dtype)
+    up = grouped_gemm(rows, w_up, route, width, hidden, out_dtype=x.dtype)
+    act = silu_mul(gate, up)
+    down = grouped_gemm(act, w_down, route, hidden, width, out_dtype=x.dtype)
+    return combine_all(down, route, width)

@@ -48,6 +48,7 @@ SIGNATURES = {
     "qutai_amd_transpose_last2": [_p, _p, _i64, _i64, _i64, _i32, _p],
     "qutai_amd_softmax_rows": [_p, _p, _i64, _i64, _f64, _i32, _p],
     "qutai_amd_silu_mul": [_p, _p, _p, _i64, _i32, _p],
+    "qutai_amd_silu_mul_backward": [_p, _p, _p, _p, _p, _i64, _i32, _p],
     "qutai_amd_route": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p],
     "qutai_amd_route_gather": [_p, _p, _p, _i64, _i64, _i32, _i32, _p],
     "qutai_amd_combine": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p],

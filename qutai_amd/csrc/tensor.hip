@@ -244,6 +244,35 @@ __global__ void add_rows_kernel(const void* x, const void* bias, void* out, int6
   }
 }
 
+// Gradients of y = silu(g) * u: dg = dy * u * s * (1 + g (1 - s)), du = dy * silu(g)
+// (the derivative of lm_silu, lm.cu:54, times the multiply's rule).
+__global__ void silu_mul_backward_kernel(const void* dy, const void* g, const void* u, void* dg, void* du, int64_t n,
+                                         int d) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    if (d == F64) {
+      double v = ((const double*)g)[i], w = ((const double*)u)[i], y = ((const double*)dy)[i];
+      double s = v >= 0 ? 1.0 / (1.0 + exp(-v)) : exp(v) / (1.0 + exp(v));
+      ((double*)dg)[i] = y * w * s * (1.0 + v * (1.0 - s));
+      ((double*)du)[i] = y * (v * s);
+    } else {
+      float v, w, y;
+      if (d == F32) {
+        v = ((const float*)g)[i]; w = ((const float*)u)[i]; y = ((const float*)dy)[i];
+      } else {
+        v = bf16_to_f32(((const bf16_t*)g)[i]); w = bf16_to_f32(((const bf16_t*)u)[i]);
+        y = bf16_to_f32(((const bf16_t*)dy)[i]);
+      }
+      float s = v >= 0.f ? 1.f / (1.f + expf(-v)) : expf(v) / (1.f + expf(v));
+      float a = y * w * s * (1.f + v * (1.f - s)), b = y * (v * s);
+      if (d == F32) {
+        ((float*)dg)[i] = a; ((float*)du)[i] = b;
+      } else {
+        ((bf16_t*)dg)[i] = f32_to_bf16(a); ((bf16_t*)du)[i] = f32_to_bf16(b);
+      }
+    }
+  }
+}
+
 bool float_dtype(int d) { return d == F32 || d == F64 || d == BF16; }
 
 }  // namespace
@@ -336,6 +365,15 @@ int qutai_amd_silu_mul(const void* gate, const void* up, void* out, int64_t n, i
   if (n == 0) return QA_OK;
   hipLaunchKernelGGL(silu_mul_kernel, dim3(grid_for(n)), dim3(THREADS), 0, (hipStream_t)stream, gate, up, out, n,
                      dtype);
+  return (int)hipGetLastError();
+}
+
+int qutai_amd_silu_mul_backward(const void* dy, const void* gate, const void* up, void* dgate, void* dup, int64_t n,
+                                int dtype, void* stream) {
+  if (n < 0 || !float_dtype(dtype)) return QA_EINVAL;
+  if (n == 0) return QA_OK;
+  hipLaunchKernelGGL(silu_mul_backward_kernel, dim3(grid_for(n)), dim3(THREADS), 0, (hipStream_t)stream, dy, gate, up,
+                     dgate, dup, n, dtype);
   return (int)hipGetLastError();
 }
 

@@ -1,0 +1,156 @@
+"""LM layers on the GEMM path (src/qutai/lm/layers.py:9-449, contraction parts).
+
+``linear`` / ``Projection`` / ``SwiGLU`` follow the reference call patterns
+(weights stored (out, in), ``Y = X W^T`` forward, ``dX = G W`` and
+``dW = G^T X`` backward, precision captured in forward and restored in
+backward).  ``SparseMoE`` keeps the reference routing semantics but stores
+each projection of all experts as one stacked tensor, so the expert
+projections run as grouped GEMMs over device-resident row ranges instead of
+a Python loop of per-expert GEMMs.  ``attention_products`` is the score /
+value product pair of the attention layers (S = Q K^T, P = softmax(S/sqrt D),
+O = P V) on the batched GEMM.
+"""
+from __future__ import annotations
+
+from math import prod, sqrt
+
+from ..backends import amd, amd_lm
+from ..backends.precision import matmul_precision, set_matmul_precision
+from ..core.grad import record
+from ..core.tensor import Tensor
+
+
+def backend(value):
+    device = value if isinstance(value, str) else value.device
+    if device == "amd":
+        return amd_lm
+    raise ValueError("no LM kernels for this device")
+
+
+def activation_dtype(x, weight):
+    """bf16 activations on the GPU with fp32 weights under autocast or bf16
+    inputs (src/qutai/lm/layers.py:20-28)."""
+    if weight.dtype == "float32" and (matmul_precision() == "bfloat16" or x.dtype == "bfloat16"):
+        return "bfloat16"
+    return weight.dtype
+
+
+def linear(x, weight):
+    """Y = X W^T with W stored (out, in) (src/qutai/lm/layers.py:35-74)."""
+    b = backend(x)
+    rows = x.size // x.shape[-1]
+    out_features, inner = weight.shape
+    precision = matmul_precision()
+    values = b.gemm(x.storage, weight.storage, rows, inner, out_features, transpose_right=True,
+                    out_dtype=activation_dtype(x, weight))
+
+    def backward(g):
+        with set_matmul_precision(precision):
+            dx = b.gemm(g, weight.storage, rows, out_features, inner, out_dtype=x.dtype) if x.requires_grad else None
+            dw = (b.gemm(g, x.storage, out_features, rows, inner, transpose_left=True, out_dtype=weight.dtype)
+                  if weight.requires_grad else None)
+        return dx, dw
+
+    return record(Tensor(values, shape=(*x.shape[:-1], out_features)), (x, weight), backward)
+
+
+def silu_mul(gate, up):
+    """silu(gate) * up as one recorded op (SwiGLU's activation, lm/layers.py:310-311)."""
+    b = backend(gate)
+    values = b.silu_mul(gate.storage, up.storage)
+    return record(Tensor(values, shape=gate.shape), (gate, up),
+                  lambda g: b.silu_mul_backward(g, gate.storage, up.storage))
+
+
+class Projection:
+    def __init__(self, inputs, outputs, *, device="amd", dtype="float32", seed=None, std=0.02):
+        self.weight = Tensor(backend(device).normal(inputs * outputs, std=std, seed=seed, dtype=dtype),
+                             shape=(outputs, inputs), requires_grad=True)
+
+    def __call__(self, x):
+        return linear(x, self.weight)
+
+    def parameters(self):
+        return (self.weight,)
+
+
+class SwiGLU:
+    """down(silu(gate(x)) * up(x)); seeds seed, seed+1, seed+2 (lm/layers.py:291-314)."""
+
+    def __init__(self, width, hidden, *, device="amd", dtype="float32", seed=None, std=0.02):
+        self.gate = Projection(width, hidden, device=device, dtype=dtype, seed=seed)
+        self.up = Projection(width, hidden, device=device, dtype=dtype, seed=None if seed is None else seed + 1)
+        self.down = Projection(hidden, width, device=device, dtype=dtype, seed=None if seed is None else seed + 2,
+                               std=std)
+
+    def __call__(self, x):
+        return self.down(silu_mul(self.gate(x), self.up(x)))
+
+    def parameters(self):
+        return (*self.gate.parameters(), *self.up.parameters(), *self.down.parameters())
+
+
+class SparseMoE:
+    """Top-k routed SwiGLU experts (lm/layers.py:353-406).
+
+    Expert e's gate/up weights are ``w_gate[e]`` / ``w_up[e]`` (hidden, width)
+    and its down weight ``w_down[e]`` (width, hidden); expert e is initialised
+    from seeds seed+1+3e, +1, +2 like the reference's per-expert SwiGLU."""
+
+    def __init__(self, width, hidden, experts, top_k, *, device="amd", dtype="float32", seed=None, std=0.02):
+        self.router = Projection(width, experts, device=device, dtype=dtype, seed=seed)
+        self.width, self.hidden, self.n_experts, self.top_k = width, hidden, experts, top_k
+        b = backend(device)
+
+        def stacked(rows, cols, offset, scale):
+            parts = [b.normal(rows * cols, std=scale, seed=None if seed is None else seed + 1 + 3 * e + offset,
+                              dtype=dtype) for e in range(experts)]
+            block = amd.AMDStorage(experts * rows * cols, dtype)
+            item = 2 if dtype == "bfloat16" else 4
+            for e, part in enumerate(parts):
+                block.runtime.copy(block.ptr + e * rows * cols * item, part.ptr, part.nbytes)
+            return Tensor(block, shape=(experts, rows, cols), requires_grad=True)
+
+        self.w_gate = stacked(hidden, width, 0, 0.02)
+        self.w_up = stacked(hidden, width, 1, 0.02)
+        self.w_down = stacked(width, hidden, 2, std)
+        self.last_counts = (0,) * experts
+        self.utilization = None
+
+    def __call__(self, x):
+        with set_matmul_precision(None):
+            scores = self.router(x.to(dtype=self.router.weight.dtype))
+        b = backend(x)
+        rows = x.size // x.shape[-1]
+        route = b.routing(scores.storage, rows, self.n_experts, self.top_k, download_counts=False)
+        self.utilization = Tensor(route["utilization"], shape=(self.n_experts,))
+        aux = Tensor(route["aux"], shape=())
+        values = b.moe_experts_forward(x.storage, route, self.w_gate.storage, self.w_up.storage,
+                                       self.w_down.storage, self.width, self.hidden)
+        if x.dtype != values.dtype:
+            values = amd.from_storage(values, dtype=x.dtype)
+        result = Tensor(values, shape=x.shape)
+        return result, aux, route
+
+    def parameters(self):
+        return (*self.router.parameters(), self.w_gate, self.w_up, self.w_down)
+
+
+def attention_products(q, k, v, *, scale=None):
+    """Score and value products of attention on (groups, T, D) tensors:
+    S = Q K^T (NT, no materialised K^T), P = softmax(scale * S) row-wise,
+    O = P V (NN); fp32 accumulation in both GEMMs, storage dtype kept
+    (src/qutai/nn/layers.py:334-354)."""
+    if q.shape != k.shape or q.shape != v.shape or q.ndim != 3:
+        raise ValueError("attention_products takes equal (groups, T, D) q, k, v")
+    groups, time, dim = q.shape
+    scale = 1 / sqrt(dim) if scale is None else scale
+    scores = amd.gemm(q.storage, k.storage, time, dim, time, batch=groups, transpose_right=True,
+                      out_dtype=q.dtype)
+    probs = amd.softmax(scores, (groups * time, time), -1, scale=scale)
+    out = amd.gemm(probs, v.storage, time, time, dim, batch=groups, out_dtype=q.dtype)
+    return Tensor(out, shape=(groups, time, dim)), Tensor(probs, shape=(groups, time, time))
+
+
+def parameter_count(layer):
+    return sum(prod(p.shape) for p in layer.parameters())

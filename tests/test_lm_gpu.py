@@ -1,0 +1,347 @@
+"""LM-path parity on the MI355X: routing (bit-exact indices), gather,
+grouped expert GEMMs, combine, MoE forward, lm linear
+forward/backward (config 4), attention products (config 3), and the
+reference's Tensor/nn known answers on the amd device."""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import reference as ora
+from tests.helpers import download, normal, stored, upload
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = 1e-2
+FP32_TOL = 1e-5
+
+
+@pytest.fixture(scope="module")
+def amd():
+    from qutai_amd.backends import amd as backend
+
+    backend.get_runtime()
+    return backend
+
+
+@pytest.fixture(scope="module")
+def lm():
+    from qutai_amd.backends import amd_lm
+
+    return amd_lm
+
+
+def per_expert(route, name, experts):
+    values = download(route[name]).tolist()
+    cap = route["capacity"]
+    counts = route["counts"]
+    return [values[e * cap:e * cap + counts[e]] for e in range(experts)]
+
+
+# ---- routing -----------------------------------------------------------------------
+
+def test_routing_golden_vector(amd, lm):
+    # tests/test_lm_moe.py:65-71
+    scores = amd.storage([3.0, 2.0, -1.0, -1.0, 2.0, 3.0], dtype="float32")
+    route = lm.routing(scores, 2, 3, 2)
+    assert download(route["indices"]).tolist() == [0, 1, 2, 1]
+    assert route["counts"] == (1, 2, 1)
+    weights = download(route["weights"])
+    assert weights[:2].sum() == pytest.approx(1, abs=1e-6)
+    assert weights[2:].sum() == pytest.approx(1, abs=1e-6)
+
+
+def test_route_pack_is_stable_across_blocks(amd, lm):
+    # tests/test_lm_moe.py:140-162
+    rows, experts, top_k = 517, 5, 3
+    scores = [((row * 37 + expert * 11) % 101) / 13 for row in range(rows) for expert in range(experts)]
+    reference = ora.routing([float(np.float32(s)) for s in scores], rows, experts, top_k)
+    values = amd.storage(scores, dtype="float32")
+    for _ in range(3):
+        route = lm.routing(values, rows, experts, top_k)
+        assert route["counts"] == reference["counts"]
+        assert per_expert(route, "ids", experts) == reference["ids"]
+        assert per_expert(route, "slots", experts) == reference["slots"]
+
+
+def c5_route(amd, lm):
+    rows, experts, top_k = 8192, 8, 2
+    logits = normal(4, rows * experts)  # router logits N(0,1), seed 4
+    route = lm.routing(upload(logits, "float32"), rows, experts, top_k)
+    reference = ora.routing(logits.astype(np.float64).tolist(), rows, experts, top_k)
+    return logits, route, reference
+
+
+def test_config5_routing_indices_bit_exact(amd, lm):
+    logits, route, reference = c5_route(amd, lm)
+    rows, experts, top_k = 8192, 8, 2
+    assert download(route["indices"]).tolist() == reference["indices"]
+    assert route["counts"] == reference["counts"]
+    assert len(set(route["counts"])) > 1  # uneven per-expert counts
+    assert per_expert(route, "ids", experts) == reference["ids"]
+    assert per_expert(route, "slots", experts) == reference["slots"]
+    # locations: position of (row, slot) inside its expert list
+    locations = download(route["locations"]).tolist()
+    for e in range(experts):
+        for position, (row, slot) in enumerate(zip(reference["ids"][e], reference["slots"][e])):
+            assert locations[row * top_k + slot] == position
+    offsets = download(route["offsets"]).tolist()
+    assert offsets == [sum(reference["counts"][:e]) for e in range(experts + 1)]
+    order = download(route["order"]).tolist()
+    assert order == [row for e in range(experts) for row in reference["ids"][e]]
+    # floating outputs within fp32 tolerance of the float64 oracle
+    assert np.abs(download(route["weights"]) - reference["weights"]).max() <= 1e-6
+    assert np.abs(download(route["probs"]) - reference["probs"]).max() <= 1e-6
+    assert download(route["utilization"]).tolist() == pytest.approx(reference["utilization"], rel=1e-7)
+    assert download(route["aux"])[0] == pytest.approx(reference["aux"], rel=1e-5)
+
+
+def test_config5_gather_and_combine(amd, lm):
+    logits, route, reference = c5_route(amd, lm)
+    rows, width, top_k = 8192, 2048, 2
+    x = normal(5, rows * width)
+    xs = upload(x, "bfloat16")
+    gathered = download(lm.route_gather_all(xs, route, width)).reshape(-1, width)
+    xr = stored(x, "bfloat16").reshape(rows, width)
+    order = [row for e in range(8) for row in reference["ids"][e]]
+    assert np.array_equal(gathered, xr[order])  # a copy: bit-exact
+    # per-expert gather (reference-shaped API) and its backward scatter
+    for e in (0, 7):
+        part = download(lm.route_gather(xs, route, e, width)).reshape(-1, width)
+        assert np.array_equal(part, xr[reference["ids"][e]])
+        back = download(lm.route_gather_backward(lm.route_gather(xs, route, e, width), route, e, width))
+        expected = np.zeros((rows, width))
+        expected[reference["ids"][e]] = xr[reference["ids"][e]]
+        assert np.array_equal(back.reshape(rows, width), expected)
+    # combine of the gathered rows = sum_slot w * x[row] = x[row] (weights sum to 1)
+    y = download(lm.combine_all(lm.route_gather_all(upload(x, "float32"), route, width), route, width))
+    assert ora.rel_frobenius(y.reshape(rows, width), x.reshape(rows, width)) <= FP32_TOL
+    # against the oracle's combine on a few rows with distinct expert outputs
+    block = normal(6, route["capacity"] * width)
+    y = download(lm.combine_all(upload(block, "float32"), route, width)).reshape(rows, width)
+    offsets = download(route["offsets"]).tolist()
+    outputs = [(e, block.reshape(-1, width)[offsets[e]:offsets[e + 1]].astype(np.float64).ravel().tolist())
+               for e in range(8)]
+    sample = {0, 1, 4095, 8191}
+    small = dict(reference, rows=rows)
+    small_ids = [[r for r in reference["ids"][e] if r in sample] for e in range(8)]
+    small_slots = [[s for r, s in zip(reference["ids"][e], reference["slots"][e]) if r in sample] for e in range(8)]
+    picked = []
+    for e, values in outputs:
+        rows_e = reference["ids"][e]
+        keep = [i for i, r in enumerate(rows_e) if r in sample]
+        picked.append((e, [values[i * width + j] for i in keep for j in range(width)]))
+    expected = ora.combine(picked, reference["weights"], dict(small, ids=small_ids, slots=small_slots), width)
+    expected = np.array(expected).reshape(rows, width)
+    for r in sorted(sample):
+        assert ora.rel_frobenius(y[r], expected[r]) <= FP32_TOL
+
+
+def test_config5_grouped_expert_gemm_and_moe_forward(amd, lm):
+    logits, route, reference = c5_route(amd, lm)
+    rows, width, hidden, experts = 8192, 2048, 1408, 8
+    x = normal(7, rows * width)
+    w_gate = normal(8, experts * hidden * width, 0.02)
+    w_up = normal(9, experts * hidden * width, 0.02)
+    w_down = normal(10, experts * width * hidden, 0.02)
+    xs, gs, us, ds = (upload(v, "bfloat16") for v in (x, w_gate, w_up, w_down))
+    gathered = lm.route_gather_all(xs, route, width)
+    gate = download(lm.grouped_gemm(gathered, gs, route, width, hidden, out_dtype="float32")).reshape(-1, hidden)
+    offsets = download(route["offsets"]).tolist()
+    xr = stored(x, "bfloat16").reshape(rows, width)
+    gr = stored(w_gate, "bfloat16").reshape(experts, hidden, width)
+    for e in range(experts):
+        lo, hi = offsets[e], offsets[e + 1]
+        sample = sorted({lo, hi - 1, (lo + hi) // 2})
+        tokens = [reference["ids"][e][i - lo] for i in sample]
+        exact = ora.gemm_f64(xr[tokens], gr[e], len(tokens), width, hidden, transpose_right=True)
+        assert ora.rel_frobenius(gate[sample], exact) <= FP32_TOL
+    # full expert SwiGLU + combine against a float64 composition on sampled tokens
+    y = download(lm.moe_experts_forward(xs, route, gs, us, ds, width, hidden)).reshape(rows, width)
+    ur = stored(w_up, "bfloat16").reshape(experts, hidden, width)
+    dr = stored(w_down, "bfloat16").reshape(experts, width, hidden)
+    weights = reference["weights"]
+    for token in (0, 17, 4096, 8191):
+        total = np.zeros(width)
+        for slot in range(2):
+            e = reference["indices"][token * 2 + slot]
+            g = gr[e] @ xr[token]
+            u = ur[e] @ xr[token]
+            act = np.array(ora.silu(g.tolist())) * u
+            total += weights[token * 2 + slot] * (dr[e] @ act)
+        assert ora.rel_frobenius(y[token], total) <= BF16_TOL
+
+
+# ---- dense Linear forward / backward (config 4 shapes) ------------------------------
+
+def test_config4_lm_linear_forward_backward(amd):
+    from qutai_amd import Tensor
+    from qutai_amd.lm.layers import linear
+
+    tokens, width, hidden = 4096, 2048, 5632
+    x = normal(3, tokens * width)
+    w = normal(31, hidden * width, 0.02)
+    g = normal(32, tokens * hidden)
+    xt = Tensor(upload(x, "bfloat16"), shape=(8, 512, width), requires_grad=True)
+    wt = Tensor(upload(w, "bfloat16"), shape=(hidden, width), requires_grad=True)
+    y = linear(xt, wt)
+    assert y.shape == (8, 512, hidden) and y.dtype == "bfloat16"
+    y.backward(Tensor(upload(g, "bfloat16"), shape=y.shape))
+    xr, wr, gr = stored(x, "bfloat16").reshape(tokens, width), stored(w, "bfloat16").reshape(hidden, width), \
+        stored(g, "bfloat16").reshape(tokens, hidden)
+    rows = [0, 1, 777, 2048, 4095]
+    got_y = download(y.storage).reshape(tokens, hidden)[rows]
+    assert ora.rel_frobenius(got_y, ora.gemm_f64(xr[rows], wr, len(rows), width, hidden,
+                                                 transpose_right=True)) <= BF16_TOL
+    got_dx = download(xt.grad.storage).reshape(tokens, width)[rows]
+    assert ora.rel_frobenius(got_dx, ora.gemm_f64(gr[rows], wr, len(rows), hidden, width)) <= BF16_TOL
+    w_rows = [0, 100, 5631]
+    got_dw = download(wt.grad.storage).reshape(hidden, width)[w_rows]
+    exact_dw = ora.gemm_f64(gr, xr, hidden, tokens, width, transpose_left=True, row_list=w_rows)
+    assert ora.rel_frobenius(got_dw, exact_dw) <= BF16_TOL
+
+
+def test_swiglu_forward_backward_small(amd):
+    from qutai_amd import Tensor
+    from qutai_amd.lm.layers import SwiGLU
+
+    width, hidden, tokens = 64, 96, 40
+    layer = SwiGLU(width, hidden, seed=5, std=0.05)
+    x = normal(11, tokens * width)
+    xt = Tensor(upload(x, "float32"), shape=(tokens, width), requires_grad=True)
+    y = layer(xt)
+    g = normal(12, tokens * width)
+    y.backward(Tensor(upload(g, "float32"), shape=y.shape))
+    wg, wu, wd = (download(p.storage).astype(np.float64).reshape(p.shape) for p in layer.parameters())
+    xr = x.astype(np.float64).reshape(tokens, width)
+    a = xr @ wg.T
+    b = xr @ wu.T
+    s = 1 / (1 + np.exp(-a))
+    act = a * s * b
+    expected = act @ wd.T
+    assert ora.rel_frobenius(download(y.storage).reshape(tokens, width), expected) <= FP32_TOL
+    gr = g.astype(np.float64).reshape(tokens, width)
+    dact = gr @ wd
+    da = dact * b * s * (1 + a * (1 - s))
+    db = dact * a * s
+    dx = da @ wg + db @ wu
+    assert ora.rel_frobenius(download(xt.grad.storage).reshape(tokens, width), dx) <= FP32_TOL
+    dwd = gr.T @ act
+    assert ora.rel_frobenius(download(layer.down.weight.grad.storage).reshape(width, hidden), dwd) <= FP32_TOL
+
+
+# ---- attention products (config 3) ----------------------------------------------------
+
+def attention_reference(q, k, v, scale):
+    s = q @ k.T
+    s = ora.bf16_round_array(s.astype(np.float32)).astype(np.float64) * scale
+    p = np.exp(s - s.max(axis=1, keepdims=True))
+    p /= p.sum(axis=1, keepdims=True)
+    return p @ v
+
+
+def test_attention_products_small_and_config3_heads(amd):
+    from qutai_amd import Tensor
+    from qutai_amd.lm.layers import attention_products
+
+    for groups, time, dim in ((3, 300, 64), (128, 2048, 64)):
+        q, k, v = (normal(2 + i, groups * time * dim) for i in range(3))
+        tensors = [Tensor(upload(a, "bfloat16"), shape=(groups, time, dim)) for a in (q, k, v)]
+        out, probs = attention_products(*tensors)
+        o = download(out.storage).reshape(groups, time, dim)
+        p = download(probs.storage).reshape(groups, time, time)
+        heads = range(groups) if groups <= 3 else (0, 57, 127)
+        for h in heads:
+            qr, kr, vr = (stored(a, "bfloat16").reshape(groups, time, dim)[h] for a in (q, k, v))
+            expected = attention_reference(qr, kr, vr, dim ** -0.5)
+            assert ora.rel_frobenius(o[h], expected) <= BF16_TOL
+        sums = p[list(heads)].astype(np.float64).sum(axis=-1)
+        assert np.abs(sums - 1).max() <= 2e-2  # bf16 probabilities, each rounded
+        assert np.isfinite(o).all()
+
+
+# ---- Tensor / nn known answers on the amd device ----------------------------------------
+
+def test_tensor_matmul_known_answers(amd):
+    import qutai_amd as qt
+    from qutai_amd import Tensor
+
+    # tests/test_batched_matmul.py:28-42
+    assert qt.matmul(Tensor([1, 2, 3]), Tensor([4, 5, 6])).item() == 32
+    assert qt.matmul(Tensor([1, 2]), Tensor([[3, 4, 5], [6, 7, 8]])).tolist() == [15, 18, 21]
+    assert qt.matmul(Tensor([[1, 2], [3, 4]]), Tensor([5, 6])).tolist() == [17, 39]
+    matrices = Tensor([[[1, 2], [3, 4]], [[5, 6], [7, 8]]])
+    assert qt.matmul(Tensor([1, 2]), matrices).tolist() == [[7, 10], [19, 22]]
+    assert qt.matmul(matrices, Tensor([1, 2])).tolist() == [[5, 11], [17, 23]]
+    # tests/test_batched_matmul.py:44-53 (both batch axes broadcast)
+    left = Tensor(list(range(1, 13)), shape=(2, 1, 2, 3))
+    right = Tensor(list(range(1, 19)), shape=(1, 3, 3, 2))
+    expected = np.array(ora.matmul(list(range(1, 13)), list(range(1, 19)), (2, 1, 2, 3), (1, 3, 3, 2)))
+    result = qt.matmul(left, right)
+    assert result.shape == (2, 3, 2, 2)
+    assert np.array_equal(np.array(result.tolist()).ravel(), expected)
+
+
+def test_tensor_matmul_gradients_known_answers(amd):
+    import qutai_amd as qt
+    from qutai_amd import Tensor
+
+    # tests/test_batched_matmul.py:55-60
+    left = Tensor(list(range(1, 13)), shape=(2, 2, 3), requires_grad=True)
+    weight = Tensor([[7, 8], [9, 10], [11, 12]], requires_grad=True)
+    qt.sum(qt.matmul(left, weight)).backward()
+    assert left.grad.tolist() == [[[15, 19, 23]] * 2] * 2
+    assert weight.grad.tolist() == [[22, 22], [26, 26], [30, 30]]
+    # tests/test_batched_matmul.py:62-67
+    vector = Tensor([1, 2], requires_grad=True)
+    mats = Tensor([[[3, 4], [5, 6]], [[7, 8], [9, 10]]], requires_grad=True)
+    qt.matmul(vector, mats).backward(Tensor([[1, 2], [3, 4]]))
+    assert vector.grad.tolist() == [64, 84]
+    assert mats.grad.tolist() == [[[1, 2], [2, 4]], [[3, 4], [6, 8]]]
+    # tests/test_batched_matmul.py:81-84
+    tensor = Tensor([[[1, 2], [3, 4]], [[5, 6], [7, 8]]], requires_grad=True)
+    qt.sum(qt.matmul(tensor, tensor)).backward()
+    assert tensor.grad.tolist() == [[[7, 11], [9, 13]], [[23, 27], [25, 29]]]
+
+
+def test_tensor_bf16_matmul_backward(amd):
+    from qutai_amd import Tensor
+
+    # tests/test_bfloat16_storage.py:61-71 without the elementwise ops: d/dX sum(X @ W) etc.
+    x = Tensor([[1, 2], [3, 4]], dtype="bfloat16", requires_grad=True)
+    w = Tensor([[1], [2]], dtype="bfloat16", requires_grad=True)
+    y = x @ w
+    assert y.tolist() == [[5], [11]] and y.dtype == "bfloat16"
+    y.backward(Tensor([[1], [1]], dtype="bfloat16"))
+    assert x.grad.dtype == "bfloat16"
+    assert x.grad.tolist() == [[1, 2], [1, 2]]
+    assert w.grad.tolist() == [[4], [6]]
+
+
+def test_nn_linear_known_answers(amd):
+    import qutai_amd as qt
+    from qutai_amd import Tensor, nn
+
+    # tests/test_layers.py:23-43
+    layer = nn.Linear(2, 3, seed=42)
+    layer.weight = Tensor([[1, 2, 3], [4, 5, 6]], requires_grad=True)
+    layer.bias = Tensor([0.5, -0.5, 1], requires_grad=True)
+    assert layer(Tensor([[1, 2], [-1, 0]])).tolist() == [[9.5, 11.5, 16], [-0.5, -2.5, -2]]
+    layer = nn.Linear(2, 2, seed=42)
+    layer.weight = Tensor([[1, 2], [3, 4]], requires_grad=True)
+    layer.bias = Tensor([0.5, -0.5], requires_grad=True)
+    inputs = Tensor([[1, 2], [3, 4]], requires_grad=True)
+    qt.sum(layer(inputs)).backward()
+    assert inputs.grad.tolist() == [[3, 7], [3, 7]]
+    assert layer.weight.grad.tolist() == [[4, 4], [6, 6]]
+    assert layer.bias.grad.tolist() == [2, 2]
+    # tests/test_attention.py:80-90 sequence Linear shares weight gradients
+    layer = nn.Linear(2, 1, seed=42)
+    layer.weight = Tensor([[2.0], [3.0]], requires_grad=True)
+    inputs = Tensor([[[1, 2], [3, 4]], [[5, 6], [7, 8]]], requires_grad=True)
+    output = layer(inputs)
+    assert output.tolist() == [[[8.0], [18.0]], [[28.0], [38.0]]]
+    output.sum().backward()
+    assert layer.weight.grad.tolist() == [[16.0], [20.0]]
+    assert layer.bias.grad.tolist() == [4.0]
+    assert np.array(inputs.grad.tolist()).ravel().tolist() == [2.0, 3.0] * 4
