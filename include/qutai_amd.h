@@ -41,7 +41,9 @@ extern "C" {
  * operand over the batch.  fp32 x fp32 runs on v_mfma_f32_32x32x2_f32; any
  * bf16 operand, or bf16_compute != 0 (autocast), runs on
  * v_mfma_f32_32x32x16_bf16 with fp32 accumulation, an fp32 operand being
- * rounded to bf16 (nearest even) into `workspace` first; fp64 runs a SIMT
+ * rounded to bf16 (nearest even) into `workspace` first (see
+ * qutai_amd_gemm_workspace_size for when a workspace is needed and how
+ * large); fp64 runs a SIMT
  * kernel.  accumulate != 0 adds the old output before the single rounding
  * to out_dtype.  inner == 0 writes zeros (or keeps out when accumulating).
  * Replaces: `cuda.gemm` (src/qutai/backends/cuda.py:305-362) and the kernels
@@ -53,12 +55,17 @@ int qutai_amd_gemm(const void* a, const void* b, void* out, int64_t rows, int64_
                    int transpose_right, int a_dtype, int b_dtype, int out_dtype, int accumulate,
                    int bf16_compute, void* workspace, size_t workspace_bytes, void* stream);
 
-/* Bytes of workspace qutai_amd_gemm needs for these arguments (0 when no
- * operand has to be narrowed to bf16).  Helper of qutai_amd_gemm; the
- * reference narrows inside its kernels (gemm.cu:21-24, 105-142). */
+/* Bytes of workspace qutai_amd_gemm needs for these arguments with
+ * 256-byte-aligned operands (0 when both operands are used in place).  An
+ * operand is re-laid out into the workspace when its dtype differs from the
+ * MFMA input type (fp32 into the bf16 path) or when its rows are not 16-byte
+ * aligned (e.g. a 4097-wide row-major matrix): it then gets a zero-padded
+ * pitch so every kernel load is a 16-byte vector load.  Helper of
+ * qutai_amd_gemm with no reference counterpart (the reference narrows inside
+ * its kernels, gemm.cu:21-24, and uses scalar loads). */
 size_t qutai_amd_gemm_workspace_size(int64_t rows, int64_t inner, int64_t cols, int64_t batch,
-                                     int64_t left_stride, int64_t right_stride, int a_dtype, int b_dtype,
-                                     int bf16_compute);
+                                     int64_t left_stride, int64_t right_stride, int transpose_left,
+                                     int transpose_right, int a_dtype, int b_dtype, int bf16_compute);
 
 /* Grouped GEMM for MoE experts: group g owns rows [offsets[g], offsets[g+1])
  * of a (row-major, `inner` columns) and of out (row-major, `cols` columns);

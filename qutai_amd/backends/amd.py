@@ -217,9 +217,10 @@ def gemm(left, right, rows, inner, cols, *, batch=1, transpose_left=False, trans
     mixed = not double and (left.dtype == "bfloat16" or right.dtype == "bfloat16" or matmul_precision() == "bfloat16")
     runtime = get_runtime()
     workspace = None
-    if mixed:
-        need = runtime.lib.qutai_amd_gemm_workspace_size(rows, inner, cols, batch, sa, sb, code(left.dtype),
-                                                         code(right.dtype), 1)
+    if not double:
+        need = runtime.lib.qutai_amd_gemm_workspace_size(rows, inner, cols, batch, sa, sb, int(bool(transpose_left)),
+                                                         int(bool(transpose_right)), code(left.dtype),
+                                                         code(right.dtype), int(mixed))
         if need:
             workspace = AMDStorage((need + 1) // 2, "bfloat16")
     runtime.call("qutai_amd_gemm", left.ptr, right.ptr, result.ptr, rows, inner, cols, batch, sa, sb,
@@ -274,9 +275,11 @@ def _gemm_views(a: _View, b: _View, c: _View, rows, inner, cols, item):
     dtype = a.base.dtype
     mixed = dtype == "bfloat16" or (dtype == "float32" and matmul_precision() == "bfloat16")
     workspace = None
-    if mixed and dtype == "float32":
-        need = runtime.lib.qutai_amd_gemm_workspace_size(rows, inner, cols, 1, 0, 0, 0, 0, 1)
-        workspace = AMDStorage((need + 1) // 2, "bfloat16")
+    if dtype != "float64":
+        need = runtime.lib.qutai_amd_gemm_workspace_size(rows, inner, cols, 1, 0, 0, 0, 0, code(dtype), code(dtype),
+                                                         int(mixed))
+        if need:
+            workspace = AMDStorage((need + 1) // 2, "bfloat16")
     runtime.call("qutai_amd_gemm", a.base.ptr + a.offset * item, b.base.ptr + b.offset * item,
                  c.base.ptr + c.offset * item, rows, inner, cols, 1, 0, 0, 0, 0, code(dtype), code(dtype),
                  code(dtype), 0, int(mixed), _p(workspace), workspace.nbytes if workspace is not None else 0,

@@ -39,6 +39,21 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
 }
 
+// Values that are the same for the whole wavefront but that the compiler
+// cannot prove uniform (e.g. derived from a runtime division of blockIdx)
+// are pinned to scalar registers; a buffer descriptor built from them then
+// stays in SGPRs instead of needing a per-lane waterfall loop.
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+  uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)(uint64_t)v);
+  uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ int uniform32(int v) { return __builtin_amdgcn_readfirstlane(v); }
+template <class P>
+__device__ __forceinline__ P* uniform_ptr(P* p) {
+  return reinterpret_cast<P*>(uniform64(reinterpret_cast<int64_t>(p)));
+}
+
 // MI355X has 8 XCDs, each with its own L2.  Consecutive workgroup ids are
 // dispatched round-robin over the XCDs, so id i runs on XCD i % 8.  This maps
 // the hardware id to a "logical" id such that each XCD receives one

@@ -3,6 +3,9 @@
 // `cuda.gemm` (src/qutai/backends/cuda.py:305-362) and its kernel signature
 // (src/qutai/backends/cuda/gemm.cu:35, `(a, b, out, M, K, N, sa, sb, ta, tb,
 // accumulate)`); kernel choice is MI355X-specific.
+#include <cstdlib>
+#include <string>
+
 #include "gemm_kernel.h"
 #include "qutai_amd.h"
 
@@ -59,18 +62,39 @@ __global__ void __launch_bounds__(256) gemm_f64(const double* a, const double* b
     }
 }
 
-// Narrow fp32 -> bf16 (round to nearest even) into a workspace.
-__global__ void narrow_f32_bf16(const float* x, bf16_t* y, int64_t n) {
-  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (; i < n; i += stride) y[i] = f32_to_bf16(x[i]);
+// Operand re-layout into the workspace: dst[z][o][i] = src[z*stride + o*inner + i]
+// for i < inner (converted to the compute type; fp32 -> bf16 rounds to
+// nearest even) and 0 in the padding up to `pitch`.  Used when an fp32
+// operand feeds the bf16 MFMA path (mixed inputs, autocast) or when the
+// operand's rows are not 16-byte aligned.
+__global__ void prepare_operand(const void* src, int src_bf16, void* dst, int dst_bf16, int64_t outer,
+                                int64_t inner, int64_t pitch, int64_t batches, int64_t stride) {
+  int64_t total = batches * outer * pitch;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    int64_t z = i / (outer * pitch), rest = i % (outer * pitch);
+    int64_t o = rest / pitch, c = rest % pitch;
+    float v = 0.f;
+    if (c < inner) {
+      int64_t at = z * stride + o * inner + c;
+      v = src_bf16 ? bf16_to_f32(((const bf16_t*)src)[at]) : ((const float*)src)[at];
+    }
+    if (dst_bf16) ((bf16_t*)dst)[i] = f32_to_bf16(v);
+    else ((float*)dst)[i] = v;
+  }
 }
 
-enum Tile { TILE_L, TILE_N, TILE_W, TILE_S };
+// Kernel configurations: (BM x BN, WM x WN waves, BK, LDS stages, staging).
+//   L8D2: 256x256, 8 waves (2 per SIMD), BK 64 (bf16) / 32 (fp32), two-stage
+//         direct-to-LDS ring, the next stage's copies spread over the k-steps
+//   L8R : 256x256, 8 waves, same K step, register staging
+//   L4D2: 256x256, 4 waves (one per SIMD, 128x128 per wave), two-stage ring
+//   S   : 128x128, 4 waves, BK 32 / 16, four-stage ring (small grids, short K)
+//   N   : 256x64, 4 waves (N <= 64), W : 64x256, 4 waves (M <= 64)
+enum Tile { TILE_L8D2, TILE_L8R, TILE_L4D2, TILE_S, TILE_N, TILE_W, TILE_COUNT };
 
-template <bool F32, bool TA, bool TB, int BM, int BN, int WM, int WN>
+template <bool F32, bool TA, bool TB, int BM, int BN, int WM, int WN, int BK, int ST, bool DMA>
 hipError_t launch_cfg(GemmArgs p, hipStream_t stream) {
-  typedef GemmKernel<F32, TA, TB, BM, BN, WM, WN> Kern;
+  typedef GemmKernel<F32, TA, TB, BM, BN, WM, WN, BK, ST, DMA> Kern;
   int64_t tiles_n = (p.N + BN - 1) / BN;
   if (p.groups == 0) p.tiles_m = (int)((p.M + BM - 1) / BM);
   int64_t blocks = (int64_t)p.tiles_m * tiles_n * (p.groups ? 1 : p.batch);
@@ -82,11 +106,15 @@ hipError_t launch_cfg(GemmArgs p, hipStream_t stream) {
 
 template <bool F32, bool TA, bool TB>
 hipError_t launch_tile(Tile tile, GemmArgs p, hipStream_t stream) {
+  constexpr int KB = F32 ? 16 : 32;  // K per stage of the four-stage rings
+  constexpr int KR = F32 ? 32 : 64;  // K per stage of the two-stage rings
   switch (tile) {
-    case TILE_N: return launch_cfg<F32, TA, TB, 256, 64, 4, 1>(p, stream);
-    case TILE_W: return launch_cfg<F32, TA, TB, 64, 256, 1, 4>(p, stream);
-    case TILE_S: return launch_cfg<F32, TA, TB, 128, 128, 2, 2>(p, stream);
-    default: return launch_cfg<F32, TA, TB, 256, 256, 2, 2>(p, stream);
+    case TILE_L8R: return launch_cfg<F32, TA, TB, 256, 256, 2, 4, KR, 2, false>(p, stream);
+    case TILE_L4D2: return launch_cfg<F32, TA, TB, 256, 256, 2, 2, KR, 2, true>(p, stream);
+    case TILE_S: return launch_cfg<F32, TA, TB, 128, 128, 2, 2, KB, 4, true>(p, stream);
+    case TILE_N: return launch_cfg<F32, TA, TB, 256, 64, 4, 1, KB, 4, true>(p, stream);
+    case TILE_W: return launch_cfg<F32, TA, TB, 64, 256, 1, 4, KB, 4, true>(p, stream);
+    default: return launch_cfg<F32, TA, TB, 256, 256, 2, 4, KR, 2, true>(p, stream);
   }
 }
 
@@ -96,18 +124,69 @@ hipError_t launch_mma(Tile tile, bool ta, bool tb, const GemmArgs& p, hipStream_
   return tb ? launch_tile<F32, false, true>(tile, p, stream) : launch_tile<F32, false, false>(tile, p, stream);
 }
 
-// Tile choice: 256x256 when it still gives about one tile per CU, else the
-// 128x128 tile; thin outputs use the 256x64 / 64x256 shapes.
-Tile choose_tile(int64_t M, int64_t N, int64_t batch) {
+// Tile choice: 256x256 when the grid still gives about one tile per CU,
+// else the 128x128 tile; thin outputs use the 256x64 / 64x256 shapes.
+// QUTAI_AMD_GEMM_TILE=<L8D2|L8R|L4D2|S|N|W> overrides the choice (tuning).
+Tile choose_tile(int64_t M, int64_t N, int64_t K, int64_t batch) {
+  static int forced = [] {
+    const char* v = getenv("QUTAI_AMD_GEMM_TILE");
+    if (!v) return -1;
+    const char* names[TILE_COUNT] = {"L8D2", "L8R", "L4D2", "S", "N", "W"};
+    for (int i = 0; i < TILE_COUNT; i++)
+      if (std::string(v) == names[i]) return i;
+    return -1;
+  }();
+  if (forced >= 0) return (Tile)forced;
   if (N <= 64) return TILE_N;
   if (M <= 64) return TILE_W;
   int64_t big = ((M + 255) / 256) * ((N + 255) / 256) * batch;
-  if (big < 192) return TILE_S;
-  return TILE_L;
+  if (big < 192 || K <= 128) return TILE_S;
+  return TILE_L8D2;
 }
 
-bool aligned16(const void* p, int64_t ld, int64_t esize, int64_t stride) {
-  return ((uintptr_t)p % 16 == 0) && ((ld * esize) % 16 == 0) && ((stride * esize) % 16 == 0);
+// How one operand reaches the kernel: in place, or re-laid out in the
+// workspace (dtype change and/or zero-padded 16-byte-aligned rows).
+struct Operand {
+  const void* ptr;
+  int64_t ld, stride, src_stride;
+  bool copy;
+  int64_t outer, inner, pitch, batches;
+  size_t bytes;  // workspace bytes when copied
+};
+
+Operand plan_operand(const void* p, int dtype, bool compute_bf16, int64_t outer, int64_t inner, int64_t batch,
+                     int64_t stride) {
+  const int64_t E = compute_bf16 ? 8 : 4;
+  const int64_t es = compute_bf16 ? 2 : 4;
+  bool same = (dtype == QA_BF16) == compute_bf16;
+  bool aligned = ((uintptr_t)p % 16 == 0) && (inner % E == 0) && (batch <= 1 || stride % E == 0);
+  Operand o = {p, inner, stride, stride, !(same && aligned), outer, inner, inner, 1, 0};
+  if (o.copy) {
+    o.pitch = (inner + E - 1) / E * E;
+    o.batches = (stride == 0 || batch <= 1) ? 1 : batch;
+    o.ld = o.pitch;
+    o.stride = stride == 0 ? 0 : outer * o.pitch;
+    o.bytes = (size_t)(o.batches * outer * o.pitch * es + 255) / 256 * 256;
+  }
+  return o;
+}
+
+void plan(int64_t rows, int64_t inner, int64_t cols, int64_t batch, int64_t left_stride, int64_t right_stride,
+          int ta, int tb, int a_dtype, int b_dtype, bool bf16, const void* a, const void* b, Operand* pa,
+          Operand* pb) {
+  *pa = ta ? plan_operand(a, a_dtype, bf16, inner, rows, batch, left_stride)
+           : plan_operand(a, a_dtype, bf16, rows, inner, batch, left_stride);
+  *pb = tb ? plan_operand(b, b_dtype, bf16, cols, inner, batch, right_stride)
+           : plan_operand(b, b_dtype, bf16, inner, cols, batch, right_stride);
+}
+
+void launch_prepare(Operand& o, int src_dtype, bool bf16, char* ws, hipStream_t stream) {
+  int64_t total = o.batches * o.outer * o.pitch;
+  unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 1 << 20);
+  hipLaunchKernelGGL(prepare_operand, dim3(blocks < 1 ? 1 : blocks), dim3(256), 0, stream, o.ptr,
+                     src_dtype == QA_BF16, (void*)ws, bf16 ? 1 : 0, o.outer, o.inner, o.pitch, o.batches,
+                     o.src_stride);
+  o.ptr = ws;
 }
 
 // 4-wide output stores need 4 | ldc, 4 | batch stride and an aligned base.
@@ -122,15 +201,16 @@ int esize_of(int dtype) { return dtype == QA_BF16 ? 2 : dtype == QA_F64 ? 8 : 4;
 extern "C" {
 
 size_t qutai_amd_gemm_workspace_size(int64_t rows, int64_t inner, int64_t cols, int64_t batch,
-                                     int64_t left_stride, int64_t right_stride, int a_dtype, int b_dtype,
-                                     int bf16_compute) {
-  if (a_dtype == QA_F64 || b_dtype == QA_F64) return 0;
-  bool mixed = bf16_compute || a_dtype == QA_BF16 || b_dtype == QA_BF16;
-  if (!mixed) return 0;
-  size_t bytes = 0;
-  if (a_dtype == QA_F32) bytes += (size_t)((batch - 1) * left_stride + rows * inner) * 2 + 256;
-  if (b_dtype == QA_F32) bytes += (size_t)((batch - 1) * right_stride + inner * cols) * 2 + 256;
-  return batch > 0 ? bytes : 0;
+                                     int64_t left_stride, int64_t right_stride, int transpose_left,
+                                     int transpose_right, int a_dtype, int b_dtype, int bf16_compute) {
+  if (a_dtype == QA_F64 || b_dtype == QA_F64 || batch <= 0 || rows * cols == 0 || inner == 0) return 0;
+  bool bf16 = bf16_compute || a_dtype == QA_BF16 || b_dtype == QA_BF16;
+  Operand pa, pb;
+  // 256-byte aligned pointers: only dtype and row alignment decide
+  plan(rows, inner, cols, batch, left_stride, right_stride, transpose_left, transpose_right, a_dtype, b_dtype, bf16,
+       (const void*)256, (const void*)256, &pa, &pb);
+  if (!pa.copy && !pb.copy) return 0;
+  return (pa.copy ? pa.bytes : 0) + (pb.copy ? pb.bytes : 0) + 256;
 }
 
 int qutai_amd_gemm(const void* a, const void* b, void* out, int64_t rows, int64_t inner, int64_t cols,
@@ -157,52 +237,44 @@ int qutai_amd_gemm(const void* a, const void* b, void* out, int64_t rows, int64_
                        accumulate, tiles_n, tiles_m);
     return (int)hipGetLastError();
   }
-  bool mixed = bf16_compute || a_dtype == QA_BF16 || b_dtype == QA_BF16;
-  const void* A = a;
-  const void* B = b;
-  if (mixed) {
-    size_t need = qutai_amd_gemm_workspace_size(rows, inner, cols, batch, left_stride, right_stride, a_dtype,
-                                                b_dtype, bf16_compute);
-    if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return QA_EWORKSPACE;
+  bool bf16 = bf16_compute || a_dtype == QA_BF16 || b_dtype == QA_BF16;
+  Operand pa, pb;
+  plan(rows, inner, cols, batch, left_stride, right_stride, transpose_left, transpose_right, a_dtype, b_dtype, bf16,
+       a, b, &pa, &pb);
+  if (inner > 0 && (pa.copy || pb.copy)) {
+    size_t need = (pa.copy ? pa.bytes : 0) + (pb.copy ? pb.bytes : 0) + 256;
+    if (workspace == nullptr || workspace_bytes < need) return QA_EWORKSPACE;
     char* ws = (char*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
-    if (a_dtype == QA_F32 && inner > 0) {
-      int64_t n = (batch - 1) * left_stride + rows * inner;
-      hipLaunchKernelGGL(narrow_f32_bf16, dim3((unsigned)std::min<int64_t>((n + 255) / 256, 65536)), dim3(256), 0,
-                         stream, (const float*)a, (bf16_t*)ws, n);
-      A = ws;
-      ws += ((n * 2 + 255) / 256) * 256;
+    if (pa.copy) {
+      launch_prepare(pa, a_dtype, bf16, ws, stream);
+      ws += pa.bytes;
     }
-    if (b_dtype == QA_F32 && inner > 0) {
-      int64_t n = (batch - 1) * right_stride + inner * cols;
-      hipLaunchKernelGGL(narrow_f32_bf16, dim3((unsigned)std::min<int64_t>((n + 255) / 256, 65536)), dim3(256), 0,
-                         stream, (const float*)b, (bf16_t*)ws, n);
-      B = ws;
-    }
+    if (pb.copy) launch_prepare(pb, b_dtype, bf16, ws, stream);
   }
   GemmArgs p = {};
-  p.a = A;
-  p.b = B;
+  p.a = pa.ptr;
+  p.b = pb.ptr;
   p.out = out;
   p.M = rows;
   p.N = cols;
   p.K = inner;
-  p.lda = transpose_left ? rows : inner;
-  p.ldb = transpose_right ? inner : cols;
+  p.lda = pa.ld;
+  p.ldb = pb.ld;
   p.ldc = cols;
-  p.sa = left_stride;
-  p.sb = right_stride;
+  p.sa = pa.stride;
+  p.sb = pb.stride;
   p.sc = rows * cols;
   p.batch = batch;
   p.accumulate = accumulate ? 1 : 0;
   p.out_bf16 = out_dtype == QA_BF16;
-  int es = mixed ? 2 : 4;
-  p.vec_a = aligned16(A, p.lda, es, left_stride);
-  p.vec_b = aligned16(B, p.ldb, es, right_stride);
   p.vec_c = vec_out(out, p.ldc, p.sc);
   p.alpha = 1.0f;
-  Tile tile = choose_tile(rows, cols, batch);
-  hipError_t err = mixed ? launch_mma<false>(tile, transpose_left, transpose_right, p, stream)
-                         : launch_mma<true>(tile, transpose_left, transpose_right, p, stream);
+  // buffer descriptors address at most 2^31 bytes per K step
+  int64_t es = bf16 ? 2 : 4;
+  if ((p.lda * 256 * es) >= (1ll << 31) || (p.ldb * 256 * es) >= (1ll << 31)) return QA_EINVAL;
+  Tile tile = choose_tile(rows, cols, inner, batch);
+  hipError_t err = bf16 ? launch_mma<false>(tile, transpose_left, transpose_right, p, stream)
+                        : launch_mma<true>(tile, transpose_left, transpose_right, p, stream);
   return (int)err;
 }
 
@@ -229,16 +301,15 @@ int qutai_amd_gemm_grouped(const void* a, const void* b, void* out, const int64_
   p.batch = 1;
   p.accumulate = accumulate ? 1 : 0;
   p.out_bf16 = out_dtype == QA_BF16;
-  int es = esize_of(dtype);
-  p.vec_a = aligned16(a, p.lda, es, 0);
-  p.vec_b = aligned16(b, p.ldb, es, expert_stride);
+  int64_t E = dtype == QA_BF16 ? 8 : 4;
+  if ((uintptr_t)a % 16 || (uintptr_t)b % 16 || inner % E || p.ldb % E || expert_stride % E) return QA_EINVAL;
   p.vec_c = vec_out(out, p.ldc, 0);
   p.offsets = offsets;
   p.groups = groups;
   p.alpha = 1.0f;
   // Upper bound of M tiles over all groups: sum ceil(n_g / BM) <= ceil(max_rows / BM) + groups.
-  Tile tile = cols <= 64 ? TILE_N : TILE_L;
-  int bm = tile == TILE_N ? 256 : 256;
+  Tile tile = cols <= 64 ? TILE_N : TILE_L8D2;
+  int bm = 256;
   p.tiles_m = (int)((max_rows + bm - 1) / bm + groups);
   bool f32 = dtype == QA_F32;
   hipError_t err = f32 ? launch_mma<true>(tile, false, transpose_right, p, stream)

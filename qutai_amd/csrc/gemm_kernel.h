@@ -13,16 +13,19 @@
 //    fp32 accumulators stay in registers for the whole K loop;
 //  * bf16 operands feed v_mfma_f32_32x32x16_bf16, fp32 operands feed
 //    v_mfma_f32_32x32x2_f32 (true fp32 products, fp32 accumulation);
-//  * A and B tiles are staged HBM -> registers -> LDS with 16-byte loads,
-//    double-buffered in LDS so the loads of step k+1 are in flight while the
-//    MFMAs of step k run; one barrier per K step;
+//  * A and B tiles move HBM -> LDS in 16-byte chunks with buffer loads,
+//    either straight into LDS (`buffer_load_dwordx4 ... lds`, DMA = true,
+//    STAGES-deep ring so several K steps are in flight while the MFMAs run)
+//    or through registers (DMA = false, two LDS stages); a chunk outside the
+//    matrix gets an out-of-range buffer offset and reads as zeros, so the
+//    loop has no branches;
 //  * an operand whose K index is contiguous in HBM ("K-major") sits in LDS
 //    as [row][k] and is read with ds_read_b128; an operand whose M/N index is
 //    contiguous ("MN-major", e.g. B of a plain row-major A@B) keeps its HBM
 //    layout [k][row] in LDS and is read with the gfx950 transpose read
 //    ds_read_b64_tr_b16, so no transpose pass or register shuffle is needed;
 //  * LDS rows are XOR-swizzled in 16-byte chunks so the fragment reads and the
-//    staging writes are free of bank conflicts;
+//    stage writes are free of bank conflicts;
 //  * workgroup ids are remapped so that each XCD (own L2) works on one
 //    compact block of output tiles.
 #pragma once
@@ -40,7 +43,6 @@ struct GemmArgs {
   int64_t batch;
   int accumulate;         // out = old + A@B
   int out_bf16;           // output element type: bf16 (1) or fp32 (0)
-  int vec_a, vec_b;       // operand rows are 16-byte aligned
   int vec_c;              // output rows allow 16-byte (fp32) / 8-byte (bf16) stores
   // Grouped mode (groups > 0): group g owns rows [offsets[g], offsets[g+1])
   // of A (K-major, lda) and of out (ldc); its B operand is b + g*sb.
@@ -53,100 +55,119 @@ struct GemmArgs {
 template <bool F32> struct MmaTraits;
 template <> struct MmaTraits<false> {  // bf16 in, fp32 accumulate
   typedef bf16_t T;
-  static constexpr int E = 8;    // elements per 16-byte chunk
-  static constexpr int BK = 64;  // K per LDS stage (8 chunks per K-major row)
+  static constexpr int E = 8;  // elements per 16-byte chunk
 };
 template <> struct MmaTraits<true> {   // fp32 in, fp32 accumulate
   typedef float T;
   static constexpr int E = 4;
-  static constexpr int BK = 32;
 };
 
-// ---- LDS swizzles ---------------------------------------------------------
-// K-major tile [R][BK], 8 chunks of 16 B per row.  Fragment reads take 32
-// consecutive rows at one chunk; (r ^ r>>3) & 7 makes any 8 consecutive rows,
-// and any 8 rows of equal parity among 16 consecutive rows, hit different
-// chunks, so 8 or 16 lanes serviced together touch distinct banks.
-__device__ __forceinline__ int swz_k(int r) { return (r ^ (r >> 3)) & 7; }
+// ---- LDS swizzles -------------------------------------------------------------
+// K-major tile [R][BK] with CK 16-byte chunks per row.  Fragment reads take
+// 32 consecutive rows at one logical chunk; the XOR below sends any 8
+// consecutive rows (128-byte bank window) and any 16 consecutive rows
+// (256-byte window) to distinct banks.
+template <int CK>
+__device__ __forceinline__ int swz_k(int r) {
+  if constexpr (CK == 8) return (r ^ (r >> 3)) & 7;
+  else return ((r >> 1) ^ (r >> 3)) & 3;  // 64-byte rows: pair parity with row/2
+}
 
 // MN-major tile [BK][R] of bf16 read by ds_read_b64_tr_b16: 32 lanes read 4
 // consecutive k-rows x 64 bytes; shifting each of the 4 rows into its own
 // 64-byte quarter of a 256-byte bank window removes the 4-way conflict.
-template <int CR> __device__ __forceinline__ int swz_mn16(int k) {
+template <int CR>
+__device__ __forceinline__ int swz_mn16(int k) {
   return CR >= 16 ? (k & 3) * 4 : ((k >> 1) & 1) * 4;
 }
 // MN-major tile of fp32 read with ds_read_b32: the two lane halves read
 // k-rows 8 apart; put them in different 128-byte bank halves.
 __device__ __forceinline__ int swz_mn32(int k) { return ((k >> 3) & 1) * 8; }
 
-template <bool F32, bool KMAJOR, int R>
+// Physical LDS chunk q of one operand stage <-> logical chunk of the tile.
+// K-major: q = r * CK + p holds row r, logical chunk c = p ^ swz(r).
+// MN-major: q = k * CR + p holds k-row k, logical chunk c = p ^ swz(k).
+template <bool F32, bool KMAJOR, int R, int BK>
 struct OperandTile {
   typedef MmaTraits<F32> Tr;
-  typedef typename Tr::T T;
-  static constexpr int E = Tr::E, BK = Tr::BK;
-  static constexpr int CHUNKS = R * BK / E;          // 16-byte chunks per stage
-  static constexpr int CR = R / E;                   // chunks per MN-major row
-  static constexpr int ELEMS = R * BK;
+  static constexpr int E = Tr::E;
+  static constexpr int CK = BK / E;        // chunks per K-major row
+  static constexpr int CR = R / E;         // chunks per MN-major row
+  static constexpr int CHUNKS = R * BK / E;
+  static_assert(!KMAJOR || CK == 4 || CK == 8, "K-major rows of 4 or 8 chunks");
 
-  // element offset of chunk (row, c) inside one stage
-  __device__ static __forceinline__ int chunk_offset(int idx) {
-    if (KMAJOR) {
-      int r = idx >> 3, c = idx & 7;
-      return r * BK + ((c ^ swz_k(r)) * E);
+  __device__ static __forceinline__ int swz(int outer) {
+    if constexpr (KMAJOR) return swz_k<CK>(outer);
+    else return F32 ? swz_mn32(outer) : swz_mn16<CR>(outer);
+  }
+  // (outer, logical chunk) of physical chunk q
+  __device__ static __forceinline__ void coords(int q, int& outer, int& c) {
+    if constexpr (KMAJOR) {
+      outer = q / CK;
+      c = (q % CK) ^ swz(outer);
     } else {
-      int k = idx / CR, c = idx % CR;
-      int s = F32 ? swz_mn32(k) : swz_mn16<CR>(k);
-      return k * R + ((c ^ s) * E);
+      outer = q / CR;
+      c = (q % CR) ^ swz(outer);
     }
+  }
+  // element offset inside the stage of logical chunk (outer, c)
+  __device__ static __forceinline__ int offset(int outer, int c) {
+    return KMAJOR ? outer * BK + ((c ^ swz(outer)) * E) : outer * R + ((c ^ swz(outer)) * E);
   }
 };
 
-template <bool F32, bool TA, bool TB, int BM, int BN, int WM, int WN>
+template <bool F32, bool TA, bool TB, int BM, int BN, int WM, int WN, int BK, int STAGES, bool DMA>
 struct GemmKernel {
   typedef MmaTraits<F32> Tr;
   typedef typename Tr::T T;
-  static constexpr int E = Tr::E, BK = Tr::BK;
-  static constexpr int NT = 64 * WM * WN;
+  static constexpr int E = Tr::E;
+  static constexpr int NW = WM * WN;
+  static constexpr int NT = 64 * NW;
   static constexpr int TM = BM / WM, TN = BN / WN;  // wave tile
   static constexpr int FM = TM / 32, FN = TN / 32;  // 32x32 blocks per wave
   static constexpr bool KA = !TA;                   // A K-major?
   static constexpr bool KB = TB;                    // B K-major?
-  typedef OperandTile<F32, KA, BM> TileA;
-  typedef OperandTile<F32, KB, BN> TileB;
-  static constexpr int LA = TileA::CHUNKS / NT;     // chunks per thread
+  typedef OperandTile<F32, KA, BM, BK> TileA;
+  typedef OperandTile<F32, KB, BN, BK> TileB;
+  static constexpr int LA = TileA::CHUNKS / NT;     // chunks per thread and stage
   static constexpr int LB = TileB::CHUNKS / NT;
   static constexpr int STAGE = (BM + BN) * BK;      // elements per stage
-  static constexpr int LDS_BYTES = 2 * STAGE * (int)sizeof(T);
+  static constexpr int LDS_BYTES = STAGES * STAGE * (int)sizeof(T);
   static_assert(TileA::CHUNKS % NT == 0 && TileB::CHUNKS % NT == 0, "staging split");
-  static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile");
-  static_assert(LDS_BYTES <= 160 * 1024, "LDS");
+  static_assert(TM % 32 == 0 && TN % 32 == 0 && BK % 16 == 0, "tile shape");
+  static_assert(DMA || STAGES == 2, "register staging is double-buffered");
+  static_assert(STAGES >= 2 && LDS_BYTES <= 160 * 1024, "LDS");
 
-  // One 16-byte chunk of an operand from HBM: E elements along the
-  // contiguous axis starting at (outer, inner); zero outside [0,rows)x[0,cols).
-  __device__ static __forceinline__ u32x4 load_chunk(const T* base, int64_t ld, int64_t outer,
-                                                      int64_t inner, int64_t outer_n, int64_t inner_n,
-                                                      bool vec) {
-    if (vec && outer < outer_n && inner + E <= inner_n) {
-      return *reinterpret_cast<const u32x4*>(base + outer * ld + inner);
-    }
-    T v[E];
-#pragma unroll
-    for (int j = 0; j < E; j++) {
-      bool ok = outer < outer_n && inner + j < inner_n;
-      v[j] = ok ? base[outer * ld + inner + j] : (T)0;
-    }
-    u32x4 r;
-    __builtin_memcpy(&r, v, 16);
-    return r;
+  // Operand chunks are fetched with buffer loads: the descriptor's base is
+  // the first element this workgroup reads in the current K step, every
+  // lane's byte offset is fixed for the whole K loop, and a chunk outside the
+  // matrix gets an offset beyond the descriptor's range, for which the
+  // hardware returns zeros.  Operands whose rows are not 16-byte aligned are
+  // re-laid out (zero-padded pitch) by the host entry point before the launch.
+  static constexpr uint32_t OOB = 0x80000000u;
+  __device__ static __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const T* base, int64_t bytes) {
+    uint32_t n = bytes > 0x7ffffff0 ? 0x7ffffff0u : (uint32_t)bytes;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(base), 0, n, 0x00020000);
   }
+  __device__ static __forceinline__ u32x4 fetch(__amdgpu_buffer_rsrc_t r, uint32_t offset) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, 0));
+  }
+  typedef __attribute__((address_space(3))) void* lds_void;
+  __device__ static __forceinline__ void fetch_lds(__amdgpu_buffer_rsrc_t r, char* lds, uint32_t offset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void)lds, 16, offset, 0, 0, 0);
+  }
+  template <int N>
+  __device__ static __forceinline__ void wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+  }
+  __device__ static __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory"); }
 
   // Fragment reads -----------------------------------------------------------
   // bf16, K-major: lane l takes row (l & 31), k = 16 s + 8 (l >> 5) + [0, 8).
   __device__ static __forceinline__ bf16x8 frag_k16(const T* t, int row, int s, int lane) {
     int r = row + (lane & 31);
     int c = 2 * s + (lane >> 5);
-    const T* p = t + r * BK + ((c ^ swz_k(r)) * E);
-    return *reinterpret_cast<const bf16x8*>(p);
+    return *reinterpret_cast<const bf16x8*>(t + r * BK + ((c ^ swz_k<BK / E>(r)) * E));
   }
   // bf16, MN-major [BK][R]: two transpose reads of 4 k-values each.  Within a
   // 16-lane group, source lane i reads k-row kb + i/4, columns cb + 4 (i&3);
@@ -169,10 +190,11 @@ struct GemmKernel {
   }
   // fp32, K-major: lane takes row (l & 31), k = 16 s + 8 (l >> 5) + [0, 8).
   __device__ static __forceinline__ void frag_k32(const T* t, int row, int s, int lane, float (&v)[8]) {
+    constexpr int CK = BK / E;
     int r = row + (lane & 31);
     int c0 = 4 * s + 2 * (lane >> 5);
-    f32x4 x = *reinterpret_cast<const f32x4*>(t + r * BK + ((c0 ^ swz_k(r)) * E));
-    f32x4 y = *reinterpret_cast<const f32x4*>(t + r * BK + (((c0 + 1) ^ swz_k(r)) * E));
+    f32x4 x = *reinterpret_cast<const f32x4*>(t + r * BK + ((c0 ^ swz_k<CK>(r)) * E));
+    f32x4 y = *reinterpret_cast<const f32x4*>(t + r * BK + (((c0 + 1) ^ swz_k<CK>(r)) * E));
     v[0] = x[0]; v[1] = x[1]; v[2] = x[2]; v[3] = x[3];
     v[4] = y[0]; v[5] = y[1]; v[6] = y[2]; v[7] = y[3];
   }
@@ -188,16 +210,88 @@ struct GemmKernel {
     }
   }
 
+  // MFMAs of one LDS stage.  bf16: the fragments of k-step s+1 are read
+  // while the MFMAs of step s run (two fragment register sets), and the
+  // scheduler is asked to interleave one LDS read between MFMAs.
+  static constexpr int READS = (KA ? 1 : 2) * FM + (KB ? 1 : 2) * FN;  // ds_read per k-step
+  __device__ static __forceinline__ void frags16(const T* sa, const T* sb, bf16x8 (&fa)[FM], bf16x8 (&fb)[FN],
+                                                 int wm, int wn, int s, int lane) {
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+      fa[i] = KA ? frag_k16(sa, wm * TM + i * 32, s, lane) : frag_mn16<BM>(sa, wm * TM + i * 32, s, lane);
+#pragma unroll
+    for (int j = 0; j < FN; j++)
+      fb[j] = KB ? frag_k16(sb, wn * TN + j * 32, s, lane) : frag_mn16<BN>(sb, wn * TN + j * 32, s, lane);
+  }
+  __device__ static __forceinline__ void mfma16(const bf16x8 (&fa)[FM], const bf16x8 (&fb)[FN],
+                                                f32x16 (&acc)[FM][FN]) {
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+      for (int j = 0; j < FN; j++)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+  }
+  __device__ static __forceinline__ void compute(const T* sa, const T* sb, f32x16 (&acc)[FM][FN], int wm, int wn,
+                                                 int lane) {
+    if constexpr (!F32) {
+      constexpr int S = BK / 16;
+      bf16x8 fa[2][FM], fb[2][FN];
+      frags16(sa, sb, fa[0], fb[0], wm, wn, 0, lane);
+#pragma unroll
+      for (int s = 0; s < S; s++) {
+        if (s + 1 < S) frags16(sa, sb, fa[(s + 1) & 1], fb[(s + 1) & 1], wm, wn, s + 1, lane);
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+          for (int j = 0; j < FN; j++)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[s & 1][i], fb[s & 1][j], acc[i][j], 0, 0, 0);
+      }
+#ifdef QA_SCHED_INTERLEAVE
+      // one group per MFMA, one LDS read after each of the first ones
+#pragma unroll
+      for (int s = 0; s < S; s++) {
+#pragma unroll
+        for (int m = 0; m < FM * FN; m++) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          if (s + 1 < S && m < READS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+      }
+#endif
+    } else {
+#pragma unroll
+      for (int s = 0; s < BK / 16; s++) {
+        float fa[FM][8], fb[FN][8];
+#pragma unroll
+        for (int i = 0; i < FM; i++) {
+          if (KA) frag_k32(sa, wm * TM + i * 32, s, lane, fa[i]);
+          else frag_mn32<BM>(sa, wm * TM + i * 32, s, lane, fa[i]);
+        }
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+          if (KB) frag_k32(sb, wn * TN + j * 32, s, lane, fb[j]);
+          else frag_mn32<BN>(sb, wn * TN + j * 32, s, lane, fb[j]);
+        }
+#pragma unroll
+        for (int q = 0; q < 8; q++)
+#pragma unroll
+          for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int j = 0; j < FN; j++)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][q], fb[j][q], acc[i][j], 0, 0, 0);
+      }
+    }
+  }
+
   __device__ static __forceinline__ void run(const GemmArgs& p, char* smem) {
     T* lds = reinterpret_cast<T*>(smem);
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = uniform32(tid >> 6);
     const int wm = wave / WN, wn = wave % WN;
 
     // ---- tile scheduling -------------------------------------------------
     const int tiles_n = (int)((p.N + BN - 1) / BN);
     const int tiles_per = p.tiles_m * tiles_n;
     const int total = (int)gridDim.x;
-    int pid = xcd_remap((int)blockIdx.x, total);
+    int pid = uniform32(xcd_remap((int)blockIdx.x, total));
     int64_t bz = pid / tiles_per;
     int t = pid % tiles_per;
     // grouped ordering: 4 M-tiles per group, N fastest inside a group
@@ -235,46 +329,14 @@ struct GemmKernel {
       outp += bz * p.sc * osize;
       row0 = (int64_t)tile_m * BM;
     }
-    const int64_t col0 = (int64_t)tile_n * BN;
+    A = uniform_ptr(A);
+    B = uniform_ptr(B);
+    outp = uniform_ptr(outp);
+    M = uniform64(M);
+    row0 = uniform64(row0);
+    const int64_t col0 = uniform64((int64_t)tile_n * BN);
     const int64_t K = p.K, N = p.N;
-    const bool vec_a = p.vec_a, vec_b = p.vec_b;
-
-    // ---- staging -----------------------------------------------------------
-    u32x4 ra[LA], rb[LB];
-    auto load = [&](int64_t k0) {
-#pragma unroll
-      for (int i = 0; i < LA; i++) {
-        int idx = tid + i * NT;
-        if (KA) {  // rows of A, K contiguous
-          int r = idx >> 3, c = idx & 7;
-          ra[i] = load_chunk(A, p.lda, row0 + r, k0 + c * E, M, K, vec_a);
-        } else {   // A^T stored [K][M]
-          int k = idx / TileA::CR, c = idx % TileA::CR;
-          ra[i] = load_chunk(A, p.lda, k0 + k, row0 + c * E, K, M, vec_a);
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < LB; i++) {
-        int idx = tid + i * NT;
-        if (KB) {  // B^T stored [N][K]
-          int r = idx >> 3, c = idx & 7;
-          rb[i] = load_chunk(B, p.ldb, col0 + r, k0 + c * E, N, K, vec_b);
-        } else {   // B stored [K][N]
-          int k = idx / TileB::CR, c = idx % TileB::CR;
-          rb[i] = load_chunk(B, p.ldb, k0 + k, col0 + c * E, K, N, vec_b);
-        }
-      }
-    };
-    auto store = [&](int stage) {
-      T* sa = lds + stage * STAGE;
-      T* sb = sa + BM * BK;
-#pragma unroll
-      for (int i = 0; i < LA; i++)
-        *reinterpret_cast<u32x4*>(sa + TileA::chunk_offset(tid + i * NT)) = ra[i];
-#pragma unroll
-      for (int i = 0; i < LB; i++)
-        *reinterpret_cast<u32x4*>(sb + TileB::chunk_offset(tid + i * NT)) = rb[i];
-    };
+    const int64_t lda = p.lda, ldb = p.ldb;
 
     f32x16 acc[FM][FN];
 #pragma unroll
@@ -285,56 +347,159 @@ struct GemmKernel {
         for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
 
     const int nk = (int)((K + BK - 1) / BK);
-    if (nk > 0) {
-      load(0);
-      store(0);
-      __syncthreads();
-    }
-    for (int kt = 0; kt < nk; kt++) {
-      const int cur = kt & 1;
-      if (kt + 1 < nk) load((int64_t)(kt + 1) * BK);
-      const T* sa = lds + cur * STAGE;
-      const T* sb = sa + BM * BK;
+    // descriptor of one operand for the K step starting at k0
+    auto desc_a = [&](int64_t k0) {
+      return rsrc(KA ? A + row0 * lda + k0 : A + k0 * lda + row0,
+                  (int64_t)(KA ? BM * lda : BK * lda) * (int64_t)sizeof(T));
+    };
+    auto desc_b = [&](int64_t k0) {
+      return rsrc(KB ? B + col0 * ldb + k0 : B + k0 * ldb + col0,
+                  (int64_t)(KB ? BN * ldb : BK * ldb) * (int64_t)sizeof(T));
+    };
+
+    if constexpr (DMA) {
+      // ---- direct-to-LDS ring: wave w, instruction j fills physical chunks
+      // q = (j * NW + w) * 64 + lane, i.e. 1 KB of LDS per instruction.
+      constexpr int JA = TileA::CHUNKS / (64 * NW), JB = TileB::CHUNKS / (64 * NW);
+      constexpr int L = JA + JB;  // DMA instructions per wave and stage
+      static_assert(TileA::CHUNKS % (64 * NW) == 0 && TileB::CHUNKS % (64 * NW) == 0, "DMA split");
+      static_assert(L * (STAGES - 2) <= 63, "vmcnt range");
+      uint32_t oa[JA], ob[JB];
+      int ka[JA], kb[JB];  // k coordinate of the chunk (validity per K step)
+      bool va[JA], vb[JB];
 #pragma unroll
-      for (int s = 0; s < BK / 16; s++) {
+      for (int j = 0; j < JA; j++) {
+        int q = (j * NW + wave) * 64 + lane, outer, c;
+        TileA::coords(q, outer, c);
+        oa[j] = (uint32_t)(((int64_t)outer * lda + c * E) * (int64_t)sizeof(T));
+        ka[j] = KA ? c * E : outer;
+        va[j] = KA ? (row0 + outer < M) : (row0 + c * E < M);
+      }
+#pragma unroll
+      for (int j = 0; j < JB; j++) {
+        int q = (j * NW + wave) * 64 + lane, outer, c;
+        TileB::coords(q, outer, c);
+        ob[j] = (uint32_t)(((int64_t)outer * ldb + c * E) * (int64_t)sizeof(T));
+        kb[j] = KB ? c * E : outer;
+        vb[j] = KB ? (col0 + outer < N) : (col0 + c * E < N);
+      }
+      char* base = reinterpret_cast<char*>(lds);
+      // copies of one stage, optionally only instructions [first, last)
+      auto issue_range = [&](int stage, int64_t k0, int first, int last) {
+        auto da = desc_a(k0);
+        auto db = desc_b(k0);
+        const int64_t krem = K - k0;
+        char* sa = base + stage * STAGE * (int)sizeof(T);
+        char* sb = sa + BM * BK * (int)sizeof(T);
+#pragma unroll
+        for (int j = 0; j < JA; j++)
+          if (j >= first && j < last)
+            fetch_lds(da, sa + (j * NW + wave) * 1024, (va[j] && ka[j] < krem) ? oa[j] : OOB);
+#pragma unroll
+        for (int j = 0; j < JB; j++)
+          if (JA + j >= first && JA + j < last)
+            fetch_lds(db, sb + (j * NW + wave) * 1024, (vb[j] && kb[j] < krem) ? ob[j] : OOB);
+      };
+      auto issue = [&](int stage, int64_t k0) { issue_range(stage, k0, 0, L); };
+#pragma unroll
+      for (int st = 0; st < STAGES - 1; st++)
+        if (st < nk) issue(st, (int64_t)st * BK);
+      for (int kt = 0; kt < nk; kt++) {
+        // this wave's copies of stage kt are done when at most the copies of
+        // the (up to STAGES-2) younger stages are still outstanding
+        const int younger = min(STAGES - 2, nk - 1 - kt);
+        if (younger >= 3) wait_vm<(STAGES >= 5 ? 3 : 0) * L>();
+        else if (younger == 2) wait_vm<(STAGES >= 4 ? 2 : 0) * L>();
+        else if (younger == 1) wait_vm<L>();
+        else wait_vm<0>();
+        barrier();  // every wave's copies of stage kt are in LDS; stage kt-1 is free
+        const T* sa = lds + (kt % STAGES) * STAGE;
+        const bool more = kt + STAGES - 1 < nk;
+        const int next = (kt + STAGES - 1) % STAGES;
+        const int64_t k_next = (int64_t)(kt + STAGES - 1) * BK;
         if constexpr (!F32) {
-          bf16x8 fa[FM], fb[FN];
+          // one slice of the next stage's copies per k-step, between the
+          // fragment reads and the MFMAs of that step
+          constexpr int S = BK / 16, PER = (L + S - 1) / S;
+          const T* sb = sa + BM * BK;
+          bf16x8 fa[2][FM], fb[2][FN];
+          frags16(sa, sb, fa[0], fb[0], wm, wn, 0, lane);
 #pragma unroll
-          for (int i = 0; i < FM; i++)
-            fa[i] = KA ? frag_k16(sa, wm * TM + i * 32, s, lane)
-                       : frag_mn16<BM>(sa, wm * TM + i * 32, s, lane);
-#pragma unroll
-          for (int j = 0; j < FN; j++)
-            fb[j] = KB ? frag_k16(sb, wn * TN + j * 32, s, lane)
-                       : frag_mn16<BN>(sb, wn * TN + j * 32, s, lane);
-#pragma unroll
-          for (int i = 0; i < FM; i++)
-#pragma unroll
-            for (int j = 0; j < FN; j++)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+          for (int s = 0; s < S; s++) {
+            if (more) issue_range(next, k_next, s * PER, (s + 1) * PER < L ? (s + 1) * PER : L);
+            if (s + 1 < S) frags16(sa, sb, fa[(s + 1) & 1], fb[(s + 1) & 1], wm, wn, s + 1, lane);
+            mfma16(fa[s & 1], fb[s & 1], acc);
+          }
         } else {
-          float fa[FM][8], fb[FN][8];
-#pragma unroll
-          for (int i = 0; i < FM; i++) {
-            if (KA) frag_k32(sa, wm * TM + i * 32, s, lane, fa[i]);
-            else frag_mn32<BM>(sa, wm * TM + i * 32, s, lane, fa[i]);
-          }
-#pragma unroll
-          for (int j = 0; j < FN; j++) {
-            if (KB) frag_k32(sb, wn * TN + j * 32, s, lane, fb[j]);
-            else frag_mn32<BN>(sb, wn * TN + j * 32, s, lane, fb[j]);
-          }
-#pragma unroll
-          for (int q = 0; q < 8; q++)
-#pragma unroll
-            for (int i = 0; i < FM; i++)
-#pragma unroll
-              for (int j = 0; j < FN; j++)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][q], fb[j][q], acc[i][j], 0, 0, 0);
+          if (more) issue(next, k_next);
+          compute(sa, sa + BM * BK, acc, wm, wn, lane);
         }
       }
-      if (kt + 1 < nk) store(cur ^ 1);
-      __syncthreads();
+      static_assert(STAGES <= 5, "wait table covers up to 3 younger stages");
+    } else {
+      // ---- register staging, two LDS stages --------------------------------
+      uint32_t oa[LA], ob[LB];
+      int ka[LA], kb[LB];
+      bool va[LA], vb[LB];
+#pragma unroll
+      for (int i = 0; i < LA; i++) {
+        int idx = tid + i * NT;
+        int outer = KA ? idx / TileA::CK : idx / TileA::CR;
+        int c = KA ? idx % TileA::CK : idx % TileA::CR;
+        oa[i] = (uint32_t)(((int64_t)outer * lda + c * E) * (int64_t)sizeof(T));
+        ka[i] = KA ? c * E : outer;
+        va[i] = KA ? (row0 + outer < M) : (row0 + c * E < M);
+      }
+#pragma unroll
+      for (int i = 0; i < LB; i++) {
+        int idx = tid + i * NT;
+        int outer = KB ? idx / TileB::CK : idx / TileB::CR;
+        int c = KB ? idx % TileB::CK : idx % TileB::CR;
+        ob[i] = (uint32_t)(((int64_t)outer * ldb + c * E) * (int64_t)sizeof(T));
+        kb[i] = KB ? c * E : outer;
+        vb[i] = KB ? (col0 + outer < N) : (col0 + c * E < N);
+      }
+      u32x4 ra[LA], rb[LB];
+      auto load = [&](int64_t k0) {
+        auto da = desc_a(k0);
+        auto db = desc_b(k0);
+        const int64_t krem = K - k0;
+#pragma unroll
+        for (int i = 0; i < LA; i++) ra[i] = fetch(da, (va[i] && ka[i] < krem) ? oa[i] : OOB);
+#pragma unroll
+        for (int i = 0; i < LB; i++) rb[i] = fetch(db, (vb[i] && kb[i] < krem) ? ob[i] : OOB);
+      };
+      auto store = [&](int stage) {
+        T* sa = lds + stage * STAGE;
+        T* sb = sa + BM * BK;
+#pragma unroll
+        for (int i = 0; i < LA; i++) {
+          int idx = tid + i * NT;
+          int outer = KA ? idx / TileA::CK : idx / TileA::CR;
+          int c = KA ? idx % TileA::CK : idx % TileA::CR;
+          *reinterpret_cast<u32x4*>(sa + TileA::offset(outer, c)) = ra[i];
+        }
+#pragma unroll
+        for (int i = 0; i < LB; i++) {
+          int idx = tid + i * NT;
+          int outer = KB ? idx / TileB::CK : idx / TileB::CR;
+          int c = KB ? idx % TileB::CK : idx % TileB::CR;
+          *reinterpret_cast<u32x4*>(sb + TileB::offset(outer, c)) = rb[i];
+        }
+      };
+      if (nk > 0) {
+        load(0);
+        store(0);
+        __syncthreads();
+      }
+      for (int kt = 0; kt < nk; kt++) {
+        const int cur = kt & 1;
+        if (kt + 1 < nk) load((int64_t)(kt + 1) * BK);
+        const T* sa = lds + cur * STAGE;
+        compute(sa, sa + BM * BK, acc, wm, wn, lane);
+        if (kt + 1 < nk) store(cur ^ 1);
+        __syncthreads();
+      }
     }
 
     // ---- epilogue ---------------------------------------------------------
@@ -360,7 +525,7 @@ struct GemmKernel {
   // rows.  The row pitch EP = TN + 8 floats puts the two lane halves, which
   // write rows 4 apart, into different bank halves.
   static constexpr int EP = TN + 8;
-  static_assert(WM * WN * 32 * EP * 4 <= LDS_BYTES, "epilogue staging");
+  static_assert(NW * 32 * EP * 4 <= LDS_BYTES, "epilogue staging");
 
   struct Out {
     char* ptr;

@@ -44,9 +44,15 @@ def test_bindings_apply_without_a_device():
     from qutai_amd.backends import amd_runtime
 
     library = amd_runtime.load_library()
-    # pure host helper: workspace sizing needs no GPU
-    assert library.qutai_amd_gemm_workspace_size(4, 8, 2, 1, 0, 0, 0, 5, 0) == 4 * 8 * 2 + 256
-    assert library.qutai_amd_gemm_workspace_size(4, 8, 2, 1, 0, 0, 5, 5, 0) == 0
-    assert library.qutai_amd_gemm_workspace_size(4, 8, 2, 1, 0, 0, 0, 0, 0) == 0
-    # autocast of two fp32 operands: 4*8 and 8*2 bf16 copies, 256 bytes of alignment slack each
-    assert library.qutai_amd_gemm_workspace_size(4, 8, 2, 1, 0, 0, 0, 0, 1) == (32 * 2 + 256) + (16 * 2 + 256)
+    # pure host helper: workspace sizing needs no GPU.  (rows, inner, cols,
+    # batch, strides, ta, tb, a dtype, b dtype, bf16 compute)
+    size = library.qutai_amd_gemm_workspace_size
+    assert size(64, 64, 64, 1, 0, 0, 0, 0, 5, 5, 0) == 0  # aligned bf16 x bf16: in place
+    # fp32 A into the bf16 path: a 64x64 bf16 copy (8 KiB, 256-byte rounded) + slack
+    assert size(64, 64, 64, 1, 0, 0, 0, 0, 0, 5, 0) == 64 * 64 * 2 + 256
+    # 4097-wide row-major bf16 B (NN): rows padded to 4104 elements
+    assert size(8, 16, 4097, 1, 0, 0, 0, 0, 5, 5, 0) == (16 * 4104 * 2 + 255) // 256 * 256 + 256
+    # fp32 x fp32 aligned: in place
+    assert size(64, 64, 64, 1, 0, 0, 0, 0, 0, 0, 0) == 0
+    # autocast of two fp32 operands: both copied
+    assert size(64, 64, 64, 1, 0, 0, 0, 0, 0, 0, 1) == 2 * 64 * 64 * 2 + 256
