@@ -210,6 +210,8 @@ def main():
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--only", default=None, help="run one workload")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    parser.add_argument("--calibrate-copy", action="store_true",
+                        help="run only a plain 256 MiB copy kernel (the HBM-counter calibration for rocprofv3 --pmc)")
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the GEMM path is single-device (see DESIGN.md for how it would shard)",
@@ -219,6 +221,14 @@ def main():
     from qutai_amd.backends import amd
 
     runtime = amd.get_runtime()
+    if args.calibrate_copy:
+        count = 64 * 1024 * 1024  # fp32 values: 256 MiB read + 256 MiB written per launch
+        src, dst = amd.full(count, 1.5, dtype="float32"), amd.full(count, 0.0, dtype="float32")
+        for _ in range(3):
+            runtime.call("qutai_amd_cast", src.ptr, dst.ptr, count, 0, 0)
+        runtime.synchronize()
+        print(json.dumps({"calibration": "copy", "bytes_read": count * 4, "bytes_written": count * 4}))
+        return
     timer = Timer(runtime)
     names = [args.only] if args.only else list(WORKLOADS)
     results = {}
@@ -262,7 +272,7 @@ def main():
     if value is not None:
         line["roofline"] = {"bound": "mfma", "achieved": value, "peak": PEAK["bf16"], "unit": "TFLOP/s",
                             "frac": round(value / PEAK["bf16"], 4), "traffic": traffic,
-                            "kernel": "gemm_entry<GemmKernel<bf16,NN,256x256>>",
+                            "kernel": "gemm_entry<GemmKernel<bf16 NN, 256x256 tile, 8 waves, BK 64, direct-to-LDS>>",
                             "algorithmic_flops_per_launch": 2 * 4096 ** 3}
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()

@@ -95,17 +95,33 @@ __global__ void __launch_bounds__(PACK) route_pack(const int64_t* indices, int64
 }
 
 // utilization = count / (rows * top_k); aux = experts * sum(p * util) / rows.
-__global__ void __launch_bounds__(256) route_stats(const float* probs, const int64_t* counts, float* utilization,
-                                                   float* aux, int64_t rows, int64_t experts, int64_t n) {
-  __shared__ float red[4];
+// One 1024-thread workgroup: each thread sums a contiguous block of rows,
+// then a fixed-order tree reduction in LDS (deterministic result).
+constexpr int STATS = 1024;
+__global__ void __launch_bounds__(STATS) route_stats(const float* probs, const int64_t* counts, float* utilization,
+                                                     float* aux, int64_t rows, int64_t experts, int64_t n) {
+  __shared__ float util[256];
+  __shared__ float red[STATS];
   int tid = threadIdx.x;
-  for (int64_t e = tid; e < experts; e += 256) utilization[e] = (float)counts[e] / (float)n;
-  float total = 0.f;
-  for (int64_t i = tid; i < rows * experts; i += 256) total += probs[i] * ((float)counts[i % experts] / (float)n);
-  for (int o = 32; o > 0; o >>= 1) total += __shfl_xor(total, o);
-  if ((tid & 63) == 0) red[tid >> 6] = total;
+  for (int64_t e = tid; e < experts; e += STATS) {
+    float u = (float)counts[e] / (float)n;
+    utilization[e] = u;
+    if (e < 256) util[e] = u;
+  }
   __syncthreads();
-  if (tid == 0) aux[0] = (float)experts * (red[0] + red[1] + red[2] + red[3]) / (float)rows;
+  int64_t per = (rows + STATS - 1) / STATS;
+  int64_t r0 = tid * per, r1 = min(rows, r0 + per);
+  float total = 0.f;
+  for (int64_t r = r0; r < r1; r++)
+    for (int64_t e = 0; e < experts; e++)
+      total += probs[r * experts + e] * (e < 256 ? util[e] : (float)counts[e] / (float)n);
+  red[tid] = total;
+  __syncthreads();
+  for (int s = STATS / 2; s > 0; s >>= 1) {
+    if (tid < s) red[tid] += red[tid + s];
+    __syncthreads();
+  }
+  if (tid == 0) aux[0] = (float)experts * red[0] / (float)rows;
 }
 
 // Row gather / scatter in 16-byte pieces.
@@ -183,7 +199,7 @@ int qutai_amd_route(const float* scores, float* probs, float* weights, int64_t* 
   hipLaunchKernelGGL(route_pack, dim3((unsigned)experts), dim3(PACK), 0, s, indices, counts, ids, slots, locations,
                      offsets, order, n, top_k, experts);
   if (rows > 0)
-    hipLaunchKernelGGL(route_stats, dim3(1), dim3(256), 0, s, probs, counts, utilization, aux, rows, experts, n);
+    hipLaunchKernelGGL(route_stats, dim3(1), dim3(STATS), 0, s, probs, counts, utilization, aux, rows, experts, n);
   return (int)hipGetLastError();
 }
 

@@ -179,6 +179,98 @@ __global__ void __launch_bounds__(THREADS) softmax_rows_kernel(const T* x, T* ou
   }
 }
 
+// Row softmax, one wavefront per row (4 rows per 256-thread workgroup):
+// 16-byte loads (8 bf16 or 4 fp32 per lane), the row kept in registers for
+// up to 64 * V * CH elements, max and sum reduced inside the wavefront (no
+// LDS, no barrier).  HBM sees one read and one write of every row.
+template <class T, int CH>  // CH 16-byte chunks per lane held in registers
+__global__ void __launch_bounds__(256) softmax_rows_wave(const T* x, T* out, int64_t rows, int64_t width,
+                                                         float scale) {
+  constexpr int V = 16 / sizeof(T);
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const u32x4* xr = reinterpret_cast<const u32x4*>(x + row * width);
+  u32x4* yr = reinterpret_cast<u32x4*>(out + row * width);
+  const int chunks = (int)(width / V);
+  auto unpack = [&](u32x4 w, float (&f)[V]) {
+    if constexpr (sizeof(T) == 2) {
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        f[2 * q] = __uint_as_float(w[q] << 16) * scale;
+        f[2 * q + 1] = __uint_as_float(w[q] & 0xffff0000u) * scale;
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; q++) f[q] = __uint_as_float(w[q]) * scale;
+    }
+  };
+  auto pack = [&](const float (&f)[V]) {
+    u32x4 w;
+    if constexpr (sizeof(T) == 2) {
+#pragma unroll
+      for (int q = 0; q < 4; q++) w[q] = pack_bf16x2(f[2 * q], f[2 * q + 1]);
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; q++) w[q] = __float_as_uint(f[q]);
+    }
+    return w;
+  };
+  float v[CH][V];
+  float peak = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < CH; c++) {
+    int at = lane + 64 * c;
+    if (at < chunks) {
+      unpack(xr[at], v[c]);
+#pragma unroll
+      for (int e = 0; e < V; e++) peak = fmaxf(peak, v[c][e]);
+    }
+  }
+  for (int at = lane + 64 * CH; at < chunks; at += 64) {
+    float f[V];
+    unpack(xr[at], f);
+#pragma unroll
+    for (int e = 0; e < V; e++) peak = fmaxf(peak, f[e]);
+  }
+  for (int o = 32; o > 0; o >>= 1) peak = fmaxf(peak, __shfl_xor(peak, o));
+  float total = 0.f;
+#pragma unroll
+  for (int c = 0; c < CH; c++) {
+    if (lane + 64 * c < chunks) {
+#pragma unroll
+      for (int e = 0; e < V; e++) {
+        v[c][e] = __expf(v[c][e] - peak);
+        total += v[c][e];
+      }
+    }
+  }
+  for (int at = lane + 64 * CH; at < chunks; at += 64) {
+    float f[V];
+    unpack(xr[at], f);
+#pragma unroll
+    for (int e = 0; e < V; e++) total += __expf(f[e] - peak);
+  }
+  for (int o = 32; o > 0; o >>= 1) total += __shfl_xor(total, o);
+  const float inv = 1.0f / total;
+#pragma unroll
+  for (int c = 0; c < CH; c++) {
+    int at = lane + 64 * c;
+    if (at < chunks) {
+#pragma unroll
+      for (int e = 0; e < V; e++) v[c][e] *= inv;
+      yr[at] = pack(v[c]);
+    }
+  }
+  for (int at = lane + 64 * CH; at < chunks; at += 64) {
+    float f[V];
+    unpack(xr[at], f);
+#pragma unroll
+    for (int e = 0; e < V; e++) f[e] = __expf(f[e] - peak) * inv;
+    yr[at] = pack(f);
+  }
+}
+
 __global__ void softmax_rows_f64(const double* x, double* out, int64_t rows, int64_t width, double scale) {
   __shared__ double red[THREADS];
   int64_t row = blockIdx.x;
@@ -351,12 +443,24 @@ int qutai_amd_softmax_rows(const void* x, void* out, int64_t rows, int64_t width
   if (dtype == F64)
     hipLaunchKernelGGL(softmax_rows_f64, dim3((unsigned)rows), dim3(THREADS), 0, s, (const double*)x, (double*)out,
                        rows, width, scale);
-  else if (dtype == F32)
-    hipLaunchKernelGGL((softmax_rows_kernel<float, 8>), dim3((unsigned)rows), dim3(THREADS), 0, s, (const float*)x,
-                       (float*)out, rows, width, (float)scale);
-  else
-    hipLaunchKernelGGL((softmax_rows_kernel<bf16_t, 8>), dim3((unsigned)rows), dim3(THREADS), 0, s,
-                       (const bf16_t*)x, (bf16_t*)out, rows, width, (float)scale);
+  else {
+    // vector path: whole 16-byte chunks per row and 16-byte aligned rows
+    int64_t v = dtype == F32 ? 4 : 8;
+    bool vec = width % v == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)out % 16 == 0;
+    unsigned groups = (unsigned)((rows + 3) / 4);
+    if (vec && dtype == F32)
+      hipLaunchKernelGGL((softmax_rows_wave<float, 8>), dim3(groups), dim3(256), 0, s, (const float*)x, (float*)out,
+                         rows, width, (float)scale);
+    else if (vec)
+      hipLaunchKernelGGL((softmax_rows_wave<bf16_t, 4>), dim3(groups), dim3(256), 0, s, (const bf16_t*)x,
+                         (bf16_t*)out, rows, width, (float)scale);
+    else if (dtype == F32)
+      hipLaunchKernelGGL((softmax_rows_kernel<float, 8>), dim3((unsigned)rows), dim3(THREADS), 0, s,
+                         (const float*)x, (float*)out, rows, width, (float)scale);
+    else
+      hipLaunchKernelGGL((softmax_rows_kernel<bf16_t, 8>), dim3((unsigned)rows), dim3(THREADS), 0, s,
+                         (const bf16_t*)x, (bf16_t*)out, rows, width, (float)scale);
+  }
   return (int)hipGetLastError();
 }
 
