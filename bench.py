@@ -6,8 +6,8 @@ the amd backend's ``gemm`` (the largest single-GPU
 config the headline is quoted on).  W untimed warm-up steps, then K steps
 timed with HIP events on the default stream (the stream every kernel runs
 on) between two device synchronisations.  The JSON line also carries the
-other configs (fp32 4096^3, the ragged shape, attention bmm, dense Linear
-fwd/bwd, MoE grouped experts) measured the same way, the roofline of the
+other configs (fp32 4096^3, the ragged shape, attention bmm and fused
+attention, dense Linear fwd/bwd, MoE grouped experts) measured the same way, the roofline of the
 dominant kernel and the CPU baseline (the pure-Python float64 restatement
 of the reference CPU GEMM, timed on a bounded sample on this host).
 
@@ -106,6 +106,26 @@ def attention_bmm(seed=2):
     return step, 2 * 2.0 * b * h * t * t * d, {"batch": b, "heads": h, "seq": t, "head_dim": d, "storage": "bfloat16"}
 
 
+def attention_fused(seed=2, causal=False):
+    """Score and value products in one fused kernel (S never stored): config 3
+    shape in the nn layout [B][H][T][D] non-causal, or the lm layout
+    [B][T][H][D] causal (the lm path, algorithmic FLOPs of the visible half)."""
+    from qutai_amd.backends import amd_lm
+
+    b, h, t, d = 8, 16, 2048, 64
+    rng = np.random.default_rng(seed)
+    q, k, v = (upload(rng.standard_normal(b * h * t * d), "bfloat16") for _ in range(3))
+    layout = 1 if causal else 0
+
+    def step():
+        amd_lm.attention(q, k, v, b, t, h, h, d, causal=causal, layout=layout)
+
+    pairs = t * (t + 1) / 2 if causal else t * t
+    return step, 2 * 2.0 * b * h * pairs * d, {"batch": b, "heads": h, "seq": t, "head_dim": d,
+                                                "storage": "bfloat16", "causal": causal,
+                                                "layout": "B,T,H,D" if causal else "B,H,T,D"}
+
+
 def dense_linear(seed=3):
     """SwiGLU projections of a 4096-token batch: Y = X W^T, dX = dY W, dW = dY^T X (x3)."""
     from qutai_amd.backends import amd
@@ -160,6 +180,8 @@ WORKLOADS = {
     "gemm_bf16_ragged": (lambda: gemm_ragged("bfloat16"), "bf16"),
     "gemm_fp32_ragged": (lambda: gemm_ragged("float32"), "fp32"),
     "attention_bmm": (attention_bmm, "bf16"),
+    "attention_fused": (attention_fused, "bf16"),
+    "attention_fused_causal": (lambda: attention_fused(causal=True), "bf16"),
     "dense_linear_fwd_bwd": (dense_linear, "bf16"),
     "moe_grouped": (moe_experts, "bf16"),
 }

@@ -174,6 +174,25 @@ int qutai_amd_combine(const void* expert_out, const float* weights, const int64_
                       const int64_t* locations, const int64_t* offsets, void* y, int64_t rows, int64_t width,
                       int64_t top_k, int dtype, void* stream);
 
+/* Fused attention forward, head dimension 64, bf16 storage, fp32 math:
+ *   out = softmax(scale * Q K^T [+ causal mask]) V  per (batch, head),
+ * without materialising the time x time scores.  layout 0: q/k/v/out are
+ * [batch][heads][time][64] (the nn layout); layout 1: [batch][time][heads][64]
+ * (the lm layout, head-interleaved).  kv_heads divides heads (grouped-query
+ * attention: head h reads kv head h / (heads / kv_heads)).  lse (optional,
+ * fp32) receives the natural-log sum of exponentials, laid out like q without
+ * the last axis: [batch][heads][time] (layout 0), [batch][time][heads]
+ * (layout 1, the reference's lse layout).  The normaliser sums fp32
+ * probabilities; the value product takes them rounded to bf16, as in the
+ * reference kernel.  Replaces the score/value products of
+ * `lm_attention_bf16_d64` (src/qutai/backends/cuda/lm.cu:91-157, driven by
+ * `cuda_lm.attention`, src/qutai/backends/cuda_lm.py:229-252) and the
+ * S = Q K^T / softmax / P V sequence of nn attention
+ * (src/qutai/nn/layers.py:334-354). */
+int qutai_amd_attention_fwd(const void* q, const void* k, const void* v, void* out, float* lse, int64_t batch,
+                            int64_t heads, int64_t kv_heads, int64_t time, int64_t dim, int layout, double scale,
+                            int causal, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

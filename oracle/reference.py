@@ -11,11 +11,14 @@ Contents
     (cpu_lm.py:11-42), ``softmax`` (cpu.py:250-260 with ``_axis_indices``
     cpu.py:231-237), ``silu`` (cpu_lm.py:107-111), ``routing``
     (cpu_lm.py:204-242), ``route_gather`` (cpu_lm.py:279-283), ``combine``
-    (cpu_lm.py:294-303), ``bf16`` (the RNE encoder of cuda.py:98-101 /
+    (cpu_lm.py:294-303), ``attention`` / ``attention_backward``
+    (cpu_lm.py:141-201), ``bf16`` (the RNE encoder of cuda.py:98-101 /
     tests/test_bfloat16_storage.py:10-16);
   * ``gemm_f64``: the same float64 sequential-k GEMM compiled from
     ``oracle/gemm_f64.c`` (bit-identical to ``gemm``; used at sizes the
     Python loop cannot finish);
+  * ``attention_np`` / ``attention_backward_np``: numpy float64 forms of the
+    attention loops for one (batch, head) pair, for the full-size checks;
   * numpy helpers for bf16 rounding of whole arrays.
 
 How each function is pinned (tests/test_oracle.py): reference-test golden
@@ -29,7 +32,7 @@ import ctypes
 import os
 import struct
 import subprocess
-from math import exp, fsum, prod
+from math import exp, fsum, log, prod
 from pathlib import Path
 
 import numpy as np
@@ -180,6 +183,83 @@ def combine(outputs, weights, route, width) -> list[float]:
             for j in range(width):
                 result[row * width + j] += factor * values[i * width + j]
     return result
+
+
+def attention(q, k, v, batch, time, heads, kv_heads, dim, *, causal=True, scale=None):
+    """cpu_lm.attention (src/qutai/backends/cpu_lm.py:141-173): for every
+    (b, t, h) in the lm layout ``((b*time + t)*heads + h)*dim``, scores over
+    keys s <= t (all keys when ``causal`` is False, the nn path of
+    nn/layers.py:334-354) scaled by 1/sqrt(dim) (or ``scale``), max-subtracted
+    exponentials, output = sum p v / sum p, lse = peak + log(sum p) at
+    ``(b*time + t)*heads + h``.  K/V head = h // (heads // kv_heads)."""
+    scale = 1 / dim ** 0.5 if scale is None else scale
+    out = [0.0] * (batch * time * heads * dim)
+    lse = [0.0] * (batch * time * heads)
+    for b in range(batch):
+        for t in range(time):
+            for h in range(heads):
+                qi = ((b * time + t) * heads + h) * dim
+                kh = h // (heads // kv_heads)
+                keys = range(t + 1) if causal else range(time)
+                rows = [((b * time + s) * kv_heads + kh) * dim for s in keys]
+                scores = [sum(q[qi + j] * k[r + j] for j in range(dim)) * scale for r in rows]
+                peak = max(scores)
+                weights = [exp(x - peak) for x in scores]
+                total = sum(weights)
+                lse[(b * time + t) * heads + h] = peak + log(total)
+                for j in range(dim):
+                    out[qi + j] = sum(p * v[r + j] for p, r in zip(weights, rows)) / total
+    return out, lse
+
+
+def attention_backward(gradient, q, k, v, out, lse, batch, time, heads, kv_heads, dim):
+    """cpu_lm.attention_backward (src/qutai/backends/cpu_lm.py:176-201):
+    p = exp(q.k * scale - lse), delta = g.out, ds = p (g.v - delta) scale;
+    dq += ds k, dk += ds q, dv += p g over keys s <= t."""
+    scale = 1 / dim ** 0.5
+    dq, dk, dv = [0.0] * len(q), [0.0] * len(k), [0.0] * len(v)
+    for b in range(batch):
+        for t in range(time):
+            for h in range(heads):
+                qi = ((b * time + t) * heads + h) * dim
+                kh = h // (heads // kv_heads)
+                delta = sum(gradient[qi + j] * out[qi + j] for j in range(dim))
+                for s in range(t + 1):
+                    ki = ((b * time + s) * kv_heads + kh) * dim
+                    p = exp(sum(q[qi + j] * k[ki + j] for j in range(dim)) * scale - lse[(b * time + t) * heads + h])
+                    dp = sum(gradient[qi + j] * v[ki + j] for j in range(dim))
+                    ds = p * (dp - delta) * scale
+                    for j in range(dim):
+                        dq[qi + j] += ds * k[ki + j]
+                        dk[ki + j] += ds * q[qi + j]
+                        dv[ki + j] += p * gradient[qi + j]
+    return dq, dk, dv
+
+
+def attention_np(q, k, v, *, causal=True, scale=None):
+    """numpy float64 form of ``attention`` for one (batch, head) pair at
+    sizes the loop cannot finish: q [T, D], k/v [T, D] -> (out [T, D], lse [T])."""
+    q, k, v = (np.asarray(a, dtype=np.float64) for a in (q, k, v))
+    scale = 1 / q.shape[1] ** 0.5 if scale is None else scale
+    s = (q @ k.T) * scale
+    if causal:
+        s = np.where(np.tril(np.ones(s.shape, dtype=bool)), s, -np.inf)
+    peak = s.max(axis=1, keepdims=True)
+    w = np.exp(s - peak)
+    total = w.sum(axis=1, keepdims=True)
+    return (w @ v) / total, (peak + np.log(total))[:, 0]
+
+
+def attention_backward_np(g, q, k, v, out, lse, *, scale=None):
+    """numpy float64 form of ``attention_backward`` for one (batch, head) pair
+    (causal): returns dq, dk, dv of that pair."""
+    g, q, k, v, out = (np.asarray(a, dtype=np.float64) for a in (g, q, k, v, out))
+    scale = 1 / q.shape[1] ** 0.5 if scale is None else scale
+    p = np.exp((q @ k.T) * scale - np.asarray(lse, dtype=np.float64)[:, None])
+    p = np.where(np.tril(np.ones(p.shape, dtype=bool)), p, 0.0)
+    delta = (g * out).sum(axis=1, keepdims=True)
+    ds = p * (g @ v.T - delta) * scale
+    return ds @ k, ds.T @ q, p.T @ g
 
 
 # ---- compiled float64 GEMM -----------------------------------------------------

@@ -185,3 +185,23 @@ def moe_experts_forward(x, route, w_gate, w_up, w_down, width, hidden):
     act = silu_mul(gate, up)
     down = grouped_gemm(act, w_down, route, hidden, width, out_dtype=x.dtype)
     return combine_all(down, route, width)
+
+
+def attention(q, k, v, batch, time, heads, kv_heads, dim, *, causal=True, layout=1, scale=None):
+    """Fused attention forward (cuda_lm.attention, src/qutai/backends/cuda_lm.py:229-252):
+    (out, lse) for bf16 q/k/v with head dimension 64; layout 1 is the lm
+    layout [batch][time][heads][dim], layout 0 the nn layout
+    [batch][heads][time][dim].  The score matrix is never stored."""
+    if q.dtype != "bfloat16" or k.dtype != "bfloat16" or v.dtype != "bfloat16":
+        raise ValueError("fused attention takes bfloat16 q, k, v")
+    if dim != 64 or heads % kv_heads:
+        raise ValueError("fused attention needs head dimension 64 and heads divisible by kv_heads")
+    if q.size != batch * time * heads * dim or k.size != batch * time * kv_heads * dim or v.size != k.size:
+        raise ValueError("q/k/v sizes do not match (batch, time, heads, dim)")
+    out = AMDStorage(q.size, "bfloat16")
+    lse = AMDStorage(batch * heads * time, "float32")
+    scale = dim ** -0.5 if scale is None else scale
+    if q.size:
+        out.runtime.call("qutai_amd_attention_fwd", q.ptr, k.ptr, v.ptr, out.ptr, lse.ptr, batch, heads, kv_heads,
+                         time, dim, layout, float(scale), int(bool(causal)), mfma=True)
+    return out, lse

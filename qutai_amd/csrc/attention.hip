@@ -1,0 +1,378 @@
+// Fused attention forward for D = 64, bf16 storage, fp32 accumulation
+// (C ABI `qutai_amd_attention_fwd`).  O = softmax(scale * Q K^T) V without
+// materialising the T x T scores: the reference's score and value products
+// (src/qutai/nn/layers.py:334-354 through two batched GEMMs and a softmax, and
+// the lm kernel lm_attention_bf16_d64, src/qutai/backends/cuda/lm.cu:91-157)
+// in one pass over K and V.
+//
+// Layout of the work (gfx950, 64-wide wavefronts):
+//  * a workgroup of 4 waves owns 256 consecutive queries of one (batch,
+//    head); each wave owns 64 queries as two blocks of 32 and keeps their Q
+//    fragments in registers for the whole kernel;
+//  * K and V advance in blocks of 64 keys, copied HBM -> LDS with
+//    buffer_load ... lds into a two-stage ring (8 KiB + 8 KiB per stage);
+//  * scores are computed transposed, S^T = K Q^T, with
+//    v_mfma_f32_32x32x16_bf16: in the MFMA result layout lane l then holds
+//    query l % 32 of its block and 16 keys of each 32-key block, so the
+//    running max / sum of a query live in one lane (plus its partner lane
+//    l ^ 32, exchanged once per key block);
+//  * the probabilities, rounded to bf16, are already in the B-operand layout
+//    of the value product O^T += V^T P^T (the MFMA's k index runs over the keys
+//    in the order the score layout holds them; V is read with the gfx950
+//    transpose read ds_read_b64_tr_b16 in the same key order), so P never
+//    leaves registers;
+//  * O^T's result layout gives every lane one query, so the rescaling by
+//    exp(m_old - m_new) and the final 1/l are per-lane scalars.
+#include "common.h"
+#include "qutai_amd.h"
+
+using namespace qa;
+
+namespace {
+
+constexpr int D = 64;          // head dimension
+constexpr int KB = 64;         // keys per block
+constexpr int WAVES = 4;
+constexpr int QW = 64;         // queries per wave (two 32-query blocks)
+constexpr int QB = QW / 32;
+constexpr int QPB = WAVES * QW;  // queries per workgroup
+constexpr int TILE = KB * D;     // elements of one K (or V) stage
+constexpr uint32_t OOB = 0x80000000u;
+
+struct AttnArgs {
+  const bf16_t* q;
+  const bf16_t* k;
+  const bf16_t* v;
+  bf16_t* o;
+  float* lse;  // optional natural-log sum-exp per (batch, head, token)
+  int64_t batch, heads, kv_heads, time;
+  // element strides of (batch, head, token) for q/o, for k/v and for lse
+  int64_t qb, qh, qt, kb, kh, kt, lb, lh, lt;
+  float scale_log2;  // scale * log2(e)
+  float scale;
+  int causal;
+};
+
+// K rows: 128 bytes = 8 chunks, swizzled like the GEMM's K-major tiles.
+__device__ __forceinline__ int swz_row8(int r) { return (r ^ (r >> 3)) & 7; }
+// V rows read by the transpose read in groups of 4 rows x 64 bytes.
+__device__ __forceinline__ int swz_v(int r) { return ((r >> 1) & 1) * 4; }
+
+typedef __attribute__((address_space(3))) void* lds_void;
+typedef i16x4 __attribute__((address_space(3))) * lds_i16x4;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t bytes) {
+  uint32_t n = bytes > 0x7ffffff0 ? 0x7ffffff0u : (uint32_t)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, n, 0x00020000);
+}
+
+// Both halves of the wavefront (lanes l and l ^ 32) hold the same query:
+// the gfx950 half swap exchanges them without LDS.
+__device__ __forceinline__ float pair_max(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// Two floats -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
+  f32x2 v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
+// One 64-key block for the wave's QB query blocks.  MASK: some key of the
+// block is past T or (causal) after a query; lim[qb] is then the number of
+// leading keys of the block the lane's query may see, minus 4 * half.
+template <bool MASK>
+__device__ __forceinline__ void attend_block(const bf16_t* sk, const bf16_t* sv, const bf16x8 (&qf)[QB][4],
+                                             f32x16 (&o)[QB][2], float (&m)[QB], float (&l)[QB],
+                                             const int (&lim)[QB], float c, int lane) {
+  const int half = lane >> 5, col = lane & 31;
+  // K fragments (A operand): key row 32 mb + col, d = 16 s + 8 half + [0, 8)
+  bf16x8 kf[2][4];
+#pragma unroll
+  for (int mb = 0; mb < 2; mb++)
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+      int r = 32 * mb + col, ch = 2 * s + half;
+      kf[mb][s] = *reinterpret_cast<const bf16x8*>(sk + r * D + ((ch ^ swz_row8(r)) * 8));
+    }
+  // S^T blocks for every query block first, so the value products of one
+  // query block overlap the exponentials of the next.
+  f32x16 sc[QB][2];
+#pragma unroll
+  for (int qb = 0; qb < QB; qb++)
+#pragma unroll
+    for (int mb = 0; mb < 2; mb++) {
+      f32x16 acc = {};
+#pragma unroll
+      for (int st = 0; st < 4; st++) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[mb][st], qf[qb][st], acc, 0, 0, 0);
+      sc[qb][mb] = acc;
+    }
+  // V^T fragments (A operand of O^T): lane = d column 32 db + col; keys in
+  // the score layout order: for k-step (mb, st) the 8 keys
+  // 32 mb + 16 st + 4 half + {0..3} and + 8 + {0..3}.
+  bf16x8 vf[2][2][2];  // [db][mb][st]
+  const int g = lane >> 4, i = lane & 15;
+#pragma unroll
+  for (int db = 0; db < 2; db++)
+#pragma unroll
+    for (int mb = 0; mb < 2; mb++)
+#pragma unroll
+      for (int st = 0; st < 2; st++) {
+        int cb = 32 * db + (g & 1) * 16 + 4 * (i & 3);
+        int kb0 = 32 * mb + 16 * st + 4 * (g >> 1) + (i >> 2);
+        int kb1 = kb0 + 8;
+        const bf16_t* p0 = sv + kb0 * D + (((cb >> 3) ^ swz_v(kb0)) * 8) + (cb & 7);
+        const bf16_t* p1 = sv + kb1 * D + (((cb >> 3) ^ swz_v(kb1)) * 8) + (cb & 7);
+        i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4)p0);
+        i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4)p1);
+        i16x8 w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        vf[db][mb][st] = __builtin_bit_cast(bf16x8, w);
+      }
+
+  // ---- running max (scaled log2 domain; scale > 0, so max(s) c = max(s c)).
+  // The reference point m only moves when the block's max exceeds it by more
+  // than 8 (a factor 256), so the rescaling of l and O is skipped for most
+  // blocks; the probabilities exp2(s c - m) then stay below 256 and the
+  // result is the same softmax (the normaliser uses the same m).
+  bool grow_any = false;
+  float m_new[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; qb++) {
+    // key of element e in block mb: 32 mb + 8 (e / 4) + 4 half + e % 4
+    if (MASK) {
+#pragma unroll
+      for (int mb = 0; mb < 2; mb++)
+#pragma unroll
+        for (int e = 0; e < 16; e++)
+          if (32 * mb + 8 * (e >> 2) + (e & 3) >= lim[qb]) sc[qb][mb][e] = -INFINITY;
+    }
+    float peak = -INFINITY;
+#pragma unroll
+    for (int mb = 0; mb < 2; mb++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) peak = fmaxf(peak, sc[qb][mb][e]);
+    const float cand = pair_max(peak) * c;
+    const bool grow = cand > m[qb] + 8.f;  // -inf + 8 = -inf: the first visible key always moves m
+    m_new[qb] = grow ? cand : m[qb];
+    grow_any |= grow;
+  }
+  if (__builtin_amdgcn_ballot_w64(grow_any)) {
+#pragma unroll
+    for (int qb = 0; qb < QB; qb++) {
+      // alpha = 1 for lanes whose m stays; a query that has seen no valid key
+      // keeps m = -inf and l = 0, O = 0
+      const float alpha = m_new[qb] == m[qb] ? 1.f : __builtin_amdgcn_exp2f(m[qb] - m_new[qb]);
+      m[qb] = m_new[qb];
+      l[qb] *= alpha;
+#pragma unroll
+      for (int db = 0; db < 2; db++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) o[qb][db][e] *= alpha;
+    }
+  }
+#pragma unroll
+  for (int qb = 0; qb < QB; qb++) {
+    // exp2(-inf - 0) = 0 for a query with no visible key yet
+    const float ref = m[qb] == -INFINITY ? 0.f : m[qb];
+    float sum = 0.f;
+    bf16x8 pf[2][2];
+#pragma unroll
+    for (int mb = 0; mb < 2; mb++)
+#pragma unroll
+      for (int st = 0; st < 2; st++) {
+        // the normaliser sums the fp32 probabilities; the value product takes
+        // them rounded to bf16 (lm.cu:131-134)
+        float pv[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          pv[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[qb][mb][8 * st + e], c, -ref));
+          sum += pv[e];
+        }
+        u32x4 w = {cvt_pk_bf16(pv[0], pv[1]), cvt_pk_bf16(pv[2], pv[3]), cvt_pk_bf16(pv[4], pv[5]),
+                   cvt_pk_bf16(pv[6], pv[7])};
+        pf[mb][st] = __builtin_bit_cast(bf16x8, w);
+      }
+    l[qb] += sum;
+#pragma unroll
+    for (int db = 0; db < 2; db++)
+#pragma unroll
+      for (int mb = 0; mb < 2; mb++)
+#pragma unroll
+        for (int st = 0; st < 2; st++)
+          o[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[db][mb][st], pf[mb][st], o[qb][db], 0, 0, 0);
+  }
+}
+
+__global__ void __launch_bounds__(WAVES * 64) attention_fwd_d64(AttnArgs p) {
+  __shared__ __attribute__((aligned(16))) bf16_t lds[2][2][TILE];  // [stage][K,V][64 x 64]
+  const int tid = threadIdx.x, lane = tid & 63, wave = uniform32(tid >> 6);
+  const int T = (int)p.time;
+  const int blocks_q = (T + QPB - 1) / QPB;
+  // every query block of one (batch, head) on one XCD (they share K and V in
+  // its L2); within a head the longest (causal) query blocks start first
+  const int pid = uniform32(xcd_remap(blockIdx.x, gridDim.x));
+  const int bh = uniform32(pid / blocks_q);
+  const int qblk = uniform32(p.causal ? blocks_q - 1 - pid % blocks_q : pid % blocks_q);
+  const int wg_q0 = qblk * QPB;
+  const int q0 = uniform32(wg_q0 + wave * QW);
+  const int b = bh / (int)p.heads, h = bh % (int)p.heads;
+  const int kvh = h / (int)(p.heads / p.kv_heads);
+  const bf16_t* Q = uniform_ptr(p.q + b * p.qb + h * p.qh);
+  const bf16_t* K = uniform_ptr(p.k + b * p.kb + kvh * p.kh);
+  const bf16_t* V = uniform_ptr(p.v + b * p.kb + kvh * p.kh);
+  const int half = lane >> 5, col = lane & 31;
+
+  // ---- Q fragments (B operand of S^T = K Q^T): lane holds query col of its
+  // block, d = 16 s + 8 half + [0, 8).
+  bf16x8 qf[QB][4];
+  {
+    auto rq = rsrc(Q, ((int64_t)T - 1) * p.qt * 2 + D * 2);
+#pragma unroll
+    for (int qb = 0; qb < QB; qb++) {
+      const int t = q0 + qb * 32 + col;
+#pragma unroll
+      for (int s = 0; s < 4; s++) {
+        uint32_t off = (uint32_t)((t * p.qt + 16 * s + 8 * half) * 2) + ((uint32_t)(t >= T) << 31);
+        qf[qb][s] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, 0));
+      }
+    }
+  }
+
+  // ---- K/V stage copies: 512 chunks of 16 bytes each; wave w, instruction
+  // j fills physical chunks (j * 4 + w) * 64 + lane of K, then of V.  Rows
+  // past T read as zeros (offset >= 2^31 is out of the descriptor's range).
+  uint32_t ko[2], vo[2];
+  int kr[2];
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    int qidx = (j * WAVES + wave) * 64 + lane;
+    int r = qidx >> 3, pc = qidx & 7;
+    kr[j] = r;
+    ko[j] = (uint32_t)((r * p.kt + ((pc ^ swz_row8(r)) * 8)) * 2);
+    vo[j] = (uint32_t)((r * p.kt + ((pc ^ swz_v(r)) * 8)) * 2);
+  }
+  const int nkb = p.causal ? min((wg_q0 + QPB + KB - 1) / KB, (T + KB - 1) / KB) : (T + KB - 1) / KB;
+  auto issue = [&](int stage, int kv0) {
+    auto rk = rsrc(K + (int64_t)kv0 * p.kt, (int64_t)KB * p.kt * 2);
+    auto rv = rsrc(V + (int64_t)kv0 * p.kt, (int64_t)KB * p.kt * 2);
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      uint32_t oob = (uint32_t)(kv0 + kr[j] >= T) << 31;
+      char* dk = reinterpret_cast<char*>(&lds[stage][0][0]) + (j * WAVES + wave) * 1024;
+      char* dv = reinterpret_cast<char*>(&lds[stage][1][0]) + (j * WAVES + wave) * 1024;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void)dk, 16, ko[j] + oob, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void)dv, 16, vo[j] + oob, 0, 0, 0);
+    }
+  };
+
+  f32x16 o[QB][2];  // O^T blocks: d block db (rows d = 32 db + ...), columns = queries
+  float m[QB], l[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; qb++) {
+    m[qb] = -INFINITY;
+    l[qb] = 0.f;
+#pragma unroll
+    for (int db = 0; db < 2; db++) o[qb][db] = f32x16{};
+  }
+
+  // blocks that need no mask: all keys < T and (causal) every key <= the
+  // wave's first query
+  const int last_key_full = p.causal ? min(T, q0 + 1) : T;
+  if (nkb > 0) issue(0, 0);
+  for (int kbk = 0; kbk < nkb; kbk++) {
+    const int cur = kbk & 1;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    asm volatile("s_barrier" ::: "memory");  // stage cur landed; stage cur^1 free
+    if (kbk + 1 < nkb) issue(cur ^ 1, (kbk + 1) * KB);
+    const int kv0 = kbk * KB;
+    const bf16_t* sk = &lds[cur][0][0];
+    const bf16_t* sv = &lds[cur][1][0];
+    if (kv0 + KB <= last_key_full) {
+      const int lim[QB] = {};
+      attend_block<false>(sk, sv, qf, o, m, l, lim, p.scale_log2, lane);
+    } else if (kv0 < q0 + QW || !p.causal) {
+      int lim[QB];
+#pragma unroll
+      for (int qb = 0; qb < QB; qb++) {
+        const int tq = q0 + qb * 32 + col;
+        lim[qb] = min(T - kv0, p.causal ? tq - kv0 + 1 : KB) - 4 * half;
+      }
+      attend_block<true>(sk, sv, qf, o, m, l, lim, p.scale_log2, lane);
+    }
+    // else (causal): every key of the block is after every query of this wave
+  }
+
+  // ---- normalise and store: lane holds query col, d = 32 db + 8 (e/4) + 4 half + e%4
+#pragma unroll
+  for (int qb = 0; qb < QB; qb++) {
+    const int t = q0 + qb * 32 + col;
+    const float total = pair_sum(l[qb]);
+    const float inv = total > 0.f ? 1.f / total : 0.f;
+    if (t < T) {
+      bf16_t* out = p.o + b * p.qb + h * p.qh + t * p.qt;
+#pragma unroll
+      for (int db = 0; db < 2; db++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          uint2 w;
+          w.x = cvt_pk_bf16(o[qb][db][4 * g] * inv, o[qb][db][4 * g + 1] * inv);
+          w.y = cvt_pk_bf16(o[qb][db][4 * g + 2] * inv, o[qb][db][4 * g + 3] * inv);
+          *reinterpret_cast<uint2*>(out + 32 * db + 8 * g + 4 * half) = w;
+        }
+      if (p.lse && half == 0) p.lse[b * p.lb + h * p.lh + t * p.lt] = (m[qb] + __log2f(total)) * 0.6931471805599453f;
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int qutai_amd_attention_fwd(const void* q, const void* k, const void* v, void* out, float* lse, int64_t batch,
+                            int64_t heads, int64_t kv_heads, int64_t time, int64_t dim, int layout, double scale,
+                            int causal, void* stream) {
+  if (batch < 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads || time < 0) return QA_EINVAL;
+  if (!(scale > 0.0) || scale > 1e30) return QA_EINVAL;  // the running max assumes a positive scale
+  if (time > (1 << 30) / (heads > kv_heads ? heads : kv_heads) / D) return QA_EINVAL;  // 32-bit element offsets
+  if (dim != D || (layout != 0 && layout != 1)) return QA_EINVAL;
+  if (!q || !k || !v || !out) return QA_EINVAL;
+  for (const void* ptr : {q, k, v, (const void*)out})
+    if ((uintptr_t)ptr % 16) return QA_EINVAL;
+  if (batch * time == 0) return QA_OK;
+  AttnArgs a = {};
+  a.q = (const bf16_t*)q;
+  a.k = (const bf16_t*)k;
+  a.v = (const bf16_t*)v;
+  a.o = (bf16_t*)out;
+  a.lse = lse;
+  a.batch = batch;
+  a.heads = heads;
+  a.kv_heads = kv_heads;
+  a.time = time;
+  if (layout == 0) {  // [batch][heads][time][dim]
+    a.qb = heads * time * D, a.qh = time * D, a.qt = D;
+    a.kb = kv_heads * time * D, a.kh = time * D, a.kt = D;
+    a.lb = heads * time, a.lh = time, a.lt = 1;
+  } else {            // [batch][time][heads][dim] (the lm layout)
+    a.qb = time * heads * D, a.qh = D, a.qt = heads * D;
+    a.kb = time * kv_heads * D, a.kh = D, a.kt = kv_heads * D;
+    a.lb = time * heads, a.lh = 1, a.lt = heads;
+  }
+  a.scale = (float)scale;
+  a.scale_log2 = (float)(scale * 1.4426950408889634);
+  a.causal = causal ? 1 : 0;
+  int64_t blocks = batch * heads * ((time + QPB - 1) / QPB);
+  if (blocks > 0x7fffffff) return QA_EINVAL;
+  hipLaunchKernelGGL(attention_fwd_d64, dim3((unsigned)blocks), dim3(WAVES * 64), 0, (hipStream_t)stream, a);
+  return (int)hipGetLastError();
+}
+
+}  // extern "C"

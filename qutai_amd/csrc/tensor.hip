@@ -306,6 +306,21 @@ __device__ __forceinline__ float silu_f(float v) {
   float s = v >= 0.f ? 1.f / (1.f + expf(-v)) : expf(v) / (1.f + expf(v));
   return v * s;
 }
+// bf16, 8 elements (16 bytes) per thread and step.
+__global__ void silu_mul_bf16x8(const u32x4* g, const u32x4* u, u32x4* out, int64_t n8) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += (int64_t)gridDim.x * blockDim.x) {
+    u32x4 a = g[i], b = u[i], r;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      float lo = bf16_to_f32(f32_to_bf16(silu_f(__uint_as_float(a[q] << 16)))) * __uint_as_float(b[q] << 16);
+      float hi = bf16_to_f32(f32_to_bf16(silu_f(__uint_as_float(a[q] & 0xffff0000u)))) *
+                 __uint_as_float(b[q] & 0xffff0000u);
+      r[q] = pack_bf16x2(lo, hi);
+    }
+    out[i] = r;
+  }
+}
+
 __global__ void silu_mul_kernel(const void* g, const void* u, void* out, int64_t n, int d) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
     if (d == BF16) {
@@ -467,6 +482,12 @@ int qutai_amd_softmax_rows(const void* x, void* out, int64_t rows, int64_t width
 int qutai_amd_silu_mul(const void* gate, const void* up, void* out, int64_t n, int dtype, void* stream) {
   if (n < 0 || !float_dtype(dtype)) return QA_EINVAL;
   if (n == 0) return QA_OK;
+  if (dtype == BF16 && n % 8 == 0 && (uintptr_t)gate % 16 == 0 && (uintptr_t)up % 16 == 0 &&
+      (uintptr_t)out % 16 == 0) {
+    hipLaunchKernelGGL(silu_mul_bf16x8, dim3(grid_for(n / 8)), dim3(THREADS), 0, (hipStream_t)stream,
+                       (const u32x4*)gate, (const u32x4*)up, (u32x4*)out, n / 8);
+    return (int)hipGetLastError();
+  }
   hipLaunchKernelGGL(silu_mul_kernel, dim3(grid_for(n)), dim3(THREADS), 0, (hipStream_t)stream, gate, up, out, n,
                      dtype);
   return (int)hipGetLastError();

@@ -152,5 +152,26 @@ def attention_products(q, k, v, *, scale=None):
     return Tensor(out, shape=(groups, time, dim)), Tensor(probs, shape=(groups, time, time))
 
 
+def attention(q, k, v, heads, kv_heads):
+    """Causal grouped-query attention on (batch, time, heads*64) tensors in the
+    lm layout (src/qutai/lm/layers.py:119-130), forward through the fused
+    kernel; the T x T scores are never stored."""
+    batch, time, features = q.shape
+    out, _ = backend(q).attention(q.storage, k.storage, v.storage, batch, time, heads, kv_heads,
+                                  features // heads, causal=True, layout=1)
+    return Tensor(out, shape=q.shape)
+
+
+def attention_fused(q, k, v, *, scale=None, causal=False):
+    """Score and value products of (groups, T, 64) bf16 tensors in one fused
+    pass: O = softmax(scale * Q K^T) V (scale defaults to 1/sqrt(64))."""
+    if q.shape != k.shape or q.shape != v.shape or q.ndim != 3:
+        raise ValueError("attention_fused takes equal (groups, T, D) q, k, v")
+    groups, time, dim = q.shape
+    out, _ = backend(q).attention(q.storage, k.storage, v.storage, groups, time, 1, 1, dim, causal=causal,
+                                  layout=0, scale=scale)
+    return Tensor(out, shape=q.shape)
+
+
 def parameter_count(layer):
     return sum(prod(p.shape) for p in layer.parameters())

@@ -1,0 +1,167 @@
+"""Fused attention forward on the MI355X (lm attention, cuda_lm.attention
+src/qutai/backends/cuda_lm.py:229-252; nn attention products
+src/qutai/nn/layers.py:334-354) against the float64 oracle
+(cpu_lm.attention, cpu_lm.py:141-173): bf16 inputs, output within the bf16
+tolerance 1e-2 (relative Frobenius per (batch, head)), LSE within 2e-5
+absolute (fp32 statistics), causal masking exact."""
+from random import Random
+
+import numpy as np
+import pytest
+
+from oracle import reference as ora
+from tests.helpers import download, normal, stored, upload
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = 1e-2
+LSE_TOL = 2e-5
+
+
+@pytest.fixture(scope="module")
+def lm():
+    from qutai_amd.backends import amd, amd_lm
+
+    amd.get_runtime()
+    return amd_lm
+
+
+def check_heads(out, lse, q, k, v, dims, *, causal, layout, heads_to_check=None, scale=None):
+    """Compare (out, lse) of every (or the listed) (batch, head) pair with
+    the float64 oracle on the stored bf16 values."""
+    batch, time, heads, kv_heads, dim = dims
+    if layout == 1:
+        qa = q.reshape(batch, time, heads, dim).transpose(0, 2, 1, 3)
+        ka = k.reshape(batch, time, kv_heads, dim).transpose(0, 2, 1, 3)
+        va = v.reshape(batch, time, kv_heads, dim).transpose(0, 2, 1, 3)
+        oa = out.reshape(batch, time, heads, dim).transpose(0, 2, 1, 3)
+        la = lse.reshape(batch, time, heads).transpose(0, 2, 1)
+    else:
+        qa = q.reshape(batch, heads, time, dim)
+        ka, va = (x.reshape(batch, kv_heads, time, dim) for x in (k, v))
+        oa = out.reshape(batch, heads, time, dim)
+        la = lse.reshape(batch, heads, time)
+    pairs = heads_to_check or [(b, h) for b in range(batch) for h in range(heads)]
+    group = heads // kv_heads
+    for b, h in pairs:
+        expected, expected_lse = ora.attention_np(qa[b, h], ka[b, h // group], va[b, h // group], causal=causal,
+                                                  scale=scale)
+        assert ora.rel_frobenius(oa[b, h], expected) <= BF16_TOL, (b, h)
+        assert np.abs(la[b, h] - expected_lse).max() <= LSE_TOL * max(1.0, np.abs(expected_lse).max()), (b, h)
+
+
+def test_partial_tiles_and_causal_mask_like_the_reference(lm):
+    # tests/test_lm_bfloat16.py:106-127: time 17, 33, 65; dims (1, time, 2, 1, 64);
+    # uniform(-0.4, 0.4) from Random(time); the first query ignores later values
+    for time in (17, 33, 65):
+        random = Random(time)
+        dims = (1, time, 2, 1, 64)
+        qv = np.array([random.uniform(-0.4, 0.4) for _ in range(time * 128)], dtype=np.float32)
+        kv = np.array([random.uniform(-0.4, 0.4) for _ in range(time * 64)], dtype=np.float32)
+        vv = np.array([random.uniform(-0.4, 0.4) for _ in range(time * 64)], dtype=np.float32)
+        q, k, v = (upload(x, "bfloat16") for x in (qv, kv, vv))
+        out, lse = lm.attention(q, k, v, *dims)
+        assert (out.dtype, lse.dtype) == ("bfloat16", "float32")
+        # the pure-Python restatement itself at these sizes
+        qs, ks, vs = (stored(x, "bfloat16") for x in (qv, kv, vv))
+        expected, expected_lse = ora.attention(qs.tolist(), ks.tolist(), vs.tolist(), *dims)
+        o = download(out)
+        assert ora.rel_frobenius(o, expected) <= BF16_TOL
+        assert np.abs(o - np.array(expected)).max() <= 4e-3  # the reference test's absolute bound
+        assert np.abs(download(lse) - np.array(expected_lse)).max() <= LSE_TOL
+        changed = np.concatenate([vv[:64], np.full(vv.size - 64, 100.0, dtype=np.float32)])
+        causal, _ = lm.attention(q, k, upload(changed, "bfloat16"), *dims)
+        assert download(causal)[:128].tobytes() == o[:128].tobytes()
+
+
+@pytest.mark.parametrize("time", [1, 2, 63, 64, 65, 255, 256, 257, 700])
+@pytest.mark.parametrize("causal", [True, False])
+def test_ragged_lengths_gqa_and_both_layouts(lm, time, causal):
+    dims = (2, time, 4, 2, 64)
+    batch, _, heads, kv_heads, dim = dims
+    qv = normal(10 + time, batch * time * heads * dim)
+    kv = normal(11 + time, batch * time * kv_heads * dim)
+    vv = normal(12 + time, batch * time * kv_heads * dim)
+    q, k, v = (upload(x, "bfloat16") for x in (qv, kv, vv))
+    qs, ks, vs = (stored(x, "bfloat16") for x in (qv, kv, vv))
+    for layout in (1, 0):
+        out, lse = lm.attention(q, k, v, *dims, causal=causal, layout=layout)
+        o, l = download(out), download(lse)
+        assert np.isfinite(o).all() and np.isfinite(l).all()
+        check_heads(o, l, qs, ks, vs, dims, causal=causal, layout=layout)
+
+
+def test_config3_nn_layout_non_causal_sampled_heads(lm):
+    # Q, K, V (8, 16, 2048, 64) bf16 N(0, 1), seed 2, non-causal, scale 1/8
+    dims = (8, 2048, 16, 16, 64)
+    qv, kv, vv = (normal(2 + i, 8 * 16 * 2048 * 64) for i in range(3))
+    q, k, v = (upload(x, "bfloat16") for x in (qv, kv, vv))
+    out, lse = lm.attention(q, k, v, *dims, causal=False, layout=0)
+    o, l = download(out), download(lse)
+    assert np.isfinite(o).all()
+    qs, ks, vs = (stored(x, "bfloat16") for x in (qv, kv, vv))
+    check_heads(o, l, qs, ks, vs, dims, causal=False, layout=0, heads_to_check=[(0, 0), (3, 9), (7, 15)])
+
+
+def test_lm_layout_causal_long_sequence(lm):
+    dims = (1, 4096, 8, 2, 64)
+    batch, time, heads, kv_heads, dim = dims
+    qv = normal(21, time * heads * dim)
+    kv, vv = normal(22, time * kv_heads * dim), normal(23, time * kv_heads * dim)
+    q, k, v = (upload(x, "bfloat16") for x in (qv, kv, vv))
+    out, lse = lm.attention(q, k, v, *dims)
+    qs, ks, vs = (stored(x, "bfloat16") for x in (qv, kv, vv))
+    check_heads(download(out), download(lse), qs, ks, vs, dims, causal=True, layout=1,
+                heads_to_check=[(0, 0), (0, 5)])
+
+
+def test_scale_argument_and_repeatability(lm):
+    dims = (1, 300, 2, 1, 64)
+    qv, kv, vv = normal(31, 300 * 128), normal(32, 300 * 64), normal(33, 300 * 64)
+    q, k, v = (upload(x, "bfloat16") for x in (qv, kv, vv))
+    out, lse = lm.attention(q, k, v, *dims, causal=False, scale=0.3)
+    qs, ks, vs = (stored(x, "bfloat16") for x in (qv, kv, vv))
+    check_heads(download(out), download(lse), qs, ks, vs, dims, causal=False, layout=1, scale=0.3)
+    first = download(lm.attention(q, k, v, *dims)[0]).tobytes()
+    for _ in range(3):
+        assert download(lm.attention(q, k, v, *dims)[0]).tobytes() == first
+
+
+def test_attention_rejects_unsupported_arguments(lm):
+    q = upload(np.zeros(64 * 32, dtype=np.float32), "bfloat16")
+    with pytest.raises(ValueError):
+        lm.attention(q, q, q, 1, 32, 1, 1, 64, layout=2)
+    with pytest.raises(ValueError):
+        lm.attention(q, q, q, 1, 16, 4, 3, 32)  # kv_heads does not divide heads
+    with pytest.raises(ValueError):
+        lm.attention(q, q, q, 1, 33, 1, 1, 64)  # sizes do not match
+
+
+def test_lm_layer_attention_and_nn_fused_products(lm):
+    from qutai_amd import Tensor
+    from qutai_amd.lm.layers import attention, attention_fused
+
+    batch, time, heads, kv_heads, dim = 2, 130, 4, 2, 64
+    qv = normal(41, batch * time * heads * dim)
+    kv, vv = normal(42, batch * time * kv_heads * dim), normal(43, batch * time * kv_heads * dim)
+    q = Tensor(upload(qv, "bfloat16"), shape=(batch, time, heads * dim))
+    k = Tensor(upload(kv, "bfloat16"), shape=(batch, time, kv_heads * dim))
+    v = Tensor(upload(vv, "bfloat16"), shape=(batch, time, kv_heads * dim))
+    out = attention(q, k, v, heads, kv_heads)
+    assert out.shape == q.shape
+    qs, ks, vs = (stored(x, "bfloat16") for x in (qv, kv, vv))
+    o = download(out.storage)
+    for b in range(batch):
+        for h in range(heads):
+            expected, _ = ora.attention_np(qs.reshape(batch, time, heads, dim)[b, :, h],
+                                           ks.reshape(batch, time, kv_heads, dim)[b, :, h // 2],
+                                           vs.reshape(batch, time, kv_heads, dim)[b, :, h // 2])
+            assert ora.rel_frobenius(o.reshape(batch, time, heads, dim)[b, :, h], expected) <= BF16_TOL
+    groups = 3
+    qg, kg, vg = (Tensor(upload(normal(50 + i, groups * time * dim), "bfloat16"), shape=(groups, time, dim))
+                  for i in range(3))
+    fused = download(attention_fused(qg, kg, vg).storage).reshape(groups, time, dim)
+    for g in range(groups):
+        expected, _ = ora.attention_np(*(stored(normal(50 + i, groups * time * dim), "bfloat16")
+                                         .reshape(groups, time, dim)[g] for i in range(3)), causal=False)
+        assert ora.rel_frobenius(fused[g], expected) <= BF16_TOL

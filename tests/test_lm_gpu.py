@@ -345,3 +345,19 @@ def test_nn_linear_known_answers(amd):
     assert layer.weight.grad.tolist() == [[16.0], [20.0]]
     assert layer.bias.grad.tolist() == [4.0]
     assert np.array(inputs.grad.tolist()).ravel().tolist() == [2.0, 3.0] * 4
+
+
+def test_silu_mul_bf16_vector_and_scalar_paths(amd):
+    # lm.cu silu then multiply, each rounded to bf16 (vector path for n % 8 == 0,
+    # element path otherwise); bit-exact against the float64 silu rounded the same way
+    from qutai_amd.backends import amd_lm
+
+    for n in (8 * 1000, 8 * 1000 + 3):
+        g, u = normal(60, n, 4.0), normal(61, n)
+        out = download(amd_lm.silu_mul(upload(g, "bfloat16"), upload(u, "bfloat16")))
+        gs, us = stored(g, "bfloat16"), stored(u, "bfloat16")
+        s = ora.bf16_round_array(np.array(ora.silu(gs.tolist()), dtype=np.float32)).astype(np.float64)
+        expected = ora.bf16_round_array((s * us).astype(np.float32))
+        # silu in fp32 on the device vs float64 here: allow one bf16 ulp on the product
+        assert np.abs(out - expected).max() <= 2 ** -7 * np.abs(expected).max()
+        assert ora.rel_frobenius(out, expected) <= 1e-3

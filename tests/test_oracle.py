@@ -235,3 +235,101 @@ def test_gather_and_combine_round_trip():
     # a single unit weight reproduces the expert rows exactly
     one = dict(route, top_k=1, ids=[[0, 2]], slots=[[0, 0]], rows=3)
     assert ora.combine([(0, [1.0, 2.0, 3.0, 4.0])], [1.0, 0.0, 1.0], one, 2) == [1.0, 2.0, 0.0, 0.0, 3.0, 4.0]
+
+
+# ---- attention ----------------------------------------------------------------------
+
+def test_attention_hand_computed_golden():
+    # tests/test_attention.py:10-22: identity projections of [[1,0],[0,1]],
+    # non-causal, D = 2 -> rows [p, 1-p], [1-p, p] with p = e^(1/sqrt2)/(e^(1/sqrt2)+1)
+    p = math.exp(1 / math.sqrt(2)) / (math.exp(1 / math.sqrt(2)) + 1)
+    x = [1.0, 0.0, 0.0, 1.0]
+    out, lse = ora.attention(x, x, x, 1, 2, 1, 1, 2, causal=False)
+    assert out == pytest.approx([p, 1 - p, 1 - p, p], rel=1e-15)
+    assert lse[0] == pytest.approx(math.log(math.exp(1 / math.sqrt(2)) + 1), rel=1e-15)
+    # causal: the first query sees only itself
+    out, lse = ora.attention(x, x, x, 1, 2, 1, 1, 2)
+    assert out[:2] == [1.0, 0.0] and lse[0] == pytest.approx(1 / math.sqrt(2), rel=1e-15)
+
+
+def test_attention_closed_forms_and_head_mapping():
+    rng = random.Random(5)
+    batch, time, heads, kv_heads, dim = 2, 5, 4, 2, 3
+    q = [rng.gauss(0, 1) for _ in range(batch * time * heads * dim)]
+    # K = 0: uniform weights over the visible keys -> prefix mean of V; lse = log(t + 1)
+    k0 = [0.0] * (batch * time * kv_heads * dim)
+    v = [rng.gauss(0, 1) for _ in range(batch * time * kv_heads * dim)]
+    out, lse = ora.attention(q, k0, v, batch, time, heads, kv_heads, dim)
+    for b in range(batch):
+        for t in range(time):
+            for h in range(heads):
+                kh = h // 2
+                for j in range(dim):
+                    mean = sum(v[((b * time + s) * kv_heads + kh) * dim + j] for s in range(t + 1)) / (t + 1)
+                    assert out[((b * time + t) * heads + h) * dim + j] == pytest.approx(mean, rel=1e-12, abs=1e-14)
+                assert lse[(b * time + t) * heads + h] == pytest.approx(math.log(t + 1), rel=1e-14)
+    # V constant per kv head: every output row equals its kv head's constant
+    k = [rng.gauss(0, 1) for _ in range(len(k0))]
+    vc = [float(10 * b + kh + 1) for b in range(batch) for _ in range(time) for kh in range(kv_heads)
+          for _ in range(dim)]
+    out, _ = ora.attention(q, k, vc, batch, time, heads, kv_heads, dim)
+    for b in range(batch):
+        for t in range(time):
+            for h in range(heads):
+                row = out[((b * time + t) * heads + h) * dim:((b * time + t) * heads + h + 1) * dim]
+                assert row == pytest.approx([10 * b + h // 2 + 1] * dim, rel=1e-14)
+
+
+def test_attention_numpy_form_agrees_with_the_loop():
+    rng = np.random.default_rng(6)
+    batch, time, heads, kv_heads, dim = 2, 7, 4, 2, 5
+    q = rng.standard_normal((batch, time, heads, dim))
+    k = rng.standard_normal((batch, time, kv_heads, dim))
+    v = rng.standard_normal((batch, time, kv_heads, dim))
+    for causal in (True, False):
+        out, lse = ora.attention(q.ravel().tolist(), k.ravel().tolist(), v.ravel().tolist(), batch, time, heads,
+                                 kv_heads, dim, causal=causal)
+        out = np.array(out).reshape(q.shape)
+        lse = np.array(lse).reshape(batch, time, heads)
+        for b in range(batch):
+            for h in range(heads):
+                o, l = ora.attention_np(q[b, :, h], k[b, :, h // 2], v[b, :, h // 2], causal=causal)
+                assert np.abs(o - out[b, :, h]).max() < 1e-12
+                assert np.abs(l - lse[b, :, h]).max() < 1e-12
+
+
+def test_attention_backward_matches_finite_differences_and_numpy_form():
+    rng = np.random.default_rng(7)
+    batch, time, heads, kv_heads, dim = 1, 4, 2, 1, 3
+    q = rng.standard_normal(batch * time * heads * dim) * 0.5
+    k = rng.standard_normal(batch * time * kv_heads * dim) * 0.5
+    v = rng.standard_normal(batch * time * kv_heads * dim) * 0.5
+    g = rng.standard_normal(q.size)
+    dims = (batch, time, heads, kv_heads, dim)
+    out, lse = ora.attention(q.tolist(), k.tolist(), v.tolist(), *dims)
+    dq, dk, dv = ora.attention_backward(g.tolist(), q.tolist(), k.tolist(), v.tolist(), out, lse, *dims)
+
+    def loss(qq, kk, vv):
+        o, _ = ora.attention(qq.tolist(), kk.tolist(), vv.tolist(), *dims)
+        return float(np.dot(o, g))
+
+    eps = 1e-6
+    for tensor, grad in ((q, dq), (k, dk), (v, dv)):
+        for i in range(tensor.size):
+            up, down = tensor.copy(), tensor.copy()
+            up[i] += eps
+            down[i] -= eps
+            args = [q, k, v]
+            index = [id(q), id(k), id(v)].index(id(tensor))
+            args_up, args_down = list(args), list(args)
+            args_up[index], args_down[index] = up, down
+            numeric = (loss(*args_up) - loss(*args_down)) / (2 * eps)
+            assert grad[i] == pytest.approx(numeric, rel=1e-5, abs=1e-8)
+    # numpy form, GQA: heads 0 and 1 share kv head 0, so dk/dv sum over both
+    qa, ga, oa = (np.array(x).reshape(time, heads, dim) for x in (q, g, out))
+    la = np.array(lse).reshape(time, heads)
+    ka, va = k.reshape(time, dim), v.reshape(time, dim)
+    parts = [ora.attention_backward_np(ga[:, h], qa[:, h], ka, va, oa[:, h], la[:, h]) for h in range(heads)]
+    assert np.abs(np.stack([p[0] for p in parts], 1).ravel() - dq).max() < 1e-12
+    assert np.abs(sum(p[1] for p in parts).ravel() - dk).max() < 1e-12
+    assert np.abs(sum(p[2] for p in parts).ravel() - dv).max() < 1e-12
