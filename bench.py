@@ -126,6 +126,25 @@ def attention_fused(seed=2, causal=False):
                                                 "layout": "B,T,H,D" if causal else "B,H,T,D"}
 
 
+def attention_fused_backward(seed=2):
+    """Fused causal attention backward in the lm layout at the config 3 shape:
+    dq (recomputing P) then dk/dv; algorithmic FLOPs = the five products
+    S, dP, dQ, dK, dV over the visible half."""
+    from qutai_amd.backends import amd_lm
+
+    b, h, t, d = 8, 16, 2048, 64
+    rng = np.random.default_rng(seed)
+    q, k, v, g = (upload(rng.standard_normal(b * h * t * d), "bfloat16") for _ in range(4))
+    out, lse = amd_lm.attention(q, k, v, b, t, h, h, d)
+
+    def step():
+        amd_lm.attention_backward(g, q, k, v, out, lse, b, t, h, h, d)
+
+    return step, 5 * 2.0 * b * h * (t * (t + 1) / 2) * d, {"batch": b, "heads": h, "seq": t, "head_dim": d,
+                                                            "storage": "bfloat16", "causal": True,
+                                                            "layout": "B,T,H,D"}
+
+
 def dense_linear(seed=3):
     """SwiGLU projections of a 4096-token batch: Y = X W^T, dX = dY W, dW = dY^T X (x3)."""
     from qutai_amd.backends import amd
@@ -182,6 +201,7 @@ WORKLOADS = {
     "attention_bmm": (attention_bmm, "bf16"),
     "attention_fused": (attention_fused, "bf16"),
     "attention_fused_causal": (lambda: attention_fused(causal=True), "bf16"),
+    "attention_fused_backward": (attention_fused_backward, "bf16"),
     "dense_linear_fwd_bwd": (dense_linear, "bf16"),
     "moe_grouped": (moe_experts, "bf16"),
 }

@@ -193,6 +193,23 @@ int qutai_amd_attention_fwd(const void* q, const void* k, const void* v, void* o
                             int64_t heads, int64_t kv_heads, int64_t time, int64_t dim, int layout, double scale,
                             int causal, void* stream);
 
+/* Fused attention backward for the forward above (same layouts, scale and
+ * causal flag): from dO (grad), q, k, v, the forward's bf16 output `out` and
+ * its fp32 `lse`, writes dq, dk, dv (bf16) and delta = rowsum(dO * out)
+ * (fp32, lse's layout; a caller-provided buffer of batch*heads*time floats):
+ *   P = exp(scale q k^T - lse), dS = P (dO v^T - delta) scale,
+ *   dq = dS k, dk = dS^T q (summed over the heads sharing a kv head),
+ *   dv = P^T dO.
+ * Deterministic (no atomics).  Replaces `cuda_lm.attention_backward`
+ * (src/qutai/backends/cuda_lm.py:278-365) with its kernels
+ * lm_attention_delta / lm_attention_bf16_dq / lm_attention_bf16_dkv
+ * (src/qutai/backends/cuda/lm.cu:159-295); semantics of
+ * cpu_lm.attention_backward (src/qutai/backends/cpu_lm.py:176-201). */
+int qutai_amd_attention_bwd(const void* grad, const void* q, const void* k, const void* v, const void* out,
+                            const float* lse, void* dq, void* dk, void* dv, float* delta, int64_t batch,
+                            int64_t heads, int64_t kv_heads, int64_t time, int64_t dim, int layout, double scale,
+                            int causal, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -26,6 +26,8 @@
 #include "common.h"
 #include "qutai_amd.h"
 
+#include <initializer_list>
+
 using namespace qa;
 
 namespace {
@@ -332,27 +334,443 @@ __global__ void __launch_bounds__(WAVES * 64) attention_fwd_d64(AttnArgs p) {
   }
 }
 
+
+// ============================================================================
+// Backward (cuda_lm.attention_backward, src/qutai/backends/cuda_lm.py:278-365;
+// kernels lm_attention_bf16_dq / _dkv, src/qutai/backends/cuda/lm.cu:159-285;
+// oracle cpu_lm.attention_backward, cpu_lm.py:176-201):
+//   P = exp(scale Q K^T - lse),  delta = rowsum(dO * O),
+//   dS = P (dO V^T - delta) scale,  dQ = dS K,  dK = dS^T Q,  dV = P^T dO.
+// Two kernels, each owning its outputs (no atomics, bit-repeatable):
+//   * dq: a workgroup owns 256 queries of one (batch, head), streams K and V
+//     like the forward and also writes delta (it has dO and O of its queries
+//     in registers);
+//   * dkv: a workgroup owns 256 keys of one (batch, kv head), streams Q, dO,
+//     lse and delta of every query block and every head of the group, and
+//     sums the group's contributions in registers.
+// P and dS enter the MFMAs rounded to bf16 (the reference's d64 kernels do
+// the same); all sums are fp32.
+// ============================================================================
+
+struct AttnBwdArgs {
+  const bf16_t* g;  // dO
+  const bf16_t* q;
+  const bf16_t* k;
+  const bf16_t* v;
+  const bf16_t* o;
+  const float* lse;
+  float* delta;
+  bf16_t* dq;
+  bf16_t* dk;
+  bf16_t* dv;
+  int64_t batch, heads, kv_heads, time;
+  int64_t qb, qh, qt, kb, kh, kt, lb, lh, lt;
+  float c;  // scale * log2(e)
+  float scale;
+  int causal;
+};
+
+constexpr float LOG2E = 1.4426950408889634f;
+
+// Row-fragment of a [64][64] LDS tile whose 16-byte chunks are swizzled by
+// swz_row8: row r, d = 16 s + 8 half + [0, 8) (A operand with k = d, or B
+// operand with n = r).
+__device__ __forceinline__ bf16x8 row_frag(const bf16_t* x, int r, int s, int half) {
+  const int ch = 2 * s + half;
+  return *reinterpret_cast<const bf16x8*>(x + r * D + ((ch ^ swz_row8(r)) * 8));
+}
+
+// Transposed fragment of the same tile: A operand whose rows are the tile's
+// columns 32 db + [0, 32) and whose k index runs over the tile rows
+// rb + {4 half + [0, 4), 8 + 4 half + [0, 4)} (the row order of an MFMA
+// result's element index), read with ds_read_b64_tr_b16.
+__device__ __forceinline__ bf16x8 tr_frag(const bf16_t* x, int db, int rb, int lane) {
+  const int g = lane >> 4, i = lane & 15;
+  const int cb = 32 * db + (g & 1) * 16 + 4 * (i & 3);
+  const int r0 = rb + 4 * (g >> 1) + (i >> 2), r1 = r0 + 8;
+  const bf16_t* p0 = x + r0 * D + (((cb >> 3) ^ swz_row8(r0)) * 8) + (cb & 7);
+  const bf16_t* p1 = x + r1 * D + (((cb >> 3) ^ swz_row8(r1)) * 8) + (cb & 7);
+  i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4)p0);
+  i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4)p1);
+  i16x8 w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(bf16x8, w);
+}
+
+// Stage copy of a [64][64] bf16 tile (rows `stride` elements apart, rows >= rows_left read as zeros)
+// by the 256 threads: two 16-byte chunks per lane, physical chunk (j * 4 + wave) * 64 + lane.
+__device__ __forceinline__ void copy_tile(bf16_t* dst, const bf16_t* src, int64_t stride, int rows_left, int wave,
+                                          int lane) {
+  auto r = rsrc(src, (int64_t)KB * stride * 2);
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int qidx = (j * WAVES + wave) * 64 + lane;
+    const int row = qidx >> 3, pc = qidx & 7;
+    const uint32_t off = (uint32_t)((row * stride + ((pc ^ swz_row8(row)) * 8)) * 2) + ((uint32_t)(row >= rows_left) << 31);
+    char* d = reinterpret_cast<char*>(dst) + (j * WAVES + wave) * 1024;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void)d, 16, off, 0, 0, 0);
+  }
+}
+
+template <bool MASK>
+__device__ __forceinline__ void dq_block(const bf16_t* sk, const bf16_t* sv, const bf16x8 (&qf)[QB][4],
+                                         const bf16x8 (&gf)[QB][4], const float (&lse2)[QB], const float (&dl)[QB],
+                                         f32x16 (&dqt)[QB][2], const int (&lim)[QB], float c, float scale, int lane) {
+  const int half = lane >> 5, col = lane & 31;
+  bf16x8 kf[2][4], vf[2][4];
+#pragma unroll
+  for (int mb = 0; mb < 2; mb++)
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+      kf[mb][s] = row_frag(sk, 32 * mb + col, s, half);
+      vf[mb][s] = row_frag(sv, 32 * mb + col, s, half);
+    }
+  bf16x8 ktf[2][2][2];  // K^T fragments [db][mb][st]
+#pragma unroll
+  for (int db = 0; db < 2; db++)
+#pragma unroll
+    for (int mb = 0; mb < 2; mb++)
+#pragma unroll
+      for (int st = 0; st < 2; st++) ktf[db][mb][st] = tr_frag(sk, db, 32 * mb + 16 * st, lane);
+#pragma unroll
+  for (int qb = 0; qb < QB; qb++) {
+    bf16x8 dsf[2][2];
+#pragma unroll
+    for (int mb = 0; mb < 2; mb++) {
+      f32x16 st_ = {}, dp = {};
+#pragma unroll
+      for (int s = 0; s < 4; s++) {
+        st_ = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[mb][s], qf[qb][s], st_, 0, 0, 0);
+        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[mb][s], gf[qb][s], dp, 0, 0, 0);
+      }
+      float ds[16];
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        float x = st_[e];
+        if (MASK && 32 * mb + 8 * (e >> 2) + (e & 3) >= lim[qb]) x = -INFINITY;
+        const float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(x, c, -lse2[qb]));
+        ds[e] = pr * (dp[e] - dl[qb]) * scale;
+      }
+#pragma unroll
+      for (int st = 0; st < 2; st++) {
+        u32x4 w = {cvt_pk_bf16(ds[8 * st], ds[8 * st + 1]), cvt_pk_bf16(ds[8 * st + 2], ds[8 * st + 3]),
+                   cvt_pk_bf16(ds[8 * st + 4], ds[8 * st + 5]), cvt_pk_bf16(ds[8 * st + 6], ds[8 * st + 7])};
+        dsf[mb][st] = __builtin_bit_cast(bf16x8, w);
+      }
+    }
+#pragma unroll
+    for (int db = 0; db < 2; db++)
+#pragma unroll
+      for (int mb = 0; mb < 2; mb++)
+#pragma unroll
+        for (int st = 0; st < 2; st++)
+          dqt[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ktf[db][mb][st], dsf[mb][st], dqt[qb][db], 0, 0, 0);
+  }
+}
+
+__global__ void __launch_bounds__(WAVES * 64) attention_bwd_dq_d64(AttnBwdArgs p) {
+  __shared__ __attribute__((aligned(16))) bf16_t lds[2][2][TILE];  // [stage][K,V][64 x 64]
+  const int tid = threadIdx.x, lane = tid & 63, wave = uniform32(tid >> 6);
+  const int T = (int)p.time;
+  const int blocks_q = (T + QPB - 1) / QPB;
+  const int pid = uniform32(xcd_remap(blockIdx.x, gridDim.x));
+  const int bh = uniform32(pid / blocks_q);
+  const int qblk = uniform32(p.causal ? blocks_q - 1 - pid % blocks_q : pid % blocks_q);
+  const int wg_q0 = qblk * QPB;
+  const int q0 = uniform32(wg_q0 + wave * QW);
+  const int b = bh / (int)p.heads, h = bh % (int)p.heads;
+  const int kvh = h / (int)(p.heads / p.kv_heads);
+  const int64_t qbase = b * p.qb + h * p.qh;
+  const bf16_t* K = uniform_ptr(p.k + b * p.kb + kvh * p.kh);
+  const bf16_t* V = uniform_ptr(p.v + b * p.kb + kvh * p.kh);
+  const int half = lane >> 5, col = lane & 31;
+
+  // Q and dO fragments (B operands: lane = query, d = 16 s + 8 half + [0, 8)),
+  // delta = dO . O of the lane's query (halves summed across lanes l, l ^ 32)
+  bf16x8 qf[QB][4], gf[QB][4];
+  float lse2[QB], dl[QB];
+  {
+    const int64_t bytes = ((int64_t)T - 1) * p.qt * 2 + D * 2;
+    auto rq = rsrc(p.q + qbase, bytes), rg = rsrc(p.g + qbase, bytes), ro = rsrc(p.o + qbase, bytes);
+#pragma unroll
+    for (int qb = 0; qb < QB; qb++) {
+      const int t = q0 + qb * 32 + col;
+      float dot = 0.f;
+#pragma unroll
+      for (int s = 0; s < 4; s++) {
+        uint32_t off = (uint32_t)((t * p.qt + 16 * s + 8 * half) * 2) + ((uint32_t)(t >= T) << 31);
+        qf[qb][s] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, 0));
+        gf[qb][s] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rg, off, 0, 0));
+        u32x4 ow = __builtin_amdgcn_raw_buffer_load_b128(ro, off, 0, 0);
+        u32x4 gw = __builtin_bit_cast(u32x4, gf[qb][s]);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          dot += __uint_as_float(gw[e] << 16) * __uint_as_float(ow[e] << 16);
+          dot += __uint_as_float(gw[e] & 0xffff0000u) * __uint_as_float(ow[e] & 0xffff0000u);
+        }
+      }
+      dl[qb] = pair_sum(dot);
+      const int64_t li = b * p.lb + h * p.lh + (int64_t)t * p.lt;
+      lse2[qb] = t < T ? p.lse[li] * LOG2E : 0.f;
+      if (t < T && half == 0) p.delta[li] = dl[qb];
+    }
+  }
+
+  uint32_t ko[2];
+  int kr[2];
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    int qidx = (j * WAVES + wave) * 64 + lane;
+    int r = qidx >> 3, pc = qidx & 7;
+    kr[j] = r;
+    ko[j] = (uint32_t)((r * p.kt + ((pc ^ swz_row8(r)) * 8)) * 2);
+  }
+  const int nkb = p.causal ? min((wg_q0 + QPB + KB - 1) / KB, (T + KB - 1) / KB) : (T + KB - 1) / KB;
+  auto issue = [&](int stage, int kv0) {
+    auto rk = rsrc(K + (int64_t)kv0 * p.kt, (int64_t)KB * p.kt * 2);
+    auto rv = rsrc(V + (int64_t)kv0 * p.kt, (int64_t)KB * p.kt * 2);
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      uint32_t oob = (uint32_t)(kv0 + kr[j] >= T) << 31;
+      char* dk = reinterpret_cast<char*>(&lds[stage][0][0]) + (j * WAVES + wave) * 1024;
+      char* dv = reinterpret_cast<char*>(&lds[stage][1][0]) + (j * WAVES + wave) * 1024;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void)dk, 16, ko[j] + oob, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void)dv, 16, ko[j] + oob, 0, 0, 0);
+    }
+  };
+
+  f32x16 dqt[QB][2];
+#pragma unroll
+  for (int qb = 0; qb < QB; qb++)
+#pragma unroll
+    for (int db = 0; db < 2; db++) dqt[qb][db] = f32x16{};
+
+  const int last_key_full = p.causal ? min(T, q0 + 1) : T;
+  if (nkb > 0) issue(0, 0);
+  for (int kbk = 0; kbk < nkb; kbk++) {
+    const int cur = kbk & 1;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    asm volatile("s_barrier" ::: "memory");
+    if (kbk + 1 < nkb) issue(cur ^ 1, (kbk + 1) * KB);
+    const int kv0 = kbk * KB;
+    const bf16_t* sk = &lds[cur][0][0];
+    const bf16_t* sv = &lds[cur][1][0];
+    if (kv0 + KB <= last_key_full) {
+      const int lim[QB] = {};
+      dq_block<false>(sk, sv, qf, gf, lse2, dl, dqt, lim, p.c, p.scale, lane);
+    } else if (kv0 < q0 + QW || !p.causal) {
+      int lim[QB];
+#pragma unroll
+      for (int qb = 0; qb < QB; qb++) {
+        const int tq = q0 + qb * 32 + col;
+        lim[qb] = min(T - kv0, p.causal ? tq - kv0 + 1 : KB) - 4 * half;
+      }
+      dq_block<true>(sk, sv, qf, gf, lse2, dl, dqt, lim, p.c, p.scale, lane);
+    }
+  }
+
+#pragma unroll
+  for (int qb = 0; qb < QB; qb++) {
+    const int t = q0 + qb * 32 + col;
+    if (t < T) {
+      bf16_t* out = p.dq + b * p.qb + h * p.qh + (int64_t)t * p.qt;
+#pragma unroll
+      for (int db = 0; db < 2; db++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          uint2 w;
+          w.x = cvt_pk_bf16(dqt[qb][db][4 * g], dqt[qb][db][4 * g + 1]);
+          w.y = cvt_pk_bf16(dqt[qb][db][4 * g + 2], dqt[qb][db][4 * g + 3]);
+          *reinterpret_cast<uint2*>(out + 32 * db + 8 * g + 4 * half) = w;
+        }
+    }
+  }
+}
+
+constexpr int KW = 64;               // keys per wave (two blocks of 32)
+constexpr int KPB = WAVES * KW;      // keys per workgroup
+
+// One 64-query block against the wave's 64 keys.  MASK: some query of the
+// block is >= T or (causal) before one of the keys.
+template <bool MASK>
+__device__ __forceinline__ void dkv_block(const bf16_t* sq, const bf16_t* sg, const float* slse, const float* sdl,
+                                          const bf16x8 (&kf)[2][4], const bf16x8 (&vf)[2][4], f32x16 (&dvt)[2][2],
+                                          f32x16 (&dkt)[2][2], int qrel_end, int key_rel, int causal, float c,
+                                          float scale, int lane) {
+  // qrel_end: T - (first query of the block); key_rel: (first key of the
+  // wave) - (first query of the block).  Element e of a result holds query
+  // 32 mq + 8 (e / 4) + 4 half + e % 4 and key 32 nb + col.
+  const int half = lane >> 5, col = lane & 31;
+#pragma unroll
+  for (int mq = 0; mq < 2; mq++) {
+    bf16x8 qa[4], ga[4];
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+      qa[s] = row_frag(sq, 32 * mq + col, s, half);
+      ga[s] = row_frag(sg, 32 * mq + col, s, half);
+    }
+    f32x4 l4[4], d4[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      l4[j] = *reinterpret_cast<const f32x4*>(slse + 32 * mq + 8 * j + 4 * half);
+      d4[j] = *reinterpret_cast<const f32x4*>(sdl + 32 * mq + 8 * j + 4 * half);
+    }
+    bf16x8 pf[2][2], dsf[2][2];
+#pragma unroll
+    for (int nb = 0; nb < 2; nb++) {
+      f32x16 sc = {}, dp = {};
+#pragma unroll
+      for (int s = 0; s < 4; s++) {
+        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa[s], kf[nb][s], sc, 0, 0, 0);
+        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ga[s], vf[nb][s], dp, 0, 0, 0);
+      }
+      float pr[16], ds[16];
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        float x = sc[e];
+        if (MASK) {
+          const int qrel = 32 * mq + 8 * (e >> 2) + 4 * half + (e & 3);
+          if (qrel >= qrel_end || (causal && qrel < key_rel + 32 * nb + col)) x = -INFINITY;
+        }
+        pr[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(x, c, -l4[e >> 2][e & 3] * LOG2E));
+        ds[e] = pr[e] * (dp[e] - d4[e >> 2][e & 3]) * scale;
+      }
+#pragma unroll
+      for (int st = 0; st < 2; st++) {
+        u32x4 w = {cvt_pk_bf16(pr[8 * st], pr[8 * st + 1]), cvt_pk_bf16(pr[8 * st + 2], pr[8 * st + 3]),
+                   cvt_pk_bf16(pr[8 * st + 4], pr[8 * st + 5]), cvt_pk_bf16(pr[8 * st + 6], pr[8 * st + 7])};
+        pf[nb][st] = __builtin_bit_cast(bf16x8, w);
+        u32x4 z = {cvt_pk_bf16(ds[8 * st], ds[8 * st + 1]), cvt_pk_bf16(ds[8 * st + 2], ds[8 * st + 3]),
+                   cvt_pk_bf16(ds[8 * st + 4], ds[8 * st + 5]), cvt_pk_bf16(ds[8 * st + 6], ds[8 * st + 7])};
+        dsf[nb][st] = __builtin_bit_cast(bf16x8, z);
+      }
+    }
+#pragma unroll
+    for (int db = 0; db < 2; db++)
+#pragma unroll
+      for (int st = 0; st < 2; st++) {
+        const bf16x8 got = tr_frag(sg, db, 32 * mq + 16 * st, lane);
+        const bf16x8 qt = tr_frag(sq, db, 32 * mq + 16 * st, lane);
+#pragma unroll
+        for (int nb = 0; nb < 2; nb++) {
+          dvt[db][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(got, pf[nb][st], dvt[db][nb], 0, 0, 0);
+          dkt[db][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qt, dsf[nb][st], dkt[db][nb], 0, 0, 0);
+        }
+      }
+  }
+}
+
+__global__ void __launch_bounds__(WAVES * 64) attention_bwd_dkv_d64(AttnBwdArgs p) {
+  __shared__ __attribute__((aligned(16))) bf16_t tiles[2][2][TILE];  // [stage][Q, dO][64 x 64]
+  __shared__ __attribute__((aligned(16))) float stats[2][2][KB];      // [stage][lse, delta][64]
+  const int tid = threadIdx.x, lane = tid & 63, wave = uniform32(tid >> 6);
+  const int T = (int)p.time;
+  const int blocks_k = (T + KPB - 1) / KPB;
+  // key blocks of one (batch, kv head) on one XCD; the first key blocks see
+  // the most queries (causal) and start first
+  const int pid = uniform32(xcd_remap(blockIdx.x, gridDim.x));
+  const int bkh = uniform32(pid / blocks_k);
+  const int k0 = uniform32((pid % blocks_k) * KPB);
+  const int kw = uniform32(k0 + wave * KW);
+  const int b = bkh / (int)p.kv_heads, kvh = bkh % (int)p.kv_heads;
+  const int group = (int)(p.heads / p.kv_heads);
+  const int half = lane >> 5, col = lane & 31;
+  const int64_t kbase = b * p.kb + kvh * p.kh;
+
+  // K and V of the wave's keys (B operands: lane = key 32 nb + col, d = 16 s + 8 half + [0, 8))
+  bf16x8 kf[2][4], vf[2][4];
+  {
+    const int64_t bytes = ((int64_t)T - 1) * p.kt * 2 + D * 2;
+    auto rk = rsrc(p.k + kbase, bytes), rv = rsrc(p.v + kbase, bytes);
+#pragma unroll
+    for (int nb = 0; nb < 2; nb++) {
+      const int key = kw + 32 * nb + col;
+#pragma unroll
+      for (int s = 0; s < 4; s++) {
+        uint32_t off = (uint32_t)((key * p.kt + 16 * s + 8 * half) * 2) + ((uint32_t)(key >= T) << 31);
+        kf[nb][s] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
+        vf[nb][s] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
+      }
+    }
+  }
+
+  const int qs0 = p.causal ? k0 : 0;                  // first query any key of the workgroup sees
+  const int nq = qs0 < T ? (T - qs0 + KB - 1) / KB : 0;
+  const int iterations = nq * group;
+  auto issue = [&](int stage, int it) {
+    const int g = it / nq, qs = qs0 + (it % nq) * KB;
+    const int h = kvh * group + g;
+    const int64_t base = b * p.qb + h * p.qh + (int64_t)qs * p.qt;
+    copy_tile(&tiles[stage][0][0], p.q + base, p.qt, T - qs, wave, lane);
+    copy_tile(&tiles[stage][1][0], p.g + base, p.qt, T - qs, wave, lane);
+    if (wave < 2) {  // wave 0: lse of the 64 queries, wave 1: delta
+      const float* src = wave == 0 ? p.lse : p.delta;
+      auto r = rsrc(src + b * p.lb + h * p.lh, ((int64_t)T - 1) * p.lt * 4 + 4);
+      const uint32_t off = (uint32_t)((int64_t)(qs + lane) * p.lt * 4) + ((uint32_t)(qs + lane >= T) << 31);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void)&stats[stage][wave][0], 4, off, 0, 0, 0);
+    }
+  };
+
+  f32x16 dvt[2][2], dkt[2][2];
+#pragma unroll
+  for (int db = 0; db < 2; db++)
+#pragma unroll
+    for (int nb = 0; nb < 2; nb++) dvt[db][nb] = dkt[db][nb] = f32x16{};
+
+  if (iterations > 0) issue(0, 0);
+  for (int it = 0; it < iterations; it++) {
+    const int cur = it & 1;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    asm volatile("s_barrier" ::: "memory");
+    if (it + 1 < iterations) issue(cur ^ 1, it + 1);
+    const int qs = qs0 + (it % nq) * KB;
+    // skip blocks whose every query is before every key of the wave (causal)
+    if (p.causal && qs + KB - 1 < kw) continue;
+    const bool full = qs + KB <= T && (!p.causal || qs >= kw + KW - 1);
+    if (full)
+      dkv_block<false>(&tiles[cur][0][0], &tiles[cur][1][0], &stats[cur][0][0], &stats[cur][1][0], kf, vf, dvt, dkt,
+                       T - qs, kw - qs, p.causal, p.c, p.scale, lane);
+    else
+      dkv_block<true>(&tiles[cur][0][0], &tiles[cur][1][0], &stats[cur][0][0], &stats[cur][1][0], kf, vf, dvt, dkt,
+                      T - qs, kw - qs, p.causal, p.c, p.scale, lane);
+  }
+
+  // dK^T / dV^T: lane = key 32 nb + col, rows d = 32 db + 8 (e / 4) + 4 half + e % 4
+#pragma unroll
+  for (int nb = 0; nb < 2; nb++) {
+    const int key = kw + 32 * nb + col;
+    if (key < T) {
+      bf16_t* ok = p.dk + kbase + (int64_t)key * p.kt;
+      bf16_t* ov = p.dv + kbase + (int64_t)key * p.kt;
+#pragma unroll
+      for (int db = 0; db < 2; db++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          uint2 wk, wv;
+          wk.x = cvt_pk_bf16(dkt[db][nb][4 * g], dkt[db][nb][4 * g + 1]);
+          wk.y = cvt_pk_bf16(dkt[db][nb][4 * g + 2], dkt[db][nb][4 * g + 3]);
+          wv.x = cvt_pk_bf16(dvt[db][nb][4 * g], dvt[db][nb][4 * g + 1]);
+          wv.y = cvt_pk_bf16(dvt[db][nb][4 * g + 2], dvt[db][nb][4 * g + 3]);
+          *reinterpret_cast<uint2*>(ok + 32 * db + 8 * g + 4 * half) = wk;
+          *reinterpret_cast<uint2*>(ov + 32 * db + 8 * g + 4 * half) = wv;
+        }
+    }
+  }
+}
+
 }  // namespace
 
 extern "C" {
 
-int qutai_amd_attention_fwd(const void* q, const void* k, const void* v, void* out, float* lse, int64_t batch,
-                            int64_t heads, int64_t kv_heads, int64_t time, int64_t dim, int layout, double scale,
-                            int causal, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// element strides of (batch, head, token) for q-shaped, kv-shaped and lse arrays
+template <class Args>
+int set_layout(Args& a, int64_t batch, int64_t heads, int64_t kv_heads, int64_t time, int layout) {
   if (batch < 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads || time < 0) return QA_EINVAL;
-  if (!(scale > 0.0) || scale > 1e30) return QA_EINVAL;  // the running max assumes a positive scale
+  if (layout != 0 && layout != 1) return QA_EINVAL;
   if (time > (1 << 30) / (heads > kv_heads ? heads : kv_heads) / D) return QA_EINVAL;  // 32-bit element offsets
-  if (dim != D || (layout != 0 && layout != 1)) return QA_EINVAL;
-  if (!q || !k || !v || !out) return QA_EINVAL;
-  for (const void* ptr : {q, k, v, (const void*)out})
-    if ((uintptr_t)ptr % 16) return QA_EINVAL;
-  if (batch * time == 0) return QA_OK;
-  AttnArgs a = {};
-  a.q = (const bf16_t*)q;
-  a.k = (const bf16_t*)k;
-  a.v = (const bf16_t*)v;
-  a.o = (bf16_t*)out;
-  a.lse = lse;
   a.batch = batch;
   a.heads = heads;
   a.kv_heads = kv_heads;
@@ -366,12 +784,71 @@ int qutai_amd_attention_fwd(const void* q, const void* k, const void* v, void* o
     a.kb = time * kv_heads * D, a.kh = D, a.kt = kv_heads * D;
     a.lb = time * heads, a.lh = 1, a.lt = heads;
   }
+  return QA_OK;
+}
+
+bool aligned16(std::initializer_list<const void*> ptrs) {
+  for (const void* ptr : ptrs)
+    if (!ptr || (uintptr_t)ptr % 16) return false;
+  return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+int qutai_amd_attention_fwd(const void* q, const void* k, const void* v, void* out, float* lse, int64_t batch,
+                            int64_t heads, int64_t kv_heads, int64_t time, int64_t dim, int layout, double scale,
+                            int causal, void* stream) {
+  AttnArgs a = {};
+  if (dim != D || set_layout(a, batch, heads, kv_heads, time, layout) != QA_OK) return QA_EINVAL;
+  if (!(scale > 0.0) || scale > 1e30) return QA_EINVAL;  // the running max assumes a positive scale
+  if (!aligned16({q, k, v, out})) return QA_EINVAL;
+  if (batch * time == 0) return QA_OK;
+  a.q = (const bf16_t*)q;
+  a.k = (const bf16_t*)k;
+  a.v = (const bf16_t*)v;
+  a.o = (bf16_t*)out;
+  a.lse = lse;
   a.scale = (float)scale;
   a.scale_log2 = (float)(scale * 1.4426950408889634);
   a.causal = causal ? 1 : 0;
   int64_t blocks = batch * heads * ((time + QPB - 1) / QPB);
   if (blocks > 0x7fffffff) return QA_EINVAL;
   hipLaunchKernelGGL(attention_fwd_d64, dim3((unsigned)blocks), dim3(WAVES * 64), 0, (hipStream_t)stream, a);
+  return (int)hipGetLastError();
+}
+
+int qutai_amd_attention_bwd(const void* grad, const void* q, const void* k, const void* v, const void* out,
+                            const float* lse, void* dq, void* dk, void* dv, float* delta, int64_t batch, int64_t heads,
+                            int64_t kv_heads, int64_t time, int64_t dim, int layout, double scale, int causal,
+                            void* stream) {
+  AttnBwdArgs a = {};
+  if (dim != D || set_layout(a, batch, heads, kv_heads, time, layout) != QA_OK) return QA_EINVAL;
+  if (!(scale > 0.0) || scale > 1e30) return QA_EINVAL;
+  if (!aligned16({grad, q, k, v, out, dq, dk, dv}) || !lse || !delta) return QA_EINVAL;
+  if (batch * time == 0) return QA_OK;
+  a.g = (const bf16_t*)grad;
+  a.q = (const bf16_t*)q;
+  a.k = (const bf16_t*)k;
+  a.v = (const bf16_t*)v;
+  a.o = (const bf16_t*)out;
+  a.lse = lse;
+  a.delta = delta;
+  a.dq = (bf16_t*)dq;
+  a.dk = (bf16_t*)dk;
+  a.dv = (bf16_t*)dv;
+  a.scale = (float)scale;
+  a.c = (float)(scale * 1.4426950408889634);
+  a.causal = causal ? 1 : 0;
+  const int64_t blocks_q = batch * heads * ((time + QPB - 1) / QPB);
+  const int64_t blocks_k = batch * kv_heads * ((time + KPB - 1) / KPB);
+  if (blocks_q > 0x7fffffff || blocks_k > 0x7fffffff) return QA_EINVAL;
+  // dq first: it writes delta, which the dkv kernel reads
+  hipLaunchKernelGGL(attention_bwd_dq_d64, dim3((unsigned)blocks_q), dim3(WAVES * 64), 0, (hipStream_t)stream, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  hipLaunchKernelGGL(attention_bwd_dkv_d64, dim3((unsigned)blocks_k), dim3(WAVES * 64), 0, (hipStream_t)stream, a);
   return (int)hipGetLastError();
 }
 

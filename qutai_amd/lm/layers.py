@@ -154,12 +154,14 @@ def attention_products(q, k, v, *, scale=None):
 
 def attention(q, k, v, heads, kv_heads):
     """Causal grouped-query attention on (batch, time, heads*64) tensors in the
-    lm layout (src/qutai/lm/layers.py:119-130), forward through the fused
-    kernel; the T x T scores are never stored."""
+    lm layout (src/qutai/lm/layers.py:119-130): fused forward (the T x T
+    scores are never stored) and fused backward recorded for autograd."""
+    b = backend(q)
     batch, time, features = q.shape
-    out, _ = backend(q).attention(q.storage, k.storage, v.storage, batch, time, heads, kv_heads,
-                                  features // heads, causal=True, layout=1)
-    return Tensor(out, shape=q.shape)
+    dims = (batch, time, heads, kv_heads, features // heads)
+    out, lse = b.attention(q.storage, k.storage, v.storage, *dims)
+    return record(Tensor(out, shape=q.shape), (q, k, v),
+                  lambda g: b.attention_backward(g, q.storage, k.storage, v.storage, out, lse, *dims))
 
 
 def attention_fused(q, k, v, *, scale=None, causal=False):

@@ -165,3 +165,127 @@ def test_lm_layer_attention_and_nn_fused_products(lm):
         expected, _ = ora.attention_np(*(stored(normal(50 + i, groups * time * dim), "bfloat16")
                                          .reshape(groups, time, dim)[g] for i in range(3)), causal=False)
         assert ora.rel_frobenius(fused[g], expected) <= BF16_TOL
+
+
+# ---- backward --------------------------------------------------------------------------
+
+def _lm_heads(x, batch, time, heads, dim):
+    return x.reshape(batch, time, heads, dim).transpose(0, 2, 1, 3)
+
+
+def check_backward(lm, dims, seed, *, causal=True, layout=1, pairs=None, spread=1.0):
+    """Run forward + backward on the GPU and compare dq, dk, dv with the
+    float64 oracle fed the stored bf16 inputs and the GPU's saved bf16 output
+    (as tests/test_lm_bfloat16.py:95-104 does)."""
+    batch, time, heads, kv_heads, dim = dims
+    rng = np.random.default_rng(seed)
+    qv, kv, vv = (rng.uniform(-spread, spread, n).astype(np.float32) for n in (
+        batch * time * heads * dim, batch * time * kv_heads * dim, batch * time * kv_heads * dim))
+    gv = rng.uniform(-0.5, 0.5, qv.size).astype(np.float32)
+    q, k, v, g = (upload(x, "bfloat16") for x in (qv, kv, vv, gv))
+    out, lse = lm.attention(q, k, v, *dims, causal=causal, layout=layout)
+    dq, dk, dv = lm.attention_backward(g, q, k, v, out, lse, *dims, causal=causal, layout=layout)
+    assert (dq.dtype, dk.dtype, dv.dtype) == ("bfloat16",) * 3
+    qs, ks, vs, gs = (stored(x, "bfloat16") for x in (qv, kv, vv, gv))
+    os_ = download(out).astype(np.float64)
+    if layout == 1:
+        split = lambda x, n: _lm_heads(x, batch, time, n, dim)  # noqa: E731
+    else:
+        split = lambda x, n: x.reshape(batch, n, time, dim)  # noqa: E731
+    qa, ga, oa = split(qs, heads), split(gs, heads), split(os_, heads)
+    ka, va = split(ks, kv_heads), split(vs, kv_heads)
+    dqa, dka, dva = split(download(dq), heads), split(download(dk), kv_heads), split(download(dv), kv_heads)
+    group = heads // kv_heads
+    for b in range(batch):
+        for kh in range(kv_heads):
+            if pairs is not None and (b, kh) not in pairs:
+                continue
+            dk_sum = np.zeros((time, dim))
+            dv_sum = np.zeros((time, dim))
+            for h in range(kh * group, (kh + 1) * group):
+                _, l_ref = ora.attention_np(qa[b, h], ka[b, kh], va[b, kh], causal=causal)
+                dq_ref, dk_ref, dv_ref = _backward_np(ga[b, h], qa[b, h], ka[b, kh], va[b, kh], oa[b, h], l_ref,
+                                                      causal)
+                assert ora.rel_frobenius(dqa[b, h], dq_ref) <= BF16_TOL, ("dq", b, h)
+                dk_sum += dk_ref
+                dv_sum += dv_ref
+            assert ora.rel_frobenius(dka[b, kh], dk_sum) <= BF16_TOL, ("dk", b, kh)
+            assert ora.rel_frobenius(dva[b, kh], dv_sum) <= BF16_TOL, ("dv", b, kh)
+    return dq, dk, dv
+
+
+def _backward_np(g, q, k, v, o, lse, causal):
+    if causal:
+        return ora.attention_backward_np(g, q, k, v, o, lse)
+    scale = 1 / np.sqrt(q.shape[1])
+    p = np.exp((q @ k.T) * scale - lse[:, None])
+    ds = p * (g @ v.T - (g * o).sum(axis=1, keepdims=True)) * scale
+    return ds @ k, ds.T @ q, p.T @ g
+
+
+def test_backward_small_against_the_loop_oracle(lm):
+    # tests/test_lm_bfloat16.py:73-104 at head dimension 64: dims (2, 5, 4, 2, 64),
+    # uniform(-0.4, 0.4) from Random(9), gradient uniform(-0.2, 0.2)
+    dims = (2, 5, 4, 2, 64)
+    random = Random(9)
+    qv = np.array([random.uniform(-0.4, 0.4) for _ in range(2 * 5 * 4 * 64)], dtype=np.float32)
+    kv = np.array([random.uniform(-0.4, 0.4) for _ in range(2 * 5 * 2 * 64)], dtype=np.float32)
+    vv = np.array([random.uniform(-0.4, 0.4) for _ in range(2 * 5 * 2 * 64)], dtype=np.float32)
+    gv = np.array([random.uniform(-0.2, 0.2) for _ in range(2 * 5 * 4 * 64)], dtype=np.float32)
+    q, k, v, g = (upload(x, "bfloat16") for x in (qv, kv, vv, gv))
+    out, lse = lm.attention(q, k, v, *dims)
+    grads = lm.attention_backward(g, q, k, v, out, lse, *dims)
+    qs, ks, vs, gs = (stored(x, "bfloat16").tolist() for x in (qv, kv, vv, gv))
+    _, expected_lse = ora.attention(qs, ks, vs, *dims)
+    saved = download(out).astype(np.float64).tolist()
+    expected = ora.attention_backward(gs, qs, ks, vs, saved, expected_lse, *dims)
+    for actual, reference in zip(grads, expected):
+        assert actual.dtype == "bfloat16"
+        assert ora.rel_frobenius(download(actual), reference) <= BF16_TOL
+
+
+@pytest.mark.parametrize("time", [1, 17, 64, 65, 200, 257, 513])
+def test_backward_causal_gqa_lm_layout(lm, time):
+    check_backward(lm, (2, time, 4, 2, 64), 100 + time)
+
+
+@pytest.mark.parametrize("time", [33, 300])
+def test_backward_non_causal_nn_layout(lm, time):
+    check_backward(lm, (2, time, 2, 2, 64), 200 + time, causal=False, layout=0)
+    check_backward(lm, (1, time, 4, 1, 64), 300 + time, causal=False, layout=1)
+
+
+def test_backward_long_sequence_sampled_heads(lm):
+    check_backward(lm, (1, 2048, 8, 2, 64), 7, pairs={(0, 1)}, spread=2.0)
+
+
+def test_backward_is_bitwise_repeatable(lm):
+    # tests/test_lm_decoder.py:228-246: repeated backward calls give identical bits
+    dims = (2, 130, 4, 2, 64)
+    q, k, v, g = (upload(normal(70 + i, n), "bfloat16") for i, n in enumerate(
+        (2 * 130 * 256, 2 * 130 * 128, 2 * 130 * 128, 2 * 130 * 256)))
+    out, lse = lm.attention(q, k, v, *dims)
+    first = [download(x).tobytes() for x in lm.attention_backward(g, q, k, v, out, lse, *dims)]
+    for _ in range(3):
+        assert [download(x).tobytes() for x in lm.attention_backward(g, q, k, v, out, lse, *dims)] == first
+
+
+def test_lm_attention_layer_autograd(lm):
+    from qutai_amd import Tensor
+    from qutai_amd.lm.layers import attention
+
+    batch, time, heads, kv_heads, dim = 1, 70, 2, 1, 64
+    qv, kv, vv = normal(81, time * heads * dim), normal(82, time * dim), normal(83, time * dim)
+    q = Tensor(upload(qv, "bfloat16"), shape=(batch, time, heads * dim), requires_grad=True)
+    k = Tensor(upload(kv, "bfloat16"), shape=(batch, time, dim), requires_grad=True)
+    v = Tensor(upload(vv, "bfloat16"), shape=(batch, time, dim), requires_grad=True)
+    out = attention(q, k, v, heads, kv_heads)
+    gv = normal(84, out.size)
+    out.backward(Tensor(upload(gv, "bfloat16"), shape=out.shape))
+    dims = (batch, time, heads, kv_heads, dim)
+    qs, ks, vs, gs = (stored(x, "bfloat16") for x in (qv, kv, vv, gv))
+    saved = download(out.storage).astype(np.float64)
+    _, lse = ora.attention(qs.tolist(), ks.tolist(), vs.tolist(), *dims)
+    expected = ora.attention_backward(gs.tolist(), qs.tolist(), ks.tolist(), vs.tolist(), saved.tolist(), lse, *dims)
+    for tensor, reference in zip((q, k, v), expected):
+        assert ora.rel_frobenius(download(tensor.grad.storage), reference) <= BF16_TOL
