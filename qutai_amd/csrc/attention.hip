@@ -10,7 +10,8 @@
 //    head); each wave owns 64 queries as two blocks of 32 and keeps their Q
 //    fragments in registers for the whole kernel;
 //  * K and V advance in blocks of 64 keys, copied HBM -> LDS with
-//    buffer_load ... lds into a two-stage ring (8 KiB + 8 KiB per stage);
+//    buffer_load ... lds into a two-stage ring (8 KiB + 8 KiB per stage); the
+//    copy of block j+1 overlaps the MFMAs of block j;
 //  * scores are computed transposed, S^T = K Q^T, with
 //    v_mfma_f32_32x32x16_bf16: in the MFMA result layout lane l then holds
 //    query l % 32 of its block and 16 keys of each 32-key block, so the
@@ -263,15 +264,15 @@ __global__ void __launch_bounds__(WAVES * 64) attention_fwd_d64(AttnArgs p) {
   }
   const int nkb = p.causal ? min((wg_q0 + QPB + KB - 1) / KB, (T + KB - 1) / KB) : (T + KB - 1) / KB;
   auto issue = [&](int stage, int kv0) {
-    auto rk = rsrc(K + (int64_t)kv0 * p.kt, (int64_t)KB * p.kt * 2);
-    auto rv = rsrc(V + (int64_t)kv0 * p.kt, (int64_t)KB * p.kt * 2);
+    const u32x4 rk = lds_rsrc(K + (int64_t)kv0 * p.kt, (int64_t)KB * p.kt * 2);
+    const u32x4 rv = lds_rsrc(V + (int64_t)kv0 * p.kt, (int64_t)KB * p.kt * 2);
 #pragma unroll
     for (int j = 0; j < 2; j++) {
       uint32_t oob = (uint32_t)(kv0 + kr[j] >= T) << 31;
       char* dk = reinterpret_cast<char*>(&lds[stage][0][0]) + (j * WAVES + wave) * 1024;
       char* dv = reinterpret_cast<char*>(&lds[stage][1][0]) + (j * WAVES + wave) * 1024;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void)dk, 16, ko[j] + oob, 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void)dv, 16, vo[j] + oob, 0, 0, 0);
+      lds_load16(rk, dk, ko[j] + oob);
+      lds_load16(rv, dv, vo[j] + oob);
     }
   };
 
@@ -291,7 +292,7 @@ __global__ void __launch_bounds__(WAVES * 64) attention_fwd_d64(AttnArgs p) {
   if (nkb > 0) issue(0, 0);
   for (int kbk = 0; kbk < nkb; kbk++) {
     const int cur = kbk & 1;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    wait_vmcnt<0>();
     asm volatile("s_barrier" ::: "memory");  // stage cur landed; stage cur^1 free
     if (kbk + 1 < nkb) issue(cur ^ 1, (kbk + 1) * KB);
     const int kv0 = kbk * KB;
@@ -400,14 +401,14 @@ __device__ __forceinline__ bf16x8 tr_frag(const bf16_t* x, int db, int rb, int l
 // by the 256 threads: two 16-byte chunks per lane, physical chunk (j * 4 + wave) * 64 + lane.
 __device__ __forceinline__ void copy_tile(bf16_t* dst, const bf16_t* src, int64_t stride, int rows_left, int wave,
                                           int lane) {
-  auto r = rsrc(src, (int64_t)KB * stride * 2);
+  const u32x4 r = lds_rsrc(src, (int64_t)KB * stride * 2);
 #pragma unroll
   for (int j = 0; j < 2; j++) {
     const int qidx = (j * WAVES + wave) * 64 + lane;
     const int row = qidx >> 3, pc = qidx & 7;
     const uint32_t off = (uint32_t)((row * stride + ((pc ^ swz_row8(row)) * 8)) * 2) + ((uint32_t)(row >= rows_left) << 31);
     char* d = reinterpret_cast<char*>(dst) + (j * WAVES + wave) * 1024;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void)d, 16, off, 0, 0, 0);
+    lds_load16(r, d, off);
   }
 }
 
@@ -526,15 +527,15 @@ __global__ void __launch_bounds__(WAVES * 64) attention_bwd_dq_d64(AttnBwdArgs p
   }
   const int nkb = p.causal ? min((wg_q0 + QPB + KB - 1) / KB, (T + KB - 1) / KB) : (T + KB - 1) / KB;
   auto issue = [&](int stage, int kv0) {
-    auto rk = rsrc(K + (int64_t)kv0 * p.kt, (int64_t)KB * p.kt * 2);
-    auto rv = rsrc(V + (int64_t)kv0 * p.kt, (int64_t)KB * p.kt * 2);
+    const u32x4 rk = lds_rsrc(K + (int64_t)kv0 * p.kt, (int64_t)KB * p.kt * 2);
+    const u32x4 rv = lds_rsrc(V + (int64_t)kv0 * p.kt, (int64_t)KB * p.kt * 2);
 #pragma unroll
     for (int j = 0; j < 2; j++) {
       uint32_t oob = (uint32_t)(kv0 + kr[j] >= T) << 31;
       char* dk = reinterpret_cast<char*>(&lds[stage][0][0]) + (j * WAVES + wave) * 1024;
       char* dv = reinterpret_cast<char*>(&lds[stage][1][0]) + (j * WAVES + wave) * 1024;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void)dk, 16, ko[j] + oob, 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void)dv, 16, ko[j] + oob, 0, 0, 0);
+      lds_load16(rk, dk, ko[j] + oob);
+      lds_load16(rv, dv, ko[j] + oob);
     }
   };
 
@@ -548,7 +549,7 @@ __global__ void __launch_bounds__(WAVES * 64) attention_bwd_dq_d64(AttnBwdArgs p
   if (nkb > 0) issue(0, 0);
   for (int kbk = 0; kbk < nkb; kbk++) {
     const int cur = kbk & 1;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    wait_vmcnt<0>();
     asm volatile("s_barrier" ::: "memory");
     if (kbk + 1 < nkb) issue(cur ^ 1, (kbk + 1) * KB);
     const int kv0 = kbk * KB;
@@ -704,9 +705,9 @@ __global__ void __launch_bounds__(WAVES * 64) attention_bwd_dkv_d64(AttnBwdArgs 
     copy_tile(&tiles[stage][1][0], p.g + base, p.qt, T - qs, wave, lane);
     if (wave < 2) {  // wave 0: lse of the 64 queries, wave 1: delta
       const float* src = wave == 0 ? p.lse : p.delta;
-      auto r = rsrc(src + b * p.lb + h * p.lh, ((int64_t)T - 1) * p.lt * 4 + 4);
+      const u32x4 r = lds_rsrc(src + b * p.lb + h * p.lh, ((int64_t)T - 1) * p.lt * 4 + 4);
       const uint32_t off = (uint32_t)((int64_t)(qs + lane) * p.lt * 4) + ((uint32_t)(qs + lane >= T) << 31);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void)&stats[stage][wave][0], 4, off, 0, 0, 0);
+      lds_load4(r, &stats[stage][wave][0], off);
     }
   };
 
@@ -719,7 +720,7 @@ __global__ void __launch_bounds__(WAVES * 64) attention_bwd_dkv_d64(AttnBwdArgs 
   if (iterations > 0) issue(0, 0);
   for (int it = 0; it < iterations; it++) {
     const int cur = it & 1;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    wait_vmcnt<0>();
     asm volatile("s_barrier" ::: "memory");
     if (it + 1 < iterations) issue(cur ^ 1, it + 1);
     const int qs = qs0 + (it % nq) * KB;

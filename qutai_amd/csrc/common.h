@@ -66,4 +66,46 @@ __device__ __forceinline__ int xcd_remap(int pid, int n) {
   return xcd < rem ? xcd * (per + 1) + q : rem * (per + 1) + (xcd - rem) * per + q;
 }
 
+// ---- direct-to-LDS buffer loads ---------------------------------------------
+// Buffer descriptor words (base, stride 0, num_records, dword3) held in
+// SGPRs; an offset at or beyond num_records reads as zeros.
+__device__ __forceinline__ u32x4 lds_rsrc(const void* base, int64_t bytes) {
+  const uint32_t n = bytes > 0x7ffffff0 ? 0x7ffffff0u : (uint32_t)(bytes < 0 ? 0 : bytes);
+  const uint64_t a = (uint64_t)(uintptr_t)base;
+  u32x4 d = {(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a),
+             (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32) & 0xffffu),
+             (uint32_t)__builtin_amdgcn_readfirstlane(n), 0x00020000u};
+  return d;
+}
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// buffer_load_dwordx4 ... lds: lane l's 16 bytes at `voffset` land at
+// lds + 16 l.  Issued from inline assembly so that the compiler does not
+// treat it as a pending LDS write that every later LDS read has to wait for
+// (it cannot tell the destination apart from the buffers being read and
+// would insert s_waitcnt vmcnt(0) before them).  Callers order copies and
+// reads themselves: s_waitcnt vmcnt, then s_barrier, before reading a
+// buffer; no copy into a buffer before every wave has finished reading it.
+__device__ __forceinline__ void lds_load16(u32x4 rsrc, void* lds, uint32_t voffset) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_ptr_t)lds);
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(voffset), "s"(rsrc)
+               : "memory", "m0");
+}
+// s_waitcnt vmcnt(N) through the builtin (gfx9 encoding: vmcnt bits 3:0 and
+// 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima), so that the
+// compiler's own wait placement knows that the loads it issued are done.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00);
+}
+
+// Same with 4 bytes per lane (lane l's dword lands at lds + 4 l).
+__device__ __forceinline__ void lds_load4(u32x4 rsrc, void* lds, uint32_t voffset) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_ptr_t)lds);
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(m0), "v"(voffset), "s"(rsrc)
+               : "memory", "m0");
+}
+
 }  // namespace qa

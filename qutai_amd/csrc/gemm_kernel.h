@@ -15,7 +15,8 @@
 //    v_mfma_f32_32x32x2_f32 (true fp32 products, fp32 accumulation);
 //  * A and B tiles move HBM -> LDS in 16-byte chunks with buffer loads,
 //    either straight into LDS (`buffer_load_dwordx4 ... lds`, DMA = true,
-//    STAGES-deep ring so several K steps are in flight while the MFMAs run)
+//    STAGES-deep ring so several K steps are in flight while the MFMAs run;
+//    issued from inline assembly, see lds_load16) 
 //    or through registers (DMA = false, two LDS stages); a chunk outside the
 //    matrix gets an out-of-range buffer offset and reads as zeros, so the
 //    loop has no branches;
@@ -132,7 +133,11 @@ struct GemmKernel {
   static constexpr int LA = TileA::CHUNKS / NT;     // chunks per thread and stage
   static constexpr int LB = TileB::CHUNKS / NT;
   static constexpr int STAGE = (BM + BN) * BK;      // elements per stage
-  static constexpr int LDS_BYTES = STAGES * STAGE * (int)sizeof(T);
+  // Output staging row pitch (floats): TN + 8 puts the two lane halves, which
+  // write rows 4 apart, into different bank halves.
+  static constexpr int EP = TN + 8;
+  static constexpr int RING_BYTES = STAGES * STAGE * (int)sizeof(T);
+  static constexpr int LDS_BYTES = RING_BYTES > NW * 32 * EP * 4 ? RING_BYTES : NW * 32 * EP * 4;
   static_assert(TileA::CHUNKS % NT == 0 && TileB::CHUNKS % NT == 0, "staging split");
   static_assert(TM % 32 == 0 && TN % 32 == 0 && BK % 16 == 0, "tile shape");
   static_assert(DMA || STAGES == 2, "register staging is double-buffered");
@@ -152,13 +157,10 @@ struct GemmKernel {
   __device__ static __forceinline__ u32x4 fetch(__amdgpu_buffer_rsrc_t r, uint32_t offset) {
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, 0));
   }
-  typedef __attribute__((address_space(3))) void* lds_void;
-  __device__ static __forceinline__ void fetch_lds(__amdgpu_buffer_rsrc_t r, char* lds, uint32_t offset) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void)lds, 16, offset, 0, 0, 0);
-  }
+
   template <int N>
   __device__ static __forceinline__ void wait_vm() {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+    wait_vmcnt<N>();
   }
   __device__ static __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory"); }
 
@@ -386,19 +388,21 @@ struct GemmKernel {
       char* base = reinterpret_cast<char*>(lds);
       // copies of one stage, optionally only instructions [first, last)
       auto issue_range = [&](int stage, int64_t k0, int first, int last) {
-        auto da = desc_a(k0);
-        auto db = desc_b(k0);
+        const u32x4 da = lds_rsrc(KA ? A + row0 * lda + k0 : A + k0 * lda + row0,
+                                  (int64_t)(KA ? BM * lda : BK * lda) * (int64_t)sizeof(T));
+        const u32x4 db = lds_rsrc(KB ? B + col0 * ldb + k0 : B + k0 * ldb + col0,
+                                  (int64_t)(KB ? BN * ldb : BK * ldb) * (int64_t)sizeof(T));
         const int64_t krem = K - k0;
         char* sa = base + stage * STAGE * (int)sizeof(T);
         char* sb = sa + BM * BK * (int)sizeof(T);
 #pragma unroll
         for (int j = 0; j < JA; j++)
           if (j >= first && j < last)
-            fetch_lds(da, sa + (j * NW + wave) * 1024, (va[j] && ka[j] < krem) ? oa[j] : OOB);
+            lds_load16(da, sa + (j * NW + wave) * 1024, (va[j] && ka[j] < krem) ? oa[j] : OOB);
 #pragma unroll
         for (int j = 0; j < JB; j++)
           if (JA + j >= first && JA + j < last)
-            fetch_lds(db, sb + (j * NW + wave) * 1024, (vb[j] && kb[j] < krem) ? ob[j] : OOB);
+            lds_load16(db, sb + (j * NW + wave) * 1024, (vb[j] && kb[j] < krem) ? ob[j] : OOB);
       };
       auto issue = [&](int stage, int64_t k0) { issue_range(stage, k0, 0, L); };
 #pragma unroll
@@ -522,10 +526,7 @@ struct GemmKernel {
   // (MFMA C layout: lane l holds column l & 31 and rows
   // 8 (e/4) + 4 (l >> 5) + (e & 3) of a 32x32 block) into row-major order in
   // LDS, then writes it with 16-byte (fp32) or 8-byte (bf16) stores along
-  // rows.  The row pitch EP = TN + 8 floats puts the two lane halves, which
-  // write rows 4 apart, into different bank halves.
-  static constexpr int EP = TN + 8;
-  static_assert(NW * 32 * EP * 4 <= LDS_BYTES, "epilogue staging");
+  // rows (row pitch EP).
 
   struct Out {
     char* ptr;
