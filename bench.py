@@ -47,10 +47,17 @@ class Timer:
         self.runtime = runtime
         self.start, self.end = runtime.event(), runtime.event()
 
-    def time(self, fn, steps, warmup):
+    def time(self, fn, steps, warmup, warm_seconds=0.3):
+        # W warm-up steps, then more untimed steps until the GPU has been busy
+        # for warm_seconds (clocks settle; the first launches run slower)
         for _ in range(warmup):
             fn()
         self.runtime.synchronize()
+        begin = time.perf_counter()
+        while time.perf_counter() - begin < warm_seconds:
+            for _ in range(4):
+                fn()
+            self.runtime.synchronize()
         wall = time.perf_counter()
         self.runtime.record(self.start)
         for _ in range(steps):

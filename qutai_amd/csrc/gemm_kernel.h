@@ -422,15 +422,17 @@ struct GemmKernel {
         const int next = (kt + STAGES - 1) % STAGES;
         const int64_t k_next = (int64_t)(kt + STAGES - 1) * BK;
         if constexpr (!F32) {
-          // one slice of the next stage's copies per k-step, between the
-          // fragment reads and the MFMAs of that step
-          constexpr int S = BK / 16, PER = (L + S - 1) / S;
+          // the next stage's copies in two slices, issued in the first two
+          // k-steps between the fragment reads and the MFMAs (all copies at
+          // once stall the issuing wave; spreading them over every k-step
+          // leaves the last slice too little time)
+          constexpr int S = BK / 16, PER = S >= 2 ? (L + 1) / 2 : L;
           const T* sb = sa + BM * BK;
           bf16x8 fa[2][FM], fb[2][FN];
           frags16(sa, sb, fa[0], fb[0], wm, wn, 0, lane);
 #pragma unroll
           for (int s = 0; s < S; s++) {
-            if (more) issue_range(next, k_next, s * PER, (s + 1) * PER < L ? (s + 1) * PER : L);
+            if (more && s * PER < L) issue_range(next, k_next, s * PER, (s + 1) * PER < L ? (s + 1) * PER : L);
             if (s + 1 < S) frags16(sa, sb, fa[(s + 1) & 1], fb[(s + 1) & 1], wm, wn, s + 1, lane);
             mfma16(fa[s & 1], fb[s & 1], acc);
           }
