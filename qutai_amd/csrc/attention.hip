@@ -27,6 +27,7 @@
 #include "common.h"
 #include "qutai_amd.h"
 
+#include <cstdlib>
 #include <initializer_list>
 
 using namespace qa;
@@ -89,13 +90,13 @@ __device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
-// One 64-key block for the wave's QB query blocks.  MASK: some key of the
+// One 64-key block for the wave's NQB query blocks.  MASK: some key of the
 // block is past T or (causal) after a query; lim[qb] is then the number of
 // leading keys of the block the lane's query may see, minus 4 * half.
-template <bool MASK>
-__device__ __forceinline__ void attend_block(const bf16_t* sk, const bf16_t* sv, const bf16x8 (&qf)[QB][4],
-                                             f32x16 (&o)[QB][2], float (&m)[QB], float (&l)[QB],
-                                             const int (&lim)[QB], float c, int lane) {
+template <int NQB, bool MASK>
+__device__ __forceinline__ void attend_block(const bf16_t* sk, const bf16_t* sv, const bf16x8 (&qf)[NQB][4],
+                                             f32x16 (&o)[NQB][2], float (&m)[NQB], float (&l)[NQB],
+                                             const int (&lim)[NQB], float c, int lane) {
   const int half = lane >> 5, col = lane & 31;
   // K fragments (A operand): key row 32 mb + col, d = 16 s + 8 half + [0, 8)
   bf16x8 kf[2][4];
@@ -108,9 +109,9 @@ __device__ __forceinline__ void attend_block(const bf16_t* sk, const bf16_t* sv,
     }
   // S^T blocks for every query block first, so the value products of one
   // query block overlap the exponentials of the next.
-  f32x16 sc[QB][2];
+  f32x16 sc[NQB][2];
 #pragma unroll
-  for (int qb = 0; qb < QB; qb++)
+  for (int qb = 0; qb < NQB; qb++)
 #pragma unroll
     for (int mb = 0; mb < 2; mb++) {
       f32x16 acc = {};
@@ -146,9 +147,9 @@ __device__ __forceinline__ void attend_block(const bf16_t* sk, const bf16_t* sv,
   // blocks; the probabilities exp2(s c - m) then stay below 256 and the
   // result is the same softmax (the normaliser uses the same m).
   bool grow_any = false;
-  float m_new[QB];
+  float m_new[NQB];
 #pragma unroll
-  for (int qb = 0; qb < QB; qb++) {
+  for (int qb = 0; qb < NQB; qb++) {
     // key of element e in block mb: 32 mb + 8 (e / 4) + 4 half + e % 4
     if (MASK) {
 #pragma unroll
@@ -169,7 +170,7 @@ __device__ __forceinline__ void attend_block(const bf16_t* sk, const bf16_t* sv,
   }
   if (__builtin_amdgcn_ballot_w64(grow_any)) {
 #pragma unroll
-    for (int qb = 0; qb < QB; qb++) {
+    for (int qb = 0; qb < NQB; qb++) {
       // alpha = 1 for lanes whose m stays; a query that has seen no valid key
       // keeps m = -inf and l = 0, O = 0
       const float alpha = m_new[qb] == m[qb] ? 1.f : __builtin_amdgcn_exp2f(m[qb] - m_new[qb]);
@@ -182,7 +183,7 @@ __device__ __forceinline__ void attend_block(const bf16_t* sk, const bf16_t* sv,
     }
   }
 #pragma unroll
-  for (int qb = 0; qb < QB; qb++) {
+  for (int qb = 0; qb < NQB; qb++) {
     // exp2(-inf - 0) = 0 for a query with no visible key yet
     const float ref = m[qb] == -INFINITY ? 0.f : m[qb];
     float sum = 0.f;
@@ -214,7 +215,9 @@ __device__ __forceinline__ void attend_block(const bf16_t* sk, const bf16_t* sv,
   }
 }
 
-__global__ void __launch_bounds__(WAVES * 64) attention_fwd_d64(AttnArgs p) {
+template <int NW, int NQB>
+__global__ void __launch_bounds__(NW * 64) attention_fwd_d64(AttnArgs p) {
+  constexpr int QW = 32 * NQB, QPB = NW * QW, CP = 8 / NW;  // copies per wave and tile
   __shared__ __attribute__((aligned(16))) bf16_t lds[2][2][TILE];  // [stage][K,V][64 x 64]
   const int tid = threadIdx.x, lane = tid & 63, wave = uniform32(tid >> 6);
   const int T = (int)p.time;
@@ -235,11 +238,11 @@ __global__ void __launch_bounds__(WAVES * 64) attention_fwd_d64(AttnArgs p) {
 
   // ---- Q fragments (B operand of S^T = K Q^T): lane holds query col of its
   // block, d = 16 s + 8 half + [0, 8).
-  bf16x8 qf[QB][4];
+  bf16x8 qf[NQB][4];
   {
     auto rq = rsrc(Q, ((int64_t)T - 1) * p.qt * 2 + D * 2);
 #pragma unroll
-    for (int qb = 0; qb < QB; qb++) {
+    for (int qb = 0; qb < NQB; qb++) {
       const int t = q0 + qb * 32 + col;
 #pragma unroll
       for (int s = 0; s < 4; s++) {
@@ -252,11 +255,11 @@ __global__ void __launch_bounds__(WAVES * 64) attention_fwd_d64(AttnArgs p) {
   // ---- K/V stage copies: 512 chunks of 16 bytes each; wave w, instruction
   // j fills physical chunks (j * 4 + w) * 64 + lane of K, then of V.  Rows
   // past T read as zeros (offset >= 2^31 is out of the descriptor's range).
-  uint32_t ko[2], vo[2];
-  int kr[2];
+  uint32_t ko[CP], vo[CP];
+  int kr[CP];
 #pragma unroll
-  for (int j = 0; j < 2; j++) {
-    int qidx = (j * WAVES + wave) * 64 + lane;
+  for (int j = 0; j < CP; j++) {
+    int qidx = (j * NW + wave) * 64 + lane;
     int r = qidx >> 3, pc = qidx & 7;
     kr[j] = r;
     ko[j] = (uint32_t)((r * p.kt + ((pc ^ swz_row8(r)) * 8)) * 2);
@@ -267,19 +270,19 @@ __global__ void __launch_bounds__(WAVES * 64) attention_fwd_d64(AttnArgs p) {
     const u32x4 rk = lds_rsrc(K + (int64_t)kv0 * p.kt, (int64_t)KB * p.kt * 2);
     const u32x4 rv = lds_rsrc(V + (int64_t)kv0 * p.kt, (int64_t)KB * p.kt * 2);
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
+    for (int j = 0; j < CP; j++) {
       uint32_t oob = (uint32_t)(kv0 + kr[j] >= T) << 31;
-      char* dk = reinterpret_cast<char*>(&lds[stage][0][0]) + (j * WAVES + wave) * 1024;
-      char* dv = reinterpret_cast<char*>(&lds[stage][1][0]) + (j * WAVES + wave) * 1024;
+      char* dk = reinterpret_cast<char*>(&lds[stage][0][0]) + (j * NW + wave) * 1024;
+      char* dv = reinterpret_cast<char*>(&lds[stage][1][0]) + (j * NW + wave) * 1024;
       lds_load16(rk, dk, ko[j] + oob);
       lds_load16(rv, dv, vo[j] + oob);
     }
   };
 
-  f32x16 o[QB][2];  // O^T blocks: d block db (rows d = 32 db + ...), columns = queries
-  float m[QB], l[QB];
+  f32x16 o[NQB][2];  // O^T blocks: d block db (rows d = 32 db + ...), columns = queries
+  float m[NQB], l[NQB];
 #pragma unroll
-  for (int qb = 0; qb < QB; qb++) {
+  for (int qb = 0; qb < NQB; qb++) {
     m[qb] = -INFINITY;
     l[qb] = 0.f;
 #pragma unroll
@@ -299,23 +302,23 @@ __global__ void __launch_bounds__(WAVES * 64) attention_fwd_d64(AttnArgs p) {
     const bf16_t* sk = &lds[cur][0][0];
     const bf16_t* sv = &lds[cur][1][0];
     if (kv0 + KB <= last_key_full) {
-      const int lim[QB] = {};
-      attend_block<false>(sk, sv, qf, o, m, l, lim, p.scale_log2, lane);
+      const int lim[NQB] = {};
+      attend_block<NQB, false>(sk, sv, qf, o, m, l, lim, p.scale_log2, lane);
     } else if (kv0 < q0 + QW || !p.causal) {
-      int lim[QB];
+      int lim[NQB];
 #pragma unroll
-      for (int qb = 0; qb < QB; qb++) {
+      for (int qb = 0; qb < NQB; qb++) {
         const int tq = q0 + qb * 32 + col;
         lim[qb] = min(T - kv0, p.causal ? tq - kv0 + 1 : KB) - 4 * half;
       }
-      attend_block<true>(sk, sv, qf, o, m, l, lim, p.scale_log2, lane);
+      attend_block<NQB, true>(sk, sv, qf, o, m, l, lim, p.scale_log2, lane);
     }
     // else (causal): every key of the block is after every query of this wave
   }
 
   // ---- normalise and store: lane holds query col, d = 32 db + 8 (e/4) + 4 half + e%4
 #pragma unroll
-  for (int qb = 0; qb < QB; qb++) {
+  for (int qb = 0; qb < NQB; qb++) {
     const int t = q0 + qb * 32 + col;
     const float total = pair_sum(l[qb]);
     const float inv = total > 0.f ? 1.f / total : 0.f;
@@ -814,9 +817,19 @@ int qutai_amd_attention_fwd(const void* q, const void* k, const void* v, void* o
   a.scale = (float)scale;
   a.scale_log2 = (float)(scale * 1.4426950408889634);
   a.causal = causal ? 1 : 0;
-  int64_t blocks = batch * heads * ((time + QPB - 1) / QPB);
+  // 8 waves of 32 queries (two waves per SIMD hide each other's softmax and
+  // MFMA phases) or 4 waves of 64 queries; QUTAI_AMD_ATTN_WAVES=4|8 overrides
+  static const int waves = [] {
+    const char* v = getenv("QUTAI_AMD_ATTN_WAVES");
+    return v && atoi(v) == 4 ? 4 : 8;
+  }();
+  const int64_t qpb = 256;  // queries per workgroup in both shapes
+  int64_t blocks = batch * heads * ((time + qpb - 1) / qpb);
   if (blocks > 0x7fffffff) return QA_EINVAL;
-  hipLaunchKernelGGL(attention_fwd_d64, dim3((unsigned)blocks), dim3(WAVES * 64), 0, (hipStream_t)stream, a);
+  if (waves == 8)
+    hipLaunchKernelGGL((attention_fwd_d64<8, 1>), dim3((unsigned)blocks), dim3(512), 0, (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL((attention_fwd_d64<4, 2>), dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, a);
   return (int)hipGetLastError();
 }
 
