@@ -36,10 +36,6 @@ namespace {
 
 constexpr int D = 64;          // head dimension
 constexpr int KB = 64;         // keys per block
-constexpr int WAVES = 4;
-constexpr int QW = 64;         // queries per wave (two 32-query blocks)
-constexpr int QB = QW / 32;
-constexpr int QPB = WAVES * QW;  // queries per workgroup
 constexpr int TILE = KB * D;     // elements of one K (or V) stage
 constexpr uint32_t OOB = 0x80000000u;
 
@@ -218,6 +214,7 @@ __device__ __forceinline__ void attend_block(const bf16_t* sk, const bf16_t* sv,
 template <int NW, int NQB>
 __global__ void __launch_bounds__(NW * 64) attention_fwd_d64(AttnArgs p) {
   constexpr int QW = 32 * NQB, QPB = NW * QW, CP = 8 / NW;  // copies per wave and tile
+  static_assert(CP * NW == 8 && QPB == 256, "a tile is 8 copies of 1 KiB; 256 queries per workgroup");
   __shared__ __attribute__((aligned(16))) bf16_t lds[2][2][TILE];  // [stage][K,V][64 x 64]
   const int tid = threadIdx.x, lane = tid & 63, wave = uniform32(tid >> 6);
   const int T = (int)p.time;
@@ -401,24 +398,26 @@ __device__ __forceinline__ bf16x8 tr_frag(const bf16_t* x, int db, int rb, int l
 }
 
 // Stage copy of a [64][64] bf16 tile (rows `stride` elements apart, rows >= rows_left read as zeros)
-// by the 256 threads: two 16-byte chunks per lane, physical chunk (j * 4 + wave) * 64 + lane.
+// by NW waves: 8 / NW 16-byte chunks per lane, physical chunk (j * NW + wave) * 64 + lane.
+template <int NW>
 __device__ __forceinline__ void copy_tile(bf16_t* dst, const bf16_t* src, int64_t stride, int rows_left, int wave,
                                           int lane) {
+  static_assert(8 % NW == 0, "a tile is 8 copies of 1 KiB");
   const u32x4 r = lds_rsrc(src, (int64_t)KB * stride * 2);
 #pragma unroll
-  for (int j = 0; j < 2; j++) {
-    const int qidx = (j * WAVES + wave) * 64 + lane;
+  for (int j = 0; j < 8 / NW; j++) {
+    const int qidx = (j * NW + wave) * 64 + lane;
     const int row = qidx >> 3, pc = qidx & 7;
     const uint32_t off = (uint32_t)((row * stride + ((pc ^ swz_row8(row)) * 8)) * 2) + ((uint32_t)(row >= rows_left) << 31);
-    char* d = reinterpret_cast<char*>(dst) + (j * WAVES + wave) * 1024;
+    char* d = reinterpret_cast<char*>(dst) + (j * NW + wave) * 1024;
     lds_load16(r, d, off);
   }
 }
 
-template <bool MASK>
-__device__ __forceinline__ void dq_block(const bf16_t* sk, const bf16_t* sv, const bf16x8 (&qf)[QB][4],
-                                         const bf16x8 (&gf)[QB][4], const float (&lse2)[QB], const float (&dl)[QB],
-                                         f32x16 (&dqt)[QB][2], const int (&lim)[QB], float c, float scale, int lane) {
+template <int NQB, bool MASK>
+__device__ __forceinline__ void dq_block(const bf16_t* sk, const bf16_t* sv, const bf16x8 (&qf)[NQB][4],
+                                         const bf16x8 (&gf)[NQB][4], const float (&lse2)[NQB], const float (&dl)[NQB],
+                                         f32x16 (&dqt)[NQB][2], const int (&lim)[NQB], float c, float scale, int lane) {
   const int half = lane >> 5, col = lane & 31;
   bf16x8 kf[2][4], vf[2][4];
 #pragma unroll
@@ -436,7 +435,7 @@ __device__ __forceinline__ void dq_block(const bf16_t* sk, const bf16_t* sv, con
 #pragma unroll
       for (int st = 0; st < 2; st++) ktf[db][mb][st] = tr_frag(sk, db, 32 * mb + 16 * st, lane);
 #pragma unroll
-  for (int qb = 0; qb < QB; qb++) {
+  for (int qb = 0; qb < NQB; qb++) {
     bf16x8 dsf[2][2];
 #pragma unroll
     for (int mb = 0; mb < 2; mb++) {
@@ -471,7 +470,10 @@ __device__ __forceinline__ void dq_block(const bf16_t* sk, const bf16_t* sv, con
   }
 }
 
-__global__ void __launch_bounds__(WAVES * 64) attention_bwd_dq_d64(AttnBwdArgs p) {
+template <int NW, int NQB>
+__global__ void __launch_bounds__(NW * 64) attention_bwd_dq_d64(AttnBwdArgs p) {
+  constexpr int QW = 32 * NQB, QPB = NW * QW, CP = 8 / NW;
+  static_assert(CP * NW == 8 && QPB == 256, "a tile is 8 copies of 1 KiB; 256 queries per workgroup");
   __shared__ __attribute__((aligned(16))) bf16_t lds[2][2][TILE];  // [stage][K,V][64 x 64]
   const int tid = threadIdx.x, lane = tid & 63, wave = uniform32(tid >> 6);
   const int T = (int)p.time;
@@ -490,13 +492,13 @@ __global__ void __launch_bounds__(WAVES * 64) attention_bwd_dq_d64(AttnBwdArgs p
 
   // Q and dO fragments (B operands: lane = query, d = 16 s + 8 half + [0, 8)),
   // delta = dO . O of the lane's query (halves summed across lanes l, l ^ 32)
-  bf16x8 qf[QB][4], gf[QB][4];
-  float lse2[QB], dl[QB];
+  bf16x8 qf[NQB][4], gf[NQB][4];
+  float lse2[NQB], dl[NQB];
   {
     const int64_t bytes = ((int64_t)T - 1) * p.qt * 2 + D * 2;
     auto rq = rsrc(p.q + qbase, bytes), rg = rsrc(p.g + qbase, bytes), ro = rsrc(p.o + qbase, bytes);
 #pragma unroll
-    for (int qb = 0; qb < QB; qb++) {
+    for (int qb = 0; qb < NQB; qb++) {
       const int t = q0 + qb * 32 + col;
       float dot = 0.f;
 #pragma unroll
@@ -519,11 +521,11 @@ __global__ void __launch_bounds__(WAVES * 64) attention_bwd_dq_d64(AttnBwdArgs p
     }
   }
 
-  uint32_t ko[2];
-  int kr[2];
+  uint32_t ko[CP];
+  int kr[CP];
 #pragma unroll
-  for (int j = 0; j < 2; j++) {
-    int qidx = (j * WAVES + wave) * 64 + lane;
+  for (int j = 0; j < CP; j++) {
+    int qidx = (j * NW + wave) * 64 + lane;
     int r = qidx >> 3, pc = qidx & 7;
     kr[j] = r;
     ko[j] = (uint32_t)((r * p.kt + ((pc ^ swz_row8(r)) * 8)) * 2);
@@ -533,18 +535,18 @@ __global__ void __launch_bounds__(WAVES * 64) attention_bwd_dq_d64(AttnBwdArgs p
     const u32x4 rk = lds_rsrc(K + (int64_t)kv0 * p.kt, (int64_t)KB * p.kt * 2);
     const u32x4 rv = lds_rsrc(V + (int64_t)kv0 * p.kt, (int64_t)KB * p.kt * 2);
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
+    for (int j = 0; j < CP; j++) {
       uint32_t oob = (uint32_t)(kv0 + kr[j] >= T) << 31;
-      char* dk = reinterpret_cast<char*>(&lds[stage][0][0]) + (j * WAVES + wave) * 1024;
-      char* dv = reinterpret_cast<char*>(&lds[stage][1][0]) + (j * WAVES + wave) * 1024;
+      char* dk = reinterpret_cast<char*>(&lds[stage][0][0]) + (j * NW + wave) * 1024;
+      char* dv = reinterpret_cast<char*>(&lds[stage][1][0]) + (j * NW + wave) * 1024;
       lds_load16(rk, dk, ko[j] + oob);
       lds_load16(rv, dv, ko[j] + oob);
     }
   };
 
-  f32x16 dqt[QB][2];
+  f32x16 dqt[NQB][2];
 #pragma unroll
-  for (int qb = 0; qb < QB; qb++)
+  for (int qb = 0; qb < NQB; qb++)
 #pragma unroll
     for (int db = 0; db < 2; db++) dqt[qb][db] = f32x16{};
 
@@ -559,21 +561,21 @@ __global__ void __launch_bounds__(WAVES * 64) attention_bwd_dq_d64(AttnBwdArgs p
     const bf16_t* sk = &lds[cur][0][0];
     const bf16_t* sv = &lds[cur][1][0];
     if (kv0 + KB <= last_key_full) {
-      const int lim[QB] = {};
-      dq_block<false>(sk, sv, qf, gf, lse2, dl, dqt, lim, p.c, p.scale, lane);
+      const int lim[NQB] = {};
+      dq_block<NQB, false>(sk, sv, qf, gf, lse2, dl, dqt, lim, p.c, p.scale, lane);
     } else if (kv0 < q0 + QW || !p.causal) {
-      int lim[QB];
+      int lim[NQB];
 #pragma unroll
-      for (int qb = 0; qb < QB; qb++) {
+      for (int qb = 0; qb < NQB; qb++) {
         const int tq = q0 + qb * 32 + col;
         lim[qb] = min(T - kv0, p.causal ? tq - kv0 + 1 : KB) - 4 * half;
       }
-      dq_block<true>(sk, sv, qf, gf, lse2, dl, dqt, lim, p.c, p.scale, lane);
+      dq_block<NQB, true>(sk, sv, qf, gf, lse2, dl, dqt, lim, p.c, p.scale, lane);
     }
   }
 
 #pragma unroll
-  for (int qb = 0; qb < QB; qb++) {
+  for (int qb = 0; qb < NQB; qb++) {
     const int t = q0 + qb * 32 + col;
     if (t < T) {
       bf16_t* out = p.dq + b * p.qb + h * p.qh + (int64_t)t * p.qt;
@@ -590,15 +592,13 @@ __global__ void __launch_bounds__(WAVES * 64) attention_bwd_dq_d64(AttnBwdArgs p
   }
 }
 
-constexpr int KW = 64;               // keys per wave (two blocks of 32)
-constexpr int KPB = WAVES * KW;      // keys per workgroup
 
 // One 64-query block against the wave's 64 keys.  MASK: some query of the
 // block is >= T or (causal) before one of the keys.
-template <bool MASK>
+template <int NKB, bool MASK>
 __device__ __forceinline__ void dkv_block(const bf16_t* sq, const bf16_t* sg, const float* slse, const float* sdl,
-                                          const bf16x8 (&kf)[2][4], const bf16x8 (&vf)[2][4], f32x16 (&dvt)[2][2],
-                                          f32x16 (&dkt)[2][2], int qrel_end, int key_rel, int causal, float c,
+                                          const bf16x8 (&kf)[NKB][4], const bf16x8 (&vf)[NKB][4], f32x16 (&dvt)[2][NKB],
+                                          f32x16 (&dkt)[2][NKB], int qrel_end, int key_rel, int causal, float c,
                                           float scale, int lane) {
   // qrel_end: T - (first query of the block); key_rel: (first key of the
   // wave) - (first query of the block).  Element e of a result holds query
@@ -618,9 +618,9 @@ __device__ __forceinline__ void dkv_block(const bf16_t* sq, const bf16_t* sg, co
       l4[j] = *reinterpret_cast<const f32x4*>(slse + 32 * mq + 8 * j + 4 * half);
       d4[j] = *reinterpret_cast<const f32x4*>(sdl + 32 * mq + 8 * j + 4 * half);
     }
-    bf16x8 pf[2][2], dsf[2][2];
+    bf16x8 pf[NKB][2], dsf[NKB][2];
 #pragma unroll
-    for (int nb = 0; nb < 2; nb++) {
+    for (int nb = 0; nb < NKB; nb++) {
       f32x16 sc = {}, dp = {};
 #pragma unroll
       for (int s = 0; s < 4; s++) {
@@ -655,7 +655,7 @@ __device__ __forceinline__ void dkv_block(const bf16_t* sq, const bf16_t* sg, co
         const bf16x8 got = tr_frag(sg, db, 32 * mq + 16 * st, lane);
         const bf16x8 qt = tr_frag(sq, db, 32 * mq + 16 * st, lane);
 #pragma unroll
-        for (int nb = 0; nb < 2; nb++) {
+        for (int nb = 0; nb < NKB; nb++) {
           dvt[db][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(got, pf[nb][st], dvt[db][nb], 0, 0, 0);
           dkt[db][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qt, dsf[nb][st], dkt[db][nb], 0, 0, 0);
         }
@@ -663,7 +663,10 @@ __device__ __forceinline__ void dkv_block(const bf16_t* sq, const bf16_t* sg, co
   }
 }
 
-__global__ void __launch_bounds__(WAVES * 64) attention_bwd_dkv_d64(AttnBwdArgs p) {
+template <int NW, int NKB>
+__global__ void __launch_bounds__(NW * 64) attention_bwd_dkv_d64(AttnBwdArgs p) {
+  constexpr int KW = 32 * NKB, KPB = NW * KW;  // keys per wave / per workgroup
+  static_assert(8 % NW == 0 && KPB == 256, "copy split; 256 keys per workgroup");
   __shared__ __attribute__((aligned(16))) bf16_t tiles[2][2][TILE];  // [stage][Q, dO][64 x 64]
   __shared__ __attribute__((aligned(16))) float stats[2][2][KB];      // [stage][lse, delta][64]
   const int tid = threadIdx.x, lane = tid & 63, wave = uniform32(tid >> 6);
@@ -681,12 +684,12 @@ __global__ void __launch_bounds__(WAVES * 64) attention_bwd_dkv_d64(AttnBwdArgs 
   const int64_t kbase = b * p.kb + kvh * p.kh;
 
   // K and V of the wave's keys (B operands: lane = key 32 nb + col, d = 16 s + 8 half + [0, 8))
-  bf16x8 kf[2][4], vf[2][4];
+  bf16x8 kf[NKB][4], vf[NKB][4];
   {
     const int64_t bytes = ((int64_t)T - 1) * p.kt * 2 + D * 2;
     auto rk = rsrc(p.k + kbase, bytes), rv = rsrc(p.v + kbase, bytes);
 #pragma unroll
-    for (int nb = 0; nb < 2; nb++) {
+    for (int nb = 0; nb < NKB; nb++) {
       const int key = kw + 32 * nb + col;
 #pragma unroll
       for (int s = 0; s < 4; s++) {
@@ -704,8 +707,8 @@ __global__ void __launch_bounds__(WAVES * 64) attention_bwd_dkv_d64(AttnBwdArgs 
     const int g = it / nq, qs = qs0 + (it % nq) * KB;
     const int h = kvh * group + g;
     const int64_t base = b * p.qb + h * p.qh + (int64_t)qs * p.qt;
-    copy_tile(&tiles[stage][0][0], p.q + base, p.qt, T - qs, wave, lane);
-    copy_tile(&tiles[stage][1][0], p.g + base, p.qt, T - qs, wave, lane);
+    copy_tile<NW>(&tiles[stage][0][0], p.q + base, p.qt, T - qs, wave, lane);
+    copy_tile<NW>(&tiles[stage][1][0], p.g + base, p.qt, T - qs, wave, lane);
     if (wave < 2) {  // wave 0: lse of the 64 queries, wave 1: delta
       const float* src = wave == 0 ? p.lse : p.delta;
       const u32x4 r = lds_rsrc(src + b * p.lb + h * p.lh, ((int64_t)T - 1) * p.lt * 4 + 4);
@@ -714,11 +717,11 @@ __global__ void __launch_bounds__(WAVES * 64) attention_bwd_dkv_d64(AttnBwdArgs 
     }
   };
 
-  f32x16 dvt[2][2], dkt[2][2];
+  f32x16 dvt[2][NKB], dkt[2][NKB];
 #pragma unroll
   for (int db = 0; db < 2; db++)
 #pragma unroll
-    for (int nb = 0; nb < 2; nb++) dvt[db][nb] = dkt[db][nb] = f32x16{};
+    for (int nb = 0; nb < NKB; nb++) dvt[db][nb] = dkt[db][nb] = f32x16{};
 
   if (iterations > 0) issue(0, 0);
   for (int it = 0; it < iterations; it++) {
@@ -731,16 +734,16 @@ __global__ void __launch_bounds__(WAVES * 64) attention_bwd_dkv_d64(AttnBwdArgs 
     if (p.causal && qs + KB - 1 < kw) continue;
     const bool full = qs + KB <= T && (!p.causal || qs >= kw + KW - 1);
     if (full)
-      dkv_block<false>(&tiles[cur][0][0], &tiles[cur][1][0], &stats[cur][0][0], &stats[cur][1][0], kf, vf, dvt, dkt,
+      dkv_block<NKB, false>(&tiles[cur][0][0], &tiles[cur][1][0], &stats[cur][0][0], &stats[cur][1][0], kf, vf, dvt, dkt,
                        T - qs, kw - qs, p.causal, p.c, p.scale, lane);
     else
-      dkv_block<true>(&tiles[cur][0][0], &tiles[cur][1][0], &stats[cur][0][0], &stats[cur][1][0], kf, vf, dvt, dkt,
+      dkv_block<NKB, true>(&tiles[cur][0][0], &tiles[cur][1][0], &stats[cur][0][0], &stats[cur][1][0], kf, vf, dvt, dkt,
                       T - qs, kw - qs, p.causal, p.c, p.scale, lane);
   }
 
   // dK^T / dV^T: lane = key 32 nb + col, rows d = 32 db + 8 (e / 4) + 4 half + e % 4
 #pragma unroll
-  for (int nb = 0; nb < 2; nb++) {
+  for (int nb = 0; nb < NKB; nb++) {
     const int key = kw + 32 * nb + col;
     if (key < T) {
       bf16_t* ok = p.dk + kbase + (int64_t)key * p.kt;
@@ -791,6 +794,17 @@ int set_layout(Args& a, int64_t batch, int64_t heads, int64_t kv_heads, int64_t 
   return QA_OK;
 }
 
+// Workgroup shape of every attention kernel: 8 waves (two per SIMD, so one
+// wave's softmax overlaps the other's MFMAs) of 32 queries or keys, or 4
+// waves of 64; QUTAI_AMD_ATTN_WAVES=4|8 overrides the default 8 (tuning).
+int attention_waves() {
+  static const int waves = [] {
+    const char* v = getenv("QUTAI_AMD_ATTN_WAVES");
+    return v && atoi(v) == 4 ? 4 : 8;
+  }();
+  return waves;
+}
+
 bool aligned16(std::initializer_list<const void*> ptrs) {
   for (const void* ptr : ptrs)
     if (!ptr || (uintptr_t)ptr % 16) return false;
@@ -817,16 +831,10 @@ int qutai_amd_attention_fwd(const void* q, const void* k, const void* v, void* o
   a.scale = (float)scale;
   a.scale_log2 = (float)(scale * 1.4426950408889634);
   a.causal = causal ? 1 : 0;
-  // 8 waves of 32 queries (two waves per SIMD hide each other's softmax and
-  // MFMA phases) or 4 waves of 64 queries; QUTAI_AMD_ATTN_WAVES=4|8 overrides
-  static const int waves = [] {
-    const char* v = getenv("QUTAI_AMD_ATTN_WAVES");
-    return v && atoi(v) == 4 ? 4 : 8;
-  }();
   const int64_t qpb = 256;  // queries per workgroup in both shapes
   int64_t blocks = batch * heads * ((time + qpb - 1) / qpb);
   if (blocks > 0x7fffffff) return QA_EINVAL;
-  if (waves == 8)
+  if (attention_waves() == 8)
     hipLaunchKernelGGL((attention_fwd_d64<8, 1>), dim3((unsigned)blocks), dim3(512), 0, (hipStream_t)stream, a);
   else
     hipLaunchKernelGGL((attention_fwd_d64<4, 2>), dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, a);
@@ -855,14 +863,21 @@ int qutai_amd_attention_bwd(const void* grad, const void* q, const void* k, cons
   a.scale = (float)scale;
   a.c = (float)(scale * 1.4426950408889634);
   a.causal = causal ? 1 : 0;
-  const int64_t blocks_q = batch * heads * ((time + QPB - 1) / QPB);
-  const int64_t blocks_k = batch * kv_heads * ((time + KPB - 1) / KPB);
+  // 256 queries (dq) / 256 keys (dk, dv) per workgroup in both shapes
+  const int64_t blocks_q = batch * heads * ((time + 255) / 256);
+  const int64_t blocks_k = batch * kv_heads * ((time + 255) / 256);
   if (blocks_q > 0x7fffffff || blocks_k > 0x7fffffff) return QA_EINVAL;
   // dq first: it writes delta, which the dkv kernel reads
-  hipLaunchKernelGGL(attention_bwd_dq_d64, dim3((unsigned)blocks_q), dim3(WAVES * 64), 0, (hipStream_t)stream, a);
+  if (attention_waves() == 8)
+    hipLaunchKernelGGL((attention_bwd_dq_d64<8, 1>), dim3((unsigned)blocks_q), dim3(512), 0, (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL((attention_bwd_dq_d64<4, 2>), dim3((unsigned)blocks_q), dim3(256), 0, (hipStream_t)stream, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
-  hipLaunchKernelGGL(attention_bwd_dkv_d64, dim3((unsigned)blocks_k), dim3(WAVES * 64), 0, (hipStream_t)stream, a);
+  if (attention_waves() == 8)
+    hipLaunchKernelGGL((attention_bwd_dkv_d64<8, 1>), dim3((unsigned)blocks_k), dim3(512), 0, (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL((attention_bwd_dkv_d64<4, 2>), dim3((unsigned)blocks_k), dim3(256), 0, (hipStream_t)stream, a);
   return (int)hipGetLastError();
 }
 
