@@ -174,24 +174,27 @@ int qutai_amd_combine(const void* expert_out, const float* weights, const int64_
                       const int64_t* locations, const int64_t* offsets, void* y, int64_t rows, int64_t width,
                       int64_t top_k, int dtype, void* stream);
 
-/* Fused attention forward, head dimension 64, bf16 storage, fp32 math:
+/* Attention forward, fp32 math:
  *   out = softmax(scale * Q K^T [+ causal mask]) V  per (batch, head),
- * without materialising the time x time scores.  layout 0: q/k/v/out are
- * [batch][heads][time][64] (the nn layout); layout 1: [batch][time][heads][64]
- * (the lm layout, head-interleaved).  kv_heads divides heads (grouped-query
+ * without materialising the time x time scores.  dtype QA_BF16 or QA_F32 for
+ * q, k, v and out; head dimension `dim` <= 256.  bf16 with dim = 64 runs the
+ * fused MFMA kernel (16-byte aligned pointers required); every other case the
+ * one-wave-per-row kernel of the reference's general path.  layout 0: q/k/v/out
+ * are [batch][heads][time][dim] (the nn layout); layout 1:
+ * [batch][time][heads][dim] (the lm layout, head-interleaved).  kv_heads divides heads (grouped-query
  * attention: head h reads kv head h / (heads / kv_heads)).  lse (optional,
  * fp32) receives the natural-log sum of exponentials, laid out like q without
  * the last axis: [batch][heads][time] (layout 0), [batch][time][heads]
  * (layout 1, the reference's lse layout).  The normaliser sums fp32
  * probabilities; the value product takes them rounded to bf16, as in the
- * reference kernel.  Replaces the score/value products of
- * `lm_attention_bf16_d64` (src/qutai/backends/cuda/lm.cu:91-157, driven by
+ * reference kernel.  Replaces `lm_attention_bf16_d64` and the general
+ * `lm_attention` (src/qutai/backends/cuda/lm.cu:91-157, :65-87, driven by
  * `cuda_lm.attention`, src/qutai/backends/cuda_lm.py:229-252) and the
  * S = Q K^T / softmax / P V sequence of nn attention
  * (src/qutai/nn/layers.py:334-354). */
 int qutai_amd_attention_fwd(const void* q, const void* k, const void* v, void* out, float* lse, int64_t batch,
-                            int64_t heads, int64_t kv_heads, int64_t time, int64_t dim, int layout, double scale,
-                            int causal, void* stream);
+                            int64_t heads, int64_t kv_heads, int64_t time, int64_t dim, int dtype, int layout,
+                            double scale, int causal, void* stream);
 
 /* Fused attention backward for the forward above (same layouts, scale and
  * causal flag): from dO (grad), q, k, v, the forward's bf16 output `out` and
@@ -200,15 +203,17 @@ int qutai_amd_attention_fwd(const void* q, const void* k, const void* v, void* o
  *   P = exp(scale q k^T - lse), dS = P (dO v^T - delta) scale,
  *   dq = dS k, dk = dS^T q (summed over the heads sharing a kv head),
  *   dv = P^T dO.
- * Deterministic (no atomics).  Replaces `cuda_lm.attention_backward`
+ * Same dtype / dim / path rules as the forward.  Deterministic (no atomics).
+ * Replaces `cuda_lm.attention_backward`
  * (src/qutai/backends/cuda_lm.py:278-365) with its kernels
- * lm_attention_delta / lm_attention_bf16_dq / lm_attention_bf16_dkv
- * (src/qutai/backends/cuda/lm.cu:159-295); semantics of
+ * lm_attention_delta / lm_attention_bf16_dq / lm_attention_bf16_dkv /
+ * lm_attention_backward_q / _kv (src/qutai/backends/cuda/lm.cu:159-343);
+ * semantics of
  * cpu_lm.attention_backward (src/qutai/backends/cpu_lm.py:176-201). */
 int qutai_amd_attention_bwd(const void* grad, const void* q, const void* k, const void* v, const void* out,
                             const float* lse, void* dq, void* dk, void* dv, float* delta, int64_t batch,
-                            int64_t heads, int64_t kv_heads, int64_t time, int64_t dim, int layout, double scale,
-                            int causal, void* stream);
+                            int64_t heads, int64_t kv_heads, int64_t time, int64_t dim, int dtype, int layout,
+                            double scale, int causal, void* stream);
 
 #ifdef __cplusplus
 }

@@ -188,37 +188,41 @@ def moe_experts_forward(x, route, w_gate, w_up, w_down, width, hidden):
 
 
 def _check_attention(q, k, v, batch, time, heads, kv_heads, dim):
-    if q.dtype != "bfloat16" or k.dtype != "bfloat16" or v.dtype != "bfloat16":
-        raise ValueError("fused attention takes bfloat16 q, k, v")
-    if dim != 64 or kv_heads <= 0 or heads % kv_heads:
-        raise ValueError("fused attention needs head dimension 64 and heads divisible by kv_heads")
+    if len({q.dtype, k.dtype, v.dtype}) != 1 or q.dtype not in ("bfloat16", "float32"):
+        raise ValueError("attention takes q, k, v of one dtype, bfloat16 or float32")
+    if not 0 < dim <= 256 or kv_heads <= 0 or heads % kv_heads:
+        raise ValueError("attention needs 0 < head dimension <= 256 and heads divisible by kv_heads")
     if q.size != batch * time * heads * dim or k.size != batch * time * kv_heads * dim or v.size != k.size:
         raise ValueError("q/k/v sizes do not match (batch, time, heads, dim)")
 
 
 def attention(q, k, v, batch, time, heads, kv_heads, dim, *, causal=True, layout=1, scale=None):
-    """Fused attention forward (cuda_lm.attention, src/qutai/backends/cuda_lm.py:229-252):
-    (out, lse) for bf16 q/k/v with head dimension 64; layout 1 is the lm
-    layout [batch][time][heads][dim], layout 0 the nn layout
-    [batch][heads][time][dim].  The score matrix is never stored."""
+    """Attention forward (cuda_lm.attention, src/qutai/backends/cuda_lm.py:229-275):
+    (out, lse float32).  bf16 q/k/v with head dimension 64 run the fused MFMA
+    kernel; other head dimensions (<= 256) and float32 storage run the
+    one-wave-per-row kernel, as the reference falls back to its warp kernel.
+    layout 1 is the lm layout [batch][time][heads][dim], layout 0 the nn
+    layout [batch][heads][time][dim].  The score matrix is never stored."""
     _check_attention(q, k, v, batch, time, heads, kv_heads, dim)
-    out = AMDStorage(q.size, "bfloat16")
+    out = AMDStorage(q.size, q.dtype)
     lse = AMDStorage(batch * heads * time, "float32")
     scale = dim ** -0.5 if scale is None else scale
     if q.size:
         out.runtime.call("qutai_amd_attention_fwd", q.ptr, k.ptr, v.ptr, out.ptr, lse.ptr, batch, heads, kv_heads,
-                         time, dim, layout, float(scale), int(bool(causal)), mfma=True)
+                         time, dim, code(q.dtype), layout, float(scale), int(bool(causal)),
+                         mfma=q.dtype == "bfloat16" and dim == 64)
     return out, lse
 
 
 def attention_backward(gradient, q, k, v, out, lse, batch, time, heads, kv_heads, dim, *, causal=True, layout=1,
                        scale=None):
     """(dq, dk, dv) of ``attention`` (cuda_lm.attention_backward,
-    src/qutai/backends/cuda_lm.py:278-365): bf16 activations and gradient,
-    fp32 lse from the forward; deterministic."""
+    src/qutai/backends/cuda_lm.py:278-365): activations and gradient of one
+    dtype, float32 lse from the forward (the reference's ValueError rule,
+    cuda_lm.py:279-282); deterministic."""
     _check_attention(q, k, v, batch, time, heads, kv_heads, dim)
     if gradient.dtype != q.dtype or out.dtype != q.dtype or lse.dtype != "float32":
-        raise ValueError("attention backward needs bf16 gradient/out and the forward's float32 lse")
+        raise ValueError("attention backward needs gradient/out of the activations' dtype and a float32 lse")
     if gradient.size != q.size or out.size != q.size or lse.size != batch * time * heads:
         raise ValueError("gradient/out/lse sizes do not match (batch, time, heads, dim)")
     dq, dk, dv = AMDStorage(q.size, q.dtype), AMDStorage(k.size, k.dtype), AMDStorage(v.size, v.dtype)
@@ -226,6 +230,6 @@ def attention_backward(gradient, q, k, v, out, lse, batch, time, heads, kv_heads
     scale = dim ** -0.5 if scale is None else scale
     if q.size:
         dq.runtime.call("qutai_amd_attention_bwd", gradient.ptr, q.ptr, k.ptr, v.ptr, out.ptr, lse.ptr, dq.ptr, dk.ptr,
-                        dv.ptr, delta.ptr, batch, heads, kv_heads, time, dim, layout, float(scale),
-                        int(bool(causal)), mfma=True)
+                        dv.ptr, delta.ptr, batch, heads, kv_heads, time, dim, code(q.dtype), layout, float(scale),
+                        int(bool(causal)), mfma=q.dtype == "bfloat16" and dim == 64)
     return dq, dk, dv

@@ -764,6 +764,210 @@ __global__ void __launch_bounds__(NW * 64) attention_bwd_dkv_d64(AttnBwdArgs p) 
   }
 }
 
+
+// ============================================================================
+// Generic path: any head dimension up to 256, fp32 or bf16 storage, fp32
+// math (the reference's warp kernels lm_attention / lm_attention_delta /
+// lm_attention_backward_q / _kv, src/qutai/backends/cuda/lm.cu:65-87 and
+// :289-343, used by cuda_lm for everything but bf16 with D = 64).  One wave
+// per query row (forward, dq) or key row (dk, dv); lane l owns dimensions
+// l, l + 64, l + 128, l + 192; dot products are wave-wide sums.
+// ============================================================================
+
+struct AttnGenArgs {
+  const void* g;
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* o;
+  float* lse;
+  float* delta;
+  void* dq;  // forward: the output
+  void* dk;
+  void* dv;
+  int64_t batch, heads, kv_heads, time, dim;
+  int64_t qb, qh, qt, kb, kh, kt, lb, lh, lt;
+  float scale;
+  int causal;
+};
+
+template <class T> __device__ __forceinline__ float ld(const void* p, int64_t i);
+template <> __device__ __forceinline__ float ld<float>(const void* p, int64_t i) { return ((const float*)p)[i]; }
+template <> __device__ __forceinline__ float ld<bf16_t>(const void* p, int64_t i) {
+  return bf16_to_f32(((const bf16_t*)p)[i]);
+}
+template <class T> __device__ __forceinline__ void st(void* p, int64_t i, float x);
+template <> __device__ __forceinline__ void st<float>(void* p, int64_t i, float x) { ((float*)p)[i] = x; }
+template <> __device__ __forceinline__ void st<bf16_t>(void* p, int64_t i, float x) {
+  ((bf16_t*)p)[i] = f32_to_bf16(x);
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int off = 32; off; off >>= 1) x += __shfl_xor(x, off);
+  return x;
+}
+
+constexpr int GEN_WAVES = 4;  // rows per workgroup
+
+// row -> (b, h, t) and its element offset in a q-shaped array
+__device__ __forceinline__ void gen_row(const AttnGenArgs& p, int64_t row, int64_t heads, int64_t& b, int64_t& h,
+                                        int64_t& t) {
+  t = row % p.time;
+  h = (row / p.time) % heads;
+  b = row / (p.time * heads);
+}
+
+template <class T>
+__global__ void __launch_bounds__(GEN_WAVES * 64) attention_fwd_rows(AttnGenArgs p) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * GEN_WAVES + (threadIdx.x >> 6);
+  if (row >= p.batch * p.heads * p.time) return;  // whole wave
+  int64_t b, h, t;
+  gen_row(p, row, p.heads, b, h, t);
+  const int64_t kvh = h / (p.heads / p.kv_heads);
+  const int64_t qi = b * p.qb + h * p.qh + t * p.qt, kbase = b * p.kb + kvh * p.kh;
+  const int D = (int)p.dim;
+  float qv[4], acc[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int d = lane + 64 * j;
+    qv[j] = d < D ? ld<T>(p.q, qi + d) : 0.f;
+    acc[j] = 0.f;
+  }
+  float m = -INFINITY, l = 0.f;
+  const int64_t end = p.causal ? t + 1 : p.time;
+  for (int64_t s = 0; s < end; s++) {
+    const int64_t ki = kbase + s * p.kt;
+    float dot = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int d = lane + 64 * j;
+      if (d < D) dot += qv[j] * ld<T>(p.k, ki + d);
+    }
+    const float x = wave_sum(dot) * p.scale;
+    const float m_new = fmaxf(m, x);
+    const float alpha = __expf(m - m_new), pr = __expf(x - m_new);
+    l = l * alpha + pr;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int d = lane + 64 * j;
+      acc[j] = acc[j] * alpha + (d < D ? pr * ld<T>(p.v, ki + d) : 0.f);
+    }
+    m = m_new;
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int d = lane + 64 * j;
+    if (d < D) st<T>(p.dq, qi + d, acc[j] * inv);
+  }
+  if (p.lse && lane == 0) p.lse[b * p.lb + h * p.lh + t * p.lt] = m + __logf(l);
+}
+
+template <class T>
+__global__ void __launch_bounds__(GEN_WAVES * 64) attention_bwd_q_rows(AttnGenArgs p) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * GEN_WAVES + (threadIdx.x >> 6);
+  if (row >= p.batch * p.heads * p.time) return;
+  int64_t b, h, t;
+  gen_row(p, row, p.heads, b, h, t);
+  const int64_t kvh = h / (p.heads / p.kv_heads);
+  const int64_t qi = b * p.qb + h * p.qh + t * p.qt, kbase = b * p.kb + kvh * p.kh;
+  const int64_t li = b * p.lb + h * p.lh + t * p.lt;
+  const int D = (int)p.dim;
+  float qv[4], gv[4], acc[4], dl = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int d = lane + 64 * j;
+    qv[j] = d < D ? ld<T>(p.q, qi + d) : 0.f;
+    gv[j] = d < D ? ld<T>(p.g, qi + d) : 0.f;
+    dl += d < D ? gv[j] * ld<T>(p.o, qi + d) : 0.f;
+    acc[j] = 0.f;
+  }
+  dl = wave_sum(dl);
+  if (lane == 0) p.delta[li] = dl;
+  const float lse = p.lse[li];
+  const int64_t end = p.causal ? t + 1 : p.time;
+  for (int64_t s = 0; s < end; s++) {
+    const int64_t ki = kbase + s * p.kt;
+    float dot = 0.f, dp = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int d = lane + 64 * j;
+      if (d < D) {
+        dot += qv[j] * ld<T>(p.k, ki + d);
+        dp += gv[j] * ld<T>(p.v, ki + d);
+      }
+    }
+    const float pr = __expf(wave_sum(dot) * p.scale - lse);
+    const float ds = pr * (wave_sum(dp) - dl) * p.scale;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int d = lane + 64 * j;
+      if (d < D) acc[j] += ds * ld<T>(p.k, ki + d);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int d = lane + 64 * j;
+    if (d < D) st<T>(p.dq, qi + d, acc[j]);
+  }
+}
+
+template <class T>
+__global__ void __launch_bounds__(GEN_WAVES * 64) attention_bwd_kv_rows(AttnGenArgs p) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * GEN_WAVES + (threadIdx.x >> 6);
+  if (row >= p.batch * p.kv_heads * p.time) return;
+  int64_t b, kvh, s;
+  gen_row(p, row, p.kv_heads, b, kvh, s);
+  const int64_t ki = b * p.kb + kvh * p.kh + s * p.kt;
+  const int64_t group = p.heads / p.kv_heads;
+  const int D = (int)p.dim;
+  float kv_[4], vv[4], ak[4], av[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int d = lane + 64 * j;
+    kv_[j] = d < D ? ld<T>(p.k, ki + d) : 0.f;
+    vv[j] = d < D ? ld<T>(p.v, ki + d) : 0.f;
+    ak[j] = av[j] = 0.f;
+  }
+  for (int64_t h = kvh * group; h < (kvh + 1) * group; h++) {
+    for (int64_t t = p.causal ? s : 0; t < p.time; t++) {
+      const int64_t qi = b * p.qb + h * p.qh + t * p.qt;
+      const int64_t li = b * p.lb + h * p.lh + t * p.lt;
+      float dot = 0.f, dp = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int d = lane + 64 * j;
+        if (d < D) {
+          dot += ld<T>(p.q, qi + d) * kv_[j];
+          dp += ld<T>(p.g, qi + d) * vv[j];
+        }
+      }
+      const float pr = __expf(wave_sum(dot) * p.scale - p.lse[li]);
+      const float ds = pr * (wave_sum(dp) - p.delta[li]) * p.scale;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int d = lane + 64 * j;
+        if (d < D) {
+          ak[j] += ds * ld<T>(p.q, qi + d);
+          av[j] += pr * ld<T>(p.g, qi + d);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int d = lane + 64 * j;
+    if (d < D) {
+      st<T>(p.dk, ki + d, ak[j]);
+      st<T>(p.dv, ki + d, av[j]);
+    }
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -774,21 +978,21 @@ namespace {
 
 // element strides of (batch, head, token) for q-shaped, kv-shaped and lse arrays
 template <class Args>
-int set_layout(Args& a, int64_t batch, int64_t heads, int64_t kv_heads, int64_t time, int layout) {
-  if (batch < 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads || time < 0) return QA_EINVAL;
+int set_layout(Args& a, int64_t batch, int64_t heads, int64_t kv_heads, int64_t time, int64_t dim, int layout) {
+  if (batch < 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads || time < 0 || dim <= 0) return QA_EINVAL;
   if (layout != 0 && layout != 1) return QA_EINVAL;
-  if (time > (1 << 30) / (heads > kv_heads ? heads : kv_heads) / D) return QA_EINVAL;  // 32-bit element offsets
+  if (time > (1 << 30) / (heads > kv_heads ? heads : kv_heads) / dim) return QA_EINVAL;  // 32-bit element offsets
   a.batch = batch;
   a.heads = heads;
   a.kv_heads = kv_heads;
   a.time = time;
   if (layout == 0) {  // [batch][heads][time][dim]
-    a.qb = heads * time * D, a.qh = time * D, a.qt = D;
-    a.kb = kv_heads * time * D, a.kh = time * D, a.kt = D;
+    a.qb = heads * time * dim, a.qh = time * dim, a.qt = dim;
+    a.kb = kv_heads * time * dim, a.kh = time * dim, a.kt = dim;
     a.lb = heads * time, a.lh = time, a.lt = 1;
   } else {            // [batch][time][heads][dim] (the lm layout)
-    a.qb = time * heads * D, a.qh = D, a.qt = heads * D;
-    a.kb = time * kv_heads * D, a.kh = D, a.kt = kv_heads * D;
+    a.qb = time * heads * dim, a.qh = dim, a.qt = heads * dim;
+    a.kb = time * kv_heads * dim, a.kh = dim, a.kt = kv_heads * dim;
     a.lb = time * heads, a.lh = 1, a.lt = heads;
   }
   return QA_OK;
@@ -816,68 +1020,133 @@ bool aligned16(std::initializer_list<const void*> ptrs) {
 extern "C" {
 
 int qutai_amd_attention_fwd(const void* q, const void* k, const void* v, void* out, float* lse, int64_t batch,
-                            int64_t heads, int64_t kv_heads, int64_t time, int64_t dim, int layout, double scale,
-                            int causal, void* stream) {
-  AttnArgs a = {};
-  if (dim != D || set_layout(a, batch, heads, kv_heads, time, layout) != QA_OK) return QA_EINVAL;
+                            int64_t heads, int64_t kv_heads, int64_t time, int64_t dim, int dtype, int layout,
+                            double scale, int causal, void* stream) {
   if (!(scale > 0.0) || scale > 1e30) return QA_EINVAL;  // the running max assumes a positive scale
-  if (!aligned16({q, k, v, out})) return QA_EINVAL;
+  if (!q || !k || !v || !out) return QA_EINVAL;
+  if (dtype == BF16 && dim == D) {
+    AttnArgs a = {};
+    if (set_layout(a, batch, heads, kv_heads, time, dim, layout) != QA_OK) return QA_EINVAL;
+    if (!aligned16({q, k, v, out})) return QA_EINVAL;
+    if (batch * time == 0) return QA_OK;
+    a.q = (const bf16_t*)q;
+    a.k = (const bf16_t*)k;
+    a.v = (const bf16_t*)v;
+    a.o = (bf16_t*)out;
+    a.lse = lse;
+    a.scale = (float)scale;
+    a.scale_log2 = (float)(scale * 1.4426950408889634);
+    a.causal = causal ? 1 : 0;
+    const int64_t qpb = 256;  // queries per workgroup in both shapes
+    int64_t blocks = batch * heads * ((time + qpb - 1) / qpb);
+    if (blocks > 0x7fffffff) return QA_EINVAL;
+    if (attention_waves() == 8)
+      hipLaunchKernelGGL((attention_fwd_d64<8, 1>), dim3((unsigned)blocks), dim3(512), 0, (hipStream_t)stream, a);
+    else
+      hipLaunchKernelGGL((attention_fwd_d64<4, 2>), dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, a);
+    return (int)hipGetLastError();
+  }
+  if ((dtype != BF16 && dtype != F32) || dim > 256) return QA_EINVAL;
+  AttnGenArgs a = {};
+  if (set_layout(a, batch, heads, kv_heads, time, dim, layout) != QA_OK) return QA_EINVAL;
   if (batch * time == 0) return QA_OK;
-  a.q = (const bf16_t*)q;
-  a.k = (const bf16_t*)k;
-  a.v = (const bf16_t*)v;
-  a.o = (bf16_t*)out;
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.dq = out;
   a.lse = lse;
+  a.dim = dim;
   a.scale = (float)scale;
-  a.scale_log2 = (float)(scale * 1.4426950408889634);
   a.causal = causal ? 1 : 0;
-  const int64_t qpb = 256;  // queries per workgroup in both shapes
-  int64_t blocks = batch * heads * ((time + qpb - 1) / qpb);
+  const int64_t blocks = (batch * heads * time + GEN_WAVES - 1) / GEN_WAVES;
   if (blocks > 0x7fffffff) return QA_EINVAL;
-  if (attention_waves() == 8)
-    hipLaunchKernelGGL((attention_fwd_d64<8, 1>), dim3((unsigned)blocks), dim3(512), 0, (hipStream_t)stream, a);
+  if (dtype == BF16)
+    hipLaunchKernelGGL(attention_fwd_rows<bf16_t>, dim3((unsigned)blocks), dim3(GEN_WAVES * 64), 0,
+                       (hipStream_t)stream, a);
   else
-    hipLaunchKernelGGL((attention_fwd_d64<4, 2>), dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, a);
+    hipLaunchKernelGGL(attention_fwd_rows<float>, dim3((unsigned)blocks), dim3(GEN_WAVES * 64), 0,
+                       (hipStream_t)stream, a);
   return (int)hipGetLastError();
 }
 
 int qutai_amd_attention_bwd(const void* grad, const void* q, const void* k, const void* v, const void* out,
                             const float* lse, void* dq, void* dk, void* dv, float* delta, int64_t batch, int64_t heads,
-                            int64_t kv_heads, int64_t time, int64_t dim, int layout, double scale, int causal,
-                            void* stream) {
-  AttnBwdArgs a = {};
-  if (dim != D || set_layout(a, batch, heads, kv_heads, time, layout) != QA_OK) return QA_EINVAL;
+                            int64_t kv_heads, int64_t time, int64_t dim, int dtype, int layout, double scale,
+                            int causal, void* stream) {
   if (!(scale > 0.0) || scale > 1e30) return QA_EINVAL;
-  if (!aligned16({grad, q, k, v, out, dq, dk, dv}) || !lse || !delta) return QA_EINVAL;
+  if (!grad || !q || !k || !v || !out || !dq || !dk || !dv || !lse || !delta) return QA_EINVAL;
+  if (dtype == BF16 && dim == D) {
+    AttnBwdArgs a = {};
+    if (set_layout(a, batch, heads, kv_heads, time, dim, layout) != QA_OK) return QA_EINVAL;
+    if (!aligned16({grad, q, k, v, out, dq, dk, dv})) return QA_EINVAL;
+    if (batch * time == 0) return QA_OK;
+    a.g = (const bf16_t*)grad;
+    a.q = (const bf16_t*)q;
+    a.k = (const bf16_t*)k;
+    a.v = (const bf16_t*)v;
+    a.o = (const bf16_t*)out;
+    a.lse = lse;
+    a.delta = delta;
+    a.dq = (bf16_t*)dq;
+    a.dk = (bf16_t*)dk;
+    a.dv = (bf16_t*)dv;
+    a.scale = (float)scale;
+    a.c = (float)(scale * 1.4426950408889634);
+    a.causal = causal ? 1 : 0;
+    // 256 queries (dq) / 256 keys (dk, dv) per workgroup in both shapes
+    const int64_t blocks_q = batch * heads * ((time + 255) / 256);
+    const int64_t blocks_k = batch * kv_heads * ((time + 255) / 256);
+    if (blocks_q > 0x7fffffff || blocks_k > 0x7fffffff) return QA_EINVAL;
+    // dq first: it writes delta, which the dkv kernel reads
+    if (attention_waves() == 8)
+      hipLaunchKernelGGL((attention_bwd_dq_d64<8, 1>), dim3((unsigned)blocks_q), dim3(512), 0, (hipStream_t)stream, a);
+    else
+      hipLaunchKernelGGL((attention_bwd_dq_d64<4, 2>), dim3((unsigned)blocks_q), dim3(256), 0, (hipStream_t)stream, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+    if (attention_waves() == 8)
+      hipLaunchKernelGGL((attention_bwd_dkv_d64<8, 1>), dim3((unsigned)blocks_k), dim3(512), 0, (hipStream_t)stream,
+                         a);
+    else
+      hipLaunchKernelGGL((attention_bwd_dkv_d64<4, 2>), dim3((unsigned)blocks_k), dim3(256), 0, (hipStream_t)stream,
+                         a);
+    return (int)hipGetLastError();
+  }
+  if ((dtype != BF16 && dtype != F32) || dim > 256) return QA_EINVAL;
+  AttnGenArgs a = {};
+  if (set_layout(a, batch, heads, kv_heads, time, dim, layout) != QA_OK) return QA_EINVAL;
   if (batch * time == 0) return QA_OK;
-  a.g = (const bf16_t*)grad;
-  a.q = (const bf16_t*)q;
-  a.k = (const bf16_t*)k;
-  a.v = (const bf16_t*)v;
-  a.o = (const bf16_t*)out;
-  a.lse = lse;
+  a.g = grad;
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = out;
+  a.lse = const_cast<float*>(lse);
   a.delta = delta;
-  a.dq = (bf16_t*)dq;
-  a.dk = (bf16_t*)dk;
-  a.dv = (bf16_t*)dv;
+  a.dq = dq;
+  a.dk = dk;
+  a.dv = dv;
+  a.dim = dim;
   a.scale = (float)scale;
-  a.c = (float)(scale * 1.4426950408889634);
   a.causal = causal ? 1 : 0;
-  // 256 queries (dq) / 256 keys (dk, dv) per workgroup in both shapes
-  const int64_t blocks_q = batch * heads * ((time + 255) / 256);
-  const int64_t blocks_k = batch * kv_heads * ((time + 255) / 256);
+  const int64_t blocks_q = (batch * heads * time + GEN_WAVES - 1) / GEN_WAVES;
+  const int64_t blocks_k = (batch * kv_heads * time + GEN_WAVES - 1) / GEN_WAVES;
   if (blocks_q > 0x7fffffff || blocks_k > 0x7fffffff) return QA_EINVAL;
-  // dq first: it writes delta, which the dkv kernel reads
-  if (attention_waves() == 8)
-    hipLaunchKernelGGL((attention_bwd_dq_d64<8, 1>), dim3((unsigned)blocks_q), dim3(512), 0, (hipStream_t)stream, a);
+  // the q pass writes delta, which the kv pass reads
+  if (dtype == BF16)
+    hipLaunchKernelGGL(attention_bwd_q_rows<bf16_t>, dim3((unsigned)blocks_q), dim3(GEN_WAVES * 64), 0,
+                       (hipStream_t)stream, a);
   else
-    hipLaunchKernelGGL((attention_bwd_dq_d64<4, 2>), dim3((unsigned)blocks_q), dim3(256), 0, (hipStream_t)stream, a);
+    hipLaunchKernelGGL(attention_bwd_q_rows<float>, dim3((unsigned)blocks_q), dim3(GEN_WAVES * 64), 0,
+                       (hipStream_t)stream, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
-  if (attention_waves() == 8)
-    hipLaunchKernelGGL((attention_bwd_dkv_d64<8, 1>), dim3((unsigned)blocks_k), dim3(512), 0, (hipStream_t)stream, a);
+  if (dtype == BF16)
+    hipLaunchKernelGGL(attention_bwd_kv_rows<bf16_t>, dim3((unsigned)blocks_k), dim3(GEN_WAVES * 64), 0,
+                       (hipStream_t)stream, a);
   else
-    hipLaunchKernelGGL((attention_bwd_dkv_d64<4, 2>), dim3((unsigned)blocks_k), dim3(256), 0, (hipStream_t)stream, a);
+    hipLaunchKernelGGL(attention_bwd_kv_rows<float>, dim3((unsigned)blocks_k), dim3(GEN_WAVES * 64), 0,
+                       (hipStream_t)stream, a);
   return (int)hipGetLastError();
 }
 

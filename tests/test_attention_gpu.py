@@ -289,3 +289,87 @@ def test_lm_attention_layer_autograd(lm):
     expected = ora.attention_backward(gs.tolist(), qs.tolist(), ks.tolist(), vs.tolist(), saved.tolist(), lse, *dims)
     for tensor, reference in zip((q, k, v), expected):
         assert ora.rel_frobenius(download(tensor.grad.storage), reference) <= BF16_TOL
+
+
+# ---- general path: any head dimension <= 256, float32 or bfloat16 ------------------------
+
+def test_general_path_reference_dims_bf16_forward_and_backward(lm):
+    # tests/test_lm_bfloat16.py:73-104 as written: dims (2, 5, 4, 2, 8), bf16,
+    # uniform(-0.4, 0.4) from Random(9), gradient uniform(-0.2, 0.2); output
+    # within the bf16 tolerance, lse within 1e-5, gradients against the oracle
+    # fed the saved bf16 output
+    random = Random(9)
+    dims = (2, 5, 4, 2, 8)
+    qv = np.array([random.uniform(-0.4, 0.4) for _ in range(320)], dtype=np.float32)
+    kv = np.array([random.uniform(-0.4, 0.4) for _ in range(160)], dtype=np.float32)
+    vv = np.array([random.uniform(-0.4, 0.4) for _ in range(160)], dtype=np.float32)
+    gv = np.array([random.uniform(-0.2, 0.2) for _ in range(320)], dtype=np.float32)
+    q, k, v, g = (upload(x, "bfloat16") for x in (qv, kv, vv, gv))
+    out, lse = lm.attention(q, k, v, *dims)
+    grads = lm.attention_backward(g, q, k, v, out, lse, *dims)
+    assert (out.dtype, lse.dtype, out.nbytes) == ("bfloat16", "float32", 640)
+    qs, ks, vs, gs = (stored(x, "bfloat16").tolist() for x in (qv, kv, vv, gv))
+    expected, expected_lse = ora.attention(qs, ks, vs, *dims)
+    assert ora.rel_frobenius(download(out), expected) <= BF16_TOL
+    assert np.abs(download(lse) - np.array(expected_lse)).max() <= 1e-5
+    saved = download(out).astype(np.float64).tolist()
+    reference = ora.attention_backward(gs, qs, ks, vs, saved, expected_lse, *dims)
+    for actual, ref in zip(grads, reference):
+        assert actual.dtype == "bfloat16"
+        assert ora.rel_frobenius(download(actual), ref) <= BF16_TOL
+
+
+@pytest.mark.parametrize("dims,dtype,causal,layout", [
+    ((2, 33, 4, 2, 32), "float32", True, 1),
+    ((1, 70, 2, 1, 128), "bfloat16", True, 1),
+    ((2, 40, 2, 2, 256), "float32", False, 0),
+    ((1, 50, 3, 1, 100), "float32", True, 0),
+    ((1, 65, 2, 2, 64), "float32", True, 1),
+])
+def test_general_path_dims_and_dtypes(lm, dims, dtype, causal, layout):
+    batch, time, heads, kv_heads, dim = dims
+    rng = np.random.default_rng(sum(dims))
+    qv, kv, vv = (rng.uniform(-1, 1, n).astype(np.float32) for n in (
+        batch * time * heads * dim, batch * time * kv_heads * dim, batch * time * kv_heads * dim))
+    gv = rng.uniform(-0.5, 0.5, qv.size).astype(np.float32)
+    q, k, v, g = (upload(x, dtype) for x in (qv, kv, vv, gv))
+    out, lse = lm.attention(q, k, v, *dims, causal=causal, layout=layout)
+    assert out.dtype == dtype
+    dq, dk, dv = lm.attention_backward(g, q, k, v, out, lse, *dims, causal=causal, layout=layout)
+    tol = BF16_TOL if dtype == "bfloat16" else 1e-5
+    qs, ks, vs, gs = (stored(x, dtype) for x in (qv, kv, vv, gv))
+    if layout == 1:
+        split = lambda x, n: _lm_heads(x, batch, time, n, dim)  # noqa: E731
+    else:
+        split = lambda x, n: x.reshape(batch, n, time, dim)  # noqa: E731
+    qa, ga = split(qs, heads), split(gs, heads)
+    ka, va = split(ks, kv_heads), split(vs, kv_heads)
+    oa = split(download(out).astype(np.float64), heads)
+    la = (download(lse).reshape(batch, time, heads).transpose(0, 2, 1) if layout == 1
+          else download(lse).reshape(batch, heads, time))
+    dqa, dka, dva = split(download(dq), heads), split(download(dk), kv_heads), split(download(dv), kv_heads)
+    group = heads // kv_heads
+    for b in range(batch):
+        for kh in range(kv_heads):
+            dk_sum, dv_sum = np.zeros((time, dim)), np.zeros((time, dim))
+            for h in range(kh * group, (kh + 1) * group):
+                o_ref, l_ref = ora.attention_np(qa[b, h], ka[b, kh], va[b, kh], causal=causal)
+                assert ora.rel_frobenius(oa[b, h], o_ref) <= tol, ("out", b, h)
+                assert np.abs(la[b, h] - l_ref).max() <= 1e-4, ("lse", b, h)
+                dq_ref, dk_ref, dv_ref = _backward_np(ga[b, h], qa[b, h], ka[b, kh], va[b, kh], oa[b, h], l_ref,
+                                                      causal)
+                assert ora.rel_frobenius(dqa[b, h], dq_ref) <= tol, ("dq", b, h)
+                dk_sum += dk_ref
+                dv_sum += dv_ref
+            assert ora.rel_frobenius(dka[b, kh], dk_sum) <= tol, ("dk", b, kh)
+            assert ora.rel_frobenius(dva[b, kh], dv_sum) <= tol, ("dv", b, kh)
+
+
+def test_general_path_rejects(lm):
+    q = upload(np.zeros(300 * 4, dtype=np.float32), "float32")
+    with pytest.raises(ValueError):
+        lm.attention(q, q, q, 1, 4, 1, 1, 300)  # head dimension above 256
+    b = upload(np.zeros(8 * 4, dtype=np.float32), "bfloat16")
+    f = upload(np.zeros(8 * 4, dtype=np.float32), "float32")
+    with pytest.raises(ValueError):
+        lm.attention(b, f, f, 1, 4, 1, 1, 8)  # mixed dtypes
