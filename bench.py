@@ -200,6 +200,32 @@ def moe_experts(seed=4):
                          "hidden": hidden, "storage": "bfloat16"}
 
 
+def moe_train(seed=4):
+    """Config 5 MoE forward + backward through the SparseMoE layer (routing,
+    gather, grouped gate/up/down, combine; backward: combine backward,
+    grouped data-gradient GEMMs, grouped-K weight-gradient GEMMs, routing
+    backward, router Linear backward)."""
+    from qutai_amd import Tensor
+    from qutai_amd.backends import amd
+    from qutai_amd.lm.layers import SparseMoE
+
+    tokens, width, experts, hidden, top_k = 8192, 2048, 8, 1408, 2
+    rng = np.random.default_rng(seed)
+    layer = SparseMoE(width, hidden, experts, top_k, dtype="bfloat16", seed=seed)
+    x = Tensor(upload(rng.standard_normal(tokens * width), "bfloat16"), shape=(tokens, width), requires_grad=True)
+    g = Tensor(upload(rng.standard_normal(tokens * width), "bfloat16"), shape=(tokens, width))
+
+    def step():
+        for p in (x, *layer.parameters()):
+            p.grad = None
+        y, aux = layer(x)
+        y.backward(g)
+
+    flops = 9 * 2.0 * tokens * top_k * width * hidden
+    return step, flops, {"tokens": tokens, "d_model": width, "experts": experts, "top_k": top_k,
+                         "hidden": hidden, "storage": "bfloat16", "pass": "forward+backward"}
+
+
 WORKLOADS = {
     "gemm_bf16_4096": (lambda: gemm_square("bfloat16"), "bf16"),
     "gemm_fp32_4096": (lambda: gemm_square("float32"), "fp32"),
@@ -211,6 +237,7 @@ WORKLOADS = {
     "attention_fused_backward": (attention_fused_backward, "bf16"),
     "dense_linear_fwd_bwd": (dense_linear, "bf16"),
     "moe_grouped": (moe_experts, "bf16"),
+    "moe_train": (moe_train, "bf16"),
 }
 HEADLINE = "gemm_bf16_4096"
 

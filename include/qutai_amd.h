@@ -169,7 +169,9 @@ int qutai_amd_route_gather(const void* x, const int64_t* order, void* out, int64
  *   expert_out[offsets[indices[row][slot]] + locations[row][slot]]
  * summed in fp32 in slot order with one rounding to dtype.
  * Replaces `lm_pointer_table` + `lm_combine_all`
- * (src/qutai/backends/cuda/lm.cu:400-416, src/qutai/backends/cuda_lm.py:505-541). */
+ * (src/qutai/backends/cuda/lm.cu:400-416, src/qutai/backends/cuda_lm.py:505-541).
+ * weights may be NULL: unit weights, i.e. the sum over a token's slots (the
+ * backward of the one-launch gather). */
 int qutai_amd_combine(const void* expert_out, const float* weights, const int64_t* indices,
                       const int64_t* locations, const int64_t* offsets, void* y, int64_t rows, int64_t width,
                       int64_t top_k, int dtype, void* stream);
@@ -195,6 +197,39 @@ int qutai_amd_combine(const void* expert_out, const float* weights, const int64_
 int qutai_amd_attention_fwd(const void* q, const void* k, const void* v, void* out, float* lse, int64_t batch,
                             int64_t heads, int64_t kv_heads, int64_t time, int64_t dim, int dtype, int layout,
                             double scale, int causal, void* stream);
+
+/* Grouped-K GEMM for the MoE weight gradients: for every group g,
+ *   out[g] (rows x cols) (+)= A_g^T B_g,
+ * where A_g / B_g are the K rows [offsets[g], offsets[g+1]) of a ([K][rows])
+ * and b ([K][cols]) -- the expert-major routed rows.  E.g. dW_down[e] =
+ * dY_e^T act_e.  An empty group writes zeros (or keeps out with accumulate).
+ * dtype QA_BF16 / QA_F32 for a and b, out_dtype QA_F32 / QA_BF16; rows and
+ * cols multiples of 8 (bf16) / 4 (fp32), 16-byte aligned operands.  total_k
+ * = offsets[groups] (only used for tile choice).  Replaces the per-expert
+ * weight-gradient GEMMs of the expert SwiGLU backward (`linear` backward,
+ * src/qutai/lm/layers.py:57-66, run once per expert by SparseMoE,
+ * lm/layers.py:395-397). */
+int qutai_amd_gemm_grouped_k(const void* a, const void* b, void* out, const int64_t* offsets, int groups, int64_t rows,
+                             int64_t cols, int64_t total_k, int dtype, int out_dtype, int accumulate, void* stream);
+
+/* Backward of qutai_amd_combine for every routed (token, slot) pair: the
+ * pair's expert-major row of d_expert_out = dy[token] * weight, and
+ * d_weights[pair] = dy[token] . expert_out[row] (fp32).  Same routing arrays
+ * as qutai_amd_combine.  Replaces `cuda_lm.combine_backward`
+ * (src/qutai/backends/cuda_lm.py:544-581; cpu_lm.py:306-320). */
+int qutai_amd_combine_backward(const void* dy, const void* expert_out, const float* weights, const int64_t* indices,
+                               const int64_t* locations, const int64_t* offsets, void* d_expert_out,
+                               float* d_weights, int64_t rows, int64_t width, int64_t top_k, int dtype,
+                               void* stream);
+
+/* Gradient of the router logits from the gradient of the routing weights
+ * (auxiliary = 0: gradient [rows*top_k]) or of the auxiliary loss
+ * (auxiliary = 1: gradient [1]); out [rows*experts] fp32 is overwritten.
+ * Replaces `cuda_lm.routing_backward` (src/qutai/backends/cuda_lm.py:452-467;
+ * cpu_lm.py:245-276). */
+int qutai_amd_route_backward(const float* gradient, const float* probs, const float* weights,
+                             const int64_t* indices, const float* utilization, float* out, int64_t rows,
+                             int64_t experts, int64_t top_k, int auxiliary, void* stream);
 
 /* Fused attention backward for the forward above (same layouts, scale and
  * causal flag): from dO (grad), q, k, v, the forward's bf16 output `out` and

@@ -11,7 +11,8 @@ Contents
     (cpu_lm.py:11-42), ``softmax`` (cpu.py:250-260 with ``_axis_indices``
     cpu.py:231-237), ``silu`` (cpu_lm.py:107-111), ``routing``
     (cpu_lm.py:204-242), ``route_gather`` (cpu_lm.py:279-283), ``combine``
-    (cpu_lm.py:294-303), ``attention`` / ``attention_backward``
+    (cpu_lm.py:294-303), ``routing_backward`` (cpu_lm.py:245-276),
+    ``combine_backward`` (cpu_lm.py:306-320), ``attention`` / ``attention_backward``
     (cpu_lm.py:141-201), ``bf16`` (the RNE encoder of cuda.py:98-101 /
     tests/test_bfloat16_storage.py:10-16);
   * ``gemm_f64``: the same float64 sequential-k GEMM compiled from
@@ -183,6 +184,44 @@ def combine(outputs, weights, route, width) -> list[float]:
             for j in range(width):
                 result[row * width + j] += factor * values[i * width + j]
     return result
+
+
+def routing_backward(gradient, route, auxiliary=False) -> list[float]:
+    """cpu_lm.routing_backward (src/qutai/backends/cpu_lm.py:245-276): the
+    logit gradient of the renormalised top-k weights (gradient [rows*top_k])
+    or of the auxiliary loss (gradient [1], utilization held constant)."""
+    rows, experts, top_k = route["rows"], route["experts"], route["top_k"]
+    probs, weights, indices, util = route["probs"], route["weights"], route["indices"], route["utilization"]
+    out = [0.0] * (rows * experts)
+    for row in range(rows):
+        if auxiliary:
+            center = sum(probs[row * experts + e] * util[e] for e in range(experts))
+            for e in range(experts):
+                out[row * experts + e] = (gradient[0] * experts / rows * probs[row * experts + e]
+                                          * (util[e] - center))
+        else:
+            center = sum(gradient[row * top_k + s] * weights[row * top_k + s] for s in range(top_k))
+            for s in range(top_k):
+                e = indices[row * top_k + s]
+                out[row * experts + e] = weights[row * top_k + s] * (gradient[row * top_k + s] - center)
+    return out
+
+
+def combine_backward(gradient, outputs, weights, route, width):
+    """cpu_lm.combine_backward (src/qutai/backends/cpu_lm.py:306-320): per
+    expert output the row gradients dy * weight, and the weight gradient
+    dy . expert row."""
+    grads = []
+    dw = [0.0] * len(weights)
+    for expert, values in outputs:
+        dy = [0.0] * len(values)
+        for i, (row, slot) in enumerate(zip(route["ids"][expert], route["slots"][expert])):
+            at = row * route["top_k"] + slot
+            for j in range(width):
+                dy[i * width + j] = gradient[row * width + j] * weights[at]
+                dw[at] += gradient[row * width + j] * values[i * width + j]
+        grads.append(dy)
+    return (*grads, dw)
 
 
 def attention(q, k, v, batch, time, heads, kv_heads, dim, *, causal=True, scale=None):

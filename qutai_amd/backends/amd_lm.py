@@ -161,30 +161,145 @@ def combine(outputs, weights, route, width):
     return combine_all(block, route, width)
 
 
-def grouped_gemm(rows_block, weight_stack, route, inner, cols, *, out_dtype="bfloat16"):
-    """out[offsets[e]:offsets[e+1]] = rows_block[offsets[e]:offsets[e+1]] @ W_e^T
-    with W_e = weight_stack[e] stored (cols, inner), for every expert in one
-    launch; the row ranges are read on the device."""
+def grouped_gemm(rows_block, weight_stack, route, inner, cols, *, out_dtype="bfloat16", transpose_right=True,
+                 out=None, accumulate=False):
+    """out[offsets[e]:offsets[e+1]] (+)= rows_block[offsets[e]:offsets[e+1]] @ op(W_e)
+    for every expert in one launch, the row ranges read on the device.  With
+    ``transpose_right`` W_e = weight_stack[e] is stored (cols, inner) and used
+    transposed (the forward X W^T); without, it is stored (inner, cols) (the
+    backward dY W)."""
     experts = route["experts"]
     if weight_stack.size != experts * cols * inner or rows_block.dtype != weight_stack.dtype:
-        raise ValueError("grouped_gemm needs [experts][cols][inner] weights of the rows' dtype")
-    out = AMDStorage(route["capacity"] * cols, out_dtype)
+        raise ValueError("grouped_gemm needs [experts] weights of cols*inner values in the rows' dtype")
+    if out is None:
+        if accumulate:
+            raise ValueError("accumulate needs out")
+        out = AMDStorage(route["capacity"] * cols, out_dtype)
+    elif out.dtype != out_dtype or out.size != route["capacity"] * cols:
+        raise ValueError("out must hold capacity x cols values of out_dtype")
     if out.size:
         out.runtime.call("qutai_amd_gemm_grouped", rows_block.ptr, weight_stack.ptr, out.ptr, route["offsets"].ptr,
-                         experts, route["capacity"], inner, cols, cols * inner, 1, code(rows_block.dtype),
-                         code(out_dtype), 0, mfma=True)
+                         experts, route["capacity"], inner, cols, cols * inner, int(transpose_right),
+                         code(rows_block.dtype), code(out_dtype), int(accumulate), mfma=True)
     return out
 
 
-def moe_experts_forward(x, route, w_gate, w_up, w_down, width, hidden):
+def grouped_gemm_k(a_block, b_block, route, rows, cols, *, out_dtype="float32"):
+    """out[e] = A_e^T B_e for every expert, A_e / B_e the expert-major routed
+    rows of a_block ([capacity][rows]) and b_block ([capacity][cols]): the
+    per-expert weight gradients in one launch (an expert with no rows gets
+    zeros)."""
+    experts = route["experts"]
+    if a_block.dtype != b_block.dtype or a_block.size != route["capacity"] * rows or \
+            b_block.size != route["capacity"] * cols:
+        raise ValueError("grouped_gemm_k needs [capacity][rows] and [capacity][cols] blocks of one dtype")
+    out = AMDStorage(experts * rows * cols, out_dtype)
+    if out.size:
+        out.runtime.call("qutai_amd_gemm_grouped_k", a_block.ptr, b_block.ptr, out.ptr, route["offsets"].ptr, experts,
+                         rows, cols, route["capacity"], code(a_block.dtype), code(out_dtype), 0, mfma=True)
+    return out
+
+
+def _as_dtype(values, dtype):
+    return values if values.dtype == dtype else amd.from_storage(values, dtype=dtype)
+
+
+def moe_experts_forward(x, route, w_gate, w_up, w_down, width, hidden, *, save=False):
     """Expert SwiGLU for every routed (token, slot): gather, grouped gate/up,
-    silu(gate) * up, grouped down, weighted combine (lm/layers.py:395-399)."""
+    silu(gate) * up, grouped down, weighted combine (lm/layers.py:395-399).
+    Weights of another dtype than x (fp32 master weights, bf16 activations)
+    are rounded to x's dtype for the products, as the reference's mixed GEMM
+    does.  With ``save`` the intermediates for ``moe_experts_backward`` are
+    returned too."""
+    wg, wu, wd = (_as_dtype(w, x.dtype) for w in (w_gate, w_up, w_down))
     rows = route_gather_all(x, route, width)
-    gate = grouped_gemm(rows, w_gate, route, width, hidden, out_dtype=x.dtype)
-    up = grouped_gemm(rows, w_up, route, width, hidden, out_dtype=x.dtype)
+    gate = grouped_gemm(rows, wg, route, width, hidden, out_dtype=x.dtype)
+    up = grouped_gemm(rows, wu, route, width, hidden, out_dtype=x.dtype)
     act = silu_mul(gate, up)
-    down = grouped_gemm(act, w_down, route, hidden, width, out_dtype=x.dtype)
-    return combine_all(down, route, width)
+    down = grouped_gemm(act, wd, route, hidden, width, out_dtype=x.dtype)
+    y = combine_all(down, route, width)
+    if not save:
+        return y
+    return y, dict(rows=rows, gate=gate, up=up, act=act, down=down, w_gate=wg, w_up=wu, w_down=wd)
+
+
+def combine_backward_all(gradient, expert_rows, route, width):
+    """(d expert rows [capacity][width], d weights [rows*top_k] fp32) of
+    combine_all, one launch for every (token, slot)."""
+    d_rows = AMDStorage(expert_rows.size, expert_rows.dtype)
+    d_weights = AMDStorage(route["capacity"], "float32")
+    if route["capacity"]:
+        d_rows.runtime.call("qutai_amd_combine_backward", gradient.ptr, expert_rows.ptr, route["weights"].ptr,
+                            route["indices"].ptr, route["locations"].ptr, route["offsets"].ptr, d_rows.ptr,
+                            d_weights.ptr, route["rows"], width, route["top_k"], code(expert_rows.dtype))
+    return d_rows, d_weights
+
+
+def combine_backward(gradient, outputs, weights, route, width):
+    """Reference-shaped combine backward (cuda_lm.py:544-581): per-expert row
+    gradients in the order of ``outputs``, then the weight gradient."""
+    if weights is not route["weights"]:
+        route = dict(route, weights=weights)
+    dtype = outputs[0][1].dtype if outputs else gradient.dtype
+    block = AMDStorage(route["capacity"] * width, dtype)
+    starts = _host_offsets(route)
+    item = 2 if dtype == "bfloat16" else 4
+    for expert, values in outputs:
+        if values.size:
+            block.runtime.copy(block.ptr + starts[expert] * width * item, values.ptr, values.nbytes)
+    d_block, d_weights = combine_backward_all(_as_dtype(gradient, dtype), block, route, width)
+    grads = []
+    for expert, values in outputs:
+        part = AMDStorage(values.size, dtype)
+        if values.size:
+            part.runtime.copy(part.ptr, d_block.ptr + starts[expert] * width * item, values.nbytes)
+        grads.append(part)
+    return (*grads, d_weights)
+
+
+def route_gather_backward_all(d_rows, route, width):
+    """Token-row gradient of route_gather_all: the sum over each token's
+    slots of its expert-major rows (fp32 sum, one rounding)."""
+    out = AMDStorage(route["rows"] * width, d_rows.dtype)
+    if out.size:
+        out.runtime.call("qutai_amd_combine", d_rows.ptr, None, route["indices"].ptr, route["locations"].ptr,
+                         route["offsets"].ptr, out.ptr, route["rows"], width, route["top_k"], code(d_rows.dtype))
+    return out
+
+
+def routing_backward(gradient, route, auxiliary=False):
+    """Gradient of the router logits (cuda_lm.routing_backward,
+    cuda_lm.py:452-467): from the routing weights' gradient [rows*top_k], or
+    with ``auxiliary`` from the aux loss's scalar gradient."""
+    rows, experts = route["rows"], route["experts"]
+    g = _as_dtype(gradient, "float32")
+    if g.size != (1 if auxiliary else rows * route["top_k"]):
+        raise ValueError("routing_backward: gradient size does not match the route")
+    out = AMDStorage(rows * experts, "float32")
+    if rows:
+        out.runtime.call("qutai_amd_route_backward", g.ptr, route["probs"].ptr, route["weights"].ptr,
+                         route["indices"].ptr, route["utilization"].ptr, out.ptr, rows, experts, route["top_k"],
+                         int(bool(auxiliary)))
+    return out
+
+
+def moe_experts_backward(gradient, route, saved, width, hidden, *, x_dtype, weight_dtype):
+    """Backward of moe_experts_forward: (dx, d routing weights, dW_gate,
+    dW_up, dW_down).  Every product is one grouped launch over all experts
+    (NN for the data gradients, grouped-K TN for the weight gradients); the
+    token gradient sums each token's slots in fp32 and rounds once."""
+    dt = saved["down"].dtype
+    d_down, d_weights = combine_backward_all(_as_dtype(gradient, dt), saved["down"], route, width)
+    d_act = grouped_gemm(d_down, saved["w_down"], route, width, hidden, out_dtype=dt, transpose_right=False)
+    dw_down = grouped_gemm_k(d_down, saved["act"], route, width, hidden, out_dtype=weight_dtype)
+    d_gate, d_up = silu_mul_backward(d_act, saved["gate"], saved["up"])
+    d_rows = grouped_gemm(d_gate, saved["w_gate"], route, hidden, width, out_dtype="float32", transpose_right=False)
+    grouped_gemm(d_up, saved["w_up"], route, hidden, width, out_dtype="float32", transpose_right=False, out=d_rows,
+                 accumulate=True)
+    dw_gate = grouped_gemm_k(d_gate, saved["rows"], route, hidden, width, out_dtype=weight_dtype)
+    dw_up = grouped_gemm_k(d_up, saved["rows"], route, hidden, width, out_dtype=weight_dtype)
+    dx = _as_dtype(route_gather_backward_all(d_rows, route, width), x_dtype)
+    return dx, d_weights, dw_gate, dw_up, dw_down
 
 
 def _check_attention(q, k, v, batch, time, heads, kv_heads, dim):

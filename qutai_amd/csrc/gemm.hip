@@ -317,4 +317,40 @@ int qutai_amd_gemm_grouped(const void* a, const void* b, void* out, const int64_
   return (int)err;
 }
 
+int qutai_amd_gemm_grouped_k(const void* a, const void* b, void* out, const int64_t* offsets, int groups, int64_t rows,
+                             int64_t cols, int64_t total_k, int dtype, int out_dtype, int accumulate, void* stream_) {
+  hipStream_t stream = (hipStream_t)stream_;
+  if (groups <= 0 || rows < 0 || cols < 0 || total_k < 0) return QA_EINVAL;
+  if (dtype != QA_BF16 && dtype != QA_F32) return QA_EINVAL;
+  if (out_dtype != QA_F32 && out_dtype != QA_BF16) return QA_EINVAL;
+  if (!offsets || !out) return QA_EINVAL;
+  if (rows == 0 || cols == 0) return QA_OK;
+  const int64_t E = dtype == QA_BF16 ? 8 : 4;
+  if ((uintptr_t)a % 16 || (uintptr_t)b % 16 || rows % E || cols % E) return QA_EINVAL;
+  GemmArgs p = {};
+  p.a = a;
+  p.b = b;
+  p.out = out;
+  p.M = rows;
+  p.N = cols;
+  p.K = total_k;
+  p.lda = rows;  // A stored [K][rows]: out_g = A_g^T B_g
+  p.ldb = cols;  // B stored [K][cols]
+  p.ldc = cols;
+  p.sc = rows * cols;
+  p.batch = groups;
+  p.accumulate = accumulate ? 1 : 0;
+  p.out_bf16 = out_dtype == QA_BF16;
+  p.vec_c = vec_out(out, p.ldc, p.sc);
+  p.offsets = offsets;
+  p.group_k = 1;
+  p.alpha = 1.0f;
+  int64_t es = dtype == QA_BF16 ? 2 : 4;
+  if ((p.lda * 256 * es) >= (1ll << 31) || (p.ldb * 256 * es) >= (1ll << 31)) return QA_EINVAL;
+  Tile tile = choose_tile(rows, cols, total_k / groups + 1, groups);
+  hipError_t err = dtype == QA_F32 ? launch_mma<true>(tile, true, false, p, stream)
+                                   : launch_mma<false>(tile, true, false, p, stream);
+  return (int)err;
+}
+
 }  // extern "C"

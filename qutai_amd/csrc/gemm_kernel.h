@@ -51,6 +51,9 @@ struct GemmArgs {
   int groups;
   int tiles_m;            // M tiles in the grid (grouped: an upper bound)
   float alpha;            // scale applied to A@B before the epilogue
+  // Grouped-K mode (group_k = 1, batch = groups): group g reduces over the K
+  // rows [offsets[g], offsets[g+1]) of A and B and writes out + g*sc.
+  int group_k;
 };
 
 template <bool F32> struct MmaTraits;
@@ -306,10 +309,18 @@ struct GemmKernel {
 
     const T* A = reinterpret_cast<const T*>(p.a);
     const T* B = reinterpret_cast<const T*>(p.b);
-    int64_t M = p.M, row0 = 0;
+    int64_t M = p.M, row0 = 0, K = p.K;
     char* outp = reinterpret_cast<char*>(p.out);
     const int osize = p.out_bf16 ? 2 : 4;
-    if (p.groups > 0) {
+    if (p.group_k) {
+      // per-group K range; an empty group writes zeros (or keeps `out`)
+      const int64_t k_lo = p.offsets[bz], k_hi = p.offsets[bz + 1];
+      A += k_lo * (KA ? 1 : p.lda);
+      B += k_lo * (KB ? 1 : p.ldb);
+      outp += bz * p.sc * osize;
+      row0 = (int64_t)tile_m * BM;
+      K = k_hi - k_lo;
+    } else if (p.groups > 0) {
       // locate the group that owns M-tile `tile_m`
       int64_t before = 0;
       int g = -1;
@@ -337,7 +348,8 @@ struct GemmKernel {
     M = uniform64(M);
     row0 = uniform64(row0);
     const int64_t col0 = uniform64((int64_t)tile_n * BN);
-    const int64_t K = p.K, N = p.N;
+    K = uniform64(K);
+    const int64_t N = p.N;
     const int64_t lda = p.lda, ldb = p.ldb;
 
     f32x16 acc[FM][FN];

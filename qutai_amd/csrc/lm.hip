@@ -159,7 +159,7 @@ __global__ void combine_kernel(const T* eo, const float* w, const int64_t* idx, 
     for (int v = 0; v < V; v++) acc[v] = 0.f;
     for (int64_t s = 0; s < top_k; s++) {
       int64_t at = row * top_k + s;
-      float f = w[at];
+      float f = w ? w[at] : 1.f;
       const T* src = eo + (off[idx[at]] + loc[at]) * width + j;
 #pragma unroll
       for (int v = 0; v < V; v++) {
@@ -174,6 +174,67 @@ __global__ void combine_kernel(const T* eo, const float* w, const int64_t* idx, 
       if constexpr (sizeof(T) == 2) y[row * width + j + v] = f32_to_bf16(acc[v]);
       else y[row * width + j + v] = acc[v];
     }
+  }
+}
+
+// Backward of the weighted combine for every routed (token, slot) pair at
+// (rows*top_k pairs, one wave each; cpu_lm.combine_backward,
+// src/qutai/backends/cpu_lm.py:306-320): the pair's expert-major row
+// pos = offsets[e] + loc gets d_eo[pos] = dy[row] * w[at], and
+// dw[at] = dy[row] . eo[pos] (fp32 sum over the width).
+template <class T>
+__global__ void __launch_bounds__(256) combine_backward_kernel(const T* dy, const T* eo, const float* w,
+                                                               const int64_t* idx, const int64_t* loc,
+                                                               const int64_t* off, T* deo, float* dw,
+                                                               int64_t pairs, int64_t width, int64_t top_k) {
+  const int lane = threadIdx.x & 63;
+  const int64_t at = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (at >= pairs) return;  // whole wave
+  const int64_t row = at / top_k, pos = off[idx[at]] + loc[at];
+  const float f = w[at];
+  const T* g = dy + row * width;
+  const T* x = eo + pos * width;
+  T* d = deo + pos * width;
+  float dot = 0.f;
+  for (int64_t j = lane; j < width; j += 64) {
+    float gv, xv;
+    if constexpr (sizeof(T) == 2) {
+      gv = bf16_to_f32(g[j]);
+      xv = bf16_to_f32(x[j]);
+      d[j] = f32_to_bf16(gv * f);
+    } else {
+      gv = (float)g[j];
+      xv = (float)x[j];
+      d[j] = gv * f;
+    }
+    dot += gv * xv;
+  }
+  for (int o = 32; o > 0; o >>= 1) dot += __shfl_xor(dot, o);
+  if (lane == 0) dw[at] = dot;
+}
+
+// Gradient of the router logits (cpu_lm.routing_backward,
+// src/qutai/backends/cpu_lm.py:245-276), one thread per token row:
+//   weights: out[e_s] = w_s (g_s - sum_t g_t w_t) for the selected experts;
+//   aux:     out[e]   = g * E / rows * p_e (u_e - sum_f p_f u_f).
+__global__ void route_backward_kernel(const float* g, const float* probs, const float* weights,
+                                      const int64_t* indices, const float* util, float* out, int64_t rows,
+                                      int64_t experts, int64_t top_k, int auxiliary) {
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  float* o = out + r * experts;
+  const float* pr = probs + r * experts;
+  if (auxiliary) {
+    float center = 0.f;
+    for (int64_t e = 0; e < experts; e++) center += pr[e] * util[e];
+    const float scale = g[0] * (float)experts / (float)rows;
+    for (int64_t e = 0; e < experts; e++) o[e] = scale * pr[e] * (util[e] - center);
+  } else {
+    for (int64_t e = 0; e < experts; e++) o[e] = 0.f;
+    float center = 0.f;
+    for (int64_t s = 0; s < top_k; s++) center += g[r * top_k + s] * weights[r * top_k + s];
+    for (int64_t s = 0; s < top_k; s++)
+      o[indices[r * top_k + s]] = weights[r * top_k + s] * (g[r * top_k + s] - center);
   }
 }
 
@@ -254,6 +315,37 @@ int qutai_amd_combine(const void* expert_out, const float* weights, const int64_
                          (const float*)expert_out, weights, indices, locations, offsets, (float*)y, rows, width,
                          top_k);
   }
+  return (int)hipGetLastError();
+}
+
+int qutai_amd_combine_backward(const void* dy, const void* expert_out, const float* weights, const int64_t* indices,
+                               const int64_t* locations, const int64_t* offsets, void* d_expert_out,
+                               float* d_weights, int64_t rows, int64_t width, int64_t top_k, int dtype,
+                               void* stream) {
+  if (rows < 0 || width < 0 || top_k <= 0) return QA_EINVAL;
+  if (dtype != F32 && dtype != BF16) return QA_EINVAL;
+  const int64_t pairs = rows * top_k;
+  if (pairs == 0) return QA_OK;
+  const unsigned blocks = (unsigned)((pairs + 3) / 4);
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == BF16)
+    hipLaunchKernelGGL(combine_backward_kernel<bf16_t>, dim3(blocks), dim3(256), 0, s, (const bf16_t*)dy,
+                       (const bf16_t*)expert_out, weights, indices, locations, offsets, (bf16_t*)d_expert_out,
+                       d_weights, pairs, width, top_k);
+  else
+    hipLaunchKernelGGL(combine_backward_kernel<float>, dim3(blocks), dim3(256), 0, s, (const float*)dy,
+                       (const float*)expert_out, weights, indices, locations, offsets, (float*)d_expert_out,
+                       d_weights, pairs, width, top_k);
+  return (int)hipGetLastError();
+}
+
+int qutai_amd_route_backward(const float* gradient, const float* probs, const float* weights,
+                             const int64_t* indices, const float* utilization, float* out, int64_t rows,
+                             int64_t experts, int64_t top_k, int auxiliary, void* stream) {
+  if (rows < 0 || experts <= 0 || top_k <= 0 || top_k > experts) return QA_EINVAL;
+  if (rows == 0) return QA_OK;
+  hipLaunchKernelGGL(route_backward_kernel, dim3(blocks_for(rows)), dim3(256), 0, (hipStream_t)stream, gradient,
+                     probs, weights, indices, utilization, out, rows, experts, top_k, auxiliary ? 1 : 0);
   return (int)hipGetLastError();
 }
 

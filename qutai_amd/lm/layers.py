@@ -114,23 +114,44 @@ class SparseMoE:
         self.w_gate = stacked(hidden, width, 0, 0.02)
         self.w_up = stacked(hidden, width, 1, 0.02)
         self.w_down = stacked(width, hidden, 2, std)
-        self.last_counts = (0,) * experts
         self.utilization = None
 
     def __call__(self, x):
+        """(result, aux) like the reference (lm/layers.py:376-402); every
+        expert runs in one grouped launch per projection, forward and
+        backward, with no host synchronisation.  ``last_route`` keeps the
+        routing arrays of the call."""
         with set_matmul_precision(None):
             scores = self.router(x.to(dtype=self.router.weight.dtype))
         b = backend(x)
         rows = x.size // x.shape[-1]
         route = b.routing(scores.storage, rows, self.n_experts, self.top_k, download_counts=False)
+        self.last_route = route
+        weights = record(Tensor(route["weights"], shape=(rows, self.top_k)), (scores,),
+                         lambda g: (b.routing_backward(g, route),))
+        aux = record(Tensor(route["aux"], shape=()), (scores,), lambda g: (b.routing_backward(g, route, True),))
         self.utilization = Tensor(route["utilization"], shape=(self.n_experts,))
-        aux = Tensor(route["aux"], shape=())
-        values = b.moe_experts_forward(x.storage, route, self.w_gate.storage, self.w_up.storage,
-                                       self.w_down.storage, self.width, self.hidden)
+        values, saved = b.moe_experts_forward(x.storage, route, self.w_gate.storage, self.w_up.storage,
+                                              self.w_down.storage, self.width, self.hidden, save=True)
         if x.dtype != values.dtype:
             values = amd.from_storage(values, dtype=x.dtype)
-        result = Tensor(values, shape=x.shape)
-        return result, aux, route
+        weight_dtype = self.w_gate.dtype
+
+        def backward(g):
+            dx, dw, dwg, dwu, dwd = b.moe_experts_backward(g, route, saved, self.width, self.hidden,
+                                                           x_dtype=x.dtype, weight_dtype=weight_dtype)
+            return dx, dw, dwg, dwu, dwd
+
+        result = record(Tensor(values, shape=x.shape), (x, weights, self.w_gate, self.w_up, self.w_down), backward)
+        return result, aux
+
+    @property
+    def last_counts(self):
+        """Per-expert token counts of the last call (one device read)."""
+        route = getattr(self, "last_route", None)
+        if route is None:
+            return (0,) * self.n_experts
+        return tuple(route["count_buffer"].to_array().tolist())
 
     def parameters(self):
         return (*self.router.parameters(), self.w_gate, self.w_up, self.w_down)

@@ -333,3 +333,79 @@ def test_attention_backward_matches_finite_differences_and_numpy_form():
     assert np.abs(np.stack([p[0] for p in parts], 1).ravel() - dq).max() < 1e-12
     assert np.abs(sum(p[1] for p in parts).ravel() - dk).max() < 1e-12
     assert np.abs(sum(p[2] for p in parts).ravel() - dv).max() < 1e-12
+
+
+# ---- routing / combine backward ----------------------------------------------------
+
+def _renormalised_weights(scores, route):
+    """The routing weights as a function of the logits with the selection held
+    fixed: w_s = exp(z_e) / sum over selected exp(z_f)."""
+    rows, experts, top_k = route["rows"], route["experts"], route["top_k"]
+    out = []
+    for row in range(rows):
+        sel = route["indices"][row * top_k:(row + 1) * top_k]
+        z = [scores[row * experts + e] for e in sel]
+        m = max(z)
+        ex = [math.exp(v - m) for v in z]
+        out.extend(v / math.fsum(ex) for v in ex)
+    return out
+
+
+def test_routing_backward_matches_finite_differences():
+    rng = random.Random(12)
+    rows, experts, top_k = 5, 4, 2
+    scores = [rng.gauss(0, 1) for _ in range(rows * experts)]
+    route = ora.routing(scores, rows, experts, top_k)
+    g = [rng.gauss(0, 1) for _ in range(rows * top_k)]
+    got = ora.routing_backward(g, route)
+    eps = 1e-6
+    for i in range(rows * experts):
+        up, down = list(scores), list(scores)
+        up[i] += eps
+        down[i] -= eps
+        f = lambda s: math.fsum(a * b for a, b in zip(g, _renormalised_weights(s, route)))  # noqa: E731
+        assert got[i] == pytest.approx((f(up) - f(down)) / (2 * eps), abs=1e-8)
+    # aux: d/dz of E * sum_e util_e * mean_r softmax(z_r)_e with util fixed
+    c = [0.7]
+    aux = ora.routing_backward(c, route, auxiliary=True)
+    util = route["utilization"]
+
+    def aux_of(s):
+        total = 0.0
+        for row in range(rows):
+            z = s[row * experts:(row + 1) * experts]
+            m = max(z)
+            ex = [math.exp(v - m) for v in z]
+            total += math.fsum(u * v / math.fsum(ex) for u, v in zip(util, ex))
+        return c[0] * experts * total / rows
+
+    for i in range(rows * experts):
+        up, down = list(scores), list(scores)
+        up[i] += eps
+        down[i] -= eps
+        assert aux[i] == pytest.approx((aux_of(up) - aux_of(down)) / (2 * eps), abs=1e-8)
+
+
+def test_combine_backward_matches_finite_differences():
+    rng = random.Random(13)
+    rows, experts, top_k, width = 6, 3, 2, 4
+    route = ora.routing([rng.gauss(0, 1) for _ in range(rows * experts)], rows, experts, top_k)
+    outputs = [(e, [rng.gauss(0, 1) for _ in range(route["counts"][e] * width)]) for e in range(experts)
+               if route["counts"][e]]
+    weights = list(route["weights"])
+    g = [rng.gauss(0, 1) for _ in range(rows * width)]
+    *grads, dw = ora.combine_backward(g, outputs, weights, route, width)
+    loss = lambda outs, w: math.fsum(a * b for a, b in zip(g, ora.combine(outs, w, route, width)))  # noqa: E731
+    eps = 1e-6
+    for i in range(len(weights)):
+        up, down = list(weights), list(weights)
+        up[i] += eps
+        down[i] -= eps
+        assert dw[i] == pytest.approx((loss(outputs, up) - loss(outputs, down)) / (2 * eps), abs=1e-8)
+    for n, (e, values) in enumerate(outputs):
+        for i in range(len(values)):
+            up = [(f, list(v)) for f, v in outputs]
+            down = [(f, list(v)) for f, v in outputs]
+            up[n][1][i] += eps
+            down[n][1][i] -= eps
+            assert grads[n][i] == pytest.approx((loss(up, weights) - loss(down, weights)) / (2 * eps), abs=1e-8)
