@@ -209,9 +209,19 @@ def moe_train(seed=4):
     from qutai_amd.backends import amd
     from qutai_amd.lm.layers import SparseMoE
 
+    from qutai_amd.backends import amd_lm
+
     tokens, width, experts, hidden, top_k = 8192, 2048, 8, 1408, 2
     rng = np.random.default_rng(seed)
-    layer = SparseMoE(width, hidden, experts, top_k, dtype="bfloat16", seed=seed)
+    # random init from numpy draws (69 M Random.gauss draws in CPython would
+    # take a minute); same shapes and scales as the layer's own init
+    host_normal = amd_lm.normal
+    amd_lm.normal = lambda size, mean=0.0, std=1.0, *, seed=None, dtype="float32": upload(
+        rng.normal(mean, std, size), dtype)
+    try:
+        layer = SparseMoE(width, hidden, experts, top_k, dtype="bfloat16", seed=seed)
+    finally:
+        amd_lm.normal = host_normal
     x = Tensor(upload(rng.standard_normal(tokens * width), "bfloat16"), shape=(tokens, width), requires_grad=True)
     g = Tensor(upload(rng.standard_normal(tokens * width), "bfloat16"), shape=(tokens, width))
 
