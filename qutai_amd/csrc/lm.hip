@@ -41,62 +41,67 @@ __global__ void route_select(const float* scores, float* probs, float* weights, 
 }
 
 // One workgroup per expert: stable compaction of the (token, slot)
-// assignments routed to it, in increasing assignment order.
-constexpr int PACK = 256;
-__global__ void __launch_bounds__(PACK) route_pack(const int64_t* indices, int64_t* counts, int64_t* ids,
-                                                   int64_t* slots, int64_t* locations, int64_t* offsets,
-                                                   int64_t* order, int64_t n, int64_t top_k, int64_t experts) {
-  __shared__ int64_t wave_count[PACK / 64];
-  __shared__ int64_t lower_total;
+// assignments routed to it, in increasing assignment order.  The 16 waves
+// own contiguous segments of the assignments: one pass counts each
+// segment's matches (and the assignments to lower experts, whose total is
+// the expert's start in `order`), a prefix over the segment counts gives
+// every wave its first position, and a second pass writes positions with a
+// ballot per 64 assignments -- no barrier inside the loops.
+constexpr int PACKW = 16;
+__global__ void __launch_bounds__(PACKW * 64) route_pack(const int64_t* indices, int64_t* counts, int64_t* ids,
+                                                         int64_t* slots, int64_t* locations, int64_t* offsets,
+                                                         int64_t* order, int64_t n, int64_t top_k, int64_t experts) {
+  __shared__ int64_t seg_count[PACKW], seg_lower[PACKW];
   const int64_t e = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  // pass 1: assignments to lower experts = start of this expert in `order`
-  int64_t lower = 0;
-  for (int64_t at = tid; at < n; at += PACK) lower += indices[at] < e;
-  for (int o = 32; o > 0; o >>= 1) lower += __shfl_xor(lower, o);
-  if (lane == 0) wave_count[wave] = lower;
-  __syncthreads();
-  if (tid == 0) {
-    int64_t t = 0;
-    for (int w = 0; w < PACK / 64; w++) t += wave_count[w];
-    lower_total = t;
+  const int64_t seg = (n + PACKW - 1) / PACKW;
+  const int64_t lo = min(n, wave * seg), hi = min(n, lo + seg);
+  int64_t count = 0, lower = 0;
+  for (int64_t at = lo + lane; at < hi; at += 64) {
+    const int64_t x = indices[at];
+    count += x == e;
+    lower += x < e;
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    count += __shfl_xor(count, o);
+    lower += __shfl_xor(lower, o);
+  }
+  if (lane == 0) {
+    seg_count[wave] = count;
+    seg_lower[wave] = lower;
   }
   __syncthreads();
-  const int64_t base = lower_total;
-  // pass 2: ordered compaction, 256 assignments per step
-  int64_t written = 0;
-  for (int64_t start = 0; start < n; start += PACK) {
-    int64_t at = start + tid;
-    bool sel = at < n && indices[at] == e;
-    uint64_t mask = __ballot(sel);
-    int64_t before_lane = __popcll(mask & ((1ull << lane) - 1ull));
-    __syncthreads();
-    if (lane == 0) wave_count[wave] = __popcll(mask);
-    __syncthreads();
-    int64_t before_wave = 0, step = 0;
-    for (int w = 0; w < PACK / 64; w++) {
-      if (w < wave) before_wave += wave_count[w];
-      step += wave_count[w];
-    }
+  int64_t base = 0, written = 0, total = 0;
+  for (int w = 0; w < PACKW; w++) {
+    base += seg_lower[w];
+    total += seg_count[w];
+    if (w < wave) written += seg_count[w];
+  }
+  const uint64_t below = (1ull << lane) - 1ull;
+  for (int64_t start = lo; start < hi; start += 64) {
+    const int64_t at = start + lane;
+    const bool sel = at < hi && indices[at] == e;
+    const uint64_t mask = __ballot(sel);
     if (sel) {
-      int64_t pos = written + before_wave + before_lane;
+      const int64_t pos = written + __popcll(mask & below);
       ids[e * n + pos] = at / top_k;
       slots[e * n + pos] = at % top_k;
       locations[at] = pos;
       order[base + pos] = at / top_k;
     }
-    written += step;
+    written += __popcll(mask);
   }
   if (tid == 0) {
-    counts[e] = written;
+    counts[e] = total;
     offsets[e] = base;
     if (e == experts - 1) offsets[experts] = n;
   }
 }
 
 // utilization = count / (rows * top_k); aux = experts * sum(p * util) / rows.
-// One 1024-thread workgroup: each thread sums a contiguous block of rows,
-// then a fixed-order tree reduction in LDS (deterministic result).
+// One 1024-thread workgroup: thread t sums the probabilities t, t + 1024,
+// ... (coalesced) weighted by their expert's utilization, then a fixed-order
+// tree reduction in LDS (deterministic result).
 constexpr int STATS = 1024;
 __global__ void __launch_bounds__(STATS) route_stats(const float* probs, const int64_t* counts, float* utilization,
                                                      float* aux, int64_t rows, int64_t experts, int64_t n) {
@@ -109,12 +114,12 @@ __global__ void __launch_bounds__(STATS) route_stats(const float* probs, const i
     if (e < 256) util[e] = u;
   }
   __syncthreads();
-  int64_t per = (rows + STATS - 1) / STATS;
-  int64_t r0 = tid * per, r1 = min(rows, r0 + per);
+  const int64_t total_values = rows * experts;
   float total = 0.f;
-  for (int64_t r = r0; r < r1; r++)
-    for (int64_t e = 0; e < experts; e++)
-      total += probs[r * experts + e] * (e < 256 ? util[e] : (float)counts[e] / (float)n);
+  for (int64_t i = tid; i < total_values; i += STATS) {
+    const int64_t e = i % experts;
+    total += probs[i] * (e < 256 ? util[e] : (float)counts[e] / (float)n);
+  }
   red[tid] = total;
   __syncthreads();
   for (int s = STATS / 2; s > 0; s >>= 1) {
@@ -257,8 +262,8 @@ int qutai_amd_route(const float* scores, float* probs, float* weights, int64_t* 
   if (rows > 0)
     hipLaunchKernelGGL(route_select, dim3(blocks_for(rows)), dim3(256), 0, s, scores, probs, weights, indices, rows,
                        experts, top_k);
-  hipLaunchKernelGGL(route_pack, dim3((unsigned)experts), dim3(PACK), 0, s, indices, counts, ids, slots, locations,
-                     offsets, order, n, top_k, experts);
+  hipLaunchKernelGGL(route_pack, dim3((unsigned)experts), dim3(PACKW * 64), 0, s, indices, counts, ids, slots,
+                     locations, offsets, order, n, top_k, experts);
   if (rows > 0)
     hipLaunchKernelGGL(route_stats, dim3(1), dim3(STATS), 0, s, probs, counts, utilization, aux, rows, experts, n);
   return (int)hipGetLastError();
