@@ -90,7 +90,9 @@ __global__ void prepare_operand(const void* src, int src_bf16, void* dst, int ds
 //   L4D2: 256x256, 4 waves (one per SIMD, 128x128 per wave), two-stage ring
 //   S   : 128x128, 4 waves, BK 32 / 16, four-stage ring (small grids, short K)
 //   N   : 256x64, 4 waves (N <= 64), W : 64x256, 4 waves (M <= 64)
-enum Tile { TILE_L8D2, TILE_L8R, TILE_L4D2, TILE_S, TILE_N, TILE_W, TILE_COUNT };
+//   H   : 256x128, 8 waves 4x2 (64x64 per wave), BK 64, three-stage ring
+//         (grids of 256x256 tiles that would leave half the CUs idle)
+enum Tile { TILE_L8D2, TILE_L8R, TILE_L4D2, TILE_S, TILE_N, TILE_W, TILE_H, TILE_COUNT };
 
 template <bool F32, bool TA, bool TB, int BM, int BN, int WM, int WN, int BK, int ST, bool DMA>
 hipError_t launch_cfg(GemmArgs p, hipStream_t stream) {
@@ -114,6 +116,7 @@ hipError_t launch_tile(Tile tile, GemmArgs p, hipStream_t stream) {
     case TILE_S: return launch_cfg<F32, TA, TB, 128, 128, 2, 2, KB, 4, true>(p, stream);
     case TILE_N: return launch_cfg<F32, TA, TB, 256, 64, 4, 1, KB, 4, true>(p, stream);
     case TILE_W: return launch_cfg<F32, TA, TB, 64, 256, 1, 4, KB, 4, true>(p, stream);
+    case TILE_H: return launch_cfg<F32, TA, TB, 256, 128, 4, 2, KR, 3, true>(p, stream);
     default: return launch_cfg<F32, TA, TB, 256, 256, 2, 4, KR, 2, true>(p, stream);
   }
 }
@@ -126,12 +129,12 @@ hipError_t launch_mma(Tile tile, bool ta, bool tb, const GemmArgs& p, hipStream_
 
 // Tile choice: 256x256 when the grid still gives about one tile per CU,
 // else the 128x128 tile; thin outputs use the 256x64 / 64x256 shapes.
-// QUTAI_AMD_GEMM_TILE=<L8D2|L8R|L4D2|S|N|W> overrides the choice (tuning).
+// QUTAI_AMD_GEMM_TILE=<L8D2|L8R|L4D2|S|N|W|H> overrides the choice (tuning).
 Tile choose_tile(int64_t M, int64_t N, int64_t K, int64_t batch) {
   static int forced = [] {
     const char* v = getenv("QUTAI_AMD_GEMM_TILE");
     if (!v) return -1;
-    const char* names[TILE_COUNT] = {"L8D2", "L8R", "L4D2", "S", "N", "W"};
+    const char* names[TILE_COUNT] = {"L8D2", "L8R", "L4D2", "S", "N", "W", "H"};
     for (int i = 0; i < TILE_COUNT; i++)
       if (std::string(v) == names[i]) return i;
     return -1;
@@ -140,7 +143,11 @@ Tile choose_tile(int64_t M, int64_t N, int64_t K, int64_t batch) {
   if (N <= 64) return TILE_N;
   if (M <= 64) return TILE_W;
   int64_t big = ((M + 255) / 256) * ((N + 255) / 256) * batch;
-  if (big < 192 || K <= 128) return TILE_S;
+  if (K <= 128) return TILE_S;
+  // 256x256 tiles filling at most half the CUs over a long K: 256x128 tiles
+  // (measured on the config 4 projections: 4096x2048 outputs, K = 5632)
+  if (big <= 136 && big >= 64 && K >= 2048) return TILE_H;
+  if (big < 192) return TILE_S;
   return TILE_L8D2;
 }
 
