@@ -221,9 +221,21 @@ __global__ void __launch_bounds__(NW * 64) attention_fwd_d64(AttnArgs p) {
   const int blocks_q = (T + QPB - 1) / QPB;
   // every query block of one (batch, head) on one XCD (they share K and V in
   // its L2); within a head the longest (causal) query blocks start first
-  const int pid = uniform32(xcd_remap(blockIdx.x, gridDim.x));
-  const int bh = uniform32(pid / blocks_q);
-  const int qblk = uniform32(p.causal ? blocks_q - 1 - pid % blocks_q : pid % blocks_q);
+  // non-causal: every query block of one (batch, head) on one XCD (they
+  // share K and V in its L2).  causal: block i takes work rank i / heads, so
+  // the longest query blocks of every head are dispatched first (longest
+  // first scheduling over the CUs) while block i still lands on XCD i % 8,
+  // i.e. one head's blocks share an XCD when 8 divides batch * heads.
+  int bh, qblk;
+  if (p.causal) {
+    const int nbh = (int)(p.batch * p.heads);
+    bh = uniform32((int)blockIdx.x % nbh);
+    qblk = uniform32(blocks_q - 1 - (int)blockIdx.x / nbh);
+  } else {
+    const int pid = uniform32(xcd_remap(blockIdx.x, gridDim.x));
+    bh = uniform32(pid / blocks_q);
+    qblk = uniform32(pid % blocks_q);
+  }
   const int wg_q0 = qblk * QPB;
   const int q0 = uniform32(wg_q0 + wave * QW);
   const int b = bh / (int)p.heads, h = bh % (int)p.heads;
@@ -478,9 +490,21 @@ __global__ void __launch_bounds__(NW * 64) attention_bwd_dq_d64(AttnBwdArgs p) {
   const int tid = threadIdx.x, lane = tid & 63, wave = uniform32(tid >> 6);
   const int T = (int)p.time;
   const int blocks_q = (T + QPB - 1) / QPB;
-  const int pid = uniform32(xcd_remap(blockIdx.x, gridDim.x));
-  const int bh = uniform32(pid / blocks_q);
-  const int qblk = uniform32(p.causal ? blocks_q - 1 - pid % blocks_q : pid % blocks_q);
+  // non-causal: every query block of one (batch, head) on one XCD (they
+  // share K and V in its L2).  causal: block i takes work rank i / heads, so
+  // the longest query blocks of every head are dispatched first (longest
+  // first scheduling over the CUs) while block i still lands on XCD i % 8,
+  // i.e. one head's blocks share an XCD when 8 divides batch * heads.
+  int bh, qblk;
+  if (p.causal) {
+    const int nbh = (int)(p.batch * p.heads);
+    bh = uniform32((int)blockIdx.x % nbh);
+    qblk = uniform32(blocks_q - 1 - (int)blockIdx.x / nbh);
+  } else {
+    const int pid = uniform32(xcd_remap(blockIdx.x, gridDim.x));
+    bh = uniform32(pid / blocks_q);
+    qblk = uniform32(pid % blocks_q);
+  }
   const int wg_q0 = qblk * QPB;
   const int q0 = uniform32(wg_q0 + wave * QW);
   const int b = bh / (int)p.heads, h = bh % (int)p.heads;
@@ -674,9 +698,19 @@ __global__ void __launch_bounds__(NW * 64) attention_bwd_dkv_d64(AttnBwdArgs p) 
   const int blocks_k = (T + KPB - 1) / KPB;
   // key blocks of one (batch, kv head) on one XCD; the first key blocks see
   // the most queries (causal) and start first
-  const int pid = uniform32(xcd_remap(blockIdx.x, gridDim.x));
-  const int bkh = uniform32(pid / blocks_k);
-  const int k0 = uniform32((pid % blocks_k) * KPB);
+  // as in the forward: causal key blocks in work order (the first keys see
+  // the most queries), non-causal ones grouped per XCD
+  int bkh, kblk;
+  if (p.causal) {
+    const int nbh = (int)(p.batch * p.kv_heads);
+    bkh = uniform32((int)blockIdx.x % nbh);
+    kblk = uniform32((int)blockIdx.x / nbh);
+  } else {
+    const int pid = uniform32(xcd_remap(blockIdx.x, gridDim.x));
+    bkh = uniform32(pid / blocks_k);
+    kblk = uniform32(pid % blocks_k);
+  }
+  const int k0 = uniform32(kblk * KPB);
   const int kw = uniform32(k0 + wave * KW);
   const int b = bkh / (int)p.kv_heads, kvh = bkh % (int)p.kv_heads;
   const int group = (int)(p.heads / p.kv_heads);
