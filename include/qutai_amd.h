@@ -98,6 +98,11 @@ int qutai_amd_fill(void* dst, int64_t n, double value, int dtype, void* stream);
  * `cuda.add` for gradient accumulation (src/qutai/core/grad.py:60). */
 int qutai_amd_add(const void* left, const void* right, void* out, int64_t n, int dtype, void* stream);
 
+/* out = x * factor (element-wise, fp32 math for bf16).  Replaces `cuda.scale`
+ * (src/qutai/backends/cuda.py:198), used by the lm loss head
+ * (src/qutai/lm/layers.py:212). */
+int qutai_amd_scale(const void* x, void* out, int64_t n, double factor, int dtype, void* stream);
+
 /* out[r][c] = x[r][c] + bias[c] (rows x cols; one rounding).  The bias add
  * of nn.Linear (src/qutai/nn/layers.py:145-148, a broadcast `add`) and the
  * broadcast of a scalar gradient (cols = 1). */
@@ -249,6 +254,70 @@ int qutai_amd_attention_bwd(const void* grad, const void* q, const void* k, cons
                             const float* lse, void* dq, void* dk, void* dv, float* delta, int64_t batch,
                             int64_t heads, int64_t kv_heads, int64_t time, int64_t dim, int dtype, int layout,
                             double scale, int causal, void* stream);
+
+/* ---- decoder glue around the contractions (a full Decoder.loss step) ----
+ * Activation dtype QA_BF16 or QA_F32; embedding / RMSNorm weights, RMSNorm
+ * outputs and statistics, embedding gradients and head losses are fp32 (the
+ * reference's accumulation type for both activation types). */
+
+/* out[r] = weight[ids[r]] (count rows of width) in out_dtype.  Replaces
+ * `cuda_lm.embedding` / `lm_embedding` (src/qutai/backends/cuda_lm.py:77-93,
+ * cuda/lm.cu:30). */
+int qutai_amd_embedding(const float* weight, const int64_t* ids, void* out, int64_t count, int64_t width,
+                        int out_dtype, void* stream);
+
+/* out[tokens[g]] = sum of gradient rows rows[offsets[g] .. offsets[g+1]) (input
+ * order) for each of `groups` distinct tokens; other rows of out untouched.
+ * Replaces `cuda_lm.embedding_backward` / `lm_embedding_backward`
+ * (cuda_lm.py:96-123, cuda/lm.cu:32-38). */
+int qutai_amd_embedding_backward(const void* gradient, const int64_t* tokens, const int64_t* offsets,
+                                 const int64_t* rows, float* out, int64_t groups, int64_t width, int dtype,
+                                 void* stream);
+
+/* inverse[r] = 1/sqrt(mean(x[r]^2) + eps), out = x * inverse * weight.
+ * Replaces `cuda_lm.rms_norm` / `lm_rms` (cuda_lm.py:126-145, cuda/lm.cu:39-45). */
+int qutai_amd_rms_norm(const void* x, const float* weight, float* out, float* inverse, int64_t rows, int64_t width,
+                       double eps, int dtype, void* stream);
+
+/* Floats of the `partial` workspace qutai_amd_rms_norm_backward needs. */
+int64_t qutai_amd_rms_norm_workspace(int64_t rows, int64_t width);
+
+/* dx = inverse * (g w - x inverse^2 mean(g w x)) (dx in the activation dtype),
+ * dweight[j] = sum_r g x inverse (fp32, fixed-order chunked sum through
+ * `partial`).  Replaces `cuda_lm.rms_norm_backward` / `lm_rms_dx` / `lm_rms_dw`
+ * (cuda_lm.py:148-177, cuda/lm.cu:46-52). */
+int qutai_amd_rms_norm_backward(const float* gradient, const void* x, const float* weight, const float* inverse,
+                                void* dx, float* dweight, float* partial, int64_t rows, int64_t width, int dtype,
+                                void* stream);
+
+/* out = x sigmoid(x), or with backward = 1 out = g s (1 + x (1 - s)).
+ * Replaces `cuda_lm.silu` / `silu_backward` (cuda_lm.py:180-207, cuda/lm.cu:54). */
+int qutai_amd_silu(const void* x, const void* gradient, void* out, int64_t n, int backward, int dtype,
+                   void* stream);
+
+/* Rotary embedding of [batch][time][heads][dim] pairs (2i, 2i+1) by the angle
+ * (offset + t) theta^(-d/dim), d = 2 (i mod dim/2); inverse rotates back.
+ * Replaces `cuda_lm.rope` / `lm_rope` (cuda_lm.py:210-226, cuda/lm.cu:55-59). */
+int qutai_amd_rope(const void* x, void* out, int64_t batch, int64_t time, int64_t heads, int64_t dim, double theta,
+                   int64_t offset, int inverse, int dtype, void* stream);
+
+/* The rows start .. start+count of the (time-1) prediction positions of every
+ * sequence of a [.][time][width] block (backward = 1: add them back into it).
+ * Replaces `cuda_lm.head_rows` / `head_rows_backward` / `lm_head_rows`
+ * (cuda_lm.py:584-613, cuda/lm.cu:425-427). */
+int qutai_amd_head_rows(const void* x, void* out, int64_t count, int64_t start, int64_t width, int64_t time,
+                        int backward, int dtype, void* stream);
+
+/* out[r] = log sum exp(logits[r] - max) - (logits[r][label] - max), 0 for label
+ * -100.  Replaces `lm_head_loss` (cuda_lm.py:629-643, cuda/lm.cu:428-433). */
+int qutai_amd_head_loss(const void* logits, const int64_t* labels, float* out, int64_t rows, int64_t vocab,
+                        int dtype, void* stream);
+
+/* In place: logits = gradient[0] * factor * (softmax(logits) - onehot(label)),
+ * 0 for label -100.  Replaces `lm_head_gradient` (cuda_lm.py:646-660,
+ * cuda/lm.cu:434-440). */
+int qutai_amd_head_gradient(void* logits, const int64_t* labels, const float* gradient, int64_t rows, int64_t vocab,
+                            double factor, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

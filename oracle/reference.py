@@ -12,7 +12,11 @@ Contents
     cpu.py:231-237), ``silu`` (cpu_lm.py:107-111), ``routing``
     (cpu_lm.py:204-242), ``route_gather`` (cpu_lm.py:279-283), ``combine``
     (cpu_lm.py:294-303), ``routing_backward`` (cpu_lm.py:245-276),
-    ``combine_backward`` (cpu_lm.py:306-320), ``attention`` / ``attention_backward``
+    ``combine_backward`` (cpu_lm.py:306-320), the decoder glue ``embedding`` /
+    ``embedding_backward`` / ``rms_norm`` / ``rms_norm_backward`` /
+    ``silu_backward`` / ``rope`` / ``head_rows`` / ``head_rows_backward`` /
+    ``head_loss`` / ``head_gradient`` (cpu_lm.py:54-138, 323-371),
+    ``attention`` / ``attention_backward``
     (cpu_lm.py:141-201), ``bf16`` (the RNE encoder of cuda.py:98-101 /
     tests/test_bfloat16_storage.py:10-16);
   * ``gemm_f64``: the same float64 sequential-k GEMM compiled from
@@ -33,7 +37,7 @@ import ctypes
 import os
 import struct
 import subprocess
-from math import exp, fsum, log, prod
+from math import cos, exp, fsum, log, prod, sin, sqrt
 from pathlib import Path
 
 import numpy as np
@@ -299,6 +303,110 @@ def attention_backward_np(g, q, k, v, out, lse, *, scale=None):
     delta = (g * out).sum(axis=1, keepdims=True)
     ds = p * (g @ v.T - delta) * scale
     return ds @ k, ds.T @ q, p.T @ g
+
+
+# ---- decoder glue (cpu_lm.py) --------------------------------------------------
+
+def embedding(weight, ids, width) -> list[float]:
+    """cpu_lm.embedding (src/qutai/backends/cpu_lm.py:54-58)."""
+    return [weight[token * width + j] for token in ids for j in range(width)]
+
+
+def embedding_backward(gradient, ids, count, width) -> list[float]:
+    """cpu_lm.embedding_backward (cpu_lm.py:61-66)."""
+    result = [0.0] * (count * width)
+    for i, token in enumerate(ids):
+        for j in range(width):
+            result[token * width + j] += gradient[i * width + j]
+    return result
+
+
+def rms_norm(values, weight, width, eps):
+    """cpu_lm.rms_norm (cpu_lm.py:69-81): (out, inverse)."""
+    rows = len(values) // width
+    out, inverse = [0.0] * len(values), [0.0] * rows
+    for row in range(rows):
+        inv = 1 / sqrt(sum(values[row * width + j] ** 2 for j in range(width)) / width + eps)
+        inverse[row] = inv
+        for j in range(width):
+            out[row * width + j] = values[row * width + j] * inv * weight[j]
+    return out, inverse
+
+
+def rms_norm_backward(gradient, values, weight, inverse, width):
+    """cpu_lm.rms_norm_backward (cpu_lm.py:84-104): (dx, dw)."""
+    dx, dw = [0.0] * len(values), [0.0] * width
+    for row in range(len(inverse)):
+        inv = inverse[row]
+        projected = sum(gradient[row * width + j] * weight[j] * values[row * width + j] for j in range(width)) / width
+        for j in range(width):
+            i = row * width + j
+            dx[i] = inv * (gradient[i] * weight[j] - values[i] * inv * inv * projected)
+            dw[j] += gradient[i] * values[i] * inv
+    return dx, dw
+
+
+def silu_backward(gradient, values) -> list[float]:
+    """cpu_lm.silu_backward (cpu_lm.py:114-122)."""
+    out = []
+    for g, x in zip(gradient, values):
+        s = 1 / (1 + exp(-x)) if x >= 0 else exp(x) / (1 + exp(x))
+        out.append(g * s * (1 + x * (1 - s)))
+    return out
+
+
+def rope(values, batch, time, heads, dim, theta, offset=0, inverse=False) -> list[float]:
+    """cpu_lm.rope (cpu_lm.py:125-138)."""
+    out = [0.0] * len(values)
+    for b in range(batch):
+        for t in range(time):
+            for h in range(heads):
+                for j in range(0, dim, 2):
+                    angle = (offset + t) * theta ** (-j / dim) * (-1 if inverse else 1)
+                    c, s = cos(angle), sin(angle)
+                    i = ((b * time + t) * heads + h) * dim + j
+                    out[i], out[i + 1] = values[i] * c - values[i + 1] * s, values[i] * s + values[i + 1] * c
+    return out
+
+
+def head_rows(values, start, count, width, time) -> list[float]:
+    """cpu_lm.head_rows (cpu_lm.py:323-331)."""
+    return [values[(row // (time - 1) * time + row % (time - 1)) * width + j]
+            for row in range(start, start + count) for j in range(width)]
+
+
+def head_rows_backward(target, gradient, start, count, width, time):
+    """cpu_lm.head_rows_backward (cpu_lm.py:334-338), in place on the list."""
+    for row in range(count):
+        at = (start + row) // (time - 1) * time + (start + row) % (time - 1)
+        for j in range(width):
+            target[at * width + j] += gradient[row * width + j]
+
+
+def head_loss(logits, labels, rows, vocab, *, start=0) -> float:
+    """cpu_lm.head_loss (cpu_lm.py:345-355): summed cross entropy, -100 ignored."""
+    result = 0.0
+    for row in range(rows):
+        label = labels[start + row]
+        if label == -100:
+            continue
+        peak = max(logits[row * vocab + j] for j in range(vocab))
+        result += log(sum(exp(logits[row * vocab + j] - peak) for j in range(vocab))) - (
+            logits[row * vocab + label] - peak)
+    return result
+
+
+def head_gradient(logits, labels, rows, vocab, gradient, count, *, start=0) -> list[float]:
+    """cpu_lm.head_gradient (cpu_lm.py:358-371), returned as a new list."""
+    out = list(logits)
+    for row in range(rows):
+        label = labels[start + row]
+        peak = max(logits[row * vocab + j] for j in range(vocab))
+        total = sum(exp(logits[row * vocab + j] - peak) for j in range(vocab))
+        for j in range(vocab):
+            out[row * vocab + j] = (0 if label == -100 else
+                                    gradient[0] / count * (exp(logits[row * vocab + j] - peak) / total - (j == label)))
+    return out
 
 
 # ---- compiled float64 GEMM -----------------------------------------------------

@@ -295,6 +295,35 @@ def add(left: AMDStorage, right: AMDStorage) -> AMDStorage:
     return result
 
 
+def scale(values: AMDStorage, factor: float) -> AMDStorage:
+    """values * factor (cuda.py:198)."""
+    result = AMDStorage(values.size, values.dtype)
+    if values.size:
+        result.runtime.call("qutai_amd_scale", values.ptr, result.ptr, values.size, float(factor), code(values.dtype))
+    return result
+
+
+def concatenate(values, shapes, axis=0) -> AMDStorage:
+    """Concatenation along ``axis`` (cuda.py:383-394): the pieces of every
+    outer index copied device to device, in order."""
+    rank = len(shapes[0])
+    axis = axis % rank
+    if len({v.dtype for v in values}) != 1 or any(len(s) != rank for s in shapes):
+        raise ValueError("concatenate needs storages of one dtype and shapes of one rank")
+    outer = prod(shapes[0][:axis])
+    sizes = [prod(shape[axis:]) for shape in shapes]
+    total = sum(sizes)
+    result = AMDStorage(outer * total, values[0].dtype)
+    item = _TYPES[values[0].dtype][1]
+    start = 0
+    for data, size in zip(values, sizes):
+        for o in range(outer):
+            if size:
+                result.runtime.copy(result.ptr + (o * total + start) * item, data.ptr + o * size * item, size * item)
+        start += size
+    return result
+
+
 def transpose(values: AMDStorage, shape, axes=None) -> AMDStorage:
     """Transpose that swaps the last two axes (the form the matmul gradient
     uses, src/qutai/core/operations/linalg.py:37-38)."""

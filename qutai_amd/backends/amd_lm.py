@@ -348,3 +348,154 @@ def attention_backward(gradient, q, k, v, out, lse, batch, time, heads, kv_heads
                         dv.ptr, delta.ptr, batch, heads, kv_heads, time, dim, code(q.dtype), layout, float(scale),
                         int(bool(causal)), mfma=q.dtype == "bfloat16" and dim == 64)
     return dq, dk, dv
+
+
+# ---- decoder glue (the rest of a Decoder.loss step) ---------------------------------
+
+def _acc_dtype(dtype):
+    """Accumulation dtype of the activations (cuda_lm.py:9-11): fp32 for bf16/fp32."""
+    if dtype not in ("bfloat16", "float32"):
+        raise ValueError("amd lm kernels take bfloat16 or float32 activations")
+    return "float32"
+
+
+def add_into(target, source):
+    """target += source, element-wise in target's dtype (cuda_lm.py:64-73)."""
+    if target.dtype != source.dtype or target.size != source.size:
+        raise ValueError("add_into needs storages of equal dtype and size")
+    if target.size:
+        target.runtime.call("qutai_amd_add", target.ptr, source.ptr, target.ptr, target.size, code(target.dtype))
+
+
+def embedding(weight, ids, width, *, out_dtype=None):
+    """Rows of the fp32 embedding table for the host token ids
+    (cuda_lm.py:77-93), in out_dtype (default the table's)."""
+    dtype = out_dtype or weight.dtype
+    if _acc_dtype(dtype) != weight.dtype:
+        raise ValueError("the embedding table must be in the activations' accumulation dtype")
+    ids = [int(t) for t in ids]
+    result = AMDStorage(len(ids) * width, dtype)
+    if result.size:
+        identifiers = amd.storage(ids, dtype="int64")
+        result.runtime.call("qutai_amd_embedding", weight.ptr, identifiers.ptr, result.ptr, len(ids), width,
+                            code(dtype))
+    return result
+
+
+def embedding_backward(gradient, ids, count, width):
+    """Table gradient [count][width] (fp32): each token's gradient rows summed
+    in input order (cuda_lm.py:96-123)."""
+    groups = {}
+    for row, token in enumerate(ids):
+        groups.setdefault(int(token), []).append(row)
+    tokens = sorted(groups)
+    offsets, positions = [0], []
+    for token in tokens:
+        positions.extend(groups[token])
+        offsets.append(len(positions))
+    result = amd.full(count * width, 0.0, dtype=_acc_dtype(gradient.dtype))
+    if tokens and width:
+        # keep the index uploads referenced until the launch: freed storage is reused at once
+        index = [amd.storage(values, dtype="int64") for values in (tokens, offsets, positions)]
+        result.runtime.call("qutai_amd_embedding_backward", gradient.ptr, *(t.ptr for t in index), result.ptr,
+                            len(tokens), width, code(gradient.dtype))
+    return result
+
+
+def rms_norm(values, weight, width, eps):
+    """(out, inverse) of RMSNorm over rows of width (cuda_lm.py:126-145); both fp32."""
+    acc = _acc_dtype(values.dtype)
+    if weight.dtype != acc or weight.size != width:
+        raise ValueError("rms_norm needs an fp32 weight of width values")
+    rows = values.size // width
+    out, inverse = AMDStorage(values.size, acc), AMDStorage(rows, acc)
+    if rows:
+        out.runtime.call("qutai_amd_rms_norm", values.ptr, weight.ptr, out.ptr, inverse.ptr, rows, width, float(eps),
+                         code(values.dtype))
+    return out, inverse
+
+
+def rms_norm_backward(gradient, values, weight, inverse, width):
+    """(dx in the activation dtype, dweight fp32) (cuda_lm.py:148-177)."""
+    rows = values.size // width
+    g = gradient if gradient.dtype == "float32" else amd.from_storage(gradient, dtype="float32")
+    dx, dw = AMDStorage(values.size, values.dtype), AMDStorage(width, weight.dtype)
+    if rows:
+        runtime = get_runtime()
+        partial = AMDStorage(runtime.lib.qutai_amd_rms_norm_workspace(rows, width), "float32")
+        runtime.call("qutai_amd_rms_norm_backward", g.ptr, values.ptr, weight.ptr, inverse.ptr, dx.ptr, dw.ptr,
+                     partial.ptr, rows, width, code(values.dtype))
+    return dx, dw
+
+
+def silu(values):
+    """x * sigmoid(x) (cuda_lm.py:180-192)."""
+    out = AMDStorage(values.size, values.dtype)
+    if values.size:
+        out.runtime.call("qutai_amd_silu", values.ptr, None, out.ptr, values.size, 0, code(values.dtype))
+    return out
+
+
+def silu_backward(gradient, values):
+    """g * s * (1 + x (1 - s)) (cuda_lm.py:195-207)."""
+    out = AMDStorage(values.size, values.dtype)
+    if values.size:
+        out.runtime.call("qutai_amd_silu", values.ptr, gradient.ptr, out.ptr, values.size, 1, code(values.dtype))
+    return out
+
+
+def rope(values, batch, time, heads, dim, theta, offset=0, inverse=False):
+    """Rotary embedding of [batch][time][heads][dim] (cuda_lm.py:210-226)."""
+    result = AMDStorage(values.size, values.dtype)
+    if result.size:
+        result.runtime.call("qutai_amd_rope", values.ptr, result.ptr, batch, time, heads, dim, float(theta), offset,
+                            int(bool(inverse)), code(values.dtype))
+    return result
+
+
+def head_rows(values, start, count, width, time):
+    """Rows start .. start+count of the prediction positions (cuda_lm.py:584-598)."""
+    result = AMDStorage(count * width, values.dtype)
+    if result.size:
+        result.runtime.call("qutai_amd_head_rows", values.ptr, result.ptr, count, start, width, time, 0,
+                            code(values.dtype))
+    return result
+
+
+def head_rows_backward(target, gradient, start, count, width, time):
+    """target[prediction rows] += gradient (cuda_lm.py:601-613)."""
+    if count * width:
+        target.runtime.call("qutai_amd_head_rows", gradient.ptr, target.ptr, count, start, width, time, 1,
+                            code(target.dtype))
+
+
+def prepare_labels(labels):
+    """Labels resident on the device as int64 (cuda_lm.py:616-617)."""
+    return amd.storage([int(x) for x in labels], dtype="int64")
+
+
+def _head_labels(labels, start, rows):
+    ids = labels if isinstance(labels, AMDStorage) else prepare_labels(labels)
+    if ids.dtype != "int64" or start < 0 or start + rows > ids.size:
+        raise ValueError("invalid head label storage or range")
+    return ids, ids.ptr + 8 * start
+
+
+def head_loss(logits, labels, rows, vocab, *, start=0):
+    """Summed cross entropy of rows of logits (label -100 ignored), one fp32
+    value (cuda_lm.py:629-643)."""
+    _, pointer = _head_labels(labels, start, rows)
+    values = AMDStorage(rows, _acc_dtype(logits.dtype))
+    if rows:
+        values.runtime.call("qutai_amd_head_loss", logits.ptr, pointer, values.ptr, rows, vocab, code(logits.dtype))
+    return amd.sum_all(values) if rows else amd.full(1, 0.0, dtype=values.dtype)
+
+
+def head_gradient(logits, labels, rows, vocab, gradient, count, *, start=0):
+    """In place: logits = g / count * (softmax - onehot) (cuda_lm.py:646-660)."""
+    _, pointer = _head_labels(labels, start, rows)
+    g = gradient if gradient.dtype == "float32" else amd.from_storage(gradient, dtype="float32")
+    if rows:
+        logits.runtime.call("qutai_amd_head_gradient", logits.ptr, pointer, g.ptr, rows, vocab, 1.0 / count,
+                            code(logits.dtype))
+    return logits

@@ -55,11 +55,22 @@ SIGNATURES = {
     "qutai_amd_gemm_grouped_k": [_p, _p, _p, _p, _i32, _i64, _i64, _i64, _i32, _i32, _i32, _p],
     "qutai_amd_combine_backward": [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p],
     "qutai_amd_route_backward": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p],
+    "qutai_amd_scale": [_p, _p, _i64, _f64, _i32, _p],
+    "qutai_amd_embedding": [_p, _p, _p, _i64, _i64, _i32, _p],
+    "qutai_amd_embedding_backward": [_p, _p, _p, _p, _p, _i64, _i64, _i32, _p],
+    "qutai_amd_rms_norm": [_p, _p, _p, _p, _i64, _i64, _f64, _i32, _p],
+    "qutai_amd_rms_norm_workspace": [_i64, _i64],
+    "qutai_amd_rms_norm_backward": [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p],
+    "qutai_amd_silu": [_p, _p, _p, _i64, _i32, _i32, _p],
+    "qutai_amd_rope": [_p, _p, _i64, _i64, _i64, _i64, _f64, _i64, _i32, _i32, _p],
+    "qutai_amd_head_rows": [_p, _p, _i64, _i64, _i64, _i64, _i32, _i32, _p],
+    "qutai_amd_head_loss": [_p, _p, _p, _i64, _i64, _i32, _p],
+    "qutai_amd_head_gradient": [_p, _p, _p, _i64, _i64, _f64, _i32, _p],
     "qutai_amd_attention_fwd": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _f64, _i32, _p],
     "qutai_amd_attention_bwd": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _f64,
                                 _i32, _p],
 }
-RESTYPES = {"qutai_amd_gemm_workspace_size": _sz}
+RESTYPES = {"qutai_amd_gemm_workspace_size": _sz, "qutai_amd_rms_norm_workspace": _i64}
 
 
 def _hip_library():

@@ -1,0 +1,358 @@
+// Decoder glue kernels of the lm path (C ABI `qutai_amd_embedding`, `_rms_norm`,
+// `_silu`, `_rope`, `_head_*`): the element-wise and row work around the
+// contractions that a `Decoder.loss` step needs (src/qutai/backends/cuda/lm.cu:
+// 30-59, 417-444, driven by src/qutai/backends/cuda_lm.py:64-228, 584-660).
+// Activations are bf16 or fp32; statistics, RMSNorm/embedding weights and
+// every sum are fp32 (the reference's accumulation type for both).  All
+// reductions run in a fixed order, so results are bit-repeatable.
+#include "common.h"
+#include "qutai_amd.h"
+
+using namespace qa;
+
+namespace {
+
+template <class T> __device__ __forceinline__ float get(const T* p, int64_t i);
+template <> __device__ __forceinline__ float get<float>(const float* p, int64_t i) { return p[i]; }
+template <> __device__ __forceinline__ float get<bf16_t>(const bf16_t* p, int64_t i) { return bf16_to_f32(p[i]); }
+template <class T> __device__ __forceinline__ void put(T* p, int64_t i, float x);
+template <> __device__ __forceinline__ void put<float>(float* p, int64_t i, float x) { p[i] = x; }
+template <> __device__ __forceinline__ void put<bf16_t>(bf16_t* p, int64_t i, float x) { p[i] = f32_to_bf16(x); }
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int o = 32; o; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int o = 32; o; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+
+constexpr int ROWS_PER_BLOCK = 4;  // one wave per row, 4 waves per workgroup
+
+unsigned blocks_for(int64_t n, int64_t per_block = 256) {
+  int64_t b = (n + per_block - 1) / per_block;
+  return (unsigned)(b < 1 ? 1 : b > (1 << 20) ? (1 << 20) : b);
+}
+#define GRID_STRIDE(i, n) \
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < (n); i += (int64_t)gridDim.x * blockDim.x)
+
+// out[r][j] = w[ids[r]][j], fp32 table -> activation dtype (lm.cu:30)
+template <class T>
+__global__ void embedding_kernel(const float* w, const int64_t* ids, T* out, int64_t n, int64_t width) {
+  GRID_STRIDE(i, n) put<T>(out, i, w[ids[i / width] * width + i % width]);
+}
+
+// out[tokens[g]][f] = sum over the rows of group g (input order) of grad[row][f]
+// (lm.cu:32-38); rows of tokens that do not occur are not touched.
+template <class T>
+__global__ void embedding_grad_kernel(const T* g, const int64_t* tokens, const int64_t* offsets,
+                                      const int64_t* rows, float* out, int64_t n, int64_t width) {
+  GRID_STRIDE(i, n) {
+    const int64_t group = i / width, f = i % width;
+    float total = 0.f;
+    for (int64_t p = offsets[group]; p < offsets[group + 1]; p++) total += get<T>(g, rows[p] * width + f);
+    out[tokens[group] * width + f] = total;
+  }
+}
+
+// RMSNorm forward, one wave per row: inv = 1/sqrt(mean(x^2) + eps),
+// out = x * inv * w (fp32 out and inv, lm.cu:39-45)
+template <class T>
+__global__ void __launch_bounds__(256) rms_kernel(const T* x, const float* w, float* out, float* inv, int64_t rows,
+                                                  int64_t width, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* xr = x + row * width;
+  float total = 0.f;
+  for (int64_t j = lane; j < width; j += 64) {
+    const float v = get<T>(xr, j);
+    total += v * v;
+  }
+  const float scale = 1.f / sqrtf(wave_sum(total) / (float)width + eps);
+  if (lane == 0) inv[row] = scale;
+  for (int64_t j = lane; j < width; j += 64) out[row * width + j] = get<T>(xr, j) * scale * w[j];
+}
+
+// dx = inv * (g w - x inv^2 mean(g w x)), one wave per row (lm.cu:46-51)
+template <class T>
+__global__ void __launch_bounds__(256) rms_dx_kernel(const float* g, const T* x, const float* w, const float* inv,
+                                                     T* dx, int64_t rows, int64_t width) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  float total = 0.f;
+  for (int64_t j = lane; j < width; j += 64) total += g[row * width + j] * w[j] * get<T>(x, row * width + j);
+  const float projected = wave_sum(total) / (float)width, scale = inv[row];
+  for (int64_t j = lane; j < width; j += 64) {
+    const int64_t at = row * width + j;
+    put<T>(dx, at, scale * (g[at] * w[j] - get<T>(x, at) * scale * scale * projected));
+  }
+}
+
+// dw[j] = sum_r g x inv over rows (lm.cu:52): chunks of RC rows write
+// partial sums, then one thread per column adds the chunks in order
+constexpr int RC = 64;
+template <class T>
+__global__ void rms_dw_partial_kernel(const float* g, const T* x, const float* inv, float* partial, int64_t rows,
+                                      int64_t width) {
+  const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t chunk = blockIdx.y;
+  if (j >= width) return;
+  const int64_t r0 = chunk * RC, r1 = min(rows, r0 + RC);
+  float total = 0.f;
+  for (int64_t r = r0; r < r1; r++) total += g[r * width + j] * get<T>(x, r * width + j) * inv[r];
+  partial[chunk * width + j] = total;
+}
+__global__ void rms_dw_final_kernel(const float* partial, float* dw, int64_t chunks, int64_t width) {
+  GRID_STRIDE(j, width) {
+    float total = 0.f;
+    for (int64_t c = 0; c < chunks; c++) total += partial[c * width + j];
+    dw[j] = total;
+  }
+}
+
+__device__ __forceinline__ float sigmoid(float v) {
+  return v >= 0.f ? 1.f / (1.f + expf(-v)) : expf(v) / (1.f + expf(v));
+}
+// silu (backward = 0) or its derivative times g (lm.cu:54)
+template <class T>
+__global__ void silu_kernel(const T* x, const T* g, T* out, int64_t n, int backward) {
+  GRID_STRIDE(i, n) {
+    const float v = get<T>(x, i), s = sigmoid(v);
+    put<T>(out, i, backward ? get<T>(g, i) * s * (1.f + v * (1.f - s)) : v * s);
+  }
+}
+
+// rotary embedding of the pairs (2i, 2i+1) of [batch][time][heads][dim]:
+// angle (offset + t) * theta^(-d/dim), d = 2 (i mod dim/2); inverse rotates
+// back (lm.cu:55-59)
+template <class T>
+__global__ void rope_kernel(const T* x, T* out, int64_t pairs, int64_t time, int64_t heads, int64_t dim, float theta,
+                            int64_t offset, int inverse) {
+  GRID_STRIDE(i, pairs) {
+    const int64_t at = 2 * i, d = (i % (dim / 2)) * 2, t = (i / (heads * (dim / 2))) % time;
+    const float a = (float)(offset + t) * powf(theta, -(float)d / (float)dim) * (inverse ? -1.f : 1.f);
+    float s, c;
+    sincosf(a, &s, &c);
+    const float x0 = get<T>(x, at), x1 = get<T>(x, at + 1);
+    put<T>(out, at, x0 * c - x1 * s);
+    put<T>(out, at + 1, x0 * s + x1 * c);
+  }
+}
+
+// rows start.. of the (time-1)-long prediction positions of every sequence
+// (lm.cu:425-427); backward adds the rows back into the [.. time ..] layout
+template <class T>
+__global__ void head_rows_kernel(const T* x, T* out, int64_t n, int64_t start, int64_t width, int64_t time,
+                                 int backward) {
+  GRID_STRIDE(i, n) {
+    const int64_t row = start + i / width;
+    const int64_t at = ((row / (time - 1)) * time + row % (time - 1)) * width + i % width;
+    if (backward) put<T>(out, at, get<T>(out, at) + get<T>(x, i));
+    else put<T>(out, i, get<T>(x, at));
+  }
+}
+
+// per-row cross entropy log(sum exp(l - max)) - (l[label] - max); label
+// -100 -> 0 (lm.cu:428-433).  One wave per row.
+template <class T>
+__global__ void __launch_bounds__(256) head_loss_kernel(const T* logits, const int64_t* labels, float* out,
+                                                        int64_t rows, int64_t vocab) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* l = logits + row * vocab;
+  float peak = -INFINITY;
+  for (int64_t c = lane; c < vocab; c += 64) peak = fmaxf(peak, get<T>(l, c));
+  peak = wave_max(peak);
+  float total = 0.f;
+  for (int64_t c = lane; c < vocab; c += 64) total += expf(get<T>(l, c) - peak);
+  total = wave_sum(total);
+  const int64_t label = labels[row];
+  if (lane == 0) out[row] = label == -100 ? 0.f : logf(total) - (get<T>(l, label) - peak);
+}
+
+// in place: logits = g * factor * (softmax - onehot(label)); label -100 -> 0
+// (lm.cu:434-440)
+template <class T>
+__global__ void __launch_bounds__(256) head_gradient_kernel(T* logits, const int64_t* labels, const float* gradient,
+                                                            int64_t rows, int64_t vocab, float factor) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  T* l = logits + row * vocab;
+  float peak = -INFINITY;
+  for (int64_t c = lane; c < vocab; c += 64) peak = fmaxf(peak, get<T>(l, c));
+  peak = wave_max(peak);
+  float total = 0.f;
+  for (int64_t c = lane; c < vocab; c += 64) total += expf(get<T>(l, c) - peak);
+  total = wave_sum(total);
+  const int64_t label = labels[row];
+  const float scale = gradient[0] * factor;
+  for (int64_t c = lane; c < vocab; c += 64) {
+    const float v = label == -100 ? 0.f : scale * (expf(get<T>(l, c) - peak) / total - (c == label ? 1.f : 0.f));
+    put<T>(l, c, v);
+  }
+}
+
+bool act_dtype(int d) { return d == F32 || d == BF16; }
+
+}  // namespace
+
+extern "C" {
+
+int qutai_amd_embedding(const float* weight, const int64_t* ids, void* out, int64_t count, int64_t width,
+                        int out_dtype, void* stream) {
+  if (count < 0 || width < 0 || !act_dtype(out_dtype)) return QA_EINVAL;
+  const int64_t n = count * width;
+  if (n == 0) return QA_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (out_dtype == BF16)
+    hipLaunchKernelGGL(embedding_kernel<bf16_t>, dim3(blocks_for(n)), dim3(256), 0, s, weight, ids, (bf16_t*)out, n,
+                       width);
+  else
+    hipLaunchKernelGGL(embedding_kernel<float>, dim3(blocks_for(n)), dim3(256), 0, s, weight, ids, (float*)out, n,
+                       width);
+  return (int)hipGetLastError();
+}
+
+int qutai_amd_embedding_backward(const void* gradient, const int64_t* tokens, const int64_t* offsets,
+                                 const int64_t* rows, float* out, int64_t groups, int64_t width, int dtype,
+                                 void* stream) {
+  if (groups < 0 || width < 0 || !act_dtype(dtype)) return QA_EINVAL;
+  const int64_t n = groups * width;
+  if (n == 0) return QA_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == BF16)
+    hipLaunchKernelGGL(embedding_grad_kernel<bf16_t>, dim3(blocks_for(n)), dim3(256), 0, s, (const bf16_t*)gradient,
+                       tokens, offsets, rows, out, n, width);
+  else
+    hipLaunchKernelGGL(embedding_grad_kernel<float>, dim3(blocks_for(n)), dim3(256), 0, s, (const float*)gradient,
+                       tokens, offsets, rows, out, n, width);
+  return (int)hipGetLastError();
+}
+
+int qutai_amd_rms_norm(const void* x, const float* weight, float* out, float* inverse, int64_t rows, int64_t width,
+                       double eps, int dtype, void* stream) {
+  if (rows < 0 || width <= 0 || !act_dtype(dtype)) return QA_EINVAL;
+  if (rows == 0) return QA_OK;
+  const unsigned blocks = (unsigned)((rows + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK);
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == BF16)
+    hipLaunchKernelGGL(rms_kernel<bf16_t>, dim3(blocks), dim3(256), 0, s, (const bf16_t*)x, weight, out, inverse,
+                       rows, width, (float)eps);
+  else
+    hipLaunchKernelGGL(rms_kernel<float>, dim3(blocks), dim3(256), 0, s, (const float*)x, weight, out, inverse, rows,
+                       width, (float)eps);
+  return (int)hipGetLastError();
+}
+
+int64_t qutai_amd_rms_norm_workspace(int64_t rows, int64_t width) {
+  return rows <= 0 || width <= 0 ? 0 : ((rows + RC - 1) / RC) * width;
+}
+
+int qutai_amd_rms_norm_backward(const float* gradient, const void* x, const float* weight, const float* inverse,
+                                void* dx, float* dweight, float* partial, int64_t rows, int64_t width, int dtype,
+                                void* stream) {
+  if (rows < 0 || width <= 0 || !act_dtype(dtype)) return QA_EINVAL;
+  hipStream_t s = (hipStream_t)stream;
+  if (rows == 0) return QA_OK;
+  if (!partial) return QA_EWORKSPACE;
+  const unsigned blocks = (unsigned)((rows + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK);
+  const int64_t chunks = (rows + RC - 1) / RC;
+  if (chunks > 65535) return QA_EINVAL;
+  const dim3 grid((unsigned)((width + 255) / 256), (unsigned)chunks);
+  if (dtype == BF16) {
+    hipLaunchKernelGGL(rms_dx_kernel<bf16_t>, dim3(blocks), dim3(256), 0, s, gradient, (const bf16_t*)x, weight,
+                       inverse, (bf16_t*)dx, rows, width);
+    hipLaunchKernelGGL(rms_dw_partial_kernel<bf16_t>, grid, dim3(256), 0, s, gradient, (const bf16_t*)x, inverse,
+                       partial, rows, width);
+  } else {
+    hipLaunchKernelGGL(rms_dx_kernel<float>, dim3(blocks), dim3(256), 0, s, gradient, (const float*)x, weight,
+                       inverse, (float*)dx, rows, width);
+    hipLaunchKernelGGL(rms_dw_partial_kernel<float>, grid, dim3(256), 0, s, gradient, (const float*)x, inverse,
+                       partial, rows, width);
+  }
+  hipLaunchKernelGGL(rms_dw_final_kernel, dim3(blocks_for(width)), dim3(256), 0, s, partial, dweight, chunks, width);
+  return (int)hipGetLastError();
+}
+
+int qutai_amd_silu(const void* x, const void* gradient, void* out, int64_t n, int backward, int dtype,
+                   void* stream) {
+  if (n < 0 || !act_dtype(dtype) || (backward && !gradient)) return QA_EINVAL;
+  if (n == 0) return QA_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == BF16)
+    hipLaunchKernelGGL(silu_kernel<bf16_t>, dim3(blocks_for(n)), dim3(256), 0, s, (const bf16_t*)x,
+                       (const bf16_t*)gradient, (bf16_t*)out, n, backward ? 1 : 0);
+  else
+    hipLaunchKernelGGL(silu_kernel<float>, dim3(blocks_for(n)), dim3(256), 0, s, (const float*)x,
+                       (const float*)gradient, (float*)out, n, backward ? 1 : 0);
+  return (int)hipGetLastError();
+}
+
+int qutai_amd_rope(const void* x, void* out, int64_t batch, int64_t time, int64_t heads, int64_t dim, double theta,
+                   int64_t offset, int inverse, int dtype, void* stream) {
+  if (batch < 0 || time < 0 || heads < 0 || dim <= 0 || dim % 2 || !act_dtype(dtype)) return QA_EINVAL;
+  const int64_t pairs = batch * time * heads * dim / 2;
+  if (pairs == 0) return QA_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == BF16)
+    hipLaunchKernelGGL(rope_kernel<bf16_t>, dim3(blocks_for(pairs)), dim3(256), 0, s, (const bf16_t*)x, (bf16_t*)out,
+                       pairs, time, heads, dim, (float)theta, offset, inverse ? 1 : 0);
+  else
+    hipLaunchKernelGGL(rope_kernel<float>, dim3(blocks_for(pairs)), dim3(256), 0, s, (const float*)x, (float*)out,
+                       pairs, time, heads, dim, (float)theta, offset, inverse ? 1 : 0);
+  return (int)hipGetLastError();
+}
+
+int qutai_amd_head_rows(const void* x, void* out, int64_t count, int64_t start, int64_t width, int64_t time,
+                        int backward, int dtype, void* stream) {
+  if (count < 0 || start < 0 || width < 0 || time < 2 || !act_dtype(dtype)) return QA_EINVAL;
+  const int64_t n = count * width;
+  if (n == 0) return QA_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == BF16)
+    hipLaunchKernelGGL(head_rows_kernel<bf16_t>, dim3(blocks_for(n)), dim3(256), 0, s, (const bf16_t*)x,
+                       (bf16_t*)out, n, start, width, time, backward ? 1 : 0);
+  else
+    hipLaunchKernelGGL(head_rows_kernel<float>, dim3(blocks_for(n)), dim3(256), 0, s, (const float*)x, (float*)out,
+                       n, start, width, time, backward ? 1 : 0);
+  return (int)hipGetLastError();
+}
+
+int qutai_amd_head_loss(const void* logits, const int64_t* labels, float* out, int64_t rows, int64_t vocab,
+                        int dtype, void* stream) {
+  if (rows < 0 || vocab <= 0 || !act_dtype(dtype)) return QA_EINVAL;
+  if (rows == 0) return QA_OK;
+  const unsigned blocks = (unsigned)((rows + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK);
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == BF16)
+    hipLaunchKernelGGL(head_loss_kernel<bf16_t>, dim3(blocks), dim3(256), 0, s, (const bf16_t*)logits, labels, out,
+                       rows, vocab);
+  else
+    hipLaunchKernelGGL(head_loss_kernel<float>, dim3(blocks), dim3(256), 0, s, (const float*)logits, labels, out,
+                       rows, vocab);
+  return (int)hipGetLastError();
+}
+
+int qutai_amd_head_gradient(void* logits, const int64_t* labels, const float* gradient, int64_t rows, int64_t vocab,
+                            double factor, int dtype, void* stream) {
+  if (rows < 0 || vocab <= 0 || !act_dtype(dtype)) return QA_EINVAL;
+  if (rows == 0) return QA_OK;
+  const unsigned blocks = (unsigned)((rows + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK);
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == BF16)
+    hipLaunchKernelGGL(head_gradient_kernel<bf16_t>, dim3(blocks), dim3(256), 0, s, (bf16_t*)logits, labels, gradient,
+                       rows, vocab, (float)factor);
+  else
+    hipLaunchKernelGGL(head_gradient_kernel<float>, dim3(blocks), dim3(256), 0, s, (float*)logits, labels, gradient,
+                       rows, vocab, (float)factor);
+  return (int)hipGetLastError();
+}
+
+}  // extern "C"

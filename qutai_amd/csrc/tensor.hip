@@ -53,6 +53,14 @@ __global__ void fill_kernel(void* dst, int64_t n, double value, int d) {
   }
 }
 
+__global__ void scale_kernel(const void* a, void* out, int64_t n, double factor, int d) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    if (d == F64) ((double*)out)[i] = ((const double*)a)[i] * factor;
+    else if (d == F32) ((float*)out)[i] = ((const float*)a)[i] * (float)factor;
+    else ((bf16_t*)out)[i] = f32_to_bf16(bf16_to_f32(((const bf16_t*)a)[i]) * (float)factor);
+  }
+}
+
 __global__ void add_kernel(const void* a, const void* b, void* out, int64_t n, int d) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
     if (d == F64) {
@@ -408,6 +416,13 @@ int qutai_amd_add(const void* left, const void* right, void* out, int64_t n, int
   if (n == 0) return QA_OK;
   hipLaunchKernelGGL(add_kernel, dim3(grid_for(n)), dim3(THREADS), 0, (hipStream_t)stream, left, right, out, n,
                      dtype);
+  return (int)hipGetLastError();
+}
+
+int qutai_amd_scale(const void* x, void* out, int64_t n, double factor, int dtype, void* stream) {
+  if (n < 0 || !float_dtype(dtype)) return QA_EINVAL;
+  if (n == 0) return QA_OK;
+  hipLaunchKernelGGL(scale_kernel, dim3(grid_for(n)), dim3(THREADS), 0, (hipStream_t)stream, x, out, n, factor, dtype);
   return (int)hipGetLastError();
 }
 

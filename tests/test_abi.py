@@ -17,7 +17,7 @@ LIBRARY = ROOT / "qutai_amd" / "libqutai_amd.so"
 def declared_functions():
     text = HEADER.read_text()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return re.findall(r"^\s*(?:int|size_t)\s+(qutai_amd_\w+)\s*\(", text, flags=re.M)
+    return re.findall(r"^\s*(?:int|size_t|int64_t)\s+(qutai_amd_\w+)\s*\(", text, flags=re.M)
 
 
 def test_header_declares_the_entry_points():
@@ -56,3 +56,6 @@ def test_bindings_apply_without_a_device():
     assert size(64, 64, 64, 1, 0, 0, 0, 0, 0, 0, 0) == 0
     # autocast of two fp32 operands: both copied
     assert size(64, 64, 64, 1, 0, 0, 0, 0, 0, 0, 1) == 2 * 64 * 64 * 2 + 256
+    # RMSNorm backward partial sums: one row of floats per 64 rows
+    rms = library.qutai_amd_rms_norm_workspace
+    assert rms(4096, 2048) == 64 * 2048 and rms(65, 8) == 2 * 8 and rms(0, 8) == 0

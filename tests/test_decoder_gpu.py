@@ -1,0 +1,155 @@
+"""Decoder glue kernels on the MI355X (the rest of a Decoder.loss step:
+embedding, RMSNorm, SiLU, RoPE, the loss head's rows / cross entropy /
+gradient, add_into, scale, concatenate) against the float64 oracle
+restatements of cpu_lm (src/qutai/backends/cpu_lm.py:49-138, 323-371).
+fp32 results within 1e-5 relative Frobenius error, bf16 results within
+1e-2, gathers and scatters exact."""
+from random import Random
+
+import numpy as np
+import pytest
+
+from oracle import reference as ora
+from tests.helpers import download, normal, stored, upload
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 1e-5
+BF16_TOL = 1e-2
+
+
+@pytest.fixture(scope="module")
+def lm():
+    from qutai_amd.backends import amd, amd_lm
+
+    amd.get_runtime()
+    return amd_lm
+
+
+@pytest.fixture(scope="module")
+def base():
+    from qutai_amd.backends import amd
+
+    return amd
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_embedding_forward_and_backward(lm, dtype):
+    vocab, width = 37, 24
+    table = normal(110, vocab * width)
+    ids = [Random(1).randrange(vocab) for _ in range(200)]
+    out = lm.embedding(upload(table, "float32"), ids, width, out_dtype=dtype)
+    expected = np.array(ora.embedding(stored(table, "float32").tolist(), ids, width))
+    assert download(out).tobytes() == stored(expected, dtype).astype(np.float32).tobytes()
+    g = normal(111, len(ids) * width)
+    grad = lm.embedding_backward(upload(g, dtype), ids, vocab, width)
+    assert grad.dtype == "float32"
+    reference = ora.embedding_backward(stored(g, dtype).tolist(), ids, vocab, width)
+    assert ora.rel_frobenius(download(grad), reference) <= FP32_TOL
+    with pytest.raises(ValueError):
+        lm.embedding(upload(table, "bfloat16"), ids, width)  # bf16 table: not the accumulation dtype
+
+
+@pytest.mark.parametrize("dtype,rows,width", [("float32", 37, 40), ("bfloat16", 300, 2048), ("float32", 4096, 2048)])
+def test_rms_norm_forward_and_backward(lm, dtype, rows, width):
+    eps = 1e-5
+    x = normal(112, rows * width, 2.0)
+    w = (1 + 0.1 * normal(113, width)).astype(np.float32)
+    g = normal(114, rows * width)
+    out, inv = lm.rms_norm(upload(x, dtype), upload(w, "float32"), width, eps)
+    assert (out.dtype, inv.dtype) == ("float32", "float32")
+    sample = sorted({0, rows - 1, *Random(2).sample(range(rows), min(rows, 24))})
+    xs = stored(x, dtype).reshape(rows, width)
+    ws = w.astype(np.float64).tolist()
+    sub_x = xs[sample].ravel().tolist()
+    ref_out, ref_inv = ora.rms_norm(sub_x, ws, width, eps)
+    assert ora.rel_frobenius(download(out).reshape(rows, width)[sample], np.array(ref_out).reshape(-1, width)) <= FP32_TOL
+    assert ora.rel_frobenius(download(inv)[sample], ref_inv) <= FP32_TOL
+    dx, dw = lm.rms_norm_backward(upload(g, "float32"), upload(x, dtype), upload(w, "float32"), inv, width)
+    assert (dx.dtype, dw.dtype) == (dtype, "float32")
+    gs = g.astype(np.float64).reshape(rows, width)
+    inv_host = download(inv).astype(np.float64)
+    ref_dx, _ = ora.rms_norm_backward(gs[sample].ravel().tolist(), sub_x, ws, inv_host[sample].tolist(), width)
+    tol = FP32_TOL if dtype == "float32" else BF16_TOL
+    assert ora.rel_frobenius(download(dx).reshape(rows, width)[sample], np.array(ref_dx).reshape(-1, width)) <= tol
+    # dw over every row (numpy float64 of the same formula, fixed by the oracle's loop)
+    ref_dw = (gs * xs * inv_host[:, None]).sum(axis=0)
+    assert ora.rel_frobenius(download(dw), ref_dw) <= FP32_TOL
+    _, ref_dw_loop = ora.rms_norm_backward(gs[:8].ravel().tolist(), xs[:8].ravel().tolist(), ws,
+                                           inv_host[:8].tolist(), width)
+    assert np.allclose((gs[:8] * xs[:8] * inv_host[:8, None]).sum(axis=0), ref_dw_loop, rtol=1e-12)
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_silu_forward_and_backward(lm, dtype):
+    x, g = normal(115, 10007, 3.0), normal(116, 10007)
+    out = download(lm.silu(upload(x, dtype)))
+    xs, gs = stored(x, dtype), stored(g, dtype)
+    tol = FP32_TOL if dtype == "float32" else BF16_TOL
+    assert ora.rel_frobenius(out, ora.silu(xs.tolist())) <= tol
+    d = download(lm.silu_backward(upload(g, dtype), upload(x, dtype)))
+    assert ora.rel_frobenius(d, ora.silu_backward(gs.tolist(), xs.tolist())) <= tol
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_rope_forward_inverse_and_offset(lm, dtype):
+    batch, time, heads, dim, theta = 2, 33, 4, 16, 10000.0
+    x = normal(117, batch * time * heads * dim)
+    y = lm.rope(upload(x, dtype), batch, time, heads, dim, theta, offset=7)
+    ref = ora.rope(stored(x, dtype).tolist(), batch, time, heads, dim, theta, offset=7)
+    tol = FP32_TOL if dtype == "float32" else BF16_TOL
+    assert ora.rel_frobenius(download(y), ref) <= tol
+    back = lm.rope(y, batch, time, heads, dim, theta, offset=7, inverse=True)
+    assert ora.rel_frobenius(download(back), stored(x, dtype)) <= (1e-5 if dtype == "float32" else 2e-2)
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_head_rows_and_backward(lm, dtype):
+    batch, time, width = 3, 6, 8
+    h = normal(118, batch * time * width)
+    rows = batch * (time - 1)
+    got = download(lm.head_rows(upload(h, dtype), 4, 9, width, time))
+    assert got.tobytes() == stored(np.array(ora.head_rows(stored(h, dtype).tolist(), 4, 9, width, time)),
+                                   dtype).astype(np.float32).tobytes()
+    g = normal(119, 9 * width)
+    from qutai_amd.backends import amd
+
+    target = amd.full(batch * time * width, 0.0, dtype=dtype)
+    lm.head_rows_backward(target, upload(g, dtype), 4, 9, width, time)
+    expected = [0.0] * (batch * time * width)
+    ora.head_rows_backward(expected, stored(g, dtype).tolist(), 4, 9, width, time)
+    assert np.array_equal(download(target), stored(np.array(expected), dtype))
+    assert rows == 15
+
+
+@pytest.mark.parametrize("dtype,rows,vocab", [("float32", 7, 13), ("bfloat16", 40, 32000), ("float32", 512, 32000)])
+def test_head_loss_and_gradient(lm, dtype, rows, vocab):
+    logits = normal(120, rows * vocab, 2.0)
+    rng = Random(3)
+    labels = [rng.randrange(vocab) for _ in range(rows + 2)]
+    labels[1] = -100  # ignored position
+    prepared = lm.prepare_labels(labels)
+    start = 2
+    loss = lm.head_loss(upload(logits, dtype), prepared, rows, vocab, start=start)
+    ls = stored(logits, dtype)
+    expected = ora.head_loss(ls.tolist(), labels, rows, vocab, start=start)
+    assert abs(download(loss)[0] - expected) <= 1e-5 * max(1.0, abs(expected)) * (1 if dtype == "float32" else 10)
+    g = upload(np.array([0.75], dtype=np.float32), "float32")
+    grad = lm.head_gradient(upload(logits, dtype), prepared, rows, vocab, g, 5, start=start)
+    ref = ora.head_gradient(ls.tolist(), labels, rows, vocab, [0.75], 5, start=start)
+    assert ora.rel_frobenius(download(grad), ref) <= (FP32_TOL if dtype == "float32" else BF16_TOL)
+    with pytest.raises(ValueError):
+        lm.head_loss(upload(logits, dtype), prepared, rows, vocab, start=len(labels))  # label range
+
+
+def test_add_into_scale_concatenate(lm, base):
+    a, b = normal(121, 1000), normal(122, 1000)
+    t = upload(a, "float32")
+    lm.add_into(t, upload(b, "float32"))
+    assert np.array_equal(download(t), (a + b).astype(np.float32))
+    assert np.array_equal(download(base.scale(upload(a, "float32"), 0.25)), (a * np.float32(0.25)).astype(np.float32))
+    x = upload(np.arange(6, dtype=np.float32), "float32")
+    y = upload(np.arange(10, 13, dtype=np.float32), "float32")
+    assert download(base.concatenate((x, y), ((6,), (3,)))).tolist() == [0, 1, 2, 3, 4, 5, 10, 11, 12]
+    m = base.concatenate((x, y), ((3, 2), (3, 1)), axis=1)
+    assert download(m).tolist() == [0, 1, 10, 2, 3, 11, 4, 5, 12]

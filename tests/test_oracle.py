@@ -409,3 +409,95 @@ def test_combine_backward_matches_finite_differences():
             up[n][1][i] += eps
             down[n][1][i] -= eps
             assert grads[n][i] == pytest.approx((loss(up, weights) - loss(down, weights)) / (2 * eps), abs=1e-8)
+
+
+# ---- decoder glue ------------------------------------------------------------------
+
+def _fd(f, x, i, eps=1e-6):
+    up, down = list(x), list(x)
+    up[i] += eps
+    down[i] -= eps
+    return (f(up) - f(down)) / (2 * eps)
+
+
+def test_embedding_gather_and_scatter_round_trip():
+    width, vocab = 3, 5
+    weight = [float(i) for i in range(vocab * width)]
+    ids = [4, 0, 4, 2]
+    assert ora.embedding(weight, ids, width) == [12.0, 13.0, 14.0, 0.0, 1.0, 2.0, 12.0, 13.0, 14.0, 6.0, 7.0, 8.0]
+    g = [1.0] * (len(ids) * width)
+    grad = ora.embedding_backward(g, ids, vocab, width)
+    # token 4 appears twice, 0 and 2 once, 1 and 3 never
+    assert grad == [1.0] * 3 + [0.0] * 3 + [1.0] * 3 + [0.0] * 3 + [2.0] * 3
+
+
+def test_rms_norm_closed_form_and_backward_finite_differences():
+    # a constant row c: mean square c^2, out = c / sqrt(c^2 + eps) * w
+    out, inv = ora.rms_norm([2.0] * 4, [1.0, 2.0, 3.0, 4.0], 4, 0.0)
+    assert out == pytest.approx([1.0, 2.0, 3.0, 4.0], rel=1e-15) and inv == pytest.approx([0.5], rel=1e-15)
+    rng = random.Random(14)
+    width, rows, eps = 5, 3, 1e-5
+    x = [rng.gauss(0, 1) for _ in range(rows * width)]
+    w = [rng.gauss(1, 0.2) for _ in range(width)]
+    g = [rng.gauss(0, 1) for _ in range(rows * width)]
+    _, inv = ora.rms_norm(x, w, width, eps)
+    dx, dw = ora.rms_norm_backward(g, x, w, inv, width)
+    loss_x = lambda xx: math.fsum(a * b for a, b in zip(g, ora.rms_norm(xx, w, width, eps)[0]))  # noqa: E731
+    loss_w = lambda ww: math.fsum(a * b for a, b in zip(g, ora.rms_norm(x, ww, width, eps)[0]))  # noqa: E731
+    for i in range(len(x)):
+        assert dx[i] == pytest.approx(_fd(loss_x, x, i), rel=1e-6, abs=1e-8)
+    for j in range(width):
+        assert dw[j] == pytest.approx(_fd(loss_w, w, j), rel=1e-6, abs=1e-8)
+
+
+def test_silu_backward_finite_differences():
+    xs = [-3.0, -0.5, 0.0, 0.7, 4.0]
+    g = [1.0, -2.0, 0.5, 3.0, 1.5]
+    d = ora.silu_backward(g, xs)
+    for i, x in enumerate(xs):
+        assert d[i] == pytest.approx(g[i] * _fd(lambda v: ora.silu(v)[i], xs, i), rel=1e-7)
+
+
+def test_rope_inverse_norm_and_positions():
+    rng = random.Random(15)
+    batch, time, heads, dim, theta = 2, 3, 2, 6, 10000.0
+    x = [rng.gauss(0, 1) for _ in range(batch * time * heads * dim)]
+    y = ora.rope(x, batch, time, heads, dim, theta, offset=5)
+    back = ora.rope(y, batch, time, heads, dim, theta, offset=5, inverse=True)
+    assert back == pytest.approx(x, abs=1e-12)
+    # each pair keeps its norm
+    for i in range(0, len(x), 2):
+        assert math.hypot(y[i], y[i + 1]) == pytest.approx(math.hypot(x[i], x[i + 1]), rel=1e-12)
+    # position 0 (offset 0) is the identity; pair 0 of position t turns by t radians
+    z = ora.rope(x, batch, time, heads, dim, theta)
+    assert z[:heads * dim] == pytest.approx(x[:heads * dim], abs=1e-15)
+    i = (1 * heads + 0) * dim  # b 0, t 1, h 0, pair 0
+    assert z[i] == pytest.approx(x[i] * math.cos(1) - x[i + 1] * math.sin(1), rel=1e-12)
+
+
+def test_head_rows_select_prediction_positions():
+    width, time = 2, 4  # each sequence contributes its first time-1 rows
+    values = [float(v) for v in range(2 * time * width)]  # 2 sequences
+    rows = ora.head_rows(values, 0, 6, width, time)
+    expected_rows = [0, 1, 2, 4, 5, 6]
+    assert rows == [values[r * width + j] for r in expected_rows for j in range(width)]
+    target = [0.0] * len(values)
+    ora.head_rows_backward(target, [1.0] * 12, 0, 6, width, time)
+    assert [target[r * width] for r in range(2 * time)] == [1, 1, 1, 0, 1, 1, 1, 0]
+
+
+def test_head_loss_and_gradient_closed_forms():
+    vocab = 4
+    logits = [0.0] * vocab + [1.0, 2.0, 3.0, 4.0]
+    labels = [2, -100]
+    # uniform logits: log(V); the ignored row adds nothing
+    assert ora.head_loss(logits, labels, 2, vocab) == pytest.approx(math.log(vocab), rel=1e-15)
+    grad = ora.head_gradient(logits, labels, 2, vocab, [1.0], 1)
+    assert grad[:vocab] == pytest.approx([0.25, 0.25, -0.75, 0.25], rel=1e-15)
+    assert grad[vocab:] == [0, 0, 0, 0]
+    # the gradient is the derivative of the loss
+    rng = random.Random(16)
+    z = [rng.gauss(0, 1) for _ in range(2 * vocab)]
+    g = ora.head_gradient(z, [1, 3], 2, vocab, [1.0], 1)
+    for i in range(len(z)):
+        assert g[i] == pytest.approx(_fd(lambda v: ora.head_loss(v, [1, 3], 2, vocab), z, i), rel=1e-6, abs=1e-9)
