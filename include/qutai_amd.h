@@ -103,6 +103,16 @@ int qutai_amd_add(const void* left, const void* right, void* out, int64_t n, int
  * (src/qutai/lm/layers.py:212). */
 int qutai_amd_scale(const void* x, void* out, int64_t n, double factor, int dtype, void* stream);
 
+/* dst[z][r][c] = src[z][r][c] for r < src_rows, c < src_cols, else 0: a
+ * stack of `batches` matrices re-pitched from src_rows x src_cols to
+ * dst_rows x dst_cols (zero padding or cropping; fp32 or bf16, bits copied).
+ * Pads expert weights and routed rows to multiples of 8 columns so that the
+ * grouped expert GEMMs serve any d_model / d_expert, as the reference's
+ * per-expert `cuda.gemm` calls do (src/qutai/lm/layers.py:395-397; its tiny
+ * test models use d_model 8, d_expert 6, tests/test_lm_decoder.py:18-31). */
+int qutai_amd_repitch(const void* src, void* dst, int64_t batches, int64_t src_rows, int64_t src_cols,
+                      int64_t dst_rows, int64_t dst_cols, int dtype, void* stream);
+
 /* out[r][c] = x[r][c] + bias[c] (rows x cols; one rounding).  The bias add
  * of nn.Linear (src/qutai/nn/layers.py:145-148, a broadcast `add`) and the
  * broadcast of a scalar gradient (cols = 1). */

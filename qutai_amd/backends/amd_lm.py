@@ -204,19 +204,44 @@ def _as_dtype(values, dtype):
     return values if values.dtype == dtype else amd.from_storage(values, dtype=dtype)
 
 
+def repitch(values, batches, rows, cols, new_rows, new_cols):
+    """[batches][rows][cols] -> [batches][new_rows][new_cols], zero padded or cropped."""
+    if values.size != batches * rows * cols:
+        raise ValueError("repitch source size does not match its shape")
+    out = AMDStorage(batches * new_rows * new_cols, values.dtype)
+    if out.size:
+        out.runtime.call("qutai_amd_repitch", values.ptr, out.ptr, batches, rows, cols, new_rows, new_cols,
+                         code(values.dtype))
+    return out
+
+
+def _pad8(n):
+    return (n + 7) // 8 * 8
+
+
 def moe_experts_forward(x, route, w_gate, w_up, w_down, width, hidden, *, save=False):
     """Expert SwiGLU for every routed (token, slot): gather, grouped gate/up,
     silu(gate) * up, grouped down, weighted combine (lm/layers.py:395-399).
     Weights of another dtype than x (fp32 master weights, bf16 activations)
     are rounded to x's dtype for the products, as the reference's mixed GEMM
-    does.  With ``save`` the intermediates for ``moe_experts_backward`` are
-    returned too."""
+    does.  Widths that are not multiples of 8 run zero padded to the next
+    multiple (padded weight rows and columns are zero, so the padded outputs
+    are zero and the cropped result is exact).  With ``save`` the
+    intermediates for ``moe_experts_backward`` are returned too."""
+    wp, hp = _pad8(width), _pad8(hidden)
+    experts = route["experts"]
     wg, wu, wd = (_as_dtype(w, x.dtype) for w in (w_gate, w_up, w_down))
     rows = route_gather_all(x, route, width)
-    gate = grouped_gemm(rows, wg, route, width, hidden, out_dtype=x.dtype)
-    up = grouped_gemm(rows, wu, route, width, hidden, out_dtype=x.dtype)
+    if (wp, hp) != (width, hidden):
+        wg, wu = (repitch(w, experts, hidden, width, hp, wp) for w in (wg, wu))
+        wd = repitch(wd, experts, width, hidden, wp, hp)
+        rows = repitch(rows, 1, route["capacity"], width, route["capacity"], wp)
+    gate = grouped_gemm(rows, wg, route, wp, hp, out_dtype=x.dtype)
+    up = grouped_gemm(rows, wu, route, wp, hp, out_dtype=x.dtype)
     act = silu_mul(gate, up)
-    down = grouped_gemm(act, wd, route, hidden, width, out_dtype=x.dtype)
+    down = grouped_gemm(act, wd, route, hp, wp, out_dtype=x.dtype)
+    if wp != width:
+        down = repitch(down, 1, route["capacity"], wp, route["capacity"], width)
     y = combine_all(down, route, width)
     if not save:
         return y
@@ -287,17 +312,26 @@ def moe_experts_backward(gradient, route, saved, width, hidden, *, x_dtype, weig
     """Backward of moe_experts_forward: (dx, d routing weights, dW_gate,
     dW_up, dW_down).  Every product is one grouped launch over all experts
     (NN for the data gradients, grouped-K TN for the weight gradients); the
-    token gradient sums each token's slots in fp32 and rounds once."""
+    token gradient sums each token's slots in fp32 and rounds once.  Padded
+    widths as in the forward; weight gradients are cropped back."""
+    wp, hp = _pad8(width), _pad8(hidden)
+    experts, capacity = route["experts"], route["capacity"]
     dt = saved["down"].dtype
     d_down, d_weights = combine_backward_all(_as_dtype(gradient, dt), saved["down"], route, width)
-    d_act = grouped_gemm(d_down, saved["w_down"], route, width, hidden, out_dtype=dt, transpose_right=False)
-    dw_down = grouped_gemm_k(d_down, saved["act"], route, width, hidden, out_dtype=weight_dtype)
+    if wp != width:
+        d_down = repitch(d_down, 1, capacity, width, capacity, wp)
+    d_act = grouped_gemm(d_down, saved["w_down"], route, wp, hp, out_dtype=dt, transpose_right=False)
+    dw_down = grouped_gemm_k(d_down, saved["act"], route, wp, hp, out_dtype=weight_dtype)
     d_gate, d_up = silu_mul_backward(d_act, saved["gate"], saved["up"])
-    d_rows = grouped_gemm(d_gate, saved["w_gate"], route, hidden, width, out_dtype="float32", transpose_right=False)
-    grouped_gemm(d_up, saved["w_up"], route, hidden, width, out_dtype="float32", transpose_right=False, out=d_rows,
+    d_rows = grouped_gemm(d_gate, saved["w_gate"], route, hp, wp, out_dtype="float32", transpose_right=False)
+    grouped_gemm(d_up, saved["w_up"], route, hp, wp, out_dtype="float32", transpose_right=False, out=d_rows,
                  accumulate=True)
-    dw_gate = grouped_gemm_k(d_gate, saved["rows"], route, hidden, width, out_dtype=weight_dtype)
-    dw_up = grouped_gemm_k(d_up, saved["rows"], route, hidden, width, out_dtype=weight_dtype)
+    dw_gate = grouped_gemm_k(d_gate, saved["rows"], route, hp, wp, out_dtype=weight_dtype)
+    dw_up = grouped_gemm_k(d_up, saved["rows"], route, hp, wp, out_dtype=weight_dtype)
+    if (wp, hp) != (width, hidden):
+        d_rows = repitch(d_rows, 1, capacity, wp, capacity, width)
+        dw_gate, dw_up = (repitch(w, experts, hp, wp, hidden, width) for w in (dw_gate, dw_up))
+        dw_down = repitch(dw_down, experts, wp, hp, width, hidden)
     dx = _as_dtype(route_gather_backward_all(d_rows, route, width), x_dtype)
     return dx, d_weights, dw_gate, dw_up, dw_down
 

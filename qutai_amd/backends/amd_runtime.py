@@ -56,6 +56,7 @@ SIGNATURES = {
     "qutai_amd_combine_backward": [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p],
     "qutai_amd_route_backward": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p],
     "qutai_amd_scale": [_p, _p, _i64, _f64, _i32, _p],
+    "qutai_amd_repitch": [_p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _p],
     "qutai_amd_embedding": [_p, _p, _p, _i64, _i64, _i32, _p],
     "qutai_amd_embedding_backward": [_p, _p, _p, _p, _p, _i64, _i64, _i32, _p],
     "qutai_amd_rms_norm": [_p, _p, _p, _p, _i64, _i64, _f64, _i32, _p],

@@ -61,6 +61,21 @@ __global__ void scale_kernel(const void* a, void* out, int64_t n, double factor,
   }
 }
 
+// dst[z][r][c] = src[z][r][c] inside the source block, 0 outside it: a
+// stack of matrices re-pitched to other row and column counts (padding or
+// cropping, element size es bytes).
+__global__ void repitch_kernel(const void* src, void* dst, int64_t batches, int64_t src_rows, int64_t src_cols,
+                               int64_t dst_rows, int64_t dst_cols, int es) {
+  const int64_t per = dst_rows * dst_cols, total = batches * per;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t z = i / per, r = (i % per) / dst_cols, c = i % dst_cols;
+    const bool inside = r < src_rows && c < src_cols;
+    const int64_t at = (z * src_rows + r) * src_cols + c;
+    if (es == 2) ((bf16_t*)dst)[i] = inside ? ((const bf16_t*)src)[at] : (bf16_t)0;
+    else ((float*)dst)[i] = inside ? ((const float*)src)[at] : 0.f;
+  }
+}
+
 __global__ void add_kernel(const void* a, const void* b, void* out, int64_t n, int d) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
     if (d == F64) {
@@ -423,6 +438,18 @@ int qutai_amd_scale(const void* x, void* out, int64_t n, double factor, int dtyp
   if (n < 0 || !float_dtype(dtype)) return QA_EINVAL;
   if (n == 0) return QA_OK;
   hipLaunchKernelGGL(scale_kernel, dim3(grid_for(n)), dim3(THREADS), 0, (hipStream_t)stream, x, out, n, factor, dtype);
+  return (int)hipGetLastError();
+}
+
+int qutai_amd_repitch(const void* src, void* dst, int64_t batches, int64_t src_rows, int64_t src_cols,
+                      int64_t dst_rows, int64_t dst_cols, int dtype, void* stream) {
+  if (batches < 0 || src_rows < 0 || src_cols < 0 || dst_rows < 0 || dst_cols < 0) return QA_EINVAL;
+  if (dtype != BF16 && dtype != F32) return QA_EINVAL;
+  const int64_t n = batches * dst_rows * dst_cols;
+  if (n == 0) return QA_OK;
+  if (!src || !dst) return QA_EINVAL;
+  hipLaunchKernelGGL(repitch_kernel, dim3(grid_for(n)), dim3(THREADS), 0, (hipStream_t)stream, src, dst, batches,
+                     src_rows, src_cols, dst_rows, dst_cols, dtype == BF16 ? 2 : 4);
   return (int)hipGetLastError();
 }
 

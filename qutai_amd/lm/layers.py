@@ -54,6 +54,45 @@ def linear(x, weight):
     return record(Tensor(values, shape=(*x.shape[:-1], out_features)), (x, weight), backward)
 
 
+def residual_add(x, update):
+    """x + update cast to x's dtype (src/qutai/lm/layers.py:31-32)."""
+    return x + update.to(dtype=x.dtype)
+
+
+def scaled(x, factor):
+    """x * factor as a recorded op (the scalar products of decoder.py:131, 173)."""
+    return record(Tensor(amd.scale(x.storage, factor), shape=x.shape), (x,), lambda g: (amd.scale(g, factor),))
+
+
+def embed(ids, weight, shape):
+    """Rows of the (vocab, width) table for host token ids, shape (*shape,
+    width) (src/qutai/lm/layers.py:77-85)."""
+    b = backend(weight)
+    width = weight.shape[1]
+    values = b.embedding(weight.storage, ids, width)
+    return record(Tensor(values, shape=(*shape, width)), (weight,),
+                  lambda g: (b.embedding_backward(g, ids, weight.shape[0], width),))
+
+
+def rms_norm(x, weight, eps):
+    """RMSNorm over the last axis, fp32 output (src/qutai/lm/layers.py:88-96)."""
+    b = backend(x)
+    width = x.shape[-1]
+    out, inverse = b.rms_norm(x.storage, weight.storage, width, eps)
+    return record(Tensor(out, shape=x.shape), (x, weight),
+                  lambda g: b.rms_norm_backward(g, x.storage, weight.storage, inverse, width))
+
+
+def rope(x, heads, theta, offset=0):
+    """Rotary position embedding of (batch, time, heads*dim); backward is the
+    inverse rotation (src/qutai/lm/layers.py:108-116)."""
+    b = backend(x)
+    batch, time, features = x.shape
+    dims = (batch, time, heads, features // heads, theta, offset)
+    return record(Tensor(b.rope(x.storage, *dims), shape=x.shape), (x,),
+                  lambda g: (b.rope(g, *dims, inverse=True),))
+
+
 def silu_mul(gate, up):
     """silu(gate) * up as one recorded op (SwiGLU's activation, lm/layers.py:310-311)."""
     b = backend(gate)
@@ -155,6 +194,152 @@ class SparseMoE:
 
     def parameters(self):
         return (*self.router.parameters(), self.w_gate, self.w_up, self.w_down)
+
+
+class RMSNorm:
+    """Unit-initialised RMSNorm weight (src/qutai/lm/layers.py:275-288)."""
+
+    def __init__(self, width, eps, *, device="amd", dtype="float32"):
+        self.weight = Tensor(amd.full(width, 1.0, dtype=dtype), shape=(width,), requires_grad=True)
+        self.eps = eps
+
+    def __call__(self, x):
+        return rms_norm(x, self.weight, self.eps)
+
+    def parameters(self):
+        return (self.weight,)
+
+
+class GQA:
+    """Grouped-query attention block: q/k/v projections (seeds seed..seed+2),
+    RoPE on q and k, fused causal attention, out projection (seed+3, std
+    0.02/sqrt(2 n_layers)) (src/qutai/lm/layers.py:317-350)."""
+
+    def __init__(self, config, *, device="amd", dtype="float32", seed=None):
+        width = config.d_model
+        kv_width = config.n_kv_heads * (width // config.n_heads)
+
+        def offset(i):
+            return None if seed is None else seed + i
+
+        self.q = Projection(width, width, device=device, dtype=dtype, seed=seed)
+        self.k = Projection(width, kv_width, device=device, dtype=dtype, seed=offset(1))
+        self.v = Projection(width, kv_width, device=device, dtype=dtype, seed=offset(2))
+        self.out = Projection(width, width, device=device, dtype=dtype, seed=offset(3),
+                              std=0.02 / sqrt(2 * config.n_layers))
+        self.heads, self.kv_heads, self.theta = config.n_heads, config.n_kv_heads, config.rope_theta
+
+    def __call__(self, x):
+        q = rope(self.q(x), self.heads, self.theta)
+        k = rope(self.k(x), self.kv_heads, self.theta)
+        return self.out(attention(q, k, self.v(x), self.heads, self.kv_heads))
+
+    def parameters(self):
+        return (*self.q.parameters(), *self.k.parameters(), *self.v.parameters(), *self.out.parameters())
+
+
+class Block:
+    """Pre-norm decoder block: x + attn(norm(x)), then x + ffn(norm(x)); the
+    FFN is SwiGLU or SparseMoE (seed+4); returns (hidden, aux)
+    (src/qutai/lm/layers.py:409-446)."""
+
+    def __init__(self, config, *, device="amd", dtype="float32", seed=None):
+        self.attn_norm = RMSNorm(config.d_model, config.norm_eps, device=device, dtype=dtype)
+        self.ffn_norm = RMSNorm(config.d_model, config.norm_eps, device=device, dtype=dtype)
+        self.attn = GQA(config, device=device, dtype=dtype, seed=seed)
+        self.is_moe = config.ffn_type == "moe"
+        ffn_seed = None if seed is None else seed + 4
+        down_std = 0.02 / sqrt(2 * config.n_layers)
+        if self.is_moe:
+            self.ffn = SparseMoE(config.d_model, config.d_expert, config.n_experts, config.top_k, device=device,
+                                 dtype=dtype, seed=ffn_seed, std=down_std)
+        else:
+            self.ffn = SwiGLU(config.d_model, config.d_ff, device=device, dtype=dtype, seed=ffn_seed, std=down_std)
+
+    def __call__(self, x):
+        x = residual_add(x, self.attn(self.attn_norm(x)))
+        if self.is_moe:
+            y, aux = self.ffn(self.ffn_norm(x))
+        else:
+            y = self.ffn(self.ffn_norm(x))
+            aux = Tensor(amd.full(1, 0.0, dtype=x.dtype), shape=())
+        return residual_add(x, y), aux
+
+    def hidden(self, x):
+        return self(x)[0]
+
+    def packed(self, x):
+        return pack(*self(x))
+
+    def parameters(self):
+        return (*self.attn_norm.parameters(), *self.ffn_norm.parameters(), *self.attn.parameters(),
+                *self.ffn.parameters())
+
+
+def pack(hidden, aux):
+    """hidden and its scalar aux loss as one flat tensor, so that a recomputed
+    MoE block has one output (src/qutai/lm/layers.py:161-169)."""
+    values = amd.concatenate((hidden.storage, aux.to(dtype=hidden.dtype).storage), ((hidden.size,), (1,)))
+    size = hidden.size
+    return record(Tensor(values, shape=(size + 1,)), (hidden, aux),
+                  lambda g: (amd.take(g, 0, size), _cast(amd.take(g, size, 1), aux.dtype)))
+
+
+def unpack(packed, shape):
+    """Inverse of ``pack`` (src/qutai/lm/layers.py:172-191)."""
+    size = prod(shape)
+    hidden = record(Tensor(amd.take(packed.storage, 0, size), shape=shape), (packed,),
+                    lambda g: (amd.concatenate((g, amd.full(1, 0.0, dtype=g.dtype)), ((size,), (1,))),))
+    aux = record(Tensor(amd.take(packed.storage, size, 1), shape=()), (packed,),
+                 lambda g: (amd.concatenate((amd.full(size, 0.0, dtype=g.dtype), g), ((size,), (1,))),))
+    return hidden, aux
+
+
+def _cast(values, dtype):
+    return values if values.dtype == dtype else amd.from_storage(values, dtype=dtype)
+
+
+def projection_loss(hidden, weight, labels, chunk_size, *, prepared_labels=None):
+    """Mean next-token cross entropy of hidden (batch, time, width) against
+    the tied (vocab, width) weight, over chunks of chunk_size head rows so
+    that at most chunk_size x vocab logits exist at once; labels -100 are
+    ignored; the backward recomputes each chunk's logits and accumulates the
+    weight gradient with an accumulating GEMM (src/qutai/lm/layers.py:194-257)."""
+    b = backend(hidden)
+    _, time, width = hidden.shape
+    vocab = weight.shape[0]
+    precision = matmul_precision()
+    targets = tuple(label for row in labels for label in row[1:])
+    label_data = b.prepare_labels(targets) if prepared_labels is None else prepared_labels
+    count = max(1, sum(label != -100 for label in targets))
+    out_dtype = activation_dtype(hidden, weight)
+    result = amd.full(1, 0.0, dtype=hidden.dtype)
+    for start in range(0, len(targets), chunk_size):
+        rows = min(chunk_size, len(targets) - start)
+        inputs = b.head_rows(hidden.storage, start, rows, width, time)
+        logits = b.gemm(inputs, weight.storage, rows, width, vocab, transpose_right=True, out_dtype=out_dtype)
+        b.add_into(result, _cast(b.head_loss(logits, label_data, rows, vocab, start=start), result.dtype))
+    result = amd.scale(result, 1 / count)
+
+    def backward(gradient):
+        with set_matmul_precision(precision):
+            dx = amd.full(hidden.size, 0.0, dtype=hidden.dtype)
+            dw = amd.full(weight.size, 0.0, dtype=weight.dtype)
+            for start in range(0, len(targets), chunk_size):
+                rows = min(chunk_size, len(targets) - start)
+                inputs = b.head_rows(hidden.storage, start, rows, width, time)
+                logits = b.gemm(inputs, weight.storage, rows, width, vocab, transpose_right=True,
+                                out_dtype=activation_dtype(hidden, weight))
+                incoming = b.head_gradient(logits, label_data, rows, vocab, gradient, count, start=start)
+                if hidden.requires_grad:
+                    part = b.gemm(incoming, weight.storage, rows, vocab, width, out_dtype=hidden.dtype)
+                    b.head_rows_backward(dx, part, start, rows, width, time)
+                if weight.requires_grad:
+                    b.gemm(incoming, inputs, vocab, rows, width, transpose_left=True, out_dtype=weight.dtype,
+                           out=dw, accumulate=True)
+            return dx, dw
+
+    return record(Tensor(result, shape=()), (hidden, weight), backward)
 
 
 def attention_products(q, k, v, *, scale=None):

@@ -153,3 +153,16 @@ def test_add_into_scale_concatenate(lm, base):
     assert download(base.concatenate((x, y), ((6,), (3,)))).tolist() == [0, 1, 2, 3, 4, 5, 10, 11, 12]
     m = base.concatenate((x, y), ((3, 2), (3, 1)), axis=1)
     assert download(m).tolist() == [0, 1, 10, 2, 3, 11, 4, 5, 12]
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_repitch_pads_and_crops_exactly(lm, dtype):
+    x = normal(123, (3, 5, 6))
+    padded = lm.repitch(upload(x, dtype), 3, 5, 6, 7, 8)
+    expected = np.zeros((3, 7, 8))
+    expected[:, :5, :6] = stored(x, dtype)
+    assert np.array_equal(download(padded).reshape(3, 7, 8), expected)
+    back = lm.repitch(padded, 3, 7, 8, 5, 6)
+    assert np.array_equal(download(back).reshape(3, 5, 6), stored(x, dtype))
+    with pytest.raises(ValueError):
+        lm.repitch(padded, 3, 5, 6, 5, 6)  # size does not match the stated shape
