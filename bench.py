@@ -236,6 +236,48 @@ def moe_train(seed=4):
                          "hidden": hidden, "storage": "bfloat16", "pass": "forward+backward"}
 
 
+def decoder_train(seed=5):
+    """One Decoder.loss forward + backward under autocast on config 4's
+    shapes (4096 tokens = 2 x 2048, d_model 2048, 32 heads of 64 with 8 KV
+    heads, SwiGLU 5632, vocab 32768, 2 layers, chunked head of 1024 rows):
+    embedding, RMSNorm, RoPE, fused attention, the 9 projection GEMMs per
+    layer, the loss head and every backward kernel.  FLOPs: 6 x matmul
+    parameters x tokens plus causal attention (fwd 2 T^2 D H per sequence,
+    backward twice that)."""
+    from qutai_amd.backends import amd_lm
+    from qutai_amd.lm import Config, Decoder, autocast
+
+    config = Config(vocab_size=32768, n_layers=2, d_model=2048, n_heads=32, n_kv_heads=8, d_ff=5632,
+                    max_seq_len=2048, activation_checkpointing=False)
+    batch, time_ = 2, 2048
+    rng = np.random.default_rng(seed)
+    host_normal = amd_lm.normal
+    amd_lm.normal = lambda size, mean=0.0, std=1.0, *, seed=None, dtype="float32": upload(
+        rng.normal(mean, std, size), dtype)
+    try:
+        model = Decoder(config, seed=seed)
+    finally:
+        amd_lm.normal = host_normal
+    tokens = rng.integers(0, config.vocab_size, size=(batch, time_)).tolist()
+    params = model.parameters()
+
+    def step():
+        for p in params:
+            p.grad = None
+        with autocast():
+            loss = model.loss(tokens, chunk_size=1024)
+        loss.backward()
+
+    d, kv = config.d_model, config.n_kv_heads * (config.d_model // config.n_heads)
+    matmul_params = config.n_layers * (2 * d * d + 2 * d * kv + 3 * d * config.d_ff) + config.vocab_size * d
+    n_tokens = batch * time_
+    attention = config.n_layers * batch * 3 * 2 * time_ * time_ * d
+    flops = 6.0 * matmul_params * n_tokens + attention
+    return step, flops, {"tokens": n_tokens, "batch": batch, "seq_len": time_, "d_model": d, "n_layers": 2,
+                         "heads": 32, "kv_heads": 8, "d_ff": config.d_ff, "vocab": config.vocab_size,
+                         "storage": "fp32 weights, bf16 activations (autocast)", "pass": "loss forward+backward"}
+
+
 WORKLOADS = {
     "gemm_bf16_4096": (lambda: gemm_square("bfloat16"), "bf16"),
     "gemm_fp32_4096": (lambda: gemm_square("float32"), "fp32"),
@@ -248,6 +290,7 @@ WORKLOADS = {
     "dense_linear_fwd_bwd": (dense_linear, "bf16"),
     "moe_grouped": (moe_experts, "bf16"),
     "moe_train": (moe_train, "bf16"),
+    "decoder_train": (decoder_train, "bf16"),
 }
 HEADLINE = "gemm_bf16_4096"
 

@@ -141,6 +141,14 @@ class Runtime:
         version = ctypes.c_int()
         self._check(self._driver_version(ctypes.byref(version)), "hipDriverGetVersion")
         self.driver_version = version.value
+        free, total = ctypes.c_size_t(), ctypes.c_size_t()
+        self._check(self._mem_info(ctypes.byref(free), ctypes.byref(total)), "hipMemGetInfo")
+        self.total_memory = total.value
+        # Idle-cache cap: the reference keeps 1 GiB (a WDDM budget,
+        # cuda_runtime.py:214-216); with 288 GB of HBM a decoder step's
+        # transient buffers exceed that, and every overflow drains the device
+        # and frees the whole cache, so the cap is 1/16 of the device here.
+        self.cache_limit_bytes = max(1 << 30, self.total_memory // 16)
         atexit.register(self.close)
 
     # ---- binding -------------------------------------------------------------
@@ -163,6 +171,7 @@ class Runtime:
                                                                 ctypes.c_int])
         self._driver_version = bind("hipDriverGetVersion", [ctypes.POINTER(ctypes.c_int)])
         self._sync = bind("hipDeviceSynchronize", [])
+        self._mem_info = bind("hipMemGetInfo", [ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)])
         self._malloc = bind("hipMalloc", [ctypes.POINTER(ctypes.c_void_p), sz])
         self._free = bind("hipFree", [vp])
         self._memcpy = bind("hipMemcpy", [vp, vp, sz, ctypes.c_int])

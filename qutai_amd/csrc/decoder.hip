@@ -157,49 +157,141 @@ __global__ void head_rows_kernel(const T* x, T* out, int64_t n, int64_t start, i
   }
 }
 
-// per-row cross entropy log(sum exp(l - max)) - (l[label] - max); label
-// -100 -> 0 (lm.cu:428-433).  One wave per row.
+// Loss head rows: one 256-thread workgroup per row of logits.  Each thread
+// keeps a running (max, sum of exp(v - max)) over its 16-byte chunks of the
+// row (one exp per element; the sum is rescaled when the max grows), the
+// pairs are merged across the wave and then across the 4 waves in LDS, in a
+// fixed order.  The gradient kernel's second pass re-reads the row, which the
+// first pass has just brought into L2.
+constexpr int HEAD_THREADS = 256;
+
+struct MaxSum {
+  float m, s;
+};
+
+__device__ __forceinline__ MaxSum merge(MaxSum a, MaxSum b) {
+  const float m = fmaxf(a.m, b.m);
+  if (m == -INFINITY) return {m, 0.f};
+  return {m, a.s * expf(a.m - m) + b.s * expf(b.m - m)};
+}
+
+// Fold up to 8 values (n of them valid) into the running pair.
+__device__ __forceinline__ MaxSum fold(MaxSum a, const float* v, int n) {
+  float top = v[0];
+  for (int i = 1; i < n; i++) top = fmaxf(top, v[i]);
+  if (top > a.m) {
+    a.s = a.m == -INFINITY ? 0.f : a.s * expf(a.m - top);
+    a.m = top;
+  }
+  for (int i = 0; i < n; i++) a.s += expf(v[i] - a.m);
+  return a;
+}
+
+template <class T> constexpr int chunk_of() { return 16 / (int)sizeof(T); }
+
 template <class T>
-__global__ void __launch_bounds__(256) head_loss_kernel(const T* logits, const int64_t* labels, float* out,
-                                                        int64_t rows, int64_t vocab) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  const T* l = logits + row * vocab;
-  float peak = -INFINITY;
-  for (int64_t c = lane; c < vocab; c += 64) peak = fmaxf(peak, get<T>(l, c));
-  peak = wave_max(peak);
-  float total = 0.f;
-  for (int64_t c = lane; c < vocab; c += 64) total += expf(get<T>(l, c) - peak);
-  total = wave_sum(total);
+__device__ __forceinline__ void load_chunk(const T* p, float* v) {
+  if constexpr (sizeof(T) == 2) {
+    const uint4 raw = *(const uint4*)p;
+    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      v[2 * i] = __uint_as_float(w[i] << 16);
+      v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  } else {
+    const float4 raw = *(const float4*)p;
+    v[0] = raw.x, v[1] = raw.y, v[2] = raw.z, v[3] = raw.w;
+  }
+}
+
+// (max, sum of exp(v - max)) of one row, the same value in every thread.
+template <class T>
+__device__ MaxSum row_max_sum(const T* l, int64_t vocab, bool vec) {
+  __shared__ MaxSum partial[HEAD_THREADS / 64];
+  MaxSum a = {-INFINITY, 0.f};
+  constexpr int V = chunk_of<T>();
+  float v[8];
+  if (vec) {
+    for (int64_t c = (int64_t)threadIdx.x * V; c < vocab; c += HEAD_THREADS * V) {
+      load_chunk<T>(l + c, v);
+      a = fold(a, v, V);
+    }
+  } else {
+    for (int64_t c = threadIdx.x; c < vocab; c += HEAD_THREADS) {
+      v[0] = get<T>(l, c);
+      a = fold(a, v, 1);
+    }
+  }
+#pragma unroll
+  for (int o = 32; o; o >>= 1) a = merge(a, {__shfl_xor(a.m, o), __shfl_xor(a.s, o)});
+  if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = a;
+  __syncthreads();
+  MaxSum total = partial[0];
+#pragma unroll
+  for (int w = 1; w < HEAD_THREADS / 64; w++) total = merge(total, partial[w]);
+  return total;
+}
+
+// out[row] = log(sum exp(l - max)) - (l[label] - max), 0 for label -100
+// (lm.cu:430-433)
+template <class T>
+__global__ void __launch_bounds__(HEAD_THREADS) head_loss_kernel(const T* logits, const int64_t* labels, float* out,
+                                                                 int64_t vocab, bool vec) {
+  const int64_t row = blockIdx.x;
   const int64_t label = labels[row];
-  if (lane == 0) out[row] = label == -100 ? 0.f : logf(total) - (get<T>(l, label) - peak);
+  if (label == -100) {
+    if (threadIdx.x == 0) out[row] = 0.f;
+    return;
+  }
+  const T* l = logits + row * vocab;
+  const MaxSum t = row_max_sum<T>(l, vocab, vec);
+  if (threadIdx.x == 0) out[row] = logf(t.s) - (get<T>(l, label) - t.m);
 }
 
 // in place: logits = g * factor * (softmax - onehot(label)); label -100 -> 0
 // (lm.cu:434-440)
 template <class T>
-__global__ void __launch_bounds__(256) head_gradient_kernel(T* logits, const int64_t* labels, const float* gradient,
-                                                            int64_t rows, int64_t vocab, float factor) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  T* l = logits + row * vocab;
-  float peak = -INFINITY;
-  for (int64_t c = lane; c < vocab; c += 64) peak = fmaxf(peak, get<T>(l, c));
-  peak = wave_max(peak);
-  float total = 0.f;
-  for (int64_t c = lane; c < vocab; c += 64) total += expf(get<T>(l, c) - peak);
-  total = wave_sum(total);
+__global__ void __launch_bounds__(HEAD_THREADS) head_gradient_kernel(T* logits, const int64_t* labels,
+                                                                     const float* gradient, int64_t vocab,
+                                                                     float factor, bool vec) {
+  const int64_t row = blockIdx.x;
   const int64_t label = labels[row];
-  const float scale = gradient[0] * factor;
-  for (int64_t c = lane; c < vocab; c += 64) {
-    const float v = label == -100 ? 0.f : scale * (expf(get<T>(l, c) - peak) / total - (c == label ? 1.f : 0.f));
-    put<T>(l, c, v);
+  T* l = logits + row * vocab;
+  constexpr int V = chunk_of<T>();
+  if (label == -100) {
+    for (int64_t c = threadIdx.x; c < vocab; c += HEAD_THREADS) put<T>(l, c, 0.f);
+    return;
+  }
+  const MaxSum t = row_max_sum<T>(l, vocab, vec);
+  const float scale = gradient[0] * factor, inv = 1.f / t.s;
+  if (vec) {
+    float v[8];
+    for (int64_t c = (int64_t)threadIdx.x * V; c < vocab; c += HEAD_THREADS * V) {
+      load_chunk<T>(l + c, v);
+#pragma unroll
+      for (int i = 0; i < V; i++) v[i] = scale * (expf(v[i] - t.m) * inv - (c + i == label ? 1.f : 0.f));
+      if constexpr (sizeof(T) == 2) {
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) w[i] = (uint32_t)f32_to_bf16(v[2 * i]) | ((uint32_t)f32_to_bf16(v[2 * i + 1]) << 16);
+        *(uint4*)(l + c) = make_uint4(w[0], w[1], w[2], w[3]);
+      } else {
+        *(float4*)(l + c) = make_float4(v[0], v[1], v[2], v[3]);
+      }
+    }
+  } else {
+    for (int64_t c = threadIdx.x; c < vocab; c += HEAD_THREADS)
+      put<T>(l, c, scale * (expf(get<T>(l, c) - t.m) * inv - (c == label ? 1.f : 0.f)));
   }
 }
 
 bool act_dtype(int d) { return d == F32 || d == BF16; }
+
+// 16-byte chunks need an aligned base and rows that are whole chunks
+bool vec_rows(const void* p, int64_t vocab, int per_chunk) {
+  return (uintptr_t)p % 16 == 0 && vocab % per_chunk == 0;
+}
 
 }  // namespace
 
@@ -329,14 +421,14 @@ int qutai_amd_head_loss(const void* logits, const int64_t* labels, float* out, i
                         int dtype, void* stream) {
   if (rows < 0 || vocab <= 0 || !act_dtype(dtype)) return QA_EINVAL;
   if (rows == 0) return QA_OK;
-  const unsigned blocks = (unsigned)((rows + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK);
+  if (rows > 0x7fffffff) return QA_EINVAL;
   hipStream_t s = (hipStream_t)stream;
   if (dtype == BF16)
-    hipLaunchKernelGGL(head_loss_kernel<bf16_t>, dim3(blocks), dim3(256), 0, s, (const bf16_t*)logits, labels, out,
-                       rows, vocab);
+    hipLaunchKernelGGL(head_loss_kernel<bf16_t>, dim3((unsigned)rows), dim3(HEAD_THREADS), 0, s,
+                       (const bf16_t*)logits, labels, out, vocab, vec_rows(logits, vocab, 8));
   else
-    hipLaunchKernelGGL(head_loss_kernel<float>, dim3(blocks), dim3(256), 0, s, (const float*)logits, labels, out,
-                       rows, vocab);
+    hipLaunchKernelGGL(head_loss_kernel<float>, dim3((unsigned)rows), dim3(HEAD_THREADS), 0, s, (const float*)logits,
+                       labels, out, vocab, vec_rows(logits, vocab, 4));
   return (int)hipGetLastError();
 }
 
@@ -344,14 +436,14 @@ int qutai_amd_head_gradient(void* logits, const int64_t* labels, const float* gr
                             double factor, int dtype, void* stream) {
   if (rows < 0 || vocab <= 0 || !act_dtype(dtype)) return QA_EINVAL;
   if (rows == 0) return QA_OK;
-  const unsigned blocks = (unsigned)((rows + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK);
+  if (rows > 0x7fffffff) return QA_EINVAL;
   hipStream_t s = (hipStream_t)stream;
   if (dtype == BF16)
-    hipLaunchKernelGGL(head_gradient_kernel<bf16_t>, dim3(blocks), dim3(256), 0, s, (bf16_t*)logits, labels, gradient,
-                       rows, vocab, (float)factor);
+    hipLaunchKernelGGL(head_gradient_kernel<bf16_t>, dim3((unsigned)rows), dim3(HEAD_THREADS), 0, s,
+                       (bf16_t*)logits, labels, gradient, vocab, (float)factor, vec_rows(logits, vocab, 8));
   else
-    hipLaunchKernelGGL(head_gradient_kernel<float>, dim3(blocks), dim3(256), 0, s, (float*)logits, labels, gradient,
-                       rows, vocab, (float)factor);
+    hipLaunchKernelGGL(head_gradient_kernel<float>, dim3((unsigned)rows), dim3(HEAD_THREADS), 0, s, (float*)logits,
+                       labels, gradient, vocab, (float)factor, vec_rows(logits, vocab, 4));
   return (int)hipGetLastError();
 }
 

@@ -35,19 +35,34 @@ def activation_dtype(x, weight):
     return weight.dtype
 
 
+def _bf16_path(*operands):
+    """True when GEMMs of these operands run on the bf16 MFMA path (a bf16
+    operand or autocast), where fp32 operands are rounded to bf16 (RNE)."""
+    return matmul_precision() == "bfloat16" or any(o.dtype == "bfloat16" for o in operands)
+
+
+def _bf16(values):
+    return values if values.dtype == "bfloat16" else amd.from_storage(values, dtype="bfloat16")
+
+
 def linear(x, weight):
-    """Y = X W^T with W stored (out, in) (src/qutai/lm/layers.py:35-74)."""
+    """Y = X W^T with W stored (out, in) (src/qutai/lm/layers.py:35-74).  On
+    the bf16 path the fp32 operands are rounded to bf16 once here, the same
+    rounding the GEMM would apply, and the rounded copies serve the backward
+    products too."""
     b = backend(x)
     rows = x.size // x.shape[-1]
     out_features, inner = weight.shape
     precision = matmul_precision()
-    values = b.gemm(x.storage, weight.storage, rows, inner, out_features, transpose_right=True,
-                    out_dtype=activation_dtype(x, weight))
+    xs, ws = x.storage, weight.storage
+    if _bf16_path(x, weight):
+        xs, ws = _bf16(xs), _bf16(ws)
+    values = b.gemm(xs, ws, rows, inner, out_features, transpose_right=True, out_dtype=activation_dtype(x, weight))
 
     def backward(g):
         with set_matmul_precision(precision):
-            dx = b.gemm(g, weight.storage, rows, out_features, inner, out_dtype=x.dtype) if x.requires_grad else None
-            dw = (b.gemm(g, x.storage, out_features, rows, inner, transpose_left=True, out_dtype=weight.dtype)
+            dx = b.gemm(g, ws, rows, out_features, inner, out_dtype=x.dtype) if x.requires_grad else None
+            dw = (b.gemm(g, xs, out_features, rows, inner, transpose_left=True, out_dtype=weight.dtype)
                   if weight.requires_grad else None)
         return dx, dw
 
@@ -313,11 +328,14 @@ def projection_loss(hidden, weight, labels, chunk_size, *, prepared_labels=None)
     label_data = b.prepare_labels(targets) if prepared_labels is None else prepared_labels
     count = max(1, sum(label != -100 for label in targets))
     out_dtype = activation_dtype(hidden, weight)
+    hs, ws = hidden.storage, weight.storage
+    if _bf16_path(hidden, weight):  # round once, not once per chunk and product
+        hs, ws = _bf16(hs), _bf16(ws)
     result = amd.full(1, 0.0, dtype=hidden.dtype)
     for start in range(0, len(targets), chunk_size):
         rows = min(chunk_size, len(targets) - start)
-        inputs = b.head_rows(hidden.storage, start, rows, width, time)
-        logits = b.gemm(inputs, weight.storage, rows, width, vocab, transpose_right=True, out_dtype=out_dtype)
+        inputs = b.head_rows(hs, start, rows, width, time)
+        logits = b.gemm(inputs, ws, rows, width, vocab, transpose_right=True, out_dtype=out_dtype)
         b.add_into(result, _cast(b.head_loss(logits, label_data, rows, vocab, start=start), result.dtype))
     result = amd.scale(result, 1 / count)
 
@@ -327,12 +345,11 @@ def projection_loss(hidden, weight, labels, chunk_size, *, prepared_labels=None)
             dw = amd.full(weight.size, 0.0, dtype=weight.dtype)
             for start in range(0, len(targets), chunk_size):
                 rows = min(chunk_size, len(targets) - start)
-                inputs = b.head_rows(hidden.storage, start, rows, width, time)
-                logits = b.gemm(inputs, weight.storage, rows, width, vocab, transpose_right=True,
-                                out_dtype=activation_dtype(hidden, weight))
+                inputs = b.head_rows(hs, start, rows, width, time)
+                logits = b.gemm(inputs, ws, rows, width, vocab, transpose_right=True, out_dtype=out_dtype)
                 incoming = b.head_gradient(logits, label_data, rows, vocab, gradient, count, start=start)
                 if hidden.requires_grad:
-                    part = b.gemm(incoming, weight.storage, rows, vocab, width, out_dtype=hidden.dtype)
+                    part = b.gemm(incoming, ws, rows, vocab, width, out_dtype=hidden.dtype)
                     b.head_rows_backward(dx, part, start, rows, width, time)
                 if weight.requires_grad:
                     b.gemm(incoming, inputs, vocab, rows, width, transpose_left=True, out_dtype=weight.dtype,
