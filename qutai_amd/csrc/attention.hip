@@ -167,15 +167,19 @@ __device__ __forceinline__ void attend_block(const bf16_t* sk, const bf16_t* sv,
   if (__builtin_amdgcn_ballot_w64(grow_any)) {
 #pragma unroll
     for (int qb = 0; qb < NQB; qb++) {
-      // alpha = 1 for lanes whose m stays; a query that has seen no valid key
-      // keeps m = -inf and l = 0, O = 0
-      const float alpha = m_new[qb] == m[qb] ? 1.f : __builtin_amdgcn_exp2f(m[qb] - m_new[qb]);
-      m[qb] = m_new[qb];
-      l[qb] *= alpha;
+      // only the lanes whose m moves rescale (an exec-masked update keeps O
+      // in its registers; a wave-uniform select would make the compiler copy
+      // all of O every block).  A query that has seen no valid key keeps
+      // m = -inf and l = 0, O = 0.
+      if (m_new[qb] != m[qb]) {
+        const float alpha = __builtin_amdgcn_exp2f(m[qb] - m_new[qb]);
+        m[qb] = m_new[qb];
+        l[qb] *= alpha;
 #pragma unroll
-      for (int db = 0; db < 2; db++)
+        for (int db = 0; db < 2; db++)
 #pragma unroll
-        for (int e = 0; e < 16; e++) o[qb][db][e] *= alpha;
+          for (int e = 0; e < 16; e++) o[qb][db][e] *= alpha;
+      }
     }
   }
 #pragma unroll
@@ -298,32 +302,40 @@ __global__ void __launch_bounds__(NW * 64) attention_fwd_d64(AttnArgs p) {
     for (int db = 0; db < 2; db++) o[qb][db] = f32x16{};
   }
 
-  // blocks that need no mask: all keys < T and (causal) every key <= the
-  // wave's first query
+  // The key blocks of this wave in three uniform phases, each a loop with a
+  // straight-line body (a per-block choice between masked, unmasked and
+  // skipped blocks makes the compiler copy all of O at every block): blocks
+  // with every key visible (all keys < T and, causal, <= the wave's first
+  // query), blocks that need the mask, and (causal) blocks after every query
+  // of the wave.  Every wave still passes the same nkb barriers.
   const int last_key_full = p.causal ? min(T, q0 + 1) : T;
-  if (nkb > 0) issue(0, 0);
-  for (int kbk = 0; kbk < nkb; kbk++) {
-    const int cur = kbk & 1;
+  const int nkb_w = p.causal ? min(nkb, (q0 + QW + KB - 1) / KB) : nkb;
+  const int n_full = min(nkb_w, last_key_full / KB);
+  // wait for block kbk's stage, then start block kbk+1's copies
+  auto advance = [&](int kbk) {
     wait_vmcnt<0>();
-    asm volatile("s_barrier" ::: "memory");  // stage cur landed; stage cur^1 free
-    if (kbk + 1 < nkb) issue(cur ^ 1, (kbk + 1) * KB);
-    const int kv0 = kbk * KB;
-    const bf16_t* sk = &lds[cur][0][0];
-    const bf16_t* sv = &lds[cur][1][0];
-    if (kv0 + KB <= last_key_full) {
-      const int lim[NQB] = {};
-      attend_block<NQB, false>(sk, sv, qf, o, m, l, lim, p.scale_log2, lane);
-    } else if (kv0 < q0 + QW || !p.causal) {
-      int lim[NQB];
-#pragma unroll
-      for (int qb = 0; qb < NQB; qb++) {
-        const int tq = q0 + qb * 32 + col;
-        lim[qb] = min(T - kv0, p.causal ? tq - kv0 + 1 : KB) - 4 * half;
-      }
-      attend_block<NQB, true>(sk, sv, qf, o, m, l, lim, p.scale_log2, lane);
-    }
-    // else (causal): every key of the block is after every query of this wave
+    asm volatile("s_barrier" ::: "memory");  // stage kbk&1 landed; the other stage is free
+    if (kbk + 1 < nkb) issue((kbk & 1) ^ 1, (kbk + 1) * KB);
+  };
+  if (nkb > 0) issue(0, 0);
+  int kbk = 0;
+  for (; kbk < n_full; kbk++) {
+    advance(kbk);
+    const int lim[NQB] = {};
+    attend_block<NQB, false>(&lds[kbk & 1][0][0], &lds[kbk & 1][1][0], qf, o, m, l, lim, p.scale_log2, lane);
   }
+  for (; kbk < nkb_w; kbk++) {
+    advance(kbk);
+    const int kv0 = kbk * KB;
+    int lim[NQB];
+#pragma unroll
+    for (int qb = 0; qb < NQB; qb++) {
+      const int tq = q0 + qb * 32 + col;
+      lim[qb] = min(T - kv0, p.causal ? tq - kv0 + 1 : KB) - 4 * half;
+    }
+    attend_block<NQB, true>(&lds[kbk & 1][0][0], &lds[kbk & 1][1][0], qf, o, m, l, lim, p.scale_log2, lane);
+  }
+  for (; kbk < nkb; kbk++) advance(kbk);
 
   // ---- normalise and store: lane holds query col, d = 32 db + 8 (e/4) + 4 half + e%4
 #pragma unroll
@@ -574,29 +586,36 @@ __global__ void __launch_bounds__(NW * 64) attention_bwd_dq_d64(AttnBwdArgs p) {
 #pragma unroll
     for (int db = 0; db < 2; db++) dqt[qb][db] = f32x16{};
 
+  // key blocks in three uniform phases (every key visible / masked /
+  // causal: after every query of the wave), each a loop with a
+  // straight-line body, as in the forward; every wave passes nkb barriers
   const int last_key_full = p.causal ? min(T, q0 + 1) : T;
-  if (nkb > 0) issue(0, 0);
-  for (int kbk = 0; kbk < nkb; kbk++) {
-    const int cur = kbk & 1;
+  const int nkb_w = p.causal ? min(nkb, (q0 + QW + KB - 1) / KB) : nkb;
+  const int n_full = min(nkb_w, last_key_full / KB);
+  auto advance = [&](int kbk) {
     wait_vmcnt<0>();
     asm volatile("s_barrier" ::: "memory");
-    if (kbk + 1 < nkb) issue(cur ^ 1, (kbk + 1) * KB);
-    const int kv0 = kbk * KB;
-    const bf16_t* sk = &lds[cur][0][0];
-    const bf16_t* sv = &lds[cur][1][0];
-    if (kv0 + KB <= last_key_full) {
-      const int lim[NQB] = {};
-      dq_block<NQB, false>(sk, sv, qf, gf, lse2, dl, dqt, lim, p.c, p.scale, lane);
-    } else if (kv0 < q0 + QW || !p.causal) {
-      int lim[NQB];
-#pragma unroll
-      for (int qb = 0; qb < NQB; qb++) {
-        const int tq = q0 + qb * 32 + col;
-        lim[qb] = min(T - kv0, p.causal ? tq - kv0 + 1 : KB) - 4 * half;
-      }
-      dq_block<NQB, true>(sk, sv, qf, gf, lse2, dl, dqt, lim, p.c, p.scale, lane);
-    }
+    if (kbk + 1 < nkb) issue((kbk & 1) ^ 1, (kbk + 1) * KB);
+  };
+  if (nkb > 0) issue(0, 0);
+  int kbk = 0;
+  for (; kbk < n_full; kbk++) {
+    advance(kbk);
+    const int lim[NQB] = {};
+    dq_block<NQB, false>(&lds[kbk & 1][0][0], &lds[kbk & 1][1][0], qf, gf, lse2, dl, dqt, lim, p.c, p.scale, lane);
   }
+  for (; kbk < nkb_w; kbk++) {
+    advance(kbk);
+    const int kv0 = kbk * KB;
+    int lim[NQB];
+#pragma unroll
+    for (int qb = 0; qb < NQB; qb++) {
+      const int tq = q0 + qb * 32 + col;
+      lim[qb] = min(T - kv0, p.causal ? tq - kv0 + 1 : KB) - 4 * half;
+    }
+    dq_block<NQB, true>(&lds[kbk & 1][0][0], &lds[kbk & 1][1][0], qf, gf, lse2, dl, dqt, lim, p.c, p.scale, lane);
+  }
+  for (; kbk < nkb; kbk++) advance(kbk);
 
 #pragma unroll
   for (int qb = 0; qb < NQB; qb++) {
@@ -757,22 +776,47 @@ __global__ void __launch_bounds__(NW * 64) attention_bwd_dkv_d64(AttnBwdArgs p) 
 #pragma unroll
     for (int nb = 0; nb < NKB; nb++) dvt[db][nb] = dkt[db][nb] = f32x16{};
 
-  if (iterations > 0) issue(0, 0);
-  for (int it = 0; it < iterations; it++) {
-    const int cur = it & 1;
+  // Per head, the query blocks come in four uniform phases, each a loop with
+  // a straight-line body (a per-block choice makes the compiler copy dK and
+  // dV at every block): blocks whose every query is before every key of the
+  // wave (causal; skipped), masked blocks, blocks with every pair visible,
+  // and masked blocks at the end of the sequence.  Every wave passes
+  // `iterations` barriers.
+  auto advance = [&](int it) {
     wait_vmcnt<0>();
     asm volatile("s_barrier" ::: "memory");
-    if (it + 1 < iterations) issue(cur ^ 1, it + 1);
-    const int qs = qs0 + (it % nq) * KB;
-    // skip blocks whose every query is before every key of the wave (causal)
-    if (p.causal && qs + KB - 1 < kw) continue;
-    const bool full = qs + KB <= T && (!p.causal || qs >= kw + KW - 1);
-    if (full)
-      dkv_block<NKB, false>(&tiles[cur][0][0], &tiles[cur][1][0], &stats[cur][0][0], &stats[cur][1][0], kf, vf, dvt, dkt,
-                       T - qs, kw - qs, p.causal, p.c, p.scale, lane);
-    else
-      dkv_block<NKB, true>(&tiles[cur][0][0], &tiles[cur][1][0], &stats[cur][0][0], &stats[cur][1][0], kf, vf, dvt, dkt,
-                      T - qs, kw - qs, p.causal, p.c, p.scale, lane);
+    if (it + 1 < iterations) issue((it & 1) ^ 1, it + 1);
+  };
+  auto clampq = [&](int x, int lo) { return x < lo ? lo : x > nq ? nq : x; };
+  // qs = qs0 + qi KB.  skipped: qs + KB - 1 < kw;  full: qs >= kw + KW - 1
+  // (causal) and qs + KB <= T
+  const int a = p.causal ? clampq((kw - qs0) / KB, 0) : 0;
+  const int bq = p.causal ? clampq((kw + KW - 1 - qs0 + KB - 1) / KB, a) : a;
+  const int cq = clampq((T - qs0) / KB, bq);
+  auto masked = [&](int it, int qi) {
+    const int qs = qs0 + qi * KB;
+    dkv_block<NKB, true>(&tiles[it & 1][0][0], &tiles[it & 1][1][0], &stats[it & 1][0][0], &stats[it & 1][1][0], kf,
+                         vf, dvt, dkt, T - qs, kw - qs, p.causal, p.c, p.scale, lane);
+  };
+  if (iterations > 0) issue(0, 0);
+  int it = 0;
+  for (int g = 0; g < group; g++) {
+    int qi = 0;
+    for (; qi < a; qi++, it++) advance(it);
+    for (; qi < bq; qi++, it++) {
+      advance(it);
+      masked(it, qi);
+    }
+    for (; qi < cq; qi++, it++) {
+      advance(it);
+      const int qs = qs0 + qi * KB;
+      dkv_block<NKB, false>(&tiles[it & 1][0][0], &tiles[it & 1][1][0], &stats[it & 1][0][0], &stats[it & 1][1][0], kf,
+                            vf, dvt, dkt, T - qs, kw - qs, p.causal, p.c, p.scale, lane);
+    }
+    for (; qi < nq; qi++, it++) {
+      advance(it);
+      masked(it, qi);
+    }
   }
 
   // dK^T / dV^T: lane = key 32 nb + col, rows d = 32 db + 8 (e / 4) + 4 half + e % 4
