@@ -7,6 +7,8 @@
 #include <string>
 
 #include "gemm_kernel.h"
+
+#include <algorithm>
 #include "qutai_amd.h"
 
 using namespace qa;
@@ -130,6 +132,19 @@ hipError_t launch_mma(Tile tile, bool ta, bool tb, const GemmArgs& p, hipStream_
 // Tile choice: 256x256 when the grid still gives about one tile per CU,
 // else the 128x128 tile; thin outputs use the 256x64 / 64x256 shapes.
 // QUTAI_AMD_GEMM_TILE=<L8D2|L8R|L4D2|S|N|W|H> overrides the choice (tuning).
+// compute units of the current device (cached per device)
+int64_t cu_count() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 Tile choose_tile(int64_t M, int64_t N, int64_t K, int64_t batch) {
   static int forced = [] {
     const char* v = getenv("QUTAI_AMD_GEMM_TILE");
@@ -142,13 +157,25 @@ Tile choose_tile(int64_t M, int64_t N, int64_t K, int64_t batch) {
   if (forced >= 0) return (Tile)forced;
   if (N <= 64) return TILE_N;
   if (M <= 64) return TILE_W;
-  int64_t big = ((M + 255) / 256) * ((N + 255) / 256) * batch;
   if (K <= 128) return TILE_S;
-  // 256x256 tiles filling at most half the CUs over a long K: 256x128 tiles
-  // (measured on the config 4 projections: 4096x2048 outputs, K = 5632)
-  if (big <= 136 && big >= 64 && K >= 2048) return TILE_H;
-  if (big < 192) return TILE_S;
-  return TILE_L8D2;
+  // Wave-quantisation cost of the three large tiles, in units of one full
+  // round of 256x256 tiles over the CUs (per unit of K).  Measured on this
+  // GPU (bf16, 4096^3 and eight decoder / ragged shapes): a full round of
+  // 256x128 tiles (one per CU) costs 0.665, a full round of 128x128 tiles
+  // (two per CU) 0.70, and a partial round of at most one 128x128 tile per
+  // CU 0.5; a partial round of the others costs as much as a full one.  Ties
+  // (within 3%) go to 256x128, then 256x256.
+  const int64_t cus = cu_count();
+  const int64_t mt = (M + 255) / 256, nt = (N + 255) / 256, ms = (M + 127) / 128, ns = (N + 127) / 128;
+  const int64_t nl = mt * nt * batch, nh = mt * ns * batch, nsm = ms * ns * batch;
+  const double cost_l = (double)(nl / cus) + (nl % cus ? 1.0 : 0.0);
+  const double cost_h = 0.665 * (double)(nh / cus + (nh % cus ? 1 : 0));
+  const int64_t rs = nsm % (2 * cus);
+  const double cost_s = 0.70 * (double)(nsm / (2 * cus)) + (rs == 0 ? 0.0 : rs <= cus ? 0.5 : 0.70);
+  const double best = std::min(cost_l, std::min(cost_h, cost_s));
+  if (cost_h <= best * 1.03) return TILE_H;
+  if (cost_l <= best * 1.03) return TILE_L8D2;
+  return TILE_S;
 }
 
 // How one operand reaches the kernel: in place, or re-laid out in the
