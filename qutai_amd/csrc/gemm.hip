@@ -129,9 +129,6 @@ hipError_t launch_mma(Tile tile, bool ta, bool tb, const GemmArgs& p, hipStream_
   return tb ? launch_tile<F32, false, true>(tile, p, stream) : launch_tile<F32, false, false>(tile, p, stream);
 }
 
-// Tile choice: 256x256 when the grid still gives about one tile per CU,
-// else the 128x128 tile; thin outputs use the 256x64 / 64x256 shapes.
-// QUTAI_AMD_GEMM_TILE=<L8D2|L8R|L4D2|S|N|W|H> overrides the choice (tuning).
 // compute units of the current device (cached per device)
 int64_t cu_count() {
   static int cached[64] = {};
@@ -145,6 +142,9 @@ int64_t cu_count() {
   return cached[dev];
 }
 
+// Tile choice for an M x N output (batch of them) over K; thin outputs use
+// the 256x64 / 64x256 shapes.  QUTAI_AMD_GEMM_TILE=<L8D2|L8R|L4D2|S|N|W|H>
+// overrides the choice (tuning).
 Tile choose_tile(int64_t M, int64_t N, int64_t K, int64_t batch) {
   static int forced = [] {
     const char* v = getenv("QUTAI_AMD_GEMM_TILE");
@@ -341,9 +341,13 @@ int qutai_amd_gemm_grouped(const void* a, const void* b, void* out, const int64_
   p.offsets = offsets;
   p.groups = groups;
   p.alpha = 1.0f;
-  // Upper bound of M tiles over all groups: sum ceil(n_g / BM) <= ceil(max_rows / BM) + groups.
-  Tile tile = cols <= 64 ? TILE_N : TILE_L8D2;
-  int bm = 256;
+  // 256x256 tiles (256x64 for thin outputs): on config 5's experts the cost
+  // model's 256x128 / 128x128 picks measured slower (each group's last M tile
+  // is partial, which the model does not see).  The grid covers the upper
+  // bound sum ceil(n_g / BM) <= ceil(max_rows / BM) + groups of M tiles
+  // (tiles past the last group return at once).
+  const Tile tile = cols <= 64 ? TILE_N : TILE_L8D2;
+  const int bm = 256;
   p.tiles_m = (int)((max_rows + bm - 1) / bm + groups);
   bool f32 = dtype == QA_F32;
   hipError_t err = f32 ? launch_mma<true>(tile, false, transpose_right, p, stream)
