@@ -85,6 +85,22 @@ __global__ void prepare_operand(const void* src, int src_bf16, void* dst, int ds
   }
 }
 
+// Split-K reduction: out[b][e] = sum over s of part[b * splits + s][e] in
+// order s = 0, 1, ... (fp32), plus the old output when accumulating, one
+// rounding to the output type.
+__global__ void splitk_reduce(const float* part, void* out, int64_t n, int64_t total, int splits, int accumulate,
+                              int out_bf16) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t b = i / n, e = i - b * n;
+    const float* src = part + b * splits * n + e;
+    float acc = 0.f;
+    for (int s = 0; s < splits; s++) acc += src[s * n];
+    if (accumulate) acc += out_bf16 ? bf16_to_f32(((const bf16_t*)out)[i]) : ((const float*)out)[i];
+    if (out_bf16) ((bf16_t*)out)[i] = f32_to_bf16(acc);
+    else ((float*)out)[i] = acc;
+  }
+}
+
 // Kernel configurations: (BM x BN, WM x WN waves, BK, LDS stages, staging).
 //   L8D2: 256x256, 8 waves (2 per SIMD), BK 64 (bf16) / 32 (fp32), two-stage
 //         direct-to-LDS ring, the next stage's copies spread over the k-steps
@@ -178,6 +194,36 @@ Tile choose_tile(int64_t M, int64_t N, int64_t K, int64_t batch) {
   return TILE_S;
 }
 
+// Split-K for plain products whose tiles fill at most a quarter of the CU
+// slots over a long K (e.g. 1024 x 2048 outputs with K = 32768; a two-way
+// split of half-empty grids measured slower): the K
+// range is cut into chunks of a multiple of 64 elements, each chunk's fp32
+// partial product goes to the workspace and one pass sums them.
+// QUTAI_AMD_SPLITK=<n> forces n chunks (tuning and tests; read per call).
+size_t split_bytes(int64_t rows, int64_t cols, int64_t batch, int splits) {
+  return ((size_t)splits * batch * rows * cols * 4 + 255) / 256 * 256;
+}
+
+int choose_split(int64_t rows, int64_t cols, int64_t inner, int64_t batch, Tile tile, int64_t* chunk) {
+  int64_t bm = 256, bn = 256;
+  if (tile == TILE_S) bm = bn = 128;
+  else if (tile == TILE_H) bn = 128;
+  else if (tile == TILE_N) bn = 64;
+  else if (tile == TILE_W) bm = 64;
+  const int64_t tiles = ((rows + bm - 1) / bm) * ((cols + bn - 1) / bn) * batch;
+  const int64_t slots = (tile == TILE_S ? 2 : 1) * cu_count();
+  int64_t s = 1;
+  const char* forced = getenv("QUTAI_AMD_SPLITK");
+  if (forced && atoi(forced) > 0) s = atoi(forced);
+  else if (batch == 1 && tiles * 4 <= slots && inner >= 4096) s = std::min<int64_t>(8, slots / tiles);
+  if (s <= 1 || inner < 128) return 1;
+  const int64_t c = ((inner + s - 1) / s + 63) / 64 * 64;
+  s = (inner + c - 1) / c;
+  if (s <= 1) return 1;
+  *chunk = c;
+  return (int)s;
+}
+
 // How one operand reaches the kernel: in place, or re-laid out in the
 // workspace (dtype change and/or zero-padded 16-byte-aligned rows).
 struct Operand {
@@ -243,8 +289,11 @@ size_t qutai_amd_gemm_workspace_size(int64_t rows, int64_t inner, int64_t cols, 
   // 256-byte aligned pointers: only dtype and row alignment decide
   plan(rows, inner, cols, batch, left_stride, right_stride, transpose_left, transpose_right, a_dtype, b_dtype, bf16,
        (const void*)256, (const void*)256, &pa, &pb);
-  if (!pa.copy && !pb.copy) return 0;
-  return (pa.copy ? pa.bytes : 0) + (pb.copy ? pb.bytes : 0) + 256;
+  int64_t chunk = 0;
+  const int splits = choose_split(rows, cols, inner, batch, choose_tile(rows, cols, inner, batch), &chunk);
+  const size_t partial = splits > 1 ? split_bytes(rows, cols, batch, splits) : 0;
+  if (!pa.copy && !pb.copy && !partial) return 0;
+  return (pa.copy ? pa.bytes : 0) + (pb.copy ? pb.bytes : 0) + partial + 256;
 }
 
 int qutai_amd_gemm(const void* a, const void* b, void* out, int64_t rows, int64_t inner, int64_t cols,
@@ -275,15 +324,24 @@ int qutai_amd_gemm(const void* a, const void* b, void* out, int64_t rows, int64_
   Operand pa, pb;
   plan(rows, inner, cols, batch, left_stride, right_stride, transpose_left, transpose_right, a_dtype, b_dtype, bf16,
        a, b, &pa, &pb);
-  if (inner > 0 && (pa.copy || pb.copy)) {
-    size_t need = (pa.copy ? pa.bytes : 0) + (pb.copy ? pb.bytes : 0) + 256;
+  const Tile tile = choose_tile(rows, cols, inner, batch);
+  int64_t chunk = 0;
+  const int splits = inner > 0 ? choose_split(rows, cols, inner, batch, tile, &chunk) : 1;
+  const size_t partial = splits > 1 ? split_bytes(rows, cols, batch, splits) : 0;
+  float* part = nullptr;
+  if (inner > 0 && (pa.copy || pb.copy || partial)) {
+    size_t need = (pa.copy ? pa.bytes : 0) + (pb.copy ? pb.bytes : 0) + partial + 256;
     if (workspace == nullptr || workspace_bytes < need) return QA_EWORKSPACE;
     char* ws = (char*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
     if (pa.copy) {
       launch_prepare(pa, a_dtype, bf16, ws, stream);
       ws += pa.bytes;
     }
-    if (pb.copy) launch_prepare(pb, b_dtype, bf16, ws, stream);
+    if (pb.copy) {
+      launch_prepare(pb, b_dtype, bf16, ws, stream);
+      ws += pb.bytes;
+    }
+    if (partial) part = (float*)ws;
   }
   GemmArgs p = {};
   p.a = pa.ptr;
@@ -306,10 +364,24 @@ int qutai_amd_gemm(const void* a, const void* b, void* out, int64_t rows, int64_
   // buffer descriptors address at most 2^31 bytes per K step
   int64_t es = bf16 ? 2 : 4;
   if ((p.lda * 256 * es) >= (1ll << 31) || (p.ldb * 256 * es) >= (1ll << 31)) return QA_EINVAL;
-  Tile tile = choose_tile(rows, cols, inner, batch);
+  if (part) {
+    // fp32 partials of each K chunk, then the ordered sum into `out`
+    p.out = part;
+    p.k_split = splits;
+    p.k_chunk = chunk;
+    p.batch = batch * splits;
+    p.accumulate = 0;
+    p.out_bf16 = 0;
+    p.vec_c = vec_out(part, p.ldc, p.sc);
+  }
   hipError_t err = bf16 ? launch_mma<false>(tile, transpose_left, transpose_right, p, stream)
                         : launch_mma<true>(tile, transpose_left, transpose_right, p, stream);
-  return (int)err;
+  if (err != hipSuccess || !part) return (int)err;
+  const int64_t total = batch * rows * cols;
+  const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 1 << 20);
+  hipLaunchKernelGGL(splitk_reduce, dim3(blocks), dim3(256), 0, stream, (const float*)part, out, rows * cols, total,
+                     splits, accumulate ? 1 : 0, out_dtype == QA_BF16 ? 1 : 0);
+  return (int)hipGetLastError();
 }
 
 int qutai_amd_gemm_grouped(const void* a, const void* b, void* out, const int64_t* offsets, int groups,

@@ -54,6 +54,12 @@ struct GemmArgs {
   // Grouped-K mode (group_k = 1, batch = groups): group g reduces over the K
   // rows [offsets[g], offsets[g+1]) of A and B and writes out + g*sc.
   int group_k;
+  // Split-K (k_split > 1; batch = product batch * k_split): grid batch index
+  // z = b * k_split + s reduces K range [s * k_chunk, min(K, (s+1) * k_chunk))
+  // of product b and writes its fp32 partial tile to out + z*sc.  k_chunk is
+  // a multiple of 64, so no 16-byte chunk of a K-major row crosses a range end.
+  int k_split;
+  int64_t k_chunk;
 };
 
 template <bool F32> struct MmaTraits;
@@ -336,6 +342,13 @@ struct GemmKernel {
       B += (int64_t)g * p.sb;
       outp += lo * p.ldc * osize;
       M = hi - lo;
+    } else if (p.k_split > 1) {
+      const int64_t prod = bz / p.k_split, k_lo = (bz % p.k_split) * p.k_chunk;
+      A += prod * p.sa + k_lo * (KA ? 1 : p.lda);
+      B += prod * p.sb + k_lo * (KB ? 1 : p.ldb);
+      outp += bz * p.sc * osize;
+      row0 = (int64_t)tile_m * BM;
+      K = (K < k_lo + p.k_chunk ? K : k_lo + p.k_chunk) - k_lo;
     } else {
       A += bz * p.sa;
       B += bz * p.sb;
