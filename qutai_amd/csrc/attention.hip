@@ -475,7 +475,7 @@ __device__ __forceinline__ void dq_block(const bf16_t* sk, const bf16_t* sv, con
         float x = st_[e];
         if (MASK && 32 * mb + 8 * (e >> 2) + (e & 3) >= lim[qb]) x = -INFINITY;
         const float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(x, c, -lse2[qb]));
-        ds[e] = pr * (dp[e] - dl[qb]) * scale;
+        ds[e] = pr * (dp[e] - dl[qb]);  // the softmax scale multiplies dQ once, at the end
       }
 #pragma unroll
       for (int st = 0; st < 2; st++) {
@@ -627,8 +627,9 @@ __global__ void __launch_bounds__(NW * 64) attention_bwd_dq_d64(AttnBwdArgs p) {
 #pragma unroll
         for (int g = 0; g < 4; g++) {
           uint2 w;
-          w.x = cvt_pk_bf16(dqt[qb][db][4 * g], dqt[qb][db][4 * g + 1]);
-          w.y = cvt_pk_bf16(dqt[qb][db][4 * g + 2], dqt[qb][db][4 * g + 3]);
+          const float sc = p.scale;
+          w.x = cvt_pk_bf16(dqt[qb][db][4 * g] * sc, dqt[qb][db][4 * g + 1] * sc);
+          w.y = cvt_pk_bf16(dqt[qb][db][4 * g + 2] * sc, dqt[qb][db][4 * g + 3] * sc);
           *reinterpret_cast<uint2*>(out + 32 * db + 8 * g + 4 * half) = w;
         }
     }
@@ -678,8 +679,9 @@ __device__ __forceinline__ void dkv_block(const bf16_t* sq, const bf16_t* sg, co
           const int qrel = 32 * mq + 8 * (e >> 2) + 4 * half + (e & 3);
           if (qrel >= qrel_end || (causal && qrel < key_rel + 32 * nb + col)) x = -INFINITY;
         }
-        pr[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(x, c, -l4[e >> 2][e & 3] * LOG2E));
-        ds[e] = pr[e] * (dp[e] - d4[e >> 2][e & 3]) * scale;
+        // slse holds -lse * log2(e); the softmax scale multiplies dK once, at the end
+        pr[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(x, c, l4[e >> 2][e & 3]));
+        ds[e] = pr[e] * (dp[e] - d4[e >> 2][e & 3]);
       }
 #pragma unroll
       for (int st = 0; st < 2; st++) {
@@ -753,6 +755,7 @@ __global__ void __launch_bounds__(NW * 64) attention_bwd_dkv_d64(AttnBwdArgs p) 
     }
   }
 
+  float lse_next = 0.f;                               // wave 0: lse of the block in flight
   const int qs0 = p.causal ? k0 : 0;                  // first query any key of the workgroup sees
   const int nq = qs0 < T ? (T - qs0 + KB - 1) / KB : 0;
   const int iterations = nq * group;
@@ -762,11 +765,21 @@ __global__ void __launch_bounds__(NW * 64) attention_bwd_dkv_d64(AttnBwdArgs p) 
     const int64_t base = b * p.qb + h * p.qh + (int64_t)qs * p.qt;
     copy_tile<NW>(&tiles[stage][0][0], p.q + base, p.qt, T - qs, wave, lane);
     copy_tile<NW>(&tiles[stage][1][0], p.g + base, p.qt, T - qs, wave, lane);
-    if (wave < 2) {  // wave 0: lse of the 64 queries, wave 1: delta
-      const float* src = wave == 0 ? p.lse : p.delta;
-      const u32x4 r = lds_rsrc(src + b * p.lb + h * p.lh, ((int64_t)T - 1) * p.lt * 4 + 4);
-      const uint32_t off = (uint32_t)((int64_t)(qs + lane) * p.lt * 4) + ((uint32_t)(qs + lane >= T) << 31);
-      lds_load4(r, &stats[stage][wave][0], off);
+    const uint32_t off = (uint32_t)((int64_t)(qs + lane) * p.lt * 4) + ((uint32_t)(qs + lane >= T) << 31);
+    if (wave == 0) {  // lse of the 64 queries into a register; stored scaled by stage_lse
+      const auto r = rsrc(p.lse + b * p.lb + h * p.lh, ((int64_t)T - 1) * p.lt * 4 + 4);
+      lse_next = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+    } else if (wave == 1) {  // delta straight into LDS
+      const u32x4 r = lds_rsrc(p.delta + b * p.lb + h * p.lh, ((int64_t)T - 1) * p.lt * 4 + 4);
+      lds_load4(r, &stats[stage][1][0], off);
+    }
+  };
+  // wave 0 stores -lse * log2(e) of the block it loaded (after the wait for
+  // its load, before the barrier that publishes the stage)
+  auto stage_lse = [&](int stage) {
+    if (wave == 0) {
+      stats[stage][0][lane] = -lse_next * LOG2E;
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the store is in LDS before the barrier
     }
   };
 
@@ -784,6 +797,7 @@ __global__ void __launch_bounds__(NW * 64) attention_bwd_dkv_d64(AttnBwdArgs p) 
   // `iterations` barriers.
   auto advance = [&](int it) {
     wait_vmcnt<0>();
+    stage_lse(it & 1);
     asm volatile("s_barrier" ::: "memory");
     if (it + 1 < iterations) issue((it & 1) ^ 1, it + 1);
   };
@@ -831,8 +845,9 @@ __global__ void __launch_bounds__(NW * 64) attention_bwd_dkv_d64(AttnBwdArgs p) 
 #pragma unroll
         for (int g = 0; g < 4; g++) {
           uint2 wk, wv;
-          wk.x = cvt_pk_bf16(dkt[db][nb][4 * g], dkt[db][nb][4 * g + 1]);
-          wk.y = cvt_pk_bf16(dkt[db][nb][4 * g + 2], dkt[db][nb][4 * g + 3]);
+          const float sc = p.scale;
+          wk.x = cvt_pk_bf16(dkt[db][nb][4 * g] * sc, dkt[db][nb][4 * g + 1] * sc);
+          wk.y = cvt_pk_bf16(dkt[db][nb][4 * g + 2] * sc, dkt[db][nb][4 * g + 3] * sc);
           wv.x = cvt_pk_bf16(dvt[db][nb][4 * g], dvt[db][nb][4 * g + 1]);
           wv.y = cvt_pk_bf16(dvt[db][nb][4 * g + 2], dvt[db][nb][4 * g + 3]);
           *reinterpret_cast<uint2*>(ok + 32 * db + 8 * g + 4 * half) = wk;
