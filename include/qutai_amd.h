@@ -113,7 +113,21 @@ int qutai_amd_scale(const void* x, void* out, int64_t n, double factor, int dtyp
 int qutai_amd_repitch(const void* src, void* dst, int64_t batches, int64_t src_rows, int64_t src_cols,
                       int64_t dst_rows, int64_t dst_cols, int dtype, void* stream);
 
-/* out[r][c] = x[r][c] + bias[c] (rows x cols; one rounding).  The bias add
+/* Softmax backward along rows: out = scale * p * (g - rowsum(g * p)), p the
+ * softmax of (scale * x) (fp32 math; fp32/fp64/bf16 storage).  Replaces
+ * `_softmax_backward` (src/qutai/core/operations/normalization.py:18-25), the
+ * rule behind nn.Attention.weights (src/qutai/nn/layers.py:298-303, 334-343). */
+int qutai_amd_softmax_backward(const void* probs, const void* grad, void* out, int64_t rows, int64_t width,
+                               double scale, int dtype, void* stream);
+
+/* Causal mask of attention scores [rows][width]: row r (query r % length of
+ * its batch/head block) keeps keys c <= offset + r % length, the rest become
+ * -inf.  Replaces the host-built mask that nn.MultiHeadAttention adds to its
+ * scores (src/qutai/nn/layers.py:337-341). */
+int qutai_amd_causal_mask(const void* x, void* out, int64_t rows, int64_t width, int64_t length, int64_t offset,
+                          int dtype, void* stream);
+
+/* out[r][c] = x[r][c] + bias[c] (rows x cols; one rounding)./* out[r][c] = x[r][c] + bias[c] (rows x cols; one rounding).  The bias add
  * of nn.Linear (src/qutai/nn/layers.py:145-148, a broadcast `add`) and the
  * broadcast of a scalar gradient (cols = 1). */
 int qutai_amd_add_rows(const void* x, const void* bias, void* out, int64_t rows, int64_t cols, int dtype,
@@ -124,6 +138,14 @@ int qutai_amd_add_rows(const void* x, const void* bias, void* out, int64_t rows,
  * `cuda.unbroadcast` as called by src/qutai/core/operations/linalg.py:51,55. */
 int qutai_amd_sum_middle(const void* x, void* out, int64_t outer, int64_t count, int64_t inner, int dtype,
                          void* stream);
+
+/* Two adjacent axes swapped: x is (outer, m, n, inner), out is
+ * (outer, n, m, inner) (inner = 1: a transpose of the last two axes).
+ * Replaces the general axis permutation of `cuda.transpose`
+ * (src/qutai/backends/cuda.py:255) for the head split and merge of
+ * nn.MultiHeadAttention (src/qutai/nn/layers.py:322-325, 354). */
+int qutai_amd_swap_axes(const void* x, void* out, int64_t outer, int64_t m, int64_t n, int64_t inner, int dtype,
+                        void* stream);
 
 /* Swap the last two axes: out[z][c][r] = x[z][r][c].  Replaces the
  * `broadcast`-kernel transpose of src/qutai/backends/cuda.py:255-262 on the

@@ -293,13 +293,15 @@ def attention_np(q, k, v, *, causal=True, scale=None):
     return (w @ v) / total, (peak + np.log(total))[:, 0]
 
 
-def attention_backward_np(g, q, k, v, out, lse, *, scale=None):
+def attention_backward_np(g, q, k, v, out, lse, *, scale=None, causal=True):
     """numpy float64 form of ``attention_backward`` for one (batch, head) pair
-    (causal): returns dq, dk, dv of that pair."""
+    (causal, or every key with ``causal=False`` as for nn attention): returns
+    dq, dk, dv of that pair."""
     g, q, k, v, out = (np.asarray(a, dtype=np.float64) for a in (g, q, k, v, out))
     scale = 1 / q.shape[1] ** 0.5 if scale is None else scale
     p = np.exp((q @ k.T) * scale - np.asarray(lse, dtype=np.float64)[:, None])
-    p = np.where(np.tril(np.ones(p.shape, dtype=bool)), p, 0.0)
+    if causal:
+        p = np.where(np.tril(np.ones(p.shape, dtype=bool)), p, 0.0)
     delta = (g * out).sum(axis=1, keepdims=True)
     ds = p * (g @ v.T - delta) * scale
     return ds @ k, ds.T @ q, p.T @ g

@@ -325,17 +325,24 @@ def concatenate(values, shapes, axis=0) -> AMDStorage:
 
 
 def transpose(values: AMDStorage, shape, axes=None) -> AMDStorage:
-    """Transpose that swaps the last two axes (the form the matmul gradient
-    uses, src/qutai/core/operations/linalg.py:37-38)."""
+    """Axis permutation that swaps two adjacent axes: the last two (the form
+    the matmul gradient uses, src/qutai/core/operations/linalg.py:37-38) or
+    any other pair (the head split and merge of nn.MultiHeadAttention,
+    src/qutai/nn/layers.py:322-325, 354)."""
     rank = len(shape)
     axes = tuple(reversed(range(rank))) if axes is None else tuple(a % rank for a in axes)
-    if rank < 2 or axes != (*range(rank - 2), rank - 1, rank - 2):
-        if rank == 2 and axes == (1, 0):
-            pass
-        elif axes == tuple(range(rank)):
-            return values.copy()
-        else:
-            raise NotImplementedError("amd transpose swaps the last two axes only")
+    if axes == tuple(range(rank)):
+        return values.copy()
+    swapped = [i for i in range(rank - 1) if axes[i] == i + 1 and axes[i + 1] == i]
+    if len(swapped) != 1 or any(axes[j] != j for j in range(rank) if j not in (swapped[0], swapped[0] + 1)):
+        raise NotImplementedError("amd transpose swaps two adjacent axes")
+    i = swapped[0]
+    if i < rank - 2:
+        result = AMDStorage(values.size, values.dtype)
+        if values.size:
+            result.runtime.call("qutai_amd_swap_axes", values.ptr, result.ptr, prod(shape[:i]), shape[i],
+                                shape[i + 1], prod(shape[i + 2:]), code(values.dtype))
+        return result
     rows, cols = shape[-2], shape[-1]
     batch = prod(shape[:-2])
     result = AMDStorage(values.size, values.dtype)
@@ -374,6 +381,32 @@ def softmax(values: AMDStorage, shape, axis, *, scale: float = 1.0) -> AMDStorag
     result = AMDStorage(values.size, values.dtype)
     if values.size:
         result.runtime.call("qutai_amd_softmax_rows", values.ptr, result.ptr, rows, width, float(scale),
+                            code(values.dtype))
+    return result
+
+
+def softmax_backward(probs: AMDStorage, gradient: AMDStorage, shape, *, scale: float = 1.0) -> AMDStorage:
+    """Input gradient of ``softmax(values, shape, -1, scale=scale)`` from its
+    output and output gradient: scale * p * (g - rowsum(g * p))."""
+    if probs.dtype != gradient.dtype or probs.size != gradient.size:
+        raise ValueError("softmax_backward needs probabilities and gradient of one dtype and size")
+    width = shape[-1]
+    rows = probs.size // width if width else 0
+    result = AMDStorage(probs.size, probs.dtype)
+    if probs.size:
+        result.runtime.call("qutai_amd_softmax_backward", probs.ptr, gradient.ptr, result.ptr, rows, width,
+                            float(scale), code(probs.dtype))
+    return result
+
+
+def causal_mask(values: AMDStorage, rows: int, width: int, length: int, offset: int = 0) -> AMDStorage:
+    """Scores [rows][width] with keys after each query (row r is query
+    r % length; it sees keys <= offset + r % length) set to -inf."""
+    if values.size != rows * width:
+        raise ValueError("causal_mask size does not match rows x width")
+    result = AMDStorage(values.size, values.dtype)
+    if values.size:
+        result.runtime.call("qutai_amd_causal_mask", values.ptr, result.ptr, rows, width, length, offset,
                             code(values.dtype))
     return result
 

@@ -46,6 +46,7 @@ SIGNATURES = {
     "qutai_amd_add_rows": [_p, _p, _p, _i64, _i64, _i32, _p],
     "qutai_amd_sum_middle": [_p, _p, _i64, _i64, _i64, _i32, _p],
     "qutai_amd_transpose_last2": [_p, _p, _i64, _i64, _i64, _i32, _p],
+    "qutai_amd_swap_axes": [_p, _p, _i64, _i64, _i64, _i64, _i32, _p],
     "qutai_amd_softmax_rows": [_p, _p, _i64, _i64, _f64, _i32, _p],
     "qutai_amd_silu_mul": [_p, _p, _p, _i64, _i32, _p],
     "qutai_amd_silu_mul_backward": [_p, _p, _p, _p, _p, _i64, _i32, _p],
@@ -57,6 +58,8 @@ SIGNATURES = {
     "qutai_amd_route_backward": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p],
     "qutai_amd_scale": [_p, _p, _i64, _f64, _i32, _p],
     "qutai_amd_repitch": [_p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _p],
+    "qutai_amd_softmax_backward": [_p, _p, _p, _i64, _i64, _f64, _i32, _p],
+    "qutai_amd_causal_mask": [_p, _p, _i64, _i64, _i64, _i64, _i32, _p],
     "qutai_amd_embedding": [_p, _p, _p, _i64, _i64, _i32, _p],
     "qutai_amd_embedding_backward": [_p, _p, _p, _p, _p, _i64, _i64, _i32, _p],
     "qutai_amd_rms_norm": [_p, _p, _p, _p, _i64, _i64, _f64, _i32, _p],

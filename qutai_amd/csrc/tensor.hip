@@ -76,6 +76,59 @@ __global__ void repitch_kernel(const void* src, void* dst, int64_t batches, int6
   }
 }
 
+// Softmax backward along rows, one wave per row: dx = scale * p * (g - sum(g p))
+// (the gradient rule of qutai.softmax with the input scaled by `scale`).
+__device__ __forceinline__ float ld_any(const void* p, int64_t i, int d) {
+  return d == F64 ? (float)((const double*)p)[i] : d == F32 ? ((const float*)p)[i] : bf16_to_f32(((const bf16_t*)p)[i]);
+}
+__global__ void __launch_bounds__(256) softmax_backward_kernel(const void* probs, const void* grad, void* out,
+                                                              int64_t rows, int64_t width, float scale, int d) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t base = row * width;
+  float dot = 0.f;
+  for (int64_t j = lane; j < width; j += 64) dot += ld_any(grad, base + j, d) * ld_any(probs, base + j, d);
+  for (int o = 32; o > 0; o >>= 1) dot += __shfl_xor(dot, o);
+  for (int64_t j = lane; j < width; j += 64) {
+    const float v = scale * ld_any(probs, base + j, d) * (ld_any(grad, base + j, d) - dot);
+    if (d == F64) ((double*)out)[base + j] = v;
+    else if (d == F32) ((float*)out)[base + j] = v;
+    else ((bf16_t*)out)[base + j] = f32_to_bf16(v);
+  }
+}
+
+// Causal mask of attention scores [rows][width]: row r is query r % length of
+// its (batch, head) block and sees keys c <= offset + r % length; the others
+// become -inf.
+__global__ void causal_mask_kernel(const void* x, void* out, int64_t rows, int64_t width, int64_t length,
+                                   int64_t offset, int d) {
+  const int64_t n = rows * width;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / width, c = i - r * width;
+    const bool masked = c > offset + r % length;
+    if (d == F64) ((double*)out)[i] = masked ? -INFINITY : ((const double*)x)[i];
+    else if (d == F32) ((float*)out)[i] = masked ? -INFINITY : ((const float*)x)[i];
+    else ((bf16_t*)out)[i] = masked ? (bf16_t)0xff80 : ((const bf16_t*)x)[i];
+  }
+}
+
+// out[o][j][i][e] = x[o][i][j][e] for an (outer, m, n, inner) array: two
+// adjacent axes swapped, each element a run of `inner` values (es bytes each).
+__global__ void swap_axes_kernel(const void* x, void* out, int64_t outer, int64_t m, int64_t n, int64_t inner,
+                                 int es) {
+  const int64_t total = outer * m * n * inner;
+  for (int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; k < total; k += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t e = k % inner, rest = k / inner;
+    const int64_t i = rest % m, rest2 = rest / m;  // output index order: o, j, i, e
+    const int64_t j = rest2 % n, o = rest2 / n;
+    const int64_t src = ((o * m + i) * n + j) * inner + e;
+    if (es == 8) ((double*)out)[k] = ((const double*)x)[src];
+    else if (es == 4) ((float*)out)[k] = ((const float*)x)[src];
+    else ((bf16_t*)out)[k] = ((const bf16_t*)x)[src];
+  }
+}
+
 __global__ void add_kernel(const void* a, const void* b, void* out, int64_t n, int d) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
     if (d == F64) {
@@ -471,6 +524,17 @@ int qutai_amd_sum_middle(const void* x, void* out, int64_t outer, int64_t count,
   return (int)hipGetLastError();
 }
 
+int qutai_amd_swap_axes(const void* x, void* out, int64_t outer, int64_t m, int64_t n, int64_t inner, int dtype,
+                        void* stream) {
+  if (outer < 0 || m < 0 || n < 0 || inner < 0 || !float_dtype(dtype)) return QA_EINVAL;
+  const int64_t total = outer * m * n * inner;
+  if (total == 0) return QA_OK;
+  if (!x || !out) return QA_EINVAL;
+  hipLaunchKernelGGL(swap_axes_kernel, dim3(grid_for(total)), dim3(THREADS), 0, (hipStream_t)stream, x, out, outer, m,
+                     n, inner, dtype == F64 ? 8 : dtype == F32 ? 4 : 2);
+  return (int)hipGetLastError();
+}
+
 int qutai_amd_transpose_last2(const void* x, void* out, int64_t batch, int64_t rows, int64_t cols, int dtype,
                               void* stream) {
   if (batch < 0 || rows < 0 || cols < 0 || !float_dtype(dtype)) return QA_EINVAL;
@@ -518,6 +582,26 @@ int qutai_amd_softmax_rows(const void* x, void* out, int64_t rows, int64_t width
       hipLaunchKernelGGL((softmax_rows_kernel<bf16_t, 8>), dim3((unsigned)rows), dim3(THREADS), 0, s,
                          (const bf16_t*)x, (bf16_t*)out, rows, width, (float)scale);
   }
+  return (int)hipGetLastError();
+}
+
+int qutai_amd_softmax_backward(const void* probs, const void* grad, void* out, int64_t rows, int64_t width,
+                               double scale, int dtype, void* stream) {
+  if (rows < 0 || width < 0 || !float_dtype(dtype)) return QA_EINVAL;
+  if (rows == 0 || width == 0) return QA_OK;
+  if (!probs || !grad || !out || (rows + 3) / 4 > 0x7fffffff) return QA_EINVAL;
+  hipLaunchKernelGGL(softmax_backward_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, (hipStream_t)stream,
+                     probs, grad, out, rows, width, (float)scale, dtype);
+  return (int)hipGetLastError();
+}
+
+int qutai_amd_causal_mask(const void* x, void* out, int64_t rows, int64_t width, int64_t length, int64_t offset,
+                          int dtype, void* stream) {
+  if (rows < 0 || width < 0 || length <= 0 || offset < 0 || !float_dtype(dtype)) return QA_EINVAL;
+  if (rows == 0 || width == 0) return QA_OK;
+  if (!x || !out) return QA_EINVAL;
+  hipLaunchKernelGGL(causal_mask_kernel, dim3(grid_for(rows * width)), dim3(THREADS), 0, (hipStream_t)stream, x, out,
+                     rows, width, length, offset, dtype);
   return (int)hipGetLastError();
 }
 

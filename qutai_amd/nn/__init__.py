@@ -1,3 +1,3 @@
-from .layers import Linear
+from .layers import Attention, Linear, MultiHeadAttention, causal_mask, softmax
 
-__all__ = ["Linear"]
+__all__ = ["Attention", "Linear", "MultiHeadAttention", "causal_mask", "softmax"]

@@ -335,6 +335,27 @@ def test_attention_backward_matches_finite_differences_and_numpy_form():
     assert np.abs(sum(p[2] for p in parts).ravel() - dv).max() < 1e-12
 
 
+def test_non_causal_numpy_attention_backward_matches_finite_differences():
+    """attention_backward_np(causal=False) against central differences of
+    attention_np(causal=False) (the nn attention form)."""
+    rng = np.random.default_rng(8)
+    time, dim = 5, 3
+    q, k, v = (rng.standard_normal((time, dim)) * 0.7 for _ in range(3))
+    g = rng.standard_normal((time, dim))
+    out, lse = ora.attention_np(q, k, v, causal=False, scale=0.6)
+    dq, dk, dv = ora.attention_backward_np(g, q, k, v, out, lse, scale=0.6, causal=False)
+    eps = 1e-6
+    for tensor, grad in ((q, dq), (k, dk), (v, dv)):
+        for i in np.ndindex(tensor.shape):
+            saved = tensor[i]
+            tensor[i] = saved + eps
+            up = float((ora.attention_np(q, k, v, causal=False, scale=0.6)[0] * g).sum())
+            tensor[i] = saved - eps
+            down = float((ora.attention_np(q, k, v, causal=False, scale=0.6)[0] * g).sum())
+            tensor[i] = saved
+            assert grad[i] == pytest.approx((up - down) / (2 * eps), rel=1e-6, abs=1e-9)
+
+
 # ---- routing / combine backward ----------------------------------------------------
 
 def _renormalised_weights(scores, route):
