@@ -50,8 +50,10 @@ __global__ void route_select(const float* scores, float* probs, float* weights, 
 constexpr int PACKW = 16;
 __global__ void __launch_bounds__(PACKW * 64) route_pack(const int64_t* indices, int64_t* counts, int64_t* ids,
                                                          int64_t* slots, int64_t* locations, int64_t* offsets,
-                                                         int64_t* order, int64_t n, int64_t top_k, int64_t experts) {
+                                                         int64_t* order, int64_t n, int64_t top_k, int64_t experts,
+                                                         const float* probs, float* column) {
   __shared__ int64_t seg_count[PACKW], seg_lower[PACKW];
+  __shared__ float col_part[PACKW * 64];
   const int64_t e = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t seg = (n + PACKW - 1) / PACKW;
@@ -96,37 +98,35 @@ __global__ void __launch_bounds__(PACKW * 64) route_pack(const int64_t* indices,
     offsets[e] = base;
     if (e == experts - 1) offsets[experts] = n;
   }
-}
-
-// utilization = count / (rows * top_k); aux = experts * sum(p * util) / rows.
-// One 1024-thread workgroup: thread t sums the probabilities t, t + 1024,
-// ... (coalesced) weighted by their expert's utilization, then a fixed-order
-// tree reduction in LDS (deterministic result).
-constexpr int STATS = 1024;
-__global__ void __launch_bounds__(STATS) route_stats(const float* probs, const int64_t* counts, float* utilization,
-                                                     float* aux, int64_t rows, int64_t experts, int64_t n) {
-  __shared__ float util[256];
-  __shared__ float red[STATS];
-  int tid = threadIdx.x;
-  for (int64_t e = tid; e < experts; e += STATS) {
-    float u = (float)counts[e] / (float)n;
-    utilization[e] = u;
-    if (e < 256) util[e] = u;
-  }
+  // the expert's probability column sum (thread t: rows t, t + 1024, ...;
+  // fixed-order tree), left in column[e] for route_stats
+  const int64_t rows = n / top_k;
+  float part = 0.f;
+  for (int64_t r = tid; r < rows; r += PACKW * 64) part += probs[r * experts + e];
+  col_part[tid] = part;
   __syncthreads();
-  const int64_t total_values = rows * experts;
-  float total = 0.f;
-  for (int64_t i = tid; i < total_values; i += STATS) {
-    const int64_t e = i % experts;
-    total += probs[i] * (e < 256 ? util[e] : (float)counts[e] / (float)n);
-  }
-  red[tid] = total;
-  __syncthreads();
-  for (int s = STATS / 2; s > 0; s >>= 1) {
-    if (tid < s) red[tid] += red[tid + s];
+  for (int w = PACKW * 32; w > 0; w >>= 1) {
+    if (tid < w) col_part[tid] += col_part[tid + w];
     __syncthreads();
   }
-  if (tid == 0) aux[0] = (float)experts * red[0] / (float)rows;
+  if (tid == 0) column[e] = col_part[0];
+}
+
+// utilization = count / (rows * top_k); aux = experts * sum_e util_e *
+// colsum_e / rows, with colsum_e (the expert's probability column sum) left
+// in `utilization` by route_pack.  One wave, lanes over the experts in a
+// fixed order (deterministic result).
+__global__ void __launch_bounds__(64) route_stats(const int64_t* counts, float* utilization, float* aux, int64_t rows,
+                                                  int64_t experts, int64_t n) {
+  const int lane = threadIdx.x;
+  float total = 0.f;
+  for (int64_t e = lane; e < experts; e += 64) {
+    const float u = (float)counts[e] / (float)n;
+    total += u * utilization[e];
+    utilization[e] = u;
+  }
+  for (int o = 32; o > 0; o >>= 1) total += __shfl_xor(total, o);
+  if (lane == 0) aux[0] = (float)experts * total / (float)rows;
 }
 
 // Row gather / scatter in 16-byte pieces.
@@ -263,9 +263,9 @@ int qutai_amd_route(const float* scores, float* probs, float* weights, int64_t* 
     hipLaunchKernelGGL(route_select, dim3(blocks_for(rows)), dim3(256), 0, s, scores, probs, weights, indices, rows,
                        experts, top_k);
   hipLaunchKernelGGL(route_pack, dim3((unsigned)experts), dim3(PACKW * 64), 0, s, indices, counts, ids, slots,
-                     locations, offsets, order, n, top_k, experts);
+                     locations, offsets, order, n, top_k, experts, (const float*)probs, utilization);
   if (rows > 0)
-    hipLaunchKernelGGL(route_stats, dim3(1), dim3(STATS), 0, s, probs, counts, utilization, aux, rows, experts, n);
+    hipLaunchKernelGGL(route_stats, dim3(1), dim3(64), 0, s, counts, utilization, aux, rows, experts, n);
   return (int)hipGetLastError();
 }
 
