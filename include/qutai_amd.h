@@ -127,7 +127,7 @@ int qutai_amd_softmax_backward(const void* probs, const void* grad, void* out, i
 int qutai_amd_causal_mask(const void* x, void* out, int64_t rows, int64_t width, int64_t length, int64_t offset,
                           int dtype, void* stream);
 
-/* out[r][c] = x[r][c] + bias[c] (rows x cols; one rounding)./* out[r][c] = x[r][c] + bias[c] (rows x cols; one rounding).  The bias add
+/* out[r][c] = x[r][c] + bias[c] (rows x cols; one rounding).  The bias add
  * of nn.Linear (src/qutai/nn/layers.py:145-148, a broadcast `add`) and the
  * broadcast of a scalar gradient (cols = 1). */
 int qutai_amd_add_rows(const void* x, const void* bias, void* out, int64_t rows, int64_t cols, int dtype,

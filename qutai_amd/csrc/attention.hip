@@ -77,15 +77,6 @@ __device__ __forceinline__ float pair_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-
-// Two floats -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32).
-__device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
-  f32x2 v = {a, b};
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
-}
-
 // One 64-key block for the wave's NQB query blocks.  MASK: some key of the
 // block is past T or (causal) after a query; lim[qb] is then the number of
 // leading keys of the block the lane's query may see, minus 4 * half.
@@ -200,8 +191,8 @@ __device__ __forceinline__ void attend_block(const bf16_t* sk, const bf16_t* sv,
           pv[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[qb][mb][8 * st + e], c, -ref));
           sum += pv[e];
         }
-        u32x4 w = {cvt_pk_bf16(pv[0], pv[1]), cvt_pk_bf16(pv[2], pv[3]), cvt_pk_bf16(pv[4], pv[5]),
-                   cvt_pk_bf16(pv[6], pv[7])};
+        u32x4 w = {pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3]), pack_bf16x2(pv[4], pv[5]),
+                   pack_bf16x2(pv[6], pv[7])};
         pf[mb][st] = __builtin_bit_cast(bf16x8, w);
       }
     l[qb] += sum;
@@ -350,8 +341,8 @@ __global__ void __launch_bounds__(NW * 64) attention_fwd_d64(AttnArgs p) {
 #pragma unroll
         for (int g = 0; g < 4; g++) {
           uint2 w;
-          w.x = cvt_pk_bf16(o[qb][db][4 * g] * inv, o[qb][db][4 * g + 1] * inv);
-          w.y = cvt_pk_bf16(o[qb][db][4 * g + 2] * inv, o[qb][db][4 * g + 3] * inv);
+          w.x = pack_bf16x2(o[qb][db][4 * g] * inv, o[qb][db][4 * g + 1] * inv);
+          w.y = pack_bf16x2(o[qb][db][4 * g + 2] * inv, o[qb][db][4 * g + 3] * inv);
           *reinterpret_cast<uint2*>(out + 32 * db + 8 * g + 4 * half) = w;
         }
       if (p.lse && half == 0) p.lse[b * p.lb + h * p.lh + t * p.lt] = (m[qb] + __log2f(total)) * 0.6931471805599453f;
@@ -479,8 +470,8 @@ __device__ __forceinline__ void dq_block(const bf16_t* sk, const bf16_t* sv, con
       }
 #pragma unroll
       for (int st = 0; st < 2; st++) {
-        u32x4 w = {cvt_pk_bf16(ds[8 * st], ds[8 * st + 1]), cvt_pk_bf16(ds[8 * st + 2], ds[8 * st + 3]),
-                   cvt_pk_bf16(ds[8 * st + 4], ds[8 * st + 5]), cvt_pk_bf16(ds[8 * st + 6], ds[8 * st + 7])};
+        u32x4 w = {pack_bf16x2(ds[8 * st], ds[8 * st + 1]), pack_bf16x2(ds[8 * st + 2], ds[8 * st + 3]),
+                   pack_bf16x2(ds[8 * st + 4], ds[8 * st + 5]), pack_bf16x2(ds[8 * st + 6], ds[8 * st + 7])};
         dsf[mb][st] = __builtin_bit_cast(bf16x8, w);
       }
     }
@@ -628,8 +619,8 @@ __global__ void __launch_bounds__(NW * 64) attention_bwd_dq_d64(AttnBwdArgs p) {
         for (int g = 0; g < 4; g++) {
           uint2 w;
           const float sc = p.scale;
-          w.x = cvt_pk_bf16(dqt[qb][db][4 * g] * sc, dqt[qb][db][4 * g + 1] * sc);
-          w.y = cvt_pk_bf16(dqt[qb][db][4 * g + 2] * sc, dqt[qb][db][4 * g + 3] * sc);
+          w.x = pack_bf16x2(dqt[qb][db][4 * g] * sc, dqt[qb][db][4 * g + 1] * sc);
+          w.y = pack_bf16x2(dqt[qb][db][4 * g + 2] * sc, dqt[qb][db][4 * g + 3] * sc);
           *reinterpret_cast<uint2*>(out + 32 * db + 8 * g + 4 * half) = w;
         }
     }
@@ -685,11 +676,11 @@ __device__ __forceinline__ void dkv_block(const bf16_t* sq, const bf16_t* sg, co
       }
 #pragma unroll
       for (int st = 0; st < 2; st++) {
-        u32x4 w = {cvt_pk_bf16(pr[8 * st], pr[8 * st + 1]), cvt_pk_bf16(pr[8 * st + 2], pr[8 * st + 3]),
-                   cvt_pk_bf16(pr[8 * st + 4], pr[8 * st + 5]), cvt_pk_bf16(pr[8 * st + 6], pr[8 * st + 7])};
+        u32x4 w = {pack_bf16x2(pr[8 * st], pr[8 * st + 1]), pack_bf16x2(pr[8 * st + 2], pr[8 * st + 3]),
+                   pack_bf16x2(pr[8 * st + 4], pr[8 * st + 5]), pack_bf16x2(pr[8 * st + 6], pr[8 * st + 7])};
         pf[nb][st] = __builtin_bit_cast(bf16x8, w);
-        u32x4 z = {cvt_pk_bf16(ds[8 * st], ds[8 * st + 1]), cvt_pk_bf16(ds[8 * st + 2], ds[8 * st + 3]),
-                   cvt_pk_bf16(ds[8 * st + 4], ds[8 * st + 5]), cvt_pk_bf16(ds[8 * st + 6], ds[8 * st + 7])};
+        u32x4 z = {pack_bf16x2(ds[8 * st], ds[8 * st + 1]), pack_bf16x2(ds[8 * st + 2], ds[8 * st + 3]),
+                   pack_bf16x2(ds[8 * st + 4], ds[8 * st + 5]), pack_bf16x2(ds[8 * st + 6], ds[8 * st + 7])};
         dsf[nb][st] = __builtin_bit_cast(bf16x8, z);
       }
     }
@@ -846,10 +837,10 @@ __global__ void __launch_bounds__(NW * 64) attention_bwd_dkv_d64(AttnBwdArgs p) 
         for (int g = 0; g < 4; g++) {
           uint2 wk, wv;
           const float sc = p.scale;
-          wk.x = cvt_pk_bf16(dkt[db][nb][4 * g] * sc, dkt[db][nb][4 * g + 1] * sc);
-          wk.y = cvt_pk_bf16(dkt[db][nb][4 * g + 2] * sc, dkt[db][nb][4 * g + 3] * sc);
-          wv.x = cvt_pk_bf16(dvt[db][nb][4 * g], dvt[db][nb][4 * g + 1]);
-          wv.y = cvt_pk_bf16(dvt[db][nb][4 * g + 2], dvt[db][nb][4 * g + 3]);
+          wk.x = pack_bf16x2(dkt[db][nb][4 * g] * sc, dkt[db][nb][4 * g + 1] * sc);
+          wk.y = pack_bf16x2(dkt[db][nb][4 * g + 2] * sc, dkt[db][nb][4 * g + 3] * sc);
+          wv.x = pack_bf16x2(dvt[db][nb][4 * g], dvt[db][nb][4 * g + 1]);
+          wv.y = pack_bf16x2(dvt[db][nb][4 * g + 2], dvt[db][nb][4 * g + 3]);
           *reinterpret_cast<uint2*>(ok + 32 * db + 8 * g + 4 * half) = wk;
           *reinterpret_cast<uint2*>(ov + 32 * db + 8 * g + 4 * half) = wv;
         }

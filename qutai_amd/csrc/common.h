@@ -19,24 +19,32 @@ typedef __attribute__((__vector_size__(4 * sizeof(short)))) short i16x4;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
 typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
+typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2;
 
 // bfloat16 -> float is exact: the 16 bits become the high half of an fp32.
 __device__ __forceinline__ float bf16_to_f32(bf16_t v) {
   return __uint_as_float(((uint32_t)v) << 16);
 }
 
-// float -> bfloat16, round to nearest even; NaN stays a quiet NaN with its
-// sign and top payload bits.  Same bit rule as the reference host encoder
-// (src/qutai/backends/cuda.py:98-101) and __float2bfloat16_rn on device.
-__device__ __forceinline__ bf16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x40u);
-  return (bf16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+// float -> bfloat16 with gfx950's v_cvt_pk_bf16_f32: round to nearest even,
+// denormals kept, and a NaN becomes (bits >> 16) | 0x40 (quiet, sign and top
+// payload bits kept).  That is bit for bit the reference host encoder's rule
+// (src/qutai/backends/cuda.py:98-101), checked on the GPU over the special
+// values and 4M random bit patterns.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {  // low half = a
+  f32x2_t v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
+__device__ __forceinline__ bf16_t f32_to_bf16(float f) { return (bf16_t)(pack_bf16x2(f, 0.0f) & 0xffffu); }
 
-// Two floats -> two packed bfloat16 (low half = a).
-__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  return (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
+// Store through a global (address space 1) pointer: a generic pointer makes
+// the compiler emit flat stores, which also count against lgkmcnt, so every
+// later wait for an LDS read would wait for the stores as well.
+template <class V, class P>
+__device__ __forceinline__ void global_store(P* p, const V& v) {
+  *(__attribute__((address_space(1))) V*)(p) = v;
 }
 
 // Values that are the same for the whole wavefront but that the compiler

@@ -270,8 +270,12 @@ void launch_prepare(Operand& o, int src_dtype, bool bf16, char* ws, hipStream_t 
 }
 
 // 4-wide output stores need 4 | ldc, 4 | batch stride and an aligned base.
-bool vec_out(const void* p, int64_t ldc, int64_t stride) {
-  return ((uintptr_t)p % 16 == 0) && (ldc % 4 == 0) && (stride % 4 == 0);
+// 2: every output row starts 16-byte aligned for both element sizes;
+// 1: 16-byte aligned fp32 rows / 8-byte aligned bf16 rows; 0: neither.
+int vec_out(const void* p, int64_t ldc, int64_t stride) {
+  if ((uintptr_t)p % 16 != 0) return 0;
+  if (ldc % 8 == 0 && stride % 8 == 0) return 2;
+  return (ldc % 4 == 0 && stride % 4 == 0) ? 1 : 0;
 }
 
 int esize_of(int dtype) { return dtype == QA_BF16 ? 2 : dtype == QA_F64 ? 8 : 4; }

@@ -44,7 +44,8 @@ struct GemmArgs {
   int64_t batch;
   int accumulate;         // out = old + A@B
   int out_bf16;           // output element type: bf16 (1) or fp32 (0)
-  int vec_c;              // output rows allow 16-byte (fp32) / 8-byte (bf16) stores
+  int vec_c;              // 1: output rows allow 16-byte fp32 / 8-byte bf16 stores;
+                          // 2: also 16-byte bf16 stores
   // Grouped mode (groups > 0): group g owns rows [offsets[g], offsets[g+1])
   // of A (K-major, lda) and of out (ldc); its B operand is b + g*sb.
   const int64_t* offsets;
@@ -546,14 +547,18 @@ struct GemmKernel {
     o.vec = p.vec_c;
     o.alpha = p.alpha;
     float* stage = reinterpret_cast<float*>(smem) + wave * 32 * EP;
-    store_rows<0>(acc, stage, o, lane);
+    __syncthreads();  // every wave has read the ring's last stage
+    // full in-bounds wave tile, plain store: straight-line 16-byte stores
+    const bool fast = o.vec >= (o.bf16 ? 2 : 1) && !o.accumulate && o.row0 + TM <= o.M && o.col0 + TN <= o.N;
+    store_rows<0>(acc, stage, o, lane, fast);
   }
 
   // Output staging: each wave turns one 32-row slab of its accumulators
   // (MFMA C layout: lane l holds column l & 31 and rows
   // 8 (e/4) + 4 (l >> 5) + (e & 3) of a 32x32 block) into row-major order in
-  // LDS, then writes it with 16-byte (fp32) or 8-byte (bf16) stores along
-  // rows (row pitch EP).
+  // its own LDS area (row pitch EP), then writes it along rows.  The area is
+  // private to the wave and a wave's LDS operations complete in order, so
+  // slabs need no workgroup barrier.
 
   struct Out {
     char* ptr;
@@ -563,22 +568,22 @@ struct GemmKernel {
   };
 
   __device__ static __forceinline__ void write4(const Out& o, int64_t row, int64_t col, f32x4 v) {
+    typedef __attribute__((address_space(1))) bf16_t gbf16;
+    typedef __attribute__((address_space(1))) float gf32;
     v *= o.alpha;
     int64_t at = row * o.ldc + col;
     if (o.bf16) {
-      bf16_t* q = reinterpret_cast<bf16_t*>(o.ptr) + at;
+      gbf16* q = (gbf16*)(o.ptr) + at;
       if (o.vec && col + 4 <= o.N) {
+        typedef __attribute__((address_space(1))) u32x2 gu2;
         if (o.accumulate) {
-          uint2 old = *reinterpret_cast<const uint2*>(q);
-          v[0] += __uint_as_float(old.x << 16);
-          v[1] += __uint_as_float(old.x & 0xffff0000u);
-          v[2] += __uint_as_float(old.y << 16);
-          v[3] += __uint_as_float(old.y & 0xffff0000u);
+          u32x2 old = *(const gu2*)q;
+          v[0] += __uint_as_float(old[0] << 16);
+          v[1] += __uint_as_float(old[0] & 0xffff0000u);
+          v[2] += __uint_as_float(old[1] << 16);
+          v[3] += __uint_as_float(old[1] & 0xffff0000u);
         }
-        uint2 w;
-        w.x = pack_bf16x2(v[0], v[1]);
-        w.y = pack_bf16x2(v[2], v[3]);
-        *reinterpret_cast<uint2*>(q) = w;
+        *(gu2*)q = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
       } else {
 #pragma unroll
         for (int t = 0; t < 4; t++) {
@@ -590,10 +595,11 @@ struct GemmKernel {
         }
       }
     } else {
-      float* q = reinterpret_cast<float*>(o.ptr) + at;
+      gf32* q = (gf32*)(o.ptr) + at;
       if (o.vec && col + 4 <= o.N) {
-        if (o.accumulate) v += *reinterpret_cast<const f32x4*>(q);
-        *reinterpret_cast<f32x4*>(q) = v;
+        typedef __attribute__((address_space(1))) f32x4 gf4;
+        if (o.accumulate) v += *(const gf4*)q;
+        *(gf4*)q = v;
       } else {
 #pragma unroll
         for (int t = 0; t < 4; t++) {
@@ -609,9 +615,8 @@ struct GemmKernel {
 
   template <int I>
   __device__ static __forceinline__ void store_rows(const f32x16 (&acc)[FM][FN], float* stage, const Out& o,
-                                                    int lane) {
+                                                    int lane, bool fast) {
     if constexpr (I < FM) {
-      __syncthreads();  // staging area free (the K loop or the previous slab is done)
 #pragma unroll
       for (int j = 0; j < FN; j++)
 #pragma unroll
@@ -619,19 +624,51 @@ struct GemmKernel {
           int r = 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
           stage[r * EP + j * 32 + (lane & 31)] = acc[I][j][e];
         }
-      __syncthreads();
-      constexpr int Q = TN / 4;  // float4 per staged row
-      constexpr int ITERS = 32 * Q / 64;
+      __builtin_amdgcn_wave_barrier();
+      const int64_t row_base = o.row0 + I * 32;
+      if (fast && o.bf16) {
+        // lane -> 8 consecutive columns of one row: one 16-byte store each
+        constexpr int Q = TN / 8, ITERS = 32 * Q / 64;
+        static_assert(64 % Q == 0, "whole rows per store instruction");
+        u32x4 w[ITERS];
 #pragma unroll
-      for (int it = 0; it < ITERS; it++) {
-        int idx = it * 64 + lane;
-        int r = idx / Q, q = idx % Q;
-        f32x4 v = *reinterpret_cast<const f32x4*>(stage + r * EP + 4 * q);
-        int64_t row = o.row0 + I * 32 + r;
-        int64_t col = o.col0 + 4 * q;
-        if (row < o.M && col < o.N) write4(o, row, col, v);
+        for (int it = 0; it < ITERS; it++) {
+          int idx = it * 64 + lane, r = idx / Q, q = idx % Q;
+          f32x4 a = *reinterpret_cast<const f32x4*>(stage + r * EP + 8 * q) * o.alpha;
+          f32x4 b = *reinterpret_cast<const f32x4*>(stage + r * EP + 8 * q + 4) * o.alpha;
+          w[it] = u32x4{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3]), pack_bf16x2(b[0], b[1]),
+                        pack_bf16x2(b[2], b[3])};
+        }
+        bf16_t* dst = reinterpret_cast<bf16_t*>(o.ptr) + (row_base + lane / Q) * o.ldc + o.col0 + 8 * (lane % Q);
+#pragma unroll
+        for (int it = 0; it < ITERS; it++) global_store(dst + it * (64 / Q) * o.ldc, w[it]);
+      } else if (fast) {
+        constexpr int Q = TN / 4, ITERS = 32 * Q / 64;
+        static_assert(64 % Q == 0, "whole rows per store instruction");
+        f32x4 v[ITERS];
+#pragma unroll
+        for (int it = 0; it < ITERS; it++) {
+          int idx = it * 64 + lane, r = idx / Q, q = idx % Q;
+          v[it] = *reinterpret_cast<const f32x4*>(stage + r * EP + 4 * q) * o.alpha;
+        }
+        float* dst = reinterpret_cast<float*>(o.ptr) + (row_base + lane / Q) * o.ldc + o.col0 + 4 * (lane % Q);
+#pragma unroll
+        for (int it = 0; it < ITERS; it++) global_store(dst + it * (64 / Q) * o.ldc, v[it]);
+      } else {
+        constexpr int Q = TN / 4;  // float4 per staged row
+        constexpr int ITERS = 32 * Q / 64;
+#pragma unroll
+        for (int it = 0; it < ITERS; it++) {
+          int idx = it * 64 + lane;
+          int r = idx / Q, q = idx % Q;
+          f32x4 v = *reinterpret_cast<const f32x4*>(stage + r * EP + 4 * q);
+          int64_t row = row_base + r;
+          int64_t col = o.col0 + 4 * q;
+          if (row < o.M && col < o.N) write4(o, row, col, v);
+        }
       }
-      store_rows<I + 1>(acc, stage, o, lane);
+      __builtin_amdgcn_wave_barrier();
+      store_rows<I + 1>(acc, stage, o, lane, fast);
     }
   }
 };
