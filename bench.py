@@ -1,9 +1,11 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X GEMM hot path (BASELINE.json metric).
 
-Step = one bf16-storage 4096^3 GEMM (fp32 accumulation, fp32 output) through
-the amd backend's ``gemm`` (the largest single-GPU
-config the headline is quoted on).  W untimed warm-up steps, then K steps
+Step = one bf16-storage 4096^3 product C = A @ B through ``amd.matmul``, the
+call Tensor ``@`` makes (fp32 accumulation; the result keeps A's storage
+dtype, bf16, as the reference's matmul does; BASELINE config 2, the largest
+single-GPU config the headline is quoted on).  The same product with an fp32
+output through ``gemm`` is reported beside it.  W untimed warm-up steps, then K steps
 timed with HIP events on the default stream (the stream every kernel runs
 on) between two device synchronisations.  The JSON line also carries the
 other configs (fp32 4096^3, the ragged shape, attention bmm and fused
@@ -70,16 +72,25 @@ class Timer:
 
 # ---- workloads -----------------------------------------------------------------
 
-def gemm_square(dtype, n=4096, seed=1):
+def gemm_square(dtype, n=4096, seed=1, out_dtype=None):
+    """C = A @ B, 4096^3 row-major.  By default through ``amd.matmul``, the
+    call Tensor ``@`` makes: the output has the storage dtype of A, as in the
+    reference (src/qutai/backends/cuda.py:374, ``out_dtype=left.dtype``), so
+    bf16 storage gives a bf16 result of the fp32 accumulation.  With
+    ``out_dtype`` the product goes through ``amd.gemm`` into a preallocated
+    output of that dtype (the reference's ``gemm`` default is fp32)."""
     from qutai_amd.backends import amd
 
     rng = np.random.default_rng(seed)
     a = upload(rng.standard_normal(n * n) * n ** -0.5, dtype)
     b = upload(rng.standard_normal(n * n) * n ** -0.5, dtype)
-    out = amd.full(n * n, 0.0, dtype="float32")
     flops = 2.0 * n ** 3
-    return (lambda: amd.gemm(a, b, n, n, n, out=out)), flops, {"M": n, "N": n, "K": n, "storage": dtype,
-                                                               "layout": "row-major A@B (NN)", "out": "float32"}
+    config = {"M": n, "N": n, "K": n, "storage": dtype, "layout": "row-major A@B (NN)"}
+    if out_dtype is None:
+        return (lambda: amd.matmul(a, b, (n, n), (n, n))), flops, {**config, "out": dtype, "call": "Tensor @"}
+    out = amd.full(n * n, 0.0, dtype=out_dtype)
+    return ((lambda: amd.gemm(a, b, n, n, n, out=out, out_dtype=out_dtype)), flops,
+            {**config, "out": out_dtype, "call": "gemm"})
 
 
 def gemm_ragged(dtype, seed=1):
@@ -280,6 +291,7 @@ def decoder_train(seed=5):
 
 WORKLOADS = {
     "gemm_bf16_4096": (lambda: gemm_square("bfloat16"), "bf16"),
+    "gemm_bf16_4096_f32out": (lambda: gemm_square("bfloat16", out_dtype="float32"), "bf16"),
     "gemm_fp32_4096": (lambda: gemm_square("float32"), "fp32"),
     "gemm_bf16_ragged": (lambda: gemm_ragged("bfloat16"), "bf16"),
     "gemm_fp32_ragged": (lambda: gemm_ragged("float32"), "fp32"),
@@ -394,7 +406,8 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (numpy PCG64 draws, N(0,1)*K^-1/2, seed 1); inputs resident in HBM",
         "config": {"workload": HEADLINE, "M": 4096, "N": 4096, "K": 4096, "storage": "bfloat16",
-                   "accumulate": "float32", "out": "float32", "layout": "row-major A@B"},
+                   "accumulate": "float32", "out": "bfloat16", "call": "Tensor @ (amd.matmul)",
+                   "layout": "row-major A@B"},
         "roofline": None,
         "results": results,
     }
