@@ -82,6 +82,24 @@ int qutai_amd_gemm_grouped(const void* a, const void* b, void* out, const int64_
                            int64_t max_rows, int64_t inner, int64_t cols, int64_t expert_stride,
                            int transpose_right, int dtype, int out_dtype, int accumulate, void* stream);
 
+/* SwiGLU feed-forward input side in one GEMM (bf16 only):
+ *   out = silu(a @ w_gate^T) * (a @ w_up^T)      [rows][hidden] bf16
+ * with the roundings of the unfused form: both products rounded to bf16,
+ * silu(gate) rounded to bf16, the product rounded once.  a is [rows][inner]
+ * (row-major), w_gate / w_up are [hidden][inner] (the lm weight layout).
+ * gate_out / up_out (optional, may be null) receive the two bf16 products
+ * for the backward pass.  With offsets (device, [groups+1] int64) the rows
+ * are grouped by expert as in qutai_amd_gemm_grouped (rows = an upper bound
+ * of offsets[groups]; expert g uses w + g*expert_stride); without, one
+ * plain product.  Rows of a and the weights need 16-byte alignment (inner a
+ * multiple of 8).  Replaces `silu(self.gate(x)) * self.up(x)` of the SwiGLU
+ * block (src/qutai/lm/layers.py:310-311: two projections, lm_silu of
+ * cuda/lm.cu:54 and the elementwise multiply), run per expert by SparseMoE
+ * (lm/layers.py:395-397). */
+int qutai_amd_gemm_swiglu(const void* a, const void* w_gate, const void* w_up, void* out, void* gate_out,
+                          void* up_out, const int64_t* offsets, int groups, int64_t rows, int64_t inner,
+                          int64_t hidden, int64_t expert_stride, int dtype, void* stream);
+
 /* Element-wise dtype conversion of n values (fp32/fp64/bf16 among each
  * other; narrowing to bf16 rounds to nearest even).
  * Replaces: `cast` (src/qutai/backends/cuda/tensor.cu:21-29) as driven by

@@ -184,6 +184,32 @@ def grouped_gemm(rows_block, weight_stack, route, inner, cols, *, out_dtype="bfl
     return out
 
 
+def swiglu_gemm(rows_block, w_gate, w_up, rows, inner, hidden, *, route=None, save=False):
+    """silu(rows_block @ W_gate^T) * (rows_block @ W_up^T) in one bf16 GEMM
+    (qutai_amd_gemm_swiglu), with the unfused form's roundings.  With
+    ``route`` the rows are grouped by expert and W_* are [experts][hidden][inner]
+    stacks; without, one [hidden][inner] weight pair and ``rows`` rows.  With
+    ``save`` the bf16 gate and up products are returned too (for the
+    backward): (act, gate, up)."""
+    if route is not None:
+        rows, groups = route["capacity"], route["experts"]
+    else:
+        groups = 1
+    if rows_block.dtype != "bfloat16" or {w_gate.dtype, w_up.dtype} != {"bfloat16"}:
+        raise ValueError("swiglu_gemm runs bf16 operands")
+    if rows_block.size != rows * inner or w_gate.size != groups * hidden * inner or w_up.size != w_gate.size:
+        raise ValueError("swiglu_gemm operand sizes do not match rows, inner and hidden")
+    act = AMDStorage(rows * hidden, "bfloat16")
+    gate = AMDStorage(rows * hidden, "bfloat16") if save else None
+    up = AMDStorage(rows * hidden, "bfloat16") if save else None
+    if act.size:
+        act.runtime.call("qutai_amd_gemm_swiglu", rows_block.ptr, w_gate.ptr, w_up.ptr, act.ptr,
+                         gate.ptr if save else None, up.ptr if save else None,
+                         route["offsets"].ptr if route is not None else None, groups, rows, inner, hidden,
+                         hidden * inner, code("bfloat16"), mfma=True)
+    return (act, gate, up) if save else act
+
+
 def grouped_gemm_k(a_block, b_block, route, rows, cols, *, out_dtype="float32"):
     """out[e] = A_e^T B_e for every expert, A_e / B_e the expert-major routed
     rows of a_block ([capacity][rows]) and b_block ([capacity][cols]): the
@@ -220,8 +246,9 @@ def _pad8(n):
 
 
 def moe_experts_forward(x, route, w_gate, w_up, w_down, width, hidden, *, save=False):
-    """Expert SwiGLU for every routed (token, slot): gather, grouped gate/up,
-    silu(gate) * up, grouped down, weighted combine (lm/layers.py:395-399).
+    """Expert SwiGLU for every routed (token, slot): gather, grouped gate/up
+    and silu(gate) * up (one fused grouped GEMM for bf16, same roundings),
+    grouped down, weighted combine (lm/layers.py:395-399).
     Weights of another dtype than x (fp32 master weights, bf16 activations)
     are rounded to x's dtype for the products, as the reference's mixed GEMM
     does.  Widths that are not multiples of 8 run zero padded to the next
@@ -236,9 +263,14 @@ def moe_experts_forward(x, route, w_gate, w_up, w_down, width, hidden, *, save=F
         wg, wu = (repitch(w, experts, hidden, width, hp, wp) for w in (wg, wu))
         wd = repitch(wd, experts, width, hidden, wp, hp)
         rows = repitch(rows, 1, route["capacity"], width, route["capacity"], wp)
-    gate = grouped_gemm(rows, wg, route, wp, hp, out_dtype=x.dtype)
-    up = grouped_gemm(rows, wu, route, wp, hp, out_dtype=x.dtype)
-    act = silu_mul(gate, up)
+    if x.dtype == "bfloat16" and save:
+        act, gate, up = swiglu_gemm(rows, wg, wu, 0, wp, hp, route=route, save=True)
+    elif x.dtype == "bfloat16":
+        act, gate, up = swiglu_gemm(rows, wg, wu, 0, wp, hp, route=route), None, None
+    else:
+        gate = grouped_gemm(rows, wg, route, wp, hp, out_dtype=x.dtype)
+        up = grouped_gemm(rows, wu, route, wp, hp, out_dtype=x.dtype)
+        act = silu_mul(gate, up)
     down = grouped_gemm(act, wd, route, hp, wp, out_dtype=x.dtype)
     if wp != width:
         down = repitch(down, 1, route["capacity"], wp, route["capacity"], width)

@@ -39,6 +39,14 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {  // low half
 }
 __device__ __forceinline__ bf16_t f32_to_bf16(float f) { return (bf16_t)(pack_bf16x2(f, 0.0f) & 0xffffu); }
 
+// silu(v) = v * sigmoid(v) = v / (1 + e^-v), the function of lm_silu
+// (src/qutai/backends/cuda/lm.cu:54), from the hardware exp2 (v_exp_f32) and
+// reciprocal (v_rcp_f32): a few fp32 ulps, far inside one bf16 ulp, and
+// branch-free for every v (e^-v = inf gives v * 0).  One definition for the
+// elementwise SwiGLU kernels and the fused GEMM epilogue, so both round the
+// same values.
+__device__ __forceinline__ float silu_f(float v) { return v * __builtin_amdgcn_rcpf(1.f + __expf(-v)); }
+
 // Store through a global (address space 1) pointer: a generic pointer makes
 // the compiler emit flat stores, which also count against lgkmcnt, so every
 // later wait for an LDS read would wait for the stores as well.

@@ -112,10 +112,10 @@ __global__ void splitk_reduce(const float* part, void* out, int64_t n, int64_t t
 //         (grids of 256x256 tiles that would leave half the CUs idle)
 enum Tile { TILE_L8D2, TILE_L8R, TILE_L4D2, TILE_S, TILE_N, TILE_W, TILE_H, TILE_COUNT };
 
-template <bool F32, bool TA, bool TB, int BM, int BN, int WM, int WN, int BK, int ST, bool DMA>
+template <bool F32, bool TA, bool TB, int BM, int BN, int WM, int WN, int BK, int ST, bool DMA, bool SWIGLU = false>
 hipError_t launch_cfg(GemmArgs p, hipStream_t stream) {
-  typedef GemmKernel<F32, TA, TB, BM, BN, WM, WN, BK, ST, DMA> Kern;
-  int64_t tiles_n = (p.N + BN - 1) / BN;
+  typedef GemmKernel<F32, TA, TB, BM, BN, WM, WN, BK, ST, DMA, SWIGLU> Kern;
+  int64_t tiles_n = (p.N + Kern::BNO - 1) / Kern::BNO;
   if (p.groups == 0) p.tiles_m = (int)((p.M + BM - 1) / BM);
   int64_t blocks = (int64_t)p.tiles_m * tiles_n * (p.groups ? 1 : p.batch);
   if (blocks <= 0) return hipSuccess;
@@ -429,6 +429,46 @@ int qutai_amd_gemm_grouped(const void* a, const void* b, void* out, const int64_
   hipError_t err = f32 ? launch_mma<true>(tile, false, transpose_right, p, stream)
                        : launch_mma<false>(tile, false, transpose_right, p, stream);
   return (int)err;
+}
+
+int qutai_amd_gemm_swiglu(const void* a, const void* w_gate, const void* w_up, void* out, void* gate_out,
+                          void* up_out, const int64_t* offsets, int groups, int64_t rows, int64_t inner,
+                          int64_t hidden, int64_t expert_stride, int dtype, void* stream_) {
+  hipStream_t stream = (hipStream_t)stream_;
+  if (rows < 0 || inner < 0 || hidden < 0 || expert_stride < 0 || (offsets && groups <= 0)) return QA_EINVAL;
+  if (dtype != QA_BF16) return QA_EINVAL;
+  if (!out || (rows > 0 && hidden > 0 && (!a || !w_gate || !w_up))) return QA_EINVAL;
+  if (rows == 0 || hidden == 0) return QA_OK;
+  if ((uintptr_t)a % 16 || (uintptr_t)w_gate % 16 || (uintptr_t)w_up % 16 || inner % 8 || expert_stride % 8)
+    return QA_EINVAL;
+  for (void* o : {out, gate_out, up_out})
+    if (o && (uintptr_t)o % 16) return QA_EINVAL;
+  GemmArgs p = {};
+  p.a = a;
+  p.b = w_gate;
+  p.b2 = w_up;
+  p.out = out;
+  p.gate_out = gate_out;
+  p.up_out = up_out;
+  p.M = rows;
+  p.N = hidden;
+  p.K = inner;
+  p.lda = inner;
+  p.ldb = inner;
+  p.ldc = hidden;
+  p.sb = offsets ? expert_stride : 0;
+  p.sc = rows * hidden;
+  p.batch = 1;
+  p.out_bf16 = 1;
+  p.vec_c = vec_out(out, p.ldc, 0);
+  p.alpha = 1.0f;
+  if ((p.lda * 256 * 2) >= (1ll << 31)) return QA_EINVAL;
+  if (offsets) {
+    p.offsets = offsets;
+    p.groups = groups;
+    p.tiles_m = (int)((rows + 255) / 256 + groups);
+  }
+  return (int)launch_cfg<false, false, true, 256, 256, 2, 4, 64, 2, true, true>(p, stream);
 }
 
 int qutai_amd_gemm_grouped_k(const void* a, const void* b, void* out, const int64_t* offsets, int groups, int64_t rows,

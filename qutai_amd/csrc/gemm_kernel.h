@@ -61,7 +61,14 @@ struct GemmArgs {
   // a multiple of 64, so no 16-byte chunk of a K-major row crosses a range end.
   int k_split;
   int64_t k_chunk;
+  // SwiGLU mode (kernels built with SWIGLU): b is the gate weight and b2 the
+  // up weight, both [N][K] (K-major, ldb, group stride sb); out receives
+  // silu(gate) * up, and gate_out / up_out (when not null) the two products.
+  const void* b2;
+  void* gate_out;
+  void* up_out;
 };
+
 
 template <bool F32> struct MmaTraits;
 template <> struct MmaTraits<false> {  // bf16 in, fp32 accumulate
@@ -127,7 +134,12 @@ struct OperandTile {
   }
 };
 
-template <bool F32, bool TA, bool TB, int BM, int BN, int WM, int WN, int BK, int STAGES, bool DMA>
+// SWIGLU: the B tile's 32-row blocks alternate between the gate weight (even
+// blocks) and the up weight (odd blocks) at the same N index, so each wave's
+// two 32-column accumulator blocks hold gate and up of the same outputs and
+// the epilogue writes silu(gate) * up: an output tile is BN / 2 wide.
+template <bool F32, bool TA, bool TB, int BM, int BN, int WM, int WN, int BK, int STAGES, bool DMA,
+          bool SWIGLU = false>
 struct GemmKernel {
   typedef MmaTraits<F32> Tr;
   typedef typename Tr::T T;
@@ -136,6 +148,8 @@ struct GemmKernel {
   static constexpr int NT = 64 * NW;
   static constexpr int TM = BM / WM, TN = BN / WN;  // wave tile
   static constexpr int FM = TM / 32, FN = TN / 32;  // 32x32 blocks per wave
+  static constexpr int BNO = SWIGLU ? BN / 2 : BN;  // output columns per tile
+  static_assert(!SWIGLU || (!F32 && !TA && TB && DMA && FN == 2), "SwiGLU: bf16 NT, two blocks per wave");
   static constexpr bool KA = !TA;                   // A K-major?
   static constexpr bool KB = TB;                    // B K-major?
   typedef OperandTile<F32, KA, BM, BK> TileA;
@@ -300,9 +314,20 @@ struct GemmKernel {
     const int wm = wave / WN, wn = wave % WN;
 
     // ---- tile scheduling -------------------------------------------------
-    const int tiles_n = (int)((p.N + BN - 1) / BN);
-    const int tiles_per = p.tiles_m * tiles_n;
-    const int total = (int)gridDim.x;
+    const int tiles_n = (int)((p.N + BNO - 1) / BNO);
+    int tiles_m = p.tiles_m;
+    int total = (int)gridDim.x;
+    if (p.groups > 0 && !p.group_k) {
+      // grouped rows: the grid covers an upper bound of the M tiles; count
+      // the real ones so that they, not the grid, are spread evenly over the
+      // XCDs (surplus ids exit here instead of piling onto the last XCDs)
+      int real = 0;
+      for (int e = 0; e < p.groups; e++) real += (int)((p.offsets[e + 1] - p.offsets[e] + BM - 1) / BM);
+      tiles_m = uniform32(real);
+      total = tiles_m * tiles_n;
+      if ((int)blockIdx.x >= total) return;
+    }
+    const int tiles_per = tiles_m * tiles_n;
     int pid = uniform32(xcd_remap((int)blockIdx.x, total));
     int64_t bz = pid / tiles_per;
     int t = pid % tiles_per;
@@ -310,12 +335,13 @@ struct GemmKernel {
     constexpr int GM = 4;
     int group = t / (GM * tiles_n);
     int first_m = group * GM;
-    int gsize = min(p.tiles_m - first_m, GM);
+    int gsize = min(tiles_m - first_m, GM);
     int tile_m = first_m + (t % (GM * tiles_n)) % gsize;
     int tile_n = (t % (GM * tiles_n)) / gsize;
 
     const T* A = reinterpret_cast<const T*>(p.a);
     const T* B = reinterpret_cast<const T*>(p.b);
+    const T* B2 = reinterpret_cast<const T*>(p.b2);
     int64_t M = p.M, row0 = 0, K = p.K;
     char* outp = reinterpret_cast<char*>(p.out);
     const int osize = p.out_bf16 ? 2 : 4;
@@ -341,6 +367,7 @@ struct GemmKernel {
       if (g < 0) return;  // tile beyond the last group: nothing to do
       A += lo * p.lda;
       B += (int64_t)g * p.sb;
+      if constexpr (SWIGLU) B2 += (int64_t)g * p.sb;
       outp += lo * p.ldc * osize;
       M = hi - lo;
     } else if (p.k_split > 1) {
@@ -358,10 +385,11 @@ struct GemmKernel {
     }
     A = uniform_ptr(A);
     B = uniform_ptr(B);
+    if constexpr (SWIGLU) B2 = uniform_ptr(B2);
     outp = uniform_ptr(outp);
     M = uniform64(M);
     row0 = uniform64(row0);
-    const int64_t col0 = uniform64((int64_t)tile_n * BN);
+    const int64_t col0 = uniform64((int64_t)tile_n * BNO);
     K = uniform64(K);
     const int64_t N = p.N;
     const int64_t lda = p.lda, ldb = p.ldb;
@@ -403,10 +431,16 @@ struct GemmKernel {
         ka[j] = KA ? c * E : outer;
         va[j] = KA ? (row0 + outer < M) : (row0 + c * E < M);
       }
+      bool up[JB];  // SWIGLU: instruction j copies up-weight rows
 #pragma unroll
       for (int j = 0; j < JB; j++) {
         int q = (j * NW + wave) * 64 + lane, outer, c;
         TileB::coords(q, outer, c);
+        // SWIGLU: tile row `outer` is row (outer / 64) * 32 + outer % 32 of the
+        // gate (outer / 32 even) or up (odd) weight; one instruction covers 8
+        // rows, all in one 32-row block
+        if constexpr (SWIGLU) outer = ((outer >> 6) << 5) + (outer & 31);
+        up[j] = SWIGLU && (((j * NW + wave) >> 2) & 1);
         ob[j] = (uint32_t)(((int64_t)outer * ldb + c * E) * (int64_t)sizeof(T));
         kb[j] = KB ? c * E : outer;
         vb[j] = KB ? (col0 + outer < N) : (col0 + c * E < N);
@@ -418,6 +452,7 @@ struct GemmKernel {
                                   (int64_t)(KA ? BM * lda : BK * lda) * (int64_t)sizeof(T));
         const u32x4 db = lds_rsrc(KB ? B + col0 * ldb + k0 : B + k0 * ldb + col0,
                                   (int64_t)(KB ? BN * ldb : BK * ldb) * (int64_t)sizeof(T));
+        const u32x4 db2 = SWIGLU ? lds_rsrc(B2 + col0 * ldb + k0, (int64_t)BN * ldb * (int64_t)sizeof(T)) : db;
         const int64_t krem = K - k0;
         char* sa = base + stage * STAGE * (int)sizeof(T);
         char* sb = sa + BM * BK * (int)sizeof(T);
@@ -428,7 +463,7 @@ struct GemmKernel {
 #pragma unroll
         for (int j = 0; j < JB; j++)
           if (JA + j >= first && JA + j < last)
-            lds_load16(db, sb + (j * NW + wave) * 1024, (vb[j] && kb[j] < krem) ? ob[j] : OOB);
+            lds_load16(up[j] ? db2 : db, sb + (j * NW + wave) * 1024, (vb[j] && kb[j] < krem) ? ob[j] : OOB);
       };
       auto issue = [&](int stage, int64_t k0) { issue_range(stage, k0, 0, L); };
 #pragma unroll
@@ -541,7 +576,7 @@ struct GemmKernel {
     o.M = M;
     o.N = N;
     o.row0 = row0 + wm * TM;
-    o.col0 = col0 + wn * TN;
+    o.col0 = col0 + wn * (BNO / WN);
     o.bf16 = p.out_bf16;
     o.accumulate = p.accumulate;
     o.vec = p.vec_c;
@@ -549,8 +584,39 @@ struct GemmKernel {
     float* stage = reinterpret_cast<float*>(smem) + wave * 32 * EP;
     __syncthreads();  // every wave has read the ring's last stage
     // full in-bounds wave tile, plain store: straight-line 16-byte stores
-    const bool fast = o.vec >= (o.bf16 ? 2 : 1) && !o.accumulate && o.row0 + TM <= o.M && o.col0 + TN <= o.N;
-    store_rows<0>(acc, stage, o, lane, fast);
+    const bool fast = o.vec >= (o.bf16 ? 2 : 1) && !o.accumulate && o.row0 + TM <= o.M && o.col0 + BNO / WN <= o.N;
+    if constexpr (SWIGLU) {
+      // gate / up outputs share out's layout: same byte offset from their base
+      const int64_t shift = outp - reinterpret_cast<char*>(p.out);
+      Out og = o, ou = o;
+      og.ptr = p.gate_out ? reinterpret_cast<char*>(p.gate_out) + shift : nullptr;
+      ou.ptr = p.up_out ? reinterpret_cast<char*>(p.up_out) + shift : nullptr;
+#pragma unroll
+      for (int i = 0; i < FM; i++) {
+        // the unfused SwiGLU's roundings: gate and up are bf16 products,
+        // silu(gate) is a bf16 tensor before the multiply, one rounding after
+        f32x16 g, u, y;
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+          g[e] = bf16_to_f32(f32_to_bf16(acc[i][0][e]));
+          u[e] = bf16_to_f32(f32_to_bf16(acc[i][1][e]));
+          y[e] = bf16_to_f32(f32_to_bf16(silu_f(g[e]))) * u[e];
+        }
+        const f32x16 ys[1] = {y};
+        store_slab<1>(ys, stage, o, o.row0 + i * 32, lane, fast);
+        if (og.ptr) {
+          const f32x16 gs[1] = {g};
+          store_slab<1>(gs, stage, og, o.row0 + i * 32, lane, fast);
+        }
+        if (ou.ptr) {
+          const f32x16 us[1] = {u};
+          store_slab<1>(us, stage, ou, o.row0 + i * 32, lane, fast);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < FM; i++) store_slab<FN>(acc[i], stage, o, o.row0 + i * 32, lane, fast);
+    }
   }
 
   // Output staging: each wave turns one 32-row slab of its accumulators
@@ -613,63 +679,62 @@ struct GemmKernel {
     }
   }
 
-  template <int I>
-  __device__ static __forceinline__ void store_rows(const f32x16 (&acc)[FM][FN], float* stage, const Out& o,
-                                                    int lane, bool fast) {
-    if constexpr (I < FM) {
+  // One 32-row slab of NB 32x32 accumulator blocks (NB * 32 columns from
+  // o.col0) to rows row_base .. row_base + 31 of the output.
+  template <int NB>
+  __device__ static __forceinline__ void store_slab(const f32x16 (&blk)[NB], float* stage, const Out& o,
+                                                    int64_t row_base, int lane, bool fast) {
+    constexpr int W = NB * 32;
 #pragma unroll
-      for (int j = 0; j < FN; j++)
+    for (int j = 0; j < NB; j++)
 #pragma unroll
-        for (int e = 0; e < 16; e++) {
-          int r = 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-          stage[r * EP + j * 32 + (lane & 31)] = acc[I][j][e];
-        }
-      __builtin_amdgcn_wave_barrier();
-      const int64_t row_base = o.row0 + I * 32;
-      if (fast && o.bf16) {
-        // lane -> 8 consecutive columns of one row: one 16-byte store each
-        constexpr int Q = TN / 8, ITERS = 32 * Q / 64;
-        static_assert(64 % Q == 0, "whole rows per store instruction");
-        u32x4 w[ITERS];
-#pragma unroll
-        for (int it = 0; it < ITERS; it++) {
-          int idx = it * 64 + lane, r = idx / Q, q = idx % Q;
-          f32x4 a = *reinterpret_cast<const f32x4*>(stage + r * EP + 8 * q) * o.alpha;
-          f32x4 b = *reinterpret_cast<const f32x4*>(stage + r * EP + 8 * q + 4) * o.alpha;
-          w[it] = u32x4{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3]), pack_bf16x2(b[0], b[1]),
-                        pack_bf16x2(b[2], b[3])};
-        }
-        bf16_t* dst = reinterpret_cast<bf16_t*>(o.ptr) + (row_base + lane / Q) * o.ldc + o.col0 + 8 * (lane % Q);
-#pragma unroll
-        for (int it = 0; it < ITERS; it++) global_store(dst + it * (64 / Q) * o.ldc, w[it]);
-      } else if (fast) {
-        constexpr int Q = TN / 4, ITERS = 32 * Q / 64;
-        static_assert(64 % Q == 0, "whole rows per store instruction");
-        f32x4 v[ITERS];
-#pragma unroll
-        for (int it = 0; it < ITERS; it++) {
-          int idx = it * 64 + lane, r = idx / Q, q = idx % Q;
-          v[it] = *reinterpret_cast<const f32x4*>(stage + r * EP + 4 * q) * o.alpha;
-        }
-        float* dst = reinterpret_cast<float*>(o.ptr) + (row_base + lane / Q) * o.ldc + o.col0 + 4 * (lane % Q);
-#pragma unroll
-        for (int it = 0; it < ITERS; it++) global_store(dst + it * (64 / Q) * o.ldc, v[it]);
-      } else {
-        constexpr int Q = TN / 4;  // float4 per staged row
-        constexpr int ITERS = 32 * Q / 64;
-#pragma unroll
-        for (int it = 0; it < ITERS; it++) {
-          int idx = it * 64 + lane;
-          int r = idx / Q, q = idx % Q;
-          f32x4 v = *reinterpret_cast<const f32x4*>(stage + r * EP + 4 * q);
-          int64_t row = row_base + r;
-          int64_t col = o.col0 + 4 * q;
-          if (row < o.M && col < o.N) write4(o, row, col, v);
-        }
+      for (int e = 0; e < 16; e++) {
+        int r = 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        stage[r * EP + j * 32 + (lane & 31)] = blk[j][e];
       }
-      __builtin_amdgcn_wave_barrier();
-      store_rows<I + 1>(acc, stage, o, lane, fast);
+    __builtin_amdgcn_wave_barrier();
+    if (fast && o.bf16) {
+      // lane -> 8 consecutive columns of one row: one 16-byte store each
+      constexpr int Q = W / 8, ITERS = 32 * Q / 64;
+      static_assert(64 % Q == 0, "whole rows per store instruction");
+      u32x4 w[ITERS];
+#pragma unroll
+      for (int it = 0; it < ITERS; it++) {
+        int idx = it * 64 + lane, r = idx / Q, q = idx % Q;
+        f32x4 a = *reinterpret_cast<const f32x4*>(stage + r * EP + 8 * q) * o.alpha;
+        f32x4 b = *reinterpret_cast<const f32x4*>(stage + r * EP + 8 * q + 4) * o.alpha;
+        w[it] = u32x4{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3]), pack_bf16x2(b[0], b[1]),
+                      pack_bf16x2(b[2], b[3])};
+      }
+      bf16_t* dst = reinterpret_cast<bf16_t*>(o.ptr) + (row_base + lane / Q) * o.ldc + o.col0 + 8 * (lane % Q);
+#pragma unroll
+      for (int it = 0; it < ITERS; it++) global_store(dst + it * (64 / Q) * o.ldc, w[it]);
+    } else if (fast) {
+      constexpr int Q = W / 4, ITERS = 32 * Q / 64;
+      static_assert(64 % Q == 0, "whole rows per store instruction");
+      f32x4 v[ITERS];
+#pragma unroll
+      for (int it = 0; it < ITERS; it++) {
+        int idx = it * 64 + lane, r = idx / Q, q = idx % Q;
+        v[it] = *reinterpret_cast<const f32x4*>(stage + r * EP + 4 * q) * o.alpha;
+      }
+      float* dst = reinterpret_cast<float*>(o.ptr) + (row_base + lane / Q) * o.ldc + o.col0 + 4 * (lane % Q);
+#pragma unroll
+      for (int it = 0; it < ITERS; it++) global_store(dst + it * (64 / Q) * o.ldc, v[it]);
+    } else {
+      constexpr int Q = W / 4;  // float4 per staged row
+      constexpr int ITERS = 32 * Q / 64;
+#pragma unroll
+      for (int it = 0; it < ITERS; it++) {
+        int idx = it * 64 + lane;
+        int r = idx / Q, q = idx % Q;
+        f32x4 v = *reinterpret_cast<const f32x4*>(stage + r * EP + 4 * q);
+        int64_t row = row_base + r;
+        int64_t col = o.col0 + 4 * q;
+        if (row < o.M && col < o.N) write4(o, row, col, v);
+      }
     }
+    __builtin_amdgcn_wave_barrier();
   }
 };
 

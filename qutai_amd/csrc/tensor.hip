@@ -375,13 +375,9 @@ __global__ void softmax_rows_f64(const double* x, double* out, int64_t rows, int
   for (int64_t at = tid; at < width; at += THREADS) yr[at] = exp(xr[at] * scale - peak) / total;
 }
 
-// silu as in lm_silu (lm.cu:54): s = v >= 0 ? 1/(1+e^-v) : e^v/(1+e^v).
-// With bf16 storage the silu output is itself a bf16 tensor before the
-// multiply (two roundings), as in the unfused SwiGLU of the reference.
-__device__ __forceinline__ float silu_f(float v) {
-  float s = v >= 0.f ? 1.f / (1.f + expf(-v)) : expf(v) / (1.f + expf(v));
-  return v * s;
-}
+// silu(gate) * up with silu_f (common.h).  With bf16 storage the silu output
+// is itself a bf16 tensor before the multiply (two roundings), as in the
+// unfused SwiGLU of the reference.
 // bf16, 8 elements (16 bytes) per thread and step.
 __global__ void silu_mul_bf16x8(const u32x4* g, const u32x4* u, u32x4* out, int64_t n8) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += (int64_t)gridDim.x * blockDim.x) {

@@ -1,0 +1,103 @@
+"""Fused SwiGLU GEMM (qutai_amd_gemm_swiglu) against the unfused form it
+replaces -- two projections, lm_silu and the multiply
+(src/qutai/lm/layers.py:310-311) -- bit for bit: the fused epilogue rounds
+gate and up to bf16, silu(gate) to bf16 and the product once, exactly as
+the separate bf16 GEMMs and the elementwise kernel do, and every tile sums K
+in the same order.  Also against a float64 composition of the oracle's silu
+(tolerance 1e-2, bf16 storage), in plain form and grouped by expert with the
+config 5 routing of uneven per-expert counts (one expert with no rows)."""
+import numpy as np
+import pytest
+
+from oracle import reference as ora
+from tests.helpers import download, normal, stored, upload
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = 1e-2
+
+
+@pytest.fixture(scope="module")
+def amd():
+    from qutai_amd.backends import amd as backend
+
+    backend.get_runtime()
+    return backend
+
+
+@pytest.fixture(scope="module")
+def lm():
+    from qutai_amd.backends import amd_lm
+
+    return amd_lm
+
+
+def words(storage):
+    return np.frombuffer(storage.to_array(), dtype=np.uint16)
+
+
+def reference_act(x, wg, wu):
+    """float64 silu(x wg^T) * (x wu^T) of bf16-stored operands (rows x hidden)."""
+    g = x @ wg.T
+    u = x @ wu.T
+    return np.array(ora.silu(g.ravel().tolist())).reshape(g.shape) * u
+
+
+@pytest.mark.parametrize("rows,inner,hidden", [(512, 256, 256), (300, 136, 264), (257, 64, 8), (1000, 512, 1408)])
+def test_plain_swiglu_matches_unfused_bit_for_bit(amd, lm, rows, inner, hidden):
+    x = normal(rows, rows * inner)
+    wg, wu = normal(1, hidden * inner, 0.1), normal(2, hidden * inner, 0.1)
+    xs, gs, us = (upload(v, "bfloat16") for v in (x, wg, wu))
+    act, gate, up = lm.swiglu_gemm(xs, gs, us, rows, inner, hidden, save=True)
+    gate_ref = amd.gemm(xs, gs, rows, inner, hidden, transpose_right=True, out_dtype="bfloat16")
+    up_ref = amd.gemm(xs, us, rows, inner, hidden, transpose_right=True, out_dtype="bfloat16")
+    act_ref = lm.silu_mul(gate_ref, up_ref)
+    assert np.array_equal(words(gate), words(gate_ref))
+    assert np.array_equal(words(up), words(up_ref))
+    assert np.array_equal(words(act), words(act_ref))
+    # the form without the saved products writes the same activations
+    assert np.array_equal(words(lm.swiglu_gemm(xs, gs, us, rows, inner, hidden)), words(act_ref))
+    exact = reference_act(stored(x, "bfloat16").reshape(rows, inner), stored(wg, "bfloat16").reshape(hidden, inner),
+                          stored(wu, "bfloat16").reshape(hidden, inner))
+    assert ora.rel_frobenius(download(act).reshape(rows, hidden), exact) <= BF16_TOL
+
+
+@pytest.mark.parametrize("tokens,width,hidden,experts,top_k", [(2048, 256, 200, 8, 2), (700, 128, 1408, 8, 2),
+                                                                (64, 64, 136, 16, 1)])
+def test_grouped_swiglu_matches_unfused_bit_for_bit(amd, lm, tokens, width, hidden, experts, top_k):
+    logits = normal(tokens + 1, tokens * experts)
+    route = lm.routing(upload(logits, "float32"), tokens, experts, top_k)
+    x = normal(tokens + 2, tokens * width)
+    wg, wu = normal(3, experts * hidden * width, 0.1), normal(4, experts * hidden * width, 0.1)
+    xs, gs, us = (upload(v, "bfloat16") for v in (x, wg, wu))
+    rows = lm.route_gather_all(xs, route, width)
+    act, gate, up = lm.swiglu_gemm(rows, gs, us, 0, width, hidden, route=route, save=True)
+    gate_ref = lm.grouped_gemm(rows, gs, route, width, hidden, out_dtype="bfloat16")
+    up_ref = lm.grouped_gemm(rows, us, route, width, hidden, out_dtype="bfloat16")
+    act_ref = lm.silu_mul(gate_ref, up_ref)
+    used = int(download(route["offsets"])[-1]) * hidden  # rows past the last expert are not written
+    assert np.array_equal(words(gate)[:used], words(gate_ref)[:used])
+    assert np.array_equal(words(up)[:used], words(up_ref)[:used])
+    assert np.array_equal(words(act)[:used], words(act_ref)[:used])
+    # float64 check on every expert's first and last row
+    offsets = download(route["offsets"]).astype(int).tolist()
+    xr = stored(download(rows), "bfloat16").reshape(-1, width)
+    gr = stored(wg, "bfloat16").reshape(experts, hidden, width)
+    ur = stored(wu, "bfloat16").reshape(experts, hidden, width)
+    got = download(act).reshape(-1, hidden)
+    for e in range(experts):
+        lo, hi = offsets[e], offsets[e + 1]
+        for r in sorted({lo, hi - 1}) if hi > lo else ():
+            exact = reference_act(xr[r:r + 1], gr[e], ur[e])
+            assert ora.rel_frobenius(got[r:r + 1], exact) <= BF16_TOL
+
+
+def test_swiglu_rejects_unsupported_operands(amd, lm):
+    x = upload(normal(0, 16 * 12), "bfloat16")
+    w = upload(normal(1, 8 * 12), "bfloat16")
+    with pytest.raises(ValueError):  # inner not a multiple of 8
+        lm.swiglu_gemm(x, w, w, 16, 12, 8)
+    xf = upload(normal(0, 16 * 16), "float32")
+    wf = upload(normal(1, 8 * 16), "float32")
+    with pytest.raises(ValueError):  # fp32 storage keeps the unfused path
+        lm.swiglu_gemm(xf, wf, wf, 16, 16, 8)
