@@ -116,6 +116,45 @@ def silu_mul(gate, up):
                   lambda g: b.silu_mul_backward(g, gate.storage, up.storage))
 
 
+def swiglu(x, w_gate, w_up):
+    """silu(x W_gate^T) * (x W_up^T) as one recorded op on the fused bf16 GEMM
+    (qutai_amd_gemm_swiglu): the same roundings as ``silu_mul(linear(x,
+    w_gate), linear(x, w_up))`` on the bf16 path (x and fp32 weights rounded
+    to bf16 once, bf16 gate and up, bf16 silu, one rounding of the product).
+    The backward is the unfused one: silu_mul_backward, each projection's
+    dX = G W and dW = G^T X, and the two dX summed as autograd sums the
+    gradients of a twice-used input (src/qutai/lm/layers.py:35-74, 310-311)."""
+    b = backend(x)
+    rows = x.size // x.shape[-1]
+    hidden, inner = w_gate.shape
+    precision = matmul_precision()
+    xs, gs, us = _bf16(x.storage), _bf16(w_gate.storage), _bf16(w_up.storage)
+    act, gate, up = b.swiglu_gemm(xs, gs, us, rows, inner, hidden, save=True)
+
+    def backward(g):
+        dgate, dup = b.silu_mul_backward(g, gate, up)
+        with set_matmul_precision(precision):
+            dx = None
+            if x.requires_grad:
+                dx = amd.add(b.gemm(dgate, gs, rows, hidden, inner, out_dtype=x.dtype),
+                             b.gemm(dup, us, rows, hidden, inner, out_dtype=x.dtype))
+            dwg = (b.gemm(dgate, xs, hidden, rows, inner, transpose_left=True, out_dtype=w_gate.dtype)
+                   if w_gate.requires_grad else None)
+            dwu = (b.gemm(dup, xs, hidden, rows, inner, transpose_left=True, out_dtype=w_up.dtype)
+                   if w_up.requires_grad else None)
+        return dx, dwg, dwu
+
+    return record(Tensor(act, shape=(*x.shape[:-1], hidden)), (x, w_gate, w_up), backward)
+
+
+def _swiglu_fusable(x, w_gate, w_up):
+    """The fused GEMM covers bf16-path products with bf16 activations and
+    16-byte rows (inner a multiple of 8)."""
+    return (x.device == "amd" and w_gate.dtype == w_up.dtype and w_gate.shape == w_up.shape
+            and _bf16_path(x, w_gate, w_up) and activation_dtype(x, w_gate) == "bfloat16"
+            and x.shape[-1] % 8 == 0)
+
+
 class Projection:
     def __init__(self, inputs, outputs, *, device="amd", dtype="float32", seed=None, std=0.02):
         self.weight = Tensor(backend(device).normal(inputs * outputs, std=std, seed=seed, dtype=dtype),
@@ -138,6 +177,8 @@ class SwiGLU:
                                std=std)
 
     def __call__(self, x):
+        if _swiglu_fusable(x, self.gate.weight, self.up.weight):
+            return self.down(swiglu(x, self.gate.weight, self.up.weight))
         return self.down(silu_mul(self.gate(x), self.up(x)))
 
     def parameters(self):

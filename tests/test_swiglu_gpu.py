@@ -101,3 +101,36 @@ def test_swiglu_rejects_unsupported_operands(amd, lm):
     wf = upload(normal(1, 8 * 16), "float32")
     with pytest.raises(ValueError):  # fp32 storage keeps the unfused path
         lm.swiglu_gemm(xf, wf, wf, 16, 16, 8)
+
+
+@pytest.mark.parametrize("mode", ["autocast", "bf16"])
+def test_swiglu_layer_fused_equals_unfused(amd, mode):
+    """lm SwiGLU (lm/layers.py:291-314) on the bf16 path: the fused op's
+    output and every gradient equal the unfused composition's bit for bit."""
+    from qutai_amd import Tensor
+    from qutai_amd.lm import layers
+    from qutai_amd.lm.precision import autocast
+
+    width, hidden, tokens = 128, 200, 96
+    dtype = "bfloat16" if mode == "bf16" else "float32"
+    layer = layers.SwiGLU(width, hidden, seed=3, std=0.05, dtype=dtype)
+    x = Tensor(upload(normal(21, tokens * width), dtype), shape=(tokens, width), requires_grad=True)
+    # the output is bf16 in both modes (autocast: bf16 activations)
+    g = Tensor(upload(normal(22, tokens * width), "bfloat16"), shape=(tokens, width))
+    params = (x, *layer.parameters())
+
+    def run(fused):
+        for p in params:
+            p.grad = None
+        with autocast(mode == "autocast"):
+            assert layers._swiglu_fusable(x, layer.gate.weight, layer.up.weight)
+            if fused:
+                y = layer(x)
+            else:
+                y = layer.down(layers.silu_mul(layer.gate(x), layer.up(x)))
+        y.backward(g)
+        return [y.storage.to_array()] + [p.grad.storage.to_array() for p in params]
+
+    fused, unfused = run(True), run(False)
+    for name, a, b in zip(("y", "dx", "dWg", "dWu", "dWd"), fused, unfused):
+        assert a == b, name
