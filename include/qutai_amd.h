@@ -369,6 +369,25 @@ int qutai_amd_head_loss(const void* logits, const int64_t* labels, float* out, i
 int qutai_amd_head_gradient(void* logits, const int64_t* labels, const float* gradient, int64_t rows, int64_t vocab,
                             double factor, int dtype, void* stream);
 
+/* Vocabulary-blocked loss head.  `logits` is one block [rows][cols] of the
+ * [rows][vocab] logits, holding vocabulary columns col0 .. col0+cols.
+ * head_block_stats folds each row's (max, sum exp(v - max)) over the block
+ * into stats[row] = {max, sum} (overwritten when `first`) and stores the
+ * label's logit in picked[row] when the label lies in the block; rows with
+ * label -100 are skipped.  head_block_loss writes out[r] = log(sum) + max -
+ * picked (0 for label -100).  head_block_gradient turns a block in place into
+ * gradient[0] * factor * (exp(v - max) / sum - onehot(label)) (0 for label
+ * -100).  Together they compute what `lm_head_loss` / `lm_head_gradient` do
+ * per row chunk (cuda_lm.py:629-660, cuda/lm.cu:428-440, driven by the
+ * chunked head of src/qutai/lm/layers.py:194-257), with the chunks cut along
+ * the vocabulary instead of the rows. */
+int qutai_amd_head_block_stats(const void* logits, const int64_t* labels, float* stats, float* picked, int64_t rows,
+                               int64_t cols, int64_t col0, int first, int dtype, void* stream);
+int qutai_amd_head_block_loss(const float* stats, const float* picked, const int64_t* labels, float* out,
+                              int64_t rows, void* stream);
+int qutai_amd_head_block_gradient(void* logits, const int64_t* labels, const float* stats, const float* gradient,
+                                  int64_t rows, int64_t cols, int64_t col0, double factor, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -82,6 +82,24 @@ class AMDStorage(Storage):
         return buffer.tolist()
 
 
+class AMDView(AMDStorage):
+    """Elements [offset, offset + size) of another amd storage, sharing its
+    memory: it holds the parent alive and never frees anything itself."""
+
+    def __init__(self, base: AMDStorage, offset: int, size: int) -> None:
+        if not isinstance(base, AMDStorage) or offset < 0 or size < 0 or offset + size > base.size:
+            raise ValueError("view outside its storage")
+        self.dtype, self._size, self.runtime, self.base = base.dtype, size, base.runtime, base
+        self.ptr = base.ptr + offset * _TYPES[base.dtype][1]
+
+    def __del__(self) -> None:
+        pass
+
+
+def view(base: AMDStorage, offset: int, size: int) -> AMDView:
+    return AMDView(base, offset, size)
+
+
 def _p(value) -> int:
     return value.ptr if value is not None else 0
 

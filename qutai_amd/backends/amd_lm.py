@@ -557,6 +557,35 @@ def head_loss(logits, labels, rows, vocab, *, start=0):
     return amd.sum_all(values) if rows else amd.full(1, 0.0, dtype=values.dtype)
 
 
+def head_block_stats(logits, labels, stats, picked, rows, cols, col0, *, first):
+    """Fold one vocabulary block [rows][cols] (columns col0 ..) of the logits
+    into the per-row running (max, sum exp) pairs ``stats`` ([rows][2] fp32)
+    and the label logits ``picked`` ([rows] fp32)."""
+    ids, _ = _head_labels(labels, 0, rows)
+    if rows:
+        logits.runtime.call("qutai_amd_head_block_stats", logits.ptr, ids.ptr, stats.ptr, picked.ptr, rows, cols, col0,
+                            int(first), code(logits.dtype))
+
+
+def head_block_loss(stats, picked, labels, rows):
+    """Summed cross entropy of the rows from their folded stats (one fp32 value)."""
+    ids, _ = _head_labels(labels, 0, rows)
+    values = AMDStorage(rows, "float32")
+    if rows:
+        values.runtime.call("qutai_amd_head_block_loss", stats.ptr, picked.ptr, ids.ptr, values.ptr, rows)
+    return amd.sum_all(values) if rows else amd.full(1, 0.0, dtype="float32")
+
+
+def head_block_gradient(logits, labels, stats, gradient, rows, cols, col0, count):
+    """In place over one vocabulary block: g / count * (softmax - onehot)."""
+    ids, _ = _head_labels(labels, 0, rows)
+    g = gradient if gradient.dtype == "float32" else amd.from_storage(gradient, dtype="float32")
+    if rows:
+        logits.runtime.call("qutai_amd_head_block_gradient", logits.ptr, ids.ptr, stats.ptr, g.ptr, rows, cols, col0,
+                            1.0 / count, code(logits.dtype))
+    return logits
+
+
 def head_gradient(logits, labels, rows, vocab, gradient, count, *, start=0):
     """In place: logits = g / count * (softmax - onehot) (cuda_lm.py:646-660)."""
     _, pointer = _head_labels(labels, start, rows)

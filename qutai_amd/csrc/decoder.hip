@@ -286,6 +286,70 @@ __global__ void __launch_bounds__(HEAD_THREADS) head_gradient_kernel(T* logits, 
   }
 }
 
+// Vocabulary-blocked loss head.  The logits of all prediction rows are made
+// one block of vocabulary columns at a time ([rows][cols] holding columns
+// col0 .. col0+cols of the [rows][vocab] logits), so the weight gradient of a
+// block is one GEMM over all rows, written once, instead of a read-modify-write
+// of the whole [vocab][width] gradient per block of rows.  Per row, stats
+// holds the running (max, sum of exp(v - max)) over the blocks seen so far and
+// picked the label's logit.
+template <class T>
+__global__ void __launch_bounds__(HEAD_THREADS) head_block_stats_kernel(const T* logits, const int64_t* labels,
+                                                                        float* stats, float* picked, int64_t cols,
+                                                                        int64_t col0, int first, bool vec) {
+  const int64_t row = blockIdx.x;
+  const int64_t label = labels[row];
+  if (label == -100) return;
+  const T* l = logits + row * cols;
+  const MaxSum t = row_max_sum<T>(l, cols, vec);
+  if (threadIdx.x == 0) {
+    const MaxSum m = first ? t : merge({stats[2 * row], stats[2 * row + 1]}, t);
+    stats[2 * row] = m.m;
+    stats[2 * row + 1] = m.s;
+    if (label >= col0 && label < col0 + cols) picked[row] = get<T>(l, label - col0);
+  }
+}
+
+// out[r] = log(sum) + max - picked (the row's cross entropy), 0 for label -100
+__global__ void head_block_loss_kernel(const float* stats, const float* picked, const int64_t* labels, float* out,
+                                       int64_t rows) {
+  GRID_STRIDE(r, rows) out[r] = labels[r] == -100 ? 0.f : logf(stats[2 * r + 1]) + stats[2 * r] - picked[r];
+}
+
+// in place over one block: g * factor * (exp(v - max) / sum - onehot(label))
+template <class T>
+__global__ void __launch_bounds__(HEAD_THREADS) head_block_gradient_kernel(T* logits, const int64_t* labels,
+                                                                           const float* stats, const float* gradient,
+                                                                           int64_t cols, int64_t col0, float factor,
+                                                                           bool vec) {
+  const int64_t row = blockIdx.x;
+  const int64_t label = labels[row] == -100 ? -100 : labels[row] - col0;
+  T* l = logits + row * cols;
+  constexpr int V = chunk_of<T>();
+  if (labels[row] == -100) {
+    for (int64_t c = threadIdx.x; c < cols; c += HEAD_THREADS) put<T>(l, c, 0.f);
+    return;
+  }
+  const float m = stats[2 * row], inv = 1.f / stats[2 * row + 1], scale = gradient[0] * factor;
+  if (vec) {
+    float v[8];
+    for (int64_t c = (int64_t)threadIdx.x * V; c < cols; c += HEAD_THREADS * V) {
+      load_chunk<T>(l + c, v);
+#pragma unroll
+      for (int i = 0; i < V; i++) v[i] = scale * (expf(v[i] - m) * inv - (c + i == label ? 1.f : 0.f));
+      if constexpr (sizeof(T) == 2) {
+        *(uint4*)(l + c) = make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
+                                      pack_bf16x2(v[6], v[7]));
+      } else {
+        *(float4*)(l + c) = make_float4(v[0], v[1], v[2], v[3]);
+      }
+    }
+  } else {
+    for (int64_t c = threadIdx.x; c < cols; c += HEAD_THREADS)
+      put<T>(l, c, scale * (expf(get<T>(l, c) - m) * inv - (c == label ? 1.f : 0.f)));
+  }
+}
+
 bool act_dtype(int d) { return d == F32 || d == BF16; }
 
 // 16-byte chunks need an aligned base and rows that are whole chunks
@@ -444,6 +508,49 @@ int qutai_amd_head_gradient(void* logits, const int64_t* labels, const float* gr
   else
     hipLaunchKernelGGL(head_gradient_kernel<float>, dim3((unsigned)rows), dim3(HEAD_THREADS), 0, s, (float*)logits,
                        labels, gradient, vocab, (float)factor, vec_rows(logits, vocab, 4));
+  return (int)hipGetLastError();
+}
+
+int qutai_amd_head_block_stats(const void* logits, const int64_t* labels, float* stats, float* picked, int64_t rows,
+                               int64_t cols, int64_t col0, int first, int dtype, void* stream) {
+  if (rows < 0 || cols <= 0 || col0 < 0 || !act_dtype(dtype) || !labels || !stats || !picked) return QA_EINVAL;
+  if (rows == 0) return QA_OK;
+  if (rows > 0x7fffffff) return QA_EINVAL;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == BF16)
+    hipLaunchKernelGGL(head_block_stats_kernel<bf16_t>, dim3((unsigned)rows), dim3(HEAD_THREADS), 0, s,
+                       (const bf16_t*)logits, labels, stats, picked, cols, col0, first ? 1 : 0,
+                       vec_rows(logits, cols, 8));
+  else
+    hipLaunchKernelGGL(head_block_stats_kernel<float>, dim3((unsigned)rows), dim3(HEAD_THREADS), 0, s,
+                       (const float*)logits, labels, stats, picked, cols, col0, first ? 1 : 0,
+                       vec_rows(logits, cols, 4));
+  return (int)hipGetLastError();
+}
+
+int qutai_amd_head_block_loss(const float* stats, const float* picked, const int64_t* labels, float* out,
+                              int64_t rows, void* stream) {
+  if (rows < 0 || !stats || !picked || !labels || !out) return QA_EINVAL;
+  if (rows == 0) return QA_OK;
+  hipLaunchKernelGGL(head_block_loss_kernel, dim3(blocks_for(rows)), dim3(256), 0, (hipStream_t)stream, stats,
+                     picked, labels, out, rows);
+  return (int)hipGetLastError();
+}
+
+int qutai_amd_head_block_gradient(void* logits, const int64_t* labels, const float* stats, const float* gradient,
+                                  int64_t rows, int64_t cols, int64_t col0, double factor, int dtype, void* stream) {
+  if (rows < 0 || cols <= 0 || col0 < 0 || !act_dtype(dtype) || !labels || !stats || !gradient) return QA_EINVAL;
+  if (rows == 0) return QA_OK;
+  if (rows > 0x7fffffff) return QA_EINVAL;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == BF16)
+    hipLaunchKernelGGL(head_block_gradient_kernel<bf16_t>, dim3((unsigned)rows), dim3(HEAD_THREADS), 0, s,
+                       (bf16_t*)logits, labels, stats, gradient, cols, col0, (float)factor,
+                       vec_rows(logits, cols, 8));
+  else
+    hipLaunchKernelGGL(head_block_gradient_kernel<float>, dim3((unsigned)rows), dim3(HEAD_THREADS), 0, s,
+                       (float*)logits, labels, stats, gradient, cols, col0, (float)factor,
+                       vec_rows(logits, cols, 4));
   return (int)hipGetLastError();
 }
 

@@ -355,46 +355,74 @@ def _cast(values, dtype):
     return values if values.dtype == dtype else amd.from_storage(values, dtype=dtype)
 
 
+def vocab_block(chunk_size, rows, vocab):
+    """Vocabulary columns per block of the loss head: the most that keep a
+    block's logits within chunk_size x vocab values (the reference's bound
+    for one chunk of rows), a multiple of 8 (16-byte rows), at least 8."""
+    if rows <= chunk_size:
+        return vocab
+    return min(vocab, max(8, (chunk_size * vocab // rows) // 8 * 8))
+
+
 def projection_loss(hidden, weight, labels, chunk_size, *, prepared_labels=None):
     """Mean next-token cross entropy of hidden (batch, time, width) against
-    the tied (vocab, width) weight, over chunks of chunk_size head rows so
-    that at most chunk_size x vocab logits exist at once; labels -100 are
-    ignored; the backward recomputes each chunk's logits and accumulates the
-    weight gradient with an accumulating GEMM (src/qutai/lm/layers.py:194-257)."""
+    the tied (vocab, width) weight; labels -100 are ignored
+    (src/qutai/lm/layers.py:194-257).  As in the reference at most
+    chunk_size x vocab logits exist at once, but the blocks are cut along the
+    vocabulary instead of the rows: every block holds all prediction rows
+    for a range of vocabulary columns, the forward folds each row's running
+    (max, sum exp) over the blocks, and the backward recomputes a block's
+    logits, turns them into the softmax gradient and writes that block's rows
+    of the weight gradient with one GEMM over all rows (no read-modify-write
+    of the whole gradient per chunk), while dX accumulates in fp32."""
     b = backend(hidden)
     _, time, width = hidden.shape
     vocab = weight.shape[0]
     precision = matmul_precision()
     targets = tuple(label for row in labels for label in row[1:])
     label_data = b.prepare_labels(targets) if prepared_labels is None else prepared_labels
+    rows = len(targets)
     count = max(1, sum(label != -100 for label in targets))
     out_dtype = activation_dtype(hidden, weight)
     hs, ws = hidden.storage, weight.storage
-    if _bf16_path(hidden, weight):  # round once, not once per chunk and product
+    if _bf16_path(hidden, weight):  # round once, not once per block and product
         hs, ws = _bf16(hs), _bf16(ws)
-    result = amd.full(1, 0.0, dtype=hidden.dtype)
-    for start in range(0, len(targets), chunk_size):
-        rows = min(chunk_size, len(targets) - start)
-        inputs = b.head_rows(hs, start, rows, width, time)
-        logits = b.gemm(inputs, ws, rows, width, vocab, transpose_right=True, out_dtype=out_dtype)
-        b.add_into(result, _cast(b.head_loss(logits, label_data, rows, vocab, start=start), result.dtype))
-    result = amd.scale(result, 1 / count)
+    block = vocab_block(chunk_size, rows, vocab)
+    inputs = b.head_rows(hs, 0, rows, width, time)
+    stats = amd.AMDStorage(2 * rows, "float32")
+    picked = amd.AMDStorage(rows, "float32")
+
+    def block_logits(c0, cols):
+        return b.gemm(inputs, amd.view(ws, c0 * width, cols * width), rows, width, cols, transpose_right=True,
+                      out_dtype=out_dtype)
+
+    for c0 in range(0, vocab, block):
+        cols = min(block, vocab - c0)
+        b.head_block_stats(block_logits(c0, cols), label_data, stats, picked, rows, cols, c0, first=c0 == 0)
+    result = amd.scale(_cast(b.head_block_loss(stats, picked, label_data, rows), hidden.dtype), 1 / count)
 
     def backward(gradient):
         with set_matmul_precision(precision):
-            dx = amd.full(hidden.size, 0.0, dtype=hidden.dtype)
-            dw = amd.full(weight.size, 0.0, dtype=weight.dtype)
-            for start in range(0, len(targets), chunk_size):
-                rows = min(chunk_size, len(targets) - start)
-                inputs = b.head_rows(hs, start, rows, width, time)
-                logits = b.gemm(inputs, ws, rows, width, vocab, transpose_right=True, out_dtype=out_dtype)
-                incoming = b.head_gradient(logits, label_data, rows, vocab, gradient, count, start=start)
-                if hidden.requires_grad:
-                    part = b.gemm(incoming, ws, rows, vocab, width, out_dtype=hidden.dtype)
-                    b.head_rows_backward(dx, part, start, rows, width, time)
+            dw = amd.AMDStorage(weight.size, weight.dtype) if weight.requires_grad else None
+            part = None  # dX of the prediction rows, fp32, summed over the blocks
+            for c0 in range(0, vocab, block):
+                cols = min(block, vocab - c0)
+                incoming = b.head_block_gradient(block_logits(c0, cols), label_data, stats, gradient, rows, cols,
+                                                 c0, count)
                 if weight.requires_grad:
-                    b.gemm(incoming, inputs, vocab, rows, width, transpose_left=True, out_dtype=weight.dtype,
-                           out=dw, accumulate=True)
+                    b.gemm(incoming, inputs, cols, rows, width, transpose_left=True, out_dtype=weight.dtype,
+                           out=amd.view(dw, c0 * width, cols * width))
+                if hidden.requires_grad:
+                    w_block = amd.view(ws, c0 * width, cols * width)
+                    if part is None:
+                        part = b.gemm(incoming, w_block, rows, cols, width, out_dtype="float32")
+                    else:
+                        b.gemm(incoming, w_block, rows, cols, width, out_dtype="float32", out=part, accumulate=True)
+            dx = None
+            if hidden.requires_grad:
+                dx = amd.full(hidden.size, 0.0, dtype=hidden.dtype)
+                if part is not None:
+                    b.head_rows_backward(dx, _cast(part, hidden.dtype), 0, rows, width, time)
             return dx, dw
 
     return record(Tensor(result, shape=()), (hidden, weight), backward)

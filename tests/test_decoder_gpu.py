@@ -142,6 +142,50 @@ def test_head_loss_and_gradient(lm, dtype, rows, vocab):
         lm.head_loss(upload(logits, dtype), prepared, rows, vocab, start=len(labels))  # label range
 
 
+@pytest.mark.parametrize("dtype,rows,vocab,block", [("float32", 7, 13, 5), ("float32", 33, 1000, 256),
+                                                     ("bfloat16", 40, 32000, 8192), ("bfloat16", 64, 3000, 3000)])
+def test_head_vocab_blocks_match_row_head(lm, base, dtype, rows, vocab, block):
+    """The vocabulary-blocked head (stats folded over column blocks, ragged
+    last block, labels in every block and -100 rows) gives the row head's
+    loss and gradient (cuda_lm.py:629-660 restated by the oracle)."""
+    logits = normal(121, rows * vocab, 2.0).reshape(rows, vocab)
+    rng = Random(5)
+    labels = [rng.randrange(vocab) for _ in range(rows)]
+    labels[1] = -100
+    labels[2] = vocab - 1  # in the last (ragged) block
+    prepared = lm.prepare_labels(labels)
+    stats = base.AMDStorage(2 * rows, "float32")
+    picked = base.AMDStorage(rows, "float32")
+    blocks = [(c0, min(block, vocab - c0)) for c0 in range(0, vocab, block)]
+    for c0, cols in blocks:
+        lm.head_block_stats(upload(logits[:, c0:c0 + cols], dtype), prepared, stats, picked, rows, cols, c0,
+                            first=c0 == 0)
+    loss = download(lm.head_block_loss(stats, picked, prepared, rows))[0]
+    ls = stored(logits, dtype)
+    expected = ora.head_loss(ls.ravel().tolist(), labels, rows, vocab)
+    assert abs(loss - expected) <= 1e-5 * max(1.0, abs(expected)) * (1 if dtype == "float32" else 10)
+    g = upload(np.array([0.75], dtype=np.float32), "float32")
+    grad = np.concatenate([download(lm.head_block_gradient(upload(logits[:, c0:c0 + cols], dtype), prepared, stats,
+                                                           g, rows, cols, c0, 5)).reshape(rows, cols)
+                           for c0, cols in blocks], axis=1)
+    ref = np.array(ora.head_gradient(ls.ravel().tolist(), labels, rows, vocab, [0.75], 5)).reshape(rows, vocab)
+    assert ora.rel_frobenius(grad, ref) <= (FP32_TOL if dtype == "float32" else BF16_TOL)
+    assert not grad[1].any()  # ignored row
+
+
+def test_vocab_block_bound(lm):
+    from qutai_amd.lm.layers import vocab_block
+
+    assert vocab_block(1024, 4096, 32768) == 8192          # 4 blocks of 1024 x 32768 logits
+    assert vocab_block(128, 4096, 32768) == 1024
+    assert vocab_block(5000, 4096, 32768) == 32768         # all rows fit: one block
+    assert vocab_block(1, 4096, 1000) == 8                 # floor of 8 columns
+    for chunk, rows, vocab in ((3, 10, 13), (16, 200, 511), (100, 4096, 32000)):
+        b = vocab_block(chunk, rows, vocab)
+        assert b % 8 == 0 or b == vocab
+        assert rows * b <= max(chunk * vocab, rows * 8)
+
+
 def test_add_into_scale_concatenate(lm, base):
     a, b = normal(121, 1000), normal(122, 1000)
     t = upload(a, "float32")
