@@ -45,7 +45,8 @@ __device__ __forceinline__ bf16_t f32_to_bf16(float f) { return (bf16_t)(pack_bf
 // branch-free for every v (e^-v = inf gives v * 0).  One definition for the
 // elementwise SwiGLU kernels and the fused GEMM epilogue, so both round the
 // same values.
-__device__ __forceinline__ float silu_f(float v) { return v * __builtin_amdgcn_rcpf(1.f + __expf(-v)); }
+__device__ __forceinline__ float sigmoid_f(float v) { return __builtin_amdgcn_rcpf(1.f + __expf(-v)); }
+__device__ __forceinline__ float silu_f(float v) { return v * sigmoid_f(v); }
 
 // Store through a global (address space 1) pointer: a generic pointer makes
 // the compiler emit flat stores, which also count against lgkmcnt, so every
@@ -53,6 +54,10 @@ __device__ __forceinline__ float silu_f(float v) { return v * __builtin_amdgcn_r
 template <class V, class P>
 __device__ __forceinline__ void global_store(P* p, const V& v) {
   *(__attribute__((address_space(1))) V*)(p) = v;
+}
+template <class V, class P>
+__device__ __forceinline__ V global_load(const P* p) {
+  return *(const __attribute__((address_space(1))) V*)(p);
 }
 
 // Values that are the same for the whole wavefront but that the compiler

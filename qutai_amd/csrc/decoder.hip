@@ -115,14 +115,12 @@ __global__ void rms_dw_final_kernel(const float* partial, float* dw, int64_t chu
   }
 }
 
-__device__ __forceinline__ float sigmoid(float v) {
-  return v >= 0.f ? 1.f / (1.f + expf(-v)) : expf(v) / (1.f + expf(v));
-}
-// silu (backward = 0) or its derivative times g (lm.cu:54)
+// silu (backward = 0) or its derivative times g (lm.cu:54), s = sigmoid_f
+// (common.h)
 template <class T>
 __global__ void silu_kernel(const T* x, const T* g, T* out, int64_t n, int backward) {
   GRID_STRIDE(i, n) {
-    const float v = get<T>(x, i), s = sigmoid(v);
+    const float v = get<T>(x, i), s = sigmoid_f(v);
     put<T>(out, i, backward ? get<T>(g, i) * s * (1.f + v * (1.f - s)) : v * s);
   }
 }

@@ -583,8 +583,8 @@ struct GemmKernel {
     o.alpha = p.alpha;
     float* stage = reinterpret_cast<float*>(smem) + wave * 32 * EP;
     __syncthreads();  // every wave has read the ring's last stage
-    // full in-bounds wave tile, plain store: straight-line 16-byte stores
-    const bool fast = o.vec >= (o.bf16 ? 2 : 1) && !o.accumulate && o.row0 + TM <= o.M && o.col0 + BNO / WN <= o.N;
+    // full in-bounds wave tile: straight-line 16-byte loads (accumulate) and stores
+    const bool fast = o.vec >= (o.bf16 ? 2 : 1) && o.row0 + TM <= o.M && o.col0 + BNO / WN <= o.N;
     if constexpr (SWIGLU) {
       // gate / up outputs share out's layout: same byte offset from their base
       const int64_t shift = outp - reinterpret_cast<char*>(p.out);
@@ -695,30 +695,49 @@ struct GemmKernel {
     __builtin_amdgcn_wave_barrier();
     if (fast && o.bf16) {
       // lane -> 8 consecutive columns of one row: one 16-byte store each
+      // (accumulate: the old values are loaded first, added in fp32)
       constexpr int Q = W / 8, ITERS = 32 * Q / 64;
       static_assert(64 % Q == 0, "whole rows per store instruction");
+      bf16_t* dst = reinterpret_cast<bf16_t*>(o.ptr) + (row_base + lane / Q) * o.ldc + o.col0 + 8 * (lane % Q);
       u32x4 w[ITERS];
+      if (o.accumulate) {
+#pragma unroll
+        for (int it = 0; it < ITERS; it++) w[it] = global_load<u32x4>(dst + it * (64 / Q) * o.ldc);
+      }
 #pragma unroll
       for (int it = 0; it < ITERS; it++) {
         int idx = it * 64 + lane, r = idx / Q, q = idx % Q;
         f32x4 a = *reinterpret_cast<const f32x4*>(stage + r * EP + 8 * q) * o.alpha;
         f32x4 b = *reinterpret_cast<const f32x4*>(stage + r * EP + 8 * q + 4) * o.alpha;
+        if (o.accumulate) {
+#pragma unroll
+          for (int h = 0; h < 2; h++) {
+            a[2 * h] += __uint_as_float(w[it][h] << 16);
+            a[2 * h + 1] += __uint_as_float(w[it][h] & 0xffff0000u);
+            b[2 * h] += __uint_as_float(w[it][2 + h] << 16);
+            b[2 * h + 1] += __uint_as_float(w[it][2 + h] & 0xffff0000u);
+          }
+        }
         w[it] = u32x4{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3]), pack_bf16x2(b[0], b[1]),
                       pack_bf16x2(b[2], b[3])};
       }
-      bf16_t* dst = reinterpret_cast<bf16_t*>(o.ptr) + (row_base + lane / Q) * o.ldc + o.col0 + 8 * (lane % Q);
 #pragma unroll
       for (int it = 0; it < ITERS; it++) global_store(dst + it * (64 / Q) * o.ldc, w[it]);
     } else if (fast) {
       constexpr int Q = W / 4, ITERS = 32 * Q / 64;
       static_assert(64 % Q == 0, "whole rows per store instruction");
+      float* dst = reinterpret_cast<float*>(o.ptr) + (row_base + lane / Q) * o.ldc + o.col0 + 4 * (lane % Q);
       f32x4 v[ITERS];
+      if (o.accumulate) {
+#pragma unroll
+        for (int it = 0; it < ITERS; it++) v[it] = global_load<f32x4>(dst + it * (64 / Q) * o.ldc);
+      }
 #pragma unroll
       for (int it = 0; it < ITERS; it++) {
         int idx = it * 64 + lane, r = idx / Q, q = idx % Q;
-        v[it] = *reinterpret_cast<const f32x4*>(stage + r * EP + 4 * q) * o.alpha;
+        const f32x4 x = *reinterpret_cast<const f32x4*>(stage + r * EP + 4 * q) * o.alpha;
+        v[it] = o.accumulate ? v[it] + x : x;
       }
-      float* dst = reinterpret_cast<float*>(o.ptr) + (row_base + lane / Q) * o.ldc + o.col0 + 4 * (lane % Q);
 #pragma unroll
       for (int it = 0; it < ITERS; it++) global_store(dst + it * (64 / Q) * o.ldc, v[it]);
     } else {

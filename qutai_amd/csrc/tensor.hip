@@ -424,7 +424,34 @@ __global__ void add_rows_kernel(const void* x, const void* bias, void* out, int6
 }
 
 // Gradients of y = silu(g) * u: dg = dy * u * s * (1 + g (1 - s)), du = dy * silu(g)
-// (the derivative of lm_silu, lm.cu:54, times the multiply's rule).
+// (the derivative of lm_silu, lm.cu:54, times the multiply's rule).  bf16:
+// 8 elements (16 bytes of each operand) per thread and step, s from the
+// hardware exp2 / reciprocal (sigmoid_f, common.h).
+__global__ void silu_mul_backward_bf16x8(const u32x4* dy, const u32x4* g, const u32x4* u, u32x4* dg, u32x4* du,
+                                         int64_t n8) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += (int64_t)gridDim.x * blockDim.x) {
+    const u32x4 y8 = dy[i], g8 = g[i], u8 = u[i];
+    u32x4 a8, b8;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      float a[2], b[2];
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        const float y = __uint_as_float(h ? y8[q] & 0xffff0000u : y8[q] << 16);
+        const float v = __uint_as_float(h ? g8[q] & 0xffff0000u : g8[q] << 16);
+        const float w = __uint_as_float(h ? u8[q] & 0xffff0000u : u8[q] << 16);
+        const float s = sigmoid_f(v);
+        a[h] = y * w * s * (1.f + v * (1.f - s));
+        b[h] = y * (v * s);
+      }
+      a8[q] = pack_bf16x2(a[0], a[1]);
+      b8[q] = pack_bf16x2(b[0], b[1]);
+    }
+    dg[i] = a8;
+    du[i] = b8;
+  }
+}
+
 __global__ void silu_mul_backward_kernel(const void* dy, const void* g, const void* u, void* dg, void* du, int64_t n,
                                          int d) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
@@ -441,7 +468,7 @@ __global__ void silu_mul_backward_kernel(const void* dy, const void* g, const vo
         v = bf16_to_f32(((const bf16_t*)g)[i]); w = bf16_to_f32(((const bf16_t*)u)[i]);
         y = bf16_to_f32(((const bf16_t*)dy)[i]);
       }
-      float s = v >= 0.f ? 1.f / (1.f + expf(-v)) : expf(v) / (1.f + expf(v));
+      float s = sigmoid_f(v);
       float a = y * w * s * (1.f + v * (1.f - s)), b = y * (v * s);
       if (d == F32) {
         ((float*)dg)[i] = a; ((float*)du)[i] = b;
@@ -619,6 +646,12 @@ int qutai_amd_silu_mul_backward(const void* dy, const void* gate, const void* up
                                 int dtype, void* stream) {
   if (n < 0 || !float_dtype(dtype)) return QA_EINVAL;
   if (n == 0) return QA_OK;
+  const bool aligned = ((uintptr_t)dy | (uintptr_t)gate | (uintptr_t)up | (uintptr_t)dgate | (uintptr_t)dup) % 16 == 0;
+  if (dtype == BF16 && n % 8 == 0 && aligned) {
+    hipLaunchKernelGGL(silu_mul_backward_bf16x8, dim3(grid_for(n / 8)), dim3(THREADS), 0, (hipStream_t)stream,
+                       (const u32x4*)dy, (const u32x4*)gate, (const u32x4*)up, (u32x4*)dgate, (u32x4*)dup, n / 8);
+    return (int)hipGetLastError();
+  }
   hipLaunchKernelGGL(silu_mul_backward_kernel, dim3(grid_for(n)), dim3(THREADS), 0, (hipStream_t)stream, dy, gate, up,
                      dgate, dup, n, dtype);
   return (int)hipGetLastError();

@@ -69,3 +69,24 @@ def test_gemm_bf16_output_is_rounded_fp32_output(m, k, n, ta, tb):
     got = np.frombuffer(narrow.to_array(), dtype=np.uint16)
     want = ora.bf16_words(np.frombuffer(wide.to_array(), dtype=np.float32))
     assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("m,k,n", [(512, 256, 384), (300, 100, 264)])
+def test_gemm_accumulate_adds_old_value_before_one_rounding(m, k, n):
+    """out = round(old + A@B) (gemm.cu:25-32) on whole tiles (straight-line
+    epilogue) and ragged tiles: bit-exact against the fp32 product of the
+    same GEMM added to the old values on the host."""
+    from qutai_amd.backends import amd
+
+    rng = np.random.default_rng(m * n)
+    a = upload(rng.standard_normal(m * k), "bfloat16")
+    b = upload(rng.standard_normal(k * n), "bfloat16")
+    product = np.frombuffer(amd.gemm(a, b, m, k, n, out_dtype="float32").to_array(), dtype=np.float32)
+    old = rng.standard_normal(m * n).astype(np.float32)
+    wide = upload(old, "float32")
+    amd.gemm(a, b, m, k, n, out=wide, accumulate=True)
+    assert np.array_equal(np.frombuffer(wide.to_array(), dtype=np.float32), old + product)
+    narrow = upload(old, "bfloat16")
+    old16 = ora.bf16_values(np.frombuffer(narrow.to_array(), dtype=np.uint16)).astype(np.float32)
+    amd.gemm(a, b, m, k, n, out=narrow, out_dtype="bfloat16", accumulate=True)
+    assert np.array_equal(np.frombuffer(narrow.to_array(), dtype=np.uint16), ora.bf16_words(old16 + product))
