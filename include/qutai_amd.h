@@ -299,11 +299,23 @@ int qutai_amd_route_backward(const float* gradient, const float* probs, const fl
  * lm_attention_delta / lm_attention_bf16_dq / lm_attention_bf16_dkv /
  * lm_attention_backward_q / _kv (src/qutai/backends/cuda/lm.cu:159-343);
  * semantics of
- * cpu_lm.attention_backward (src/qutai/backends/cpu_lm.py:176-201). */
+ * cpu_lm.attention_backward (src/qutai/backends/cpu_lm.py:176-201).
+ * `workspace` (optional, 16-byte aligned) of
+ * qutai_amd_attention_bwd_workspace_size bytes lets grouped-query attention
+ * (heads > kv_heads) on small batches split each kv head's dK/dV work over
+ * its query heads and sum the fp32 partials in order; without it (or when
+ * that size is 0) one workgroup covers all query heads of a kv head. */
 int qutai_amd_attention_bwd(const void* grad, const void* q, const void* k, const void* v, const void* out,
-                            const float* lse, void* dq, void* dk, void* dv, float* delta, int64_t batch,
-                            int64_t heads, int64_t kv_heads, int64_t time, int64_t dim, int dtype, int layout,
-                            double scale, int causal, void* stream);
+                            const float* lse, void* dq, void* dk, void* dv, float* delta, void* workspace,
+                            size_t workspace_bytes, int64_t batch, int64_t heads, int64_t kv_heads, int64_t time,
+                            int64_t dim, int dtype, int layout, double scale, int causal, void* stream);
+
+/* Bytes of the optional qutai_amd_attention_bwd workspace for these
+ * arguments (0 when the split does not apply).  No reference counterpart:
+ * the reference's dK/dV kernel always loops over the query heads of a kv
+ * head in one block (src/qutai/backends/cuda/lm.cu:217-288). */
+size_t qutai_amd_attention_bwd_workspace_size(int64_t batch, int64_t heads, int64_t kv_heads, int64_t time,
+                                              int64_t dim, int dtype);
 
 /* ---- decoder glue around the contractions (a full Decoder.loss step) ----
  * Activation dtype QA_BF16 or QA_F32; embedding / RMSNorm weights, RMSNorm

@@ -410,9 +410,12 @@ def attention_backward(gradient, q, k, v, out, lse, batch, time, heads, kv_heads
     delta = AMDStorage(lse.size, "float32")
     scale = dim ** -0.5 if scale is None else scale
     if q.size:
-        dq.runtime.call("qutai_amd_attention_bwd", gradient.ptr, q.ptr, k.ptr, v.ptr, out.ptr, lse.ptr, dq.ptr, dk.ptr,
-                        dv.ptr, delta.ptr, batch, heads, kv_heads, time, dim, code(q.dtype), layout, float(scale),
-                        int(bool(causal)), mfma=q.dtype == "bfloat16" and dim == 64)
+        runtime = dq.runtime
+        need = runtime.lib.qutai_amd_attention_bwd_workspace_size(batch, heads, kv_heads, time, dim, code(q.dtype))
+        workspace = AMDStorage((need + 3) // 4, "float32") if need else None
+        runtime.call("qutai_amd_attention_bwd", gradient.ptr, q.ptr, k.ptr, v.ptr, out.ptr, lse.ptr, dq.ptr, dk.ptr,
+                     dv.ptr, delta.ptr, workspace.ptr if workspace else None, need, batch, heads, kv_heads, time, dim,
+                     code(q.dtype), layout, float(scale), int(bool(causal)), mfma=q.dtype == "bfloat16" and dim == 64)
     return dq, dk, dv
 
 

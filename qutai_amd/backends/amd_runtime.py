@@ -75,10 +75,12 @@ SIGNATURES = {
     "qutai_amd_head_loss": [_p, _p, _p, _i64, _i64, _i32, _p],
     "qutai_amd_head_gradient": [_p, _p, _p, _i64, _i64, _f64, _i32, _p],
     "qutai_amd_attention_fwd": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _f64, _i32, _p],
-    "qutai_amd_attention_bwd": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _f64,
-                                _i32, _p],
+    "qutai_amd_attention_bwd": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _i64, _i64, _i64, _i64, _i64, _i32,
+                                _i32, _f64, _i32, _p],
+    "qutai_amd_attention_bwd_workspace_size": [_i64, _i64, _i64, _i64, _i64, _i32],
 }
-RESTYPES = {"qutai_amd_gemm_workspace_size": _sz, "qutai_amd_rms_norm_workspace": _i64}
+RESTYPES = {"qutai_amd_gemm_workspace_size": _sz, "qutai_amd_rms_norm_workspace": _i64,
+            "qutai_amd_attention_bwd_workspace_size": _sz}
 
 
 def _hip_library():

@@ -27,6 +27,7 @@
 #include "common.h"
 #include "qutai_amd.h"
 
+#include <algorithm>
 #include <cstdlib>
 #include <initializer_list>
 
@@ -384,6 +385,13 @@ struct AttnBwdArgs {
   float c;  // scale * log2(e)
   float scale;
   int causal;
+  // split > 0: each dK/dV workgroup takes one query head of its kv head's
+  // group and writes unscaled fp32 partials to part_k / part_v + g *
+  // part_stride (dk's element offsets); dkv_reduce sums them over g
+  int split;
+  float* part_k;
+  float* part_v;
+  int64_t part_stride;
 };
 
 constexpr float LOG2E = 1.4426950408889634f;
@@ -712,20 +720,27 @@ __global__ void __launch_bounds__(NW * 64) attention_bwd_dkv_d64(AttnBwdArgs p) 
   // the most queries (causal) and start first
   // as in the forward: causal key blocks in work order (the first keys see
   // the most queries), non-causal ones grouped per XCD
-  int bkh, kblk;
+  const int group = (int)(p.heads / p.kv_heads);
+  const int nsplit = p.split ? group : 1;  // workgroups per (batch, kv head, key block)
+  int bkh, kblk, gsel;
   if (p.causal) {
-    const int nbh = (int)(p.batch * p.kv_heads);
-    bkh = uniform32((int)blockIdx.x % nbh);
+    const int nbh = (int)(p.batch * p.kv_heads) * nsplit;
+    const int id = (int)blockIdx.x % nbh;
+    bkh = uniform32(id / nsplit);
+    gsel = uniform32(id % nsplit);
     kblk = uniform32((int)blockIdx.x / nbh);
   } else {
     const int pid = uniform32(xcd_remap(blockIdx.x, gridDim.x));
-    bkh = uniform32(pid / blocks_k);
-    kblk = uniform32(pid % blocks_k);
+    const int rest = pid % (blocks_k * nsplit);
+    bkh = uniform32(pid / (blocks_k * nsplit));
+    kblk = uniform32(rest / nsplit);
+    gsel = uniform32(rest % nsplit);
   }
+  // query heads of the group this workgroup sums over
+  const int g_lo = p.split ? gsel : 0, g_hi = p.split ? gsel + 1 : group;
   const int k0 = uniform32(kblk * KPB);
   const int kw = uniform32(k0 + wave * KW);
   const int b = bkh / (int)p.kv_heads, kvh = bkh % (int)p.kv_heads;
-  const int group = (int)(p.heads / p.kv_heads);
   const int half = lane >> 5, col = lane & 31;
   const int64_t kbase = b * p.kb + kvh * p.kh;
 
@@ -749,9 +764,9 @@ __global__ void __launch_bounds__(NW * 64) attention_bwd_dkv_d64(AttnBwdArgs p) 
   float lse_next = 0.f;                               // wave 0: lse of the block in flight
   const int qs0 = p.causal ? k0 : 0;                  // first query any key of the workgroup sees
   const int nq = qs0 < T ? (T - qs0 + KB - 1) / KB : 0;
-  const int iterations = nq * group;
+  const int iterations = nq * (g_hi - g_lo);
   auto issue = [&](int stage, int it) {
-    const int g = it / nq, qs = qs0 + (it % nq) * KB;
+    const int g = g_lo + it / nq, qs = qs0 + (it % nq) * KB;
     const int h = kvh * group + g;
     const int64_t base = b * p.qb + h * p.qh + (int64_t)qs * p.qt;
     copy_tile<NW>(&tiles[stage][0][0], p.q + base, p.qt, T - qs, wave, lane);
@@ -805,7 +820,7 @@ __global__ void __launch_bounds__(NW * 64) attention_bwd_dkv_d64(AttnBwdArgs p) 
   };
   if (iterations > 0) issue(0, 0);
   int it = 0;
-  for (int g = 0; g < group; g++) {
+  for (int g = g_lo; g < g_hi; g++) {
     int qi = 0;
     for (; qi < a; qi++, it++) advance(it);
     for (; qi < bq; qi++, it++) {
@@ -825,6 +840,26 @@ __global__ void __launch_bounds__(NW * 64) attention_bwd_dkv_d64(AttnBwdArgs p) 
   }
 
   // dK^T / dV^T: lane = key 32 nb + col, rows d = 32 db + 8 (e / 4) + 4 half + e % 4
+  if (p.split) {
+#pragma unroll
+    for (int nb = 0; nb < NKB; nb++) {
+      const int key = kw + 32 * nb + col;
+      if (key < T) {
+        const int64_t at = gsel * p.part_stride + kbase + (int64_t)key * p.kt;
+#pragma unroll
+        for (int db = 0; db < 2; db++)
+#pragma unroll
+          for (int g = 0; g < 4; g++) {
+            const int d = 32 * db + 8 * g + 4 * half;
+            global_store(p.part_k + at + d, f32x4{dkt[db][nb][4 * g], dkt[db][nb][4 * g + 1], dkt[db][nb][4 * g + 2],
+                                                  dkt[db][nb][4 * g + 3]});
+            global_store(p.part_v + at + d, f32x4{dvt[db][nb][4 * g], dvt[db][nb][4 * g + 1], dvt[db][nb][4 * g + 2],
+                                                  dvt[db][nb][4 * g + 3]});
+          }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int nb = 0; nb < NKB; nb++) {
     const int key = kw + 32 * nb + col;
@@ -848,6 +883,22 @@ __global__ void __launch_bounds__(NW * 64) attention_bwd_dkv_d64(AttnBwdArgs p) 
   }
 }
 
+
+// dK = scale * sum_g part_k[g], dV = sum_g part_v[g] (g in order), one
+// rounding to bf16; 4 elements per lane and step.
+__global__ void dkv_reduce(const float* pk, const float* pv, bf16_t* dk, bf16_t* dv, int64_t n4, int64_t stride,
+                           int group, float scale) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (int64_t)gridDim.x * blockDim.x) {
+    f32x4 sk = global_load<f32x4>(pk + 4 * i), sv = global_load<f32x4>(pv + 4 * i);
+    for (int g = 1; g < group; g++) {
+      sk += global_load<f32x4>(pk + g * stride + 4 * i);
+      sv += global_load<f32x4>(pv + g * stride + 4 * i);
+    }
+    sk *= scale;
+    global_store(dk + 4 * i, u32x2{pack_bf16x2(sk[0], sk[1]), pack_bf16x2(sk[2], sk[3])});
+    global_store(dv + 4 * i, u32x2{pack_bf16x2(sv[0], sv[1]), pack_bf16x2(sv[2], sv[3])});
+  }
+}
 
 // ============================================================================
 // Generic path: any head dimension up to 256, fp32 or bf16 storage, fp32
@@ -1093,6 +1144,30 @@ int attention_waves() {
   return waves;
 }
 
+int64_t cu_count() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+// Workspace of the dK/dV query-head split: with grouped-query attention
+// (heads > kv_heads) the kernel has one workgroup per (batch, kv head, 256
+// keys), too few to fill the GPU when that count is below twice the CUs;
+// then each workgroup takes one query head of the group and the group's fp32
+// partials are summed by dkv_reduce.  0 when no split applies.
+size_t dkv_split_bytes(int64_t batch, int64_t heads, int64_t kv_heads, int64_t time) {
+  if (kv_heads <= 0 || heads <= kv_heads || heads % kv_heads) return 0;
+  const int64_t blocks_k = batch * kv_heads * ((time + 255) / 256);
+  if (blocks_k >= 2 * cu_count()) return 0;
+  return (size_t)2 * (heads / kv_heads) * batch * time * kv_heads * D * sizeof(float);
+}
+
 bool aligned16(std::initializer_list<const void*> ptrs) {
   for (const void* ptr : ptrs)
     if (!ptr || (uintptr_t)ptr % 16) return false;
@@ -1153,10 +1228,16 @@ int qutai_amd_attention_fwd(const void* q, const void* k, const void* v, void* o
   return (int)hipGetLastError();
 }
 
+size_t qutai_amd_attention_bwd_workspace_size(int64_t batch, int64_t heads, int64_t kv_heads, int64_t time,
+                                              int64_t dim, int dtype) {
+  if (dtype != BF16 || dim != D || batch < 0 || time < 0) return 0;
+  return dkv_split_bytes(batch, heads, kv_heads, time);
+}
+
 int qutai_amd_attention_bwd(const void* grad, const void* q, const void* k, const void* v, const void* out,
-                            const float* lse, void* dq, void* dk, void* dv, float* delta, int64_t batch, int64_t heads,
-                            int64_t kv_heads, int64_t time, int64_t dim, int dtype, int layout, double scale,
-                            int causal, void* stream) {
+                            const float* lse, void* dq, void* dk, void* dv, float* delta, void* workspace,
+                            size_t workspace_bytes, int64_t batch, int64_t heads, int64_t kv_heads, int64_t time,
+                            int64_t dim, int dtype, int layout, double scale, int causal, void* stream) {
   if (!(scale > 0.0) || scale > 1e30) return QA_EINVAL;
   if (!grad || !q || !k || !v || !out || !dq || !dk || !dv || !lse || !delta) return QA_EINVAL;
   if (dtype == BF16 && dim == D) {
@@ -1179,7 +1260,15 @@ int qutai_amd_attention_bwd(const void* grad, const void* q, const void* k, cons
     a.causal = causal ? 1 : 0;
     // 256 queries (dq) / 256 keys (dk, dv) per workgroup in both shapes
     const int64_t blocks_q = batch * heads * ((time + 255) / 256);
-    const int64_t blocks_k = batch * kv_heads * ((time + 255) / 256);
+    int64_t blocks_k = batch * kv_heads * ((time + 255) / 256);
+    const size_t split_bytes = dkv_split_bytes(batch, heads, kv_heads, time);
+    if (split_bytes && workspace && workspace_bytes >= split_bytes && (uintptr_t)workspace % 16 == 0) {
+      a.split = 1;
+      a.part_stride = batch * time * kv_heads * D;
+      a.part_k = (float*)workspace;
+      a.part_v = a.part_k + (heads / kv_heads) * a.part_stride;
+      blocks_k *= heads / kv_heads;
+    }
     if (blocks_q > 0x7fffffff || blocks_k > 0x7fffffff) return QA_EINVAL;
     // dq first: it writes delta, which the dkv kernel reads
     if (attention_waves() == 8)
@@ -1194,6 +1283,13 @@ int qutai_amd_attention_bwd(const void* grad, const void* q, const void* k, cons
     else
       hipLaunchKernelGGL((attention_bwd_dkv_d64<4, 2>), dim3((unsigned)blocks_k), dim3(256), 0, (hipStream_t)stream,
                          a);
+    if (!a.split) return (int)hipGetLastError();
+    e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+    const int64_t n4 = a.part_stride / 4;
+    const unsigned blocks = (unsigned)std::min<int64_t>((n4 + 255) / 256, 1 << 20);
+    hipLaunchKernelGGL(dkv_reduce, dim3(blocks), dim3(256), 0, (hipStream_t)stream, (const float*)a.part_k,
+                       (const float*)a.part_v, a.dk, a.dv, n4, a.part_stride, (int)(heads / kv_heads), a.scale);
     return (int)hipGetLastError();
   }
   if ((dtype != BF16 && dtype != F32) || dim > 256) return QA_EINVAL;

@@ -373,3 +373,31 @@ def test_general_path_rejects(lm):
     f = upload(np.zeros(8 * 4, dtype=np.float32), "float32")
     with pytest.raises(ValueError):
         lm.attention(b, f, f, 1, 4, 1, 1, 8)  # mixed dtypes
+
+
+def test_backward_query_head_split_matches_one_block_per_kv_head(lm):
+    """Grouped-query attention on a small batch splits each kv head's dK/dV
+    over its query heads (fp32 partials summed in order); the C ABI without
+    the workspace keeps one workgroup per kv head.  Both agree (dq exactly,
+    dk/dv to fp32 summation order before the bf16 rounding)."""
+    from qutai_amd.backends.amd import AMDStorage, code
+
+    dims = (2, 600, 8, 2, 64)
+    batch, time, heads, kv_heads, dim = dims
+    q, k, v, g = (upload(normal(80 + i, n), "bfloat16") for i, n in enumerate(
+        (batch * time * heads * dim, batch * time * kv_heads * dim, batch * time * kv_heads * dim,
+         batch * time * heads * dim)))
+    out, lse = lm.attention(q, k, v, *dims)
+    runtime = q.runtime
+    need = runtime.lib.qutai_amd_attention_bwd_workspace_size(batch, heads, kv_heads, time, dim, code("bfloat16"))
+    assert need == 2 * (heads // kv_heads) * batch * time * kv_heads * dim * 4
+    split = lm.attention_backward(g, q, k, v, out, lse, *dims)
+    whole = [AMDStorage(x.size, "bfloat16") for x in (q, k, v)]
+    delta = AMDStorage(lse.size, "float32")
+    runtime.call("qutai_amd_attention_bwd", g.ptr, q.ptr, k.ptr, v.ptr, out.ptr, lse.ptr, *(x.ptr for x in whole),
+                 delta.ptr, None, 0, batch, heads, kv_heads, time, dim, code("bfloat16"), 1, dim ** -0.5, 1)
+    assert download(split[0]).tobytes() == download(whole[0]).tobytes()
+    for a, b in zip(split[1:], whole[1:]):
+        a, b = download(a), download(b)
+        assert np.abs(a - b).max() <= 2 ** -7 * np.abs(b).max()
+        assert ora.rel_frobenius(a, b) <= 1e-3
