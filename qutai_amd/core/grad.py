@@ -14,6 +14,24 @@ def record(result, parents, rule=None):
     return result
 
 
+def owned(storage):
+    """Mark a gradient storage that its backward rule has just allocated and
+    hands to no one else: the leaf that receives it first may keep it as its
+    ``grad`` instead of copying it (the copy isolates storages a rule passes
+    on to several tensors).  Returns the storage; None passes through."""
+    if storage is not None:
+        storage.owned_gradient = True
+    return storage
+
+
+def take_owned(storage):
+    """True (once) when ``storage`` was marked by ``owned``."""
+    if getattr(storage, "owned_gradient", False):
+        storage.owned_gradient = False
+        return True
+    return False
+
+
 def _topological_order(output):
     order, seen, pending = [], set(), [(output, False)]
     while pending:

@@ -137,10 +137,13 @@ class Tensor:
             seed = gradient.storage
 
         def accumulate(tensor, values):
+            fresh = False
             if values.dtype != tensor.dtype:
-                values = transfer(values, tensor.device, tensor.dtype)
-            values = (get_backend(tensor.device).add(tensor.grad.storage, values)
-                      if tensor.grad is not None else values.copy())
+                values, fresh = transfer(values, tensor.device, tensor.dtype), True
+            if tensor.grad is not None:
+                values = get_backend(tensor.device).add(tensor.grad.storage, values)
+            elif not (fresh or autograd.take_owned(values)):
+                values = values.copy()
             tensor.grad = Tensor(values, shape=tensor.shape)
 
         autograd.backward(self, seed, retain_graph=retain_graph, leaf_sink=accumulate)

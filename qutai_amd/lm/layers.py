@@ -16,7 +16,7 @@ from math import prod, sqrt
 
 from ..backends import amd, amd_lm
 from ..backends.precision import matmul_precision, set_matmul_precision
-from ..core.grad import record
+from ..core.grad import owned, record
 from ..core.tensor import Tensor
 
 
@@ -62,7 +62,7 @@ def linear(x, weight):
     def backward(g):
         with set_matmul_precision(precision):
             dx = b.gemm(g, ws, rows, out_features, inner, out_dtype=x.dtype) if x.requires_grad else None
-            dw = (b.gemm(g, xs, out_features, rows, inner, transpose_left=True, out_dtype=weight.dtype)
+            dw = (owned(b.gemm(g, xs, out_features, rows, inner, transpose_left=True, out_dtype=weight.dtype))
                   if weight.requires_grad else None)
         return dx, dw
 
@@ -86,7 +86,7 @@ def embed(ids, weight, shape):
     width = weight.shape[1]
     values = b.embedding(weight.storage, ids, width)
     return record(Tensor(values, shape=(*shape, width)), (weight,),
-                  lambda g: (b.embedding_backward(g, ids, weight.shape[0], width),))
+                  lambda g: (owned(b.embedding_backward(g, ids, weight.shape[0], width)),))
 
 
 def rms_norm(x, weight, eps):
@@ -94,8 +94,11 @@ def rms_norm(x, weight, eps):
     b = backend(x)
     width = x.shape[-1]
     out, inverse = b.rms_norm(x.storage, weight.storage, width, eps)
-    return record(Tensor(out, shape=x.shape), (x, weight),
-                  lambda g: b.rms_norm_backward(g, x.storage, weight.storage, inverse, width))
+    def backward(g):
+        dx, dweight = b.rms_norm_backward(g, x.storage, weight.storage, inverse, width)
+        return dx, owned(dweight)
+
+    return record(Tensor(out, shape=x.shape), (x, weight), backward)
 
 
 def rope(x, heads, theta, offset=0):
@@ -138,9 +141,9 @@ def swiglu(x, w_gate, w_up):
             if x.requires_grad:
                 dx = amd.add(b.gemm(dgate, gs, rows, hidden, inner, out_dtype=x.dtype),
                              b.gemm(dup, us, rows, hidden, inner, out_dtype=x.dtype))
-            dwg = (b.gemm(dgate, xs, hidden, rows, inner, transpose_left=True, out_dtype=w_gate.dtype)
+            dwg = (owned(b.gemm(dgate, xs, hidden, rows, inner, transpose_left=True, out_dtype=w_gate.dtype))
                    if w_gate.requires_grad else None)
-            dwu = (b.gemm(dup, xs, hidden, rows, inner, transpose_left=True, out_dtype=w_up.dtype)
+            dwu = (owned(b.gemm(dup, xs, hidden, rows, inner, transpose_left=True, out_dtype=w_up.dtype))
                    if w_up.requires_grad else None)
         return dx, dwg, dwu
 
@@ -235,7 +238,7 @@ class SparseMoE:
         def backward(g):
             dx, dw, dwg, dwu, dwd = b.moe_experts_backward(g, route, saved, self.width, self.hidden,
                                                            x_dtype=x.dtype, weight_dtype=weight_dtype)
-            return dx, dw, dwg, dwu, dwd
+            return dx, dw, owned(dwg), owned(dwu), owned(dwd)
 
         result = record(Tensor(values, shape=x.shape), (x, weights, self.w_gate, self.w_up, self.w_down), backward)
         return result, aux
@@ -423,7 +426,7 @@ def projection_loss(hidden, weight, labels, chunk_size, *, prepared_labels=None)
                 dx = amd.full(hidden.size, 0.0, dtype=hidden.dtype)
                 if part is not None:
                     b.head_rows_backward(dx, _cast(part, hidden.dtype), 0, rows, width, time)
-            return dx, dw
+            return dx, owned(dw)
 
     return record(Tensor(result, shape=()), (hidden, weight), backward)
 

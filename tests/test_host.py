@@ -206,3 +206,19 @@ def test_importing_the_package_does_not_touch_the_gpu():
     out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, cwd=str(
         __import__("pathlib").Path(__file__).resolve().parent.parent))
     assert out.returncode == 0 and "lazy" in out.stdout
+
+
+def test_owned_gradient_marks_are_taken_once():
+    """A rule's freshly allocated gradient (grad.owned) is kept by the first
+    leaf that receives it; any later receiver copies (core/grad.py)."""
+    from qutai_amd.core.grad import owned, take_owned
+
+    class Box:
+        pass
+
+    box = Box()
+    assert owned(None) is None
+    assert not take_owned(box)
+    assert owned(box) is box
+    assert take_owned(box)
+    assert not take_owned(box)
