@@ -116,6 +116,12 @@ int qutai_amd_fill(void* dst, int64_t n, double value, int dtype, void* stream);
  * `cuda.add` for gradient accumulation (src/qutai/core/grad.py:60). */
 int qutai_amd_add(const void* left, const void* right, void* out, int64_t n, int dtype, void* stream);
 
+/* out = left + right with fp32 left / out and bf16 right (widened exactly):
+ * the residual update `x + update.to(x.dtype)` of the lm blocks
+ * (src/qutai/lm/layers.py:31-32), a cast and an add in the reference, in one
+ * pass with the same result. */
+int qutai_amd_add_widen(const float* left, const void* right, float* out, int64_t n, void* stream);
+
 /* out = x * factor (element-wise, fp32 math for bf16).  Replaces `cuda.scale`
  * (src/qutai/backends/cuda.py:198), used by the lm loss head
  * (src/qutai/lm/layers.py:212). */

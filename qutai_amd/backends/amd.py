@@ -304,6 +304,16 @@ def _gemm_views(a: _View, b: _View, c: _View, rows, inner, cols, item):
                  mfma=dtype != "float64")
 
 
+def add_widen(left: AMDStorage, right: AMDStorage) -> AMDStorage:
+    """fp32 left + bf16 right (exactly widened), fp32 result."""
+    if left.dtype != "float32" or right.dtype != "bfloat16" or left.size != right.size:
+        raise ValueError("add_widen takes float32 + bfloat16 storages of one size")
+    result = AMDStorage(left.size, "float32")
+    if left.size:
+        result.runtime.call("qutai_amd_add_widen", left.ptr, right.ptr, result.ptr, left.size)
+    return result
+
+
 def add(left: AMDStorage, right: AMDStorage) -> AMDStorage:
     if (left.dtype, left.size) != (right.dtype, right.size):
         raise ValueError("add needs equal dtype and size")

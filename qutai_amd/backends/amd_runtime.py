@@ -47,6 +47,7 @@ SIGNATURES = {
     "qutai_amd_cast": [_p, _p, _i64, _i32, _i32, _p],
     "qutai_amd_fill": [_p, _i64, _f64, _i32, _p],
     "qutai_amd_add": [_p, _p, _p, _i64, _i32, _p],
+    "qutai_amd_add_widen": [_p, _p, _p, _i64, _p],
     "qutai_amd_add_rows": [_p, _p, _p, _i64, _i64, _i32, _p],
     "qutai_amd_sum_middle": [_p, _p, _i64, _i64, _i64, _i32, _p],
     "qutai_amd_transpose_last2": [_p, _p, _i64, _i64, _i64, _i32, _p],

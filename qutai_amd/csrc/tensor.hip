@@ -142,6 +142,20 @@ __global__ void add_kernel(const void* a, const void* b, void* out, int64_t n, i
   }
 }
 
+// out = left + widen(right): fp32 plus bf16 (exactly widened), 4 per lane
+__global__ void add_widen_kernel(const f32x4* a, const u32x2* b, f32x4* out, int64_t n4) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (int64_t)gridDim.x * blockDim.x) {
+    const u32x2 w = b[i];
+    out[i] = a[i] + f32x4{__uint_as_float(w[0] << 16), __uint_as_float(w[0] & 0xffff0000u),
+                          __uint_as_float(w[1] << 16), __uint_as_float(w[1] & 0xffff0000u)};
+  }
+}
+
+__global__ void add_widen_tail(const float* a, const bf16_t* b, float* out, int64_t begin, int64_t n) {
+  for (int64_t i = begin + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    out[i] = a[i] + bf16_to_f32(b[i]);
+}
+
 __global__ void sum_middle_kernel(const void* x, void* out, int64_t outer, int64_t count, int64_t inner, int d) {
   int64_t n = outer * inner;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
@@ -507,6 +521,22 @@ int qutai_amd_add(const void* left, const void* right, void* out, int64_t n, int
   if (n == 0) return QA_OK;
   hipLaunchKernelGGL(add_kernel, dim3(grid_for(n)), dim3(THREADS), 0, (hipStream_t)stream, left, right, out, n,
                      dtype);
+  return (int)hipGetLastError();
+}
+
+int qutai_amd_add_widen(const float* left, const void* right, float* out, int64_t n, void* stream) {
+  if (n < 0 || (n > 0 && (!left || !right || !out))) return QA_EINVAL;
+  if (n == 0) return QA_OK;
+  int64_t head = 0;
+  if (((uintptr_t)left | (uintptr_t)out) % 16 == 0 && (uintptr_t)right % 8 == 0) {
+    head = n / 4 * 4;
+    if (head)
+      hipLaunchKernelGGL(add_widen_kernel, dim3(grid_for(head / 4)), dim3(THREADS), 0, (hipStream_t)stream,
+                         (const f32x4*)left, (const u32x2*)right, (f32x4*)out, head / 4);
+  }
+  if (head < n)
+    hipLaunchKernelGGL(add_widen_tail, dim3(grid_for(n - head)), dim3(THREADS), 0, (hipStream_t)stream, left,
+                       (const bf16_t*)right, out, head, n);
   return (int)hipGetLastError();
 }
 

@@ -45,6 +45,22 @@ def _bf16(values):
     return values if values.dtype == "bfloat16" else amd.from_storage(values, dtype="bfloat16")
 
 
+def _bf16_input(x):
+    """x's storage rounded to bf16 for the bf16-path products, made once per
+    activation: the q, k and v projections of one normalised input share the
+    copy (the rounding is the same each time).  Cached only on tensors made
+    by a recorded op, whose storage is never written again."""
+    if x.dtype == "bfloat16":
+        return x.storage
+    if getattr(x, "backward_rule", None) is None:
+        return _bf16(x.storage)
+    cached = getattr(x, "_bf16_input", None)
+    if cached is None or cached[0] is not x.storage:
+        cached = (x.storage, _bf16(x.storage))
+        x._bf16_input = cached
+    return cached[1]
+
+
 def linear(x, weight):
     """Y = X W^T with W stored (out, in) (src/qutai/lm/layers.py:35-74).  On
     the bf16 path the fp32 operands are rounded to bf16 once here, the same
@@ -56,7 +72,7 @@ def linear(x, weight):
     precision = matmul_precision()
     xs, ws = x.storage, weight.storage
     if _bf16_path(x, weight):
-        xs, ws = _bf16(xs), _bf16(ws)
+        xs, ws = _bf16_input(x), _bf16(ws)
     values = b.gemm(xs, ws, rows, inner, out_features, transpose_right=True, out_dtype=activation_dtype(x, weight))
 
     def backward(g):
@@ -70,7 +86,12 @@ def linear(x, weight):
 
 
 def residual_add(x, update):
-    """x + update cast to x's dtype (src/qutai/lm/layers.py:31-32)."""
+    """x + update cast to x's dtype (src/qutai/lm/layers.py:31-32).  fp32 x
+    with a bf16 update (autocast) adds in one pass; the backward is the
+    cast's and the add's: the gradient to x, and rounded to bf16 to update."""
+    if x.device == "amd" and x.dtype == "float32" and update.dtype == "bfloat16" and x.shape == update.shape:
+        return record(Tensor(amd.add_widen(x.storage, update.storage), shape=x.shape), (x, update),
+                      lambda g: (g, amd.from_storage(g, dtype="bfloat16")))
     return x + update.to(dtype=x.dtype)
 
 
@@ -131,7 +152,7 @@ def swiglu(x, w_gate, w_up):
     rows = x.size // x.shape[-1]
     hidden, inner = w_gate.shape
     precision = matmul_precision()
-    xs, gs, us = _bf16(x.storage), _bf16(w_gate.storage), _bf16(w_up.storage)
+    xs, gs, us = _bf16_input(x), _bf16(w_gate.storage), _bf16(w_up.storage)
     act, gate, up = b.swiglu_gemm(xs, gs, us, rows, inner, hidden, save=True)
 
     def backward(g):

@@ -210,3 +210,23 @@ def test_repitch_pads_and_crops_exactly(lm, dtype):
     assert np.array_equal(download(back).reshape(3, 5, 6), stored(x, dtype))
     with pytest.raises(ValueError):
         lm.repitch(padded, 3, 5, 6, 5, 6)  # size does not match the stated shape
+
+
+def test_residual_add_widened_equals_cast_then_add(base):
+    """residual_add (lm/layers.py:31-32) of fp32 x and a bf16 update: the
+    one-pass form equals x + update.to(float32) bit for bit, forward and both
+    gradients (ragged length: vector body and scalar tail)."""
+    from qutai_amd import Tensor
+    from qutai_amd.lm.layers import residual_add
+
+    n = 4 * 1000 + 3
+    x = Tensor(upload(normal(31, n), "float32"), shape=(n,), requires_grad=True)
+    u = Tensor(upload(normal(32, n), "bfloat16"), shape=(n,), requires_grad=True)
+    g = Tensor(upload(normal(33, n), "float32"), shape=(n,))
+    results = []
+    for fused in (True, False):
+        x.grad = u.grad = None
+        y = residual_add(x, u) if fused else x + u.to(dtype="float32")
+        y.backward(g)
+        results.append([t.storage.to_array() for t in (y, x.grad, u.grad)])
+    assert results[0] == results[1]
