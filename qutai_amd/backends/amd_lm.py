@@ -12,6 +12,8 @@ memory, so no host synchronisation sizes them).
 from __future__ import annotations
 
 from array import array
+from bisect import bisect_left
+from functools import partial
 from random import Random
 
 from . import amd
@@ -442,7 +444,8 @@ def embedding(weight, ids, width, *, out_dtype=None):
     dtype = out_dtype or weight.dtype
     if _acc_dtype(dtype) != weight.dtype:
         raise ValueError("the embedding table must be in the activations' accumulation dtype")
-    ids = [int(t) for t in ids]
+    if not (isinstance(ids, array) and ids.typecode == "q"):
+        ids = array("q", (int(t) for t in ids))
     result = AMDStorage(len(ids) * width, dtype)
     if result.size:
         identifiers = amd.storage(ids, dtype="int64")
@@ -451,23 +454,32 @@ def embedding(weight, ids, width, *, out_dtype=None):
     return result
 
 
-def embedding_backward(gradient, ids, count, width):
+def embedding_backward_index(ids):
+    """Device index of the table gradient's row sums: the distinct token ids
+    ascending, offsets into the rows, and the rows of each token in input
+    order (cuda_lm.py:96-123 groups them the same way on the host).  Built
+    with C-level sorts and searches; made once per forward, so the backward
+    launches without a host transfer."""
+    if not (isinstance(ids, array) and ids.typecode == "q"):
+        ids = array("q", (int(t) for t in ids))
+    order = sorted(range(len(ids)), key=ids.__getitem__)  # stable: input order within a token
+    grouped = array("q", map(ids.__getitem__, order))
+    tokens = sorted(set(ids))
+    offsets = array("q", map(partial(bisect_left, grouped), tokens))
+    offsets.append(len(ids))
+    return tuple(amd.storage(values, dtype="int64")
+                 for values in (array("q", tokens), offsets, array("q", order)))
+
+
+def embedding_backward(gradient, ids, count, width, *, index=None):
     """Table gradient [count][width] (fp32): each token's gradient rows summed
-    in input order (cuda_lm.py:96-123)."""
-    groups = {}
-    for row, token in enumerate(ids):
-        groups.setdefault(int(token), []).append(row)
-    tokens = sorted(groups)
-    offsets, positions = [0], []
-    for token in tokens:
-        positions.extend(groups[token])
-        offsets.append(len(positions))
+    in input order (cuda_lm.py:96-123).  ``index`` is
+    ``embedding_backward_index(ids)`` when the caller made it earlier."""
     result = amd.full(count * width, 0.0, dtype=_acc_dtype(gradient.dtype))
-    if tokens and width:
-        # keep the index uploads referenced until the launch: freed storage is reused at once
-        index = [amd.storage(values, dtype="int64") for values in (tokens, offsets, positions)]
-        result.runtime.call("qutai_amd_embedding_backward", gradient.ptr, *(t.ptr for t in index), result.ptr,
-                            len(tokens), width, code(gradient.dtype))
+    if len(ids) and width:
+        tokens, offsets, positions = embedding_backward_index(ids) if index is None else index
+        result.runtime.call("qutai_amd_embedding_backward", gradient.ptr, tokens.ptr, offsets.ptr, positions.ptr,
+                            result.ptr, tokens.size, width, code(gradient.dtype))
     return result
 
 
@@ -540,7 +552,9 @@ def head_rows_backward(target, gradient, start, count, width, time):
 
 def prepare_labels(labels):
     """Labels resident on the device as int64 (cuda_lm.py:616-617)."""
-    return amd.storage([int(x) for x in labels], dtype="int64")
+    if not (isinstance(labels, array) and labels.typecode == "q"):
+        labels = array("q", (int(x) for x in labels))
+    return amd.storage(labels, dtype="int64")
 
 
 def _head_labels(labels, start, rows):

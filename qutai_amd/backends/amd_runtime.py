@@ -126,6 +126,8 @@ class Runtime:
         self.mfma_launches = 0
         self.debug_sync = os.environ.get("QUTAI_AMD_SYNC") == "1"
         self._closed = False
+        # pinned staging ring for asynchronous host-to-device uploads
+        self._staging, self._staging_at, self._staging_pending = None, 0, []
         self.hip = _hip_library()
         self._bind_hip()
         self.lib = load_library()
@@ -186,6 +188,9 @@ class Runtime:
         self._free = bind("hipFree", [vp])
         self._memcpy = bind("hipMemcpy", [vp, vp, sz, ctypes.c_int])
         self._memcpy_async = bind("hipMemcpyAsync", [vp, vp, sz, ctypes.c_int, vp])
+        self._host_malloc = bind("hipHostMalloc", [ctypes.POINTER(ctypes.c_void_p), sz, ctypes.c_uint])
+        self._host_free = bind("hipHostFree", [vp])
+        self._event_create_flags = bind("hipEventCreateWithFlags", [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint])
         self._event_create = bind("hipEventCreate", [ctypes.POINTER(ctypes.c_void_p)])
         self._event_record = bind("hipEventRecord", [vp, vp])
         self._event_sync = bind("hipEventSynchronize", [vp])
@@ -274,12 +279,45 @@ class Runtime:
             raise ValueError("host buffer must be contiguous and writable")
         return (ctypes.c_ubyte * view.nbytes).from_buffer(buffer), view.nbytes
 
+    STAGING_BYTES = 16 << 20  # pinned ring; uploads up to a quarter of it are asynchronous
+
     def upload(self, ptr: int, buffer):
+        """Host bytes into device memory, in order with the kernels of the
+        default stream.  Small uploads are copied into a pinned staging ring
+        and sent with hipMemcpyAsync, so the host does not wait for the kernels
+        queued before them; an event per upload guards its ring region until
+        the copy has run.  Larger ones use a synchronous hipMemcpy."""
         host, nbytes = self._host_buffer(buffer)
         with self._lock:
             self._current()
-            if nbytes:
+            if not nbytes:
+                return
+            if nbytes > self.STAGING_BYTES // 4:
                 self._check(self._memcpy(ptr, host, nbytes, _MEMCPY_H2D), "hipMemcpy HtoD")
+                return
+            if self._staging is None:
+                value = ctypes.c_void_p()
+                self._check(self._host_malloc(ctypes.byref(value), self.STAGING_BYTES, 0), "hipHostMalloc")
+                self._staging = value.value
+            start = self._staging_at if self._staging_at + nbytes <= self.STAGING_BYTES else 0
+            end = start + nbytes
+            # wait for the copies that still read the region about to be overwritten
+            keep = []
+            for lo, hi, event in self._staging_pending:
+                if lo < end and start < hi:
+                    self._check(self._event_sync(event), "hipEventSynchronize")
+                    self._event_destroy(event)
+                else:
+                    keep.append((lo, hi, event))
+            ctypes.memmove(self._staging + start, host, nbytes)
+            self._check(self._memcpy_async(ptr, self._staging + start, nbytes, _MEMCPY_H2D, None),
+                        "hipMemcpyAsync HtoD")
+            event = ctypes.c_void_p()
+            self._check(self._event_create_flags(ctypes.byref(event), 2), "hipEventCreateWithFlags")  # no timing
+            self._check(self._event_record(event, None), "hipEventRecord")
+            keep.append((start, end, event.value))
+            self._staging_pending = keep
+            self._staging_at = (end + 255) // 256 * 256
 
     def download(self, ptr: int, buffer):
         host, nbytes = self._host_buffer(buffer)
@@ -343,6 +381,12 @@ class Runtime:
                 return
             self._closed = True
             self._sync()
+            for _, _, event in self._staging_pending:
+                self._event_destroy(event)
+            self._staging_pending = []
+            if self._staging is not None:
+                self._host_free(self._staging)
+                self._staging = None
             for pointer in self._blocks:
                 self._free(pointer)
             self._allocations.clear()

@@ -15,12 +15,25 @@ the reference's ``ffn.experts.{e}.gate.weight`` is row block e.
 """
 from __future__ import annotations
 
+from array import array
+from bisect import bisect_left
+from itertools import chain
+
 from ..backends import amd
 from ..core.context import set_recording
 from ..core.tensor import Tensor
 from .config import Config
 from .layers import Block, Projection, RMSNorm, backend, embed, linear, projection_loss, scaled, unpack
 from .recompute import checkpoint
+
+
+def _int_array(values):
+    """int64 array of host ids (C-level conversion; other numbers via int())."""
+    values = list(values)
+    try:
+        return array("q", values)
+    except TypeError:
+        return array("q", (int(v) for v in values))
 
 
 class Decoder:
@@ -62,11 +75,11 @@ class Decoder:
 
     # ---- forward (decoder.py:92-139) -----------------------------------------------
     def _tokens(self, tokens):
-        rows = [list(row) for row in tokens]
+        rows = [row if isinstance(row, (list, tuple)) else list(row) for row in tokens]
         if not rows or any(len(row) != len(rows[0]) for row in rows) or not 1 <= len(rows[0]) <= self.config.max_seq_len:
             raise ValueError("tokens must be a non-empty 2-D batch no longer than max_seq_len")
-        ids = tuple(int(t) for row in rows for t in row)
-        if any(t < 0 or t >= self.config.vocab_size for t in ids):
+        ids = _int_array(chain.from_iterable(rows))  # C-level loops: the ids feed every step
+        if min(ids) < 0 or max(ids) >= self.config.vocab_size:
             raise ValueError("token id outside the vocabulary")
         return ids, (len(rows), len(rows[0]))
 
@@ -108,13 +121,16 @@ class Decoder:
         if shape[1] < 2:
             raise ValueError("next-token training needs at least two positions")
         labels = tokens if labels is None else labels
-        label_rows = [list(row) for row in labels]
+        label_rows = [row if isinstance(row, (list, tuple)) else list(row) for row in labels]
         if len(label_rows) != shape[0] or any(len(row) != shape[1] for row in label_rows):
             raise ValueError("labels must have the shape of tokens")
-        if any(label != -100 and not 0 <= label < self.config.vocab_size for row in label_rows for label in row):
+        ordered = sorted(_int_array(chain.from_iterable(label_rows)))
+        first = bisect_left(ordered, -99)  # first label above the ignore id
+        if ordered[0] < -100 or ordered[-1] >= self.config.vocab_size or (first < len(ordered) and ordered[first] < 0):
             raise ValueError("labels must be vocabulary ids or -100")
         with set_recording(train):
-            prepared = backend(self.embedding.weight).prepare_labels(tuple(l for row in label_rows for l in row[1:]))
+            prepared = backend(self.embedding.weight).prepare_labels(
+                _int_array(chain.from_iterable(row[1:] for row in label_rows)))
             hidden = self.hidden(tokens, train=train)
             self.last_lm_loss = projection_loss(hidden, self.embedding.weight, label_rows, chunk_size,
                                                 prepared_labels=prepared)

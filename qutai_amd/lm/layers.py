@@ -12,6 +12,8 @@ O = P V) on the batched GEMM.
 """
 from __future__ import annotations
 
+from array import array
+from itertools import chain
 from math import prod, sqrt
 
 from ..backends import amd, amd_lm
@@ -106,8 +108,14 @@ def embed(ids, weight, shape):
     b = backend(weight)
     width = weight.shape[1]
     values = b.embedding(weight.storage, ids, width)
-    return record(Tensor(values, shape=(*shape, width)), (weight,),
-                  lambda g: (owned(b.embedding_backward(g, ids, weight.shape[0], width)),))
+    result = record(Tensor(values, shape=(*shape, width)), (weight,))
+    if result.requires_grad:
+        # the row grouping goes to the device now, with the ids, so that the
+        # backward launches without a host transfer (which would wait for
+        # every kernel queued before it)
+        index = b.embedding_backward_index(ids)
+        result.backward_rule = lambda g: (owned(b.embedding_backward(g, ids, weight.shape[0], width, index=index)),)
+    return result
 
 
 def rms_norm(x, weight, eps):
@@ -403,10 +411,13 @@ def projection_loss(hidden, weight, labels, chunk_size, *, prepared_labels=None)
     _, time, width = hidden.shape
     vocab = weight.shape[0]
     precision = matmul_precision()
-    targets = tuple(label for row in labels for label in row[1:])
+    try:  # C-level conversion of integer labels
+        targets = array("q", chain.from_iterable(row[1:] for row in labels))
+    except TypeError:
+        targets = array("q", (int(label) for row in labels for label in row[1:]))
     label_data = b.prepare_labels(targets) if prepared_labels is None else prepared_labels
     rows = len(targets)
-    count = max(1, sum(label != -100 for label in targets))
+    count = max(1, rows - targets.count(-100))
     out_dtype = activation_dtype(hidden, weight)
     hs, ws = hidden.storage, weight.storage
     if _bf16_path(hidden, weight):  # round once, not once per block and product
