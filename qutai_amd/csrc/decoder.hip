@@ -96,6 +96,7 @@ __global__ void __launch_bounds__(256) rms_dx_kernel(const float* g, const T* x,
 // dw[j] = sum_r g x inv over rows (lm.cu:52): chunks of RC rows write
 // partial sums, then one thread per column adds the chunks in order
 constexpr int RC = 64;
+constexpr int RCB = 16;  // rows per workgroup of the one-pass backward (enough workgroups for 4096 rows)
 template <class T>
 __global__ void rms_dw_partial_kernel(const float* g, const T* x, const float* inv, float* partial, int64_t rows,
                                       int64_t width) {
@@ -112,6 +113,119 @@ __global__ void rms_dw_final_kernel(const float* partial, float* dw, int64_t chu
     float total = 0.f;
     for (int64_t c = 0; c < chunks; c++) total += partial[c * width + j];
     dw[j] = total;
+  }
+}
+
+// Rows of width 256*NI (NI <= 8, e.g. d_model 2048): lane l owns columns
+// 4 l + 256 i, i < NI, read and written 16 bytes at a time; the forward keeps
+// the row in registers between the sum of squares and the output.
+template <class T, int NI>
+__device__ __forceinline__ void load_cols(const T* row, int lane, f32x4 (&v)[NI]) {
+#pragma unroll
+  for (int i = 0; i < NI; i++) {
+    const int64_t c = 4 * lane + 256 * i;
+    if constexpr (sizeof(T) == 2) {
+      const u32x2 w = global_load<u32x2>(row + c);
+      v[i] = f32x4{__uint_as_float(w[0] << 16), __uint_as_float(w[0] & 0xffff0000u), __uint_as_float(w[1] << 16),
+                   __uint_as_float(w[1] & 0xffff0000u)};
+    } else {
+      v[i] = global_load<f32x4>(row + c);
+    }
+  }
+}
+template <class T, int NI>
+__device__ __forceinline__ void store_cols(T* row, int lane, const f32x4 (&v)[NI]) {
+#pragma unroll
+  for (int i = 0; i < NI; i++) {
+    const int64_t c = 4 * lane + 256 * i;
+    if constexpr (sizeof(T) == 2) global_store(row + c, u32x2{pack_bf16x2(v[i][0], v[i][1]), pack_bf16x2(v[i][2], v[i][3])});
+    else global_store(row + c, v[i]);
+  }
+}
+
+template <class T, int NI>
+__global__ void __launch_bounds__(256) rms_cols_kernel(const T* x, const float* w, float* out, float* inv,
+                                                       int64_t rows, float eps) {
+  constexpr int W = 256 * NI;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  f32x4 v[NI], wv[NI];
+  load_cols<T, NI>(x + row * W, lane, v);
+  load_cols<float, NI>(w, lane, wv);
+  float total = 0.f;
+#pragma unroll
+  for (int i = 0; i < NI; i++) total += v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] + v[i][3] * v[i][3];
+  const float scale = 1.f / sqrtf(wave_sum(total) / (float)W + eps);
+  if (lane == 0) inv[row] = scale;
+#pragma unroll
+  for (int i = 0; i < NI; i++) v[i] = v[i] * scale * wv[i];
+  store_cols<float, NI>(out + row * W, lane, v);
+}
+
+// Backward in one pass over g and x: a workgroup takes RCB rows (wave k the
+// rows k, k + 4, ...), writes dx per row and sums g x inv per column in
+// registers; the four waves' column sums are added in wave order through LDS
+// into the workgroup's row of `partial` (rms_dw_final adds the chunks).
+template <class T, int NI>
+__global__ void __launch_bounds__(256) rms_backward_cols_kernel(const float* g, const T* x, const float* w,
+                                                                const float* inv, T* dx, float* partial,
+                                                                int64_t rows) {
+  constexpr int W = 256 * NI;
+  __shared__ f32x4 sums[4][W / 4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t r0 = (int64_t)blockIdx.x * RCB, r1 = min(rows, r0 + RCB);
+  f32x4 wv[NI], acc[NI];
+  load_cols<float, NI>(w, lane, wv);
+#pragma unroll
+  for (int i = 0; i < NI; i++) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int64_t r = r0 + wave; r < r1; r += 4) {
+    f32x4 gv[NI], xv[NI];
+    load_cols<float, NI>(g + r * W, lane, gv);
+    load_cols<T, NI>(x + r * W, lane, xv);
+    float total = 0.f;
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+      const f32x4 t = gv[i] * wv[i] * xv[i];
+      total += t[0] + t[1] + t[2] + t[3];
+    }
+    const float projected = wave_sum(total) / (float)W, scale = inv[r];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+      acc[i] += gv[i] * xv[i] * scale;
+      gv[i] = scale * (gv[i] * wv[i] - xv[i] * (scale * scale * projected));
+    }
+    store_cols<T, NI>(dx + r * W, lane, gv);
+  }
+#pragma unroll
+  for (int i = 0; i < NI; i++) sums[wave][lane + 64 * i] = acc[i];
+  __syncthreads();
+  for (int q = threadIdx.x; q < W / 4; q += 256) {
+    f32x4 t = sums[0][q];
+#pragma unroll
+    for (int k = 1; k < 4; k++) t += sums[k][q];
+    global_store(partial + (int64_t)blockIdx.x * W + 4 * q, t);
+  }
+}
+
+// dw[j] = sum over chunks c of partial[c][j]: 16 parts of consecutive
+// chunks, each summed in chunk order, then the parts added in order; 16
+// columns per workgroup
+__global__ void __launch_bounds__(256) rms_dw_final_parts(const float* partial, float* dw, int64_t chunks,
+                                                          int64_t width) {
+  __shared__ float part[16][16];
+  const int col = threadIdx.x & 15, k = threadIdx.x >> 4;
+  const int64_t j = (int64_t)blockIdx.x * 16 + col;
+  const int64_t per = (chunks + 15) / 16, c0 = k * per, c1 = min(chunks, c0 + per);
+  float total = 0.f;
+  if (j < width)
+    for (int64_t c = c0; c < c1; c++) total += partial[c * width + j];
+  part[k][col] = total;
+  __syncthreads();
+  if (k == 0 && j < width) {
+    float sum = part[0][col];
+    for (int q = 1; q < 16; q++) sum += part[q][col];
+    dw[j] = sum;
   }
 }
 
@@ -350,6 +464,11 @@ __global__ void __launch_bounds__(HEAD_THREADS) head_block_gradient_kernel(T* lo
 
 bool act_dtype(int d) { return d == F32 || d == BF16; }
 
+// rows of whole 256-column groups, at most 2048 wide, 16-byte aligned base
+bool cols_path(const void* p, int64_t width) {
+  return width % 256 == 0 && width <= 2048 && (uintptr_t)p % 16 == 0;
+}
+
 // 16-byte chunks need an aligned base and rows that are whole chunks
 bool vec_rows(const void* p, int64_t vocab, int per_chunk) {
   return (uintptr_t)p % 16 == 0 && vocab % per_chunk == 0;
@@ -396,6 +515,21 @@ int qutai_amd_rms_norm(const void* x, const float* weight, float* out, float* in
   if (rows == 0) return QA_OK;
   const unsigned blocks = (unsigned)((rows + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK);
   hipStream_t s = (hipStream_t)stream;
+  if (cols_path(x, width) && cols_path(weight, width) && cols_path(out, width)) {
+    const bool bf = dtype == BF16;
+    switch (width / 256) {
+#define QA_RMS(N)                                                                                                   \
+  case N:                                                                                                           \
+    if (bf) hipLaunchKernelGGL((rms_cols_kernel<bf16_t, N>), dim3(blocks), dim3(256), 0, s, (const bf16_t*)x, weight, \
+                               out, inverse, rows, (float)eps);                                                     \
+    else hipLaunchKernelGGL((rms_cols_kernel<float, N>), dim3(blocks), dim3(256), 0, s, (const float*)x, weight, out,   \
+                            inverse, rows, (float)eps);                                                             \
+    break;
+      QA_RMS(1) QA_RMS(2) QA_RMS(3) QA_RMS(4) QA_RMS(5) QA_RMS(6) QA_RMS(7) QA_RMS(8)
+#undef QA_RMS
+    }
+    return (int)hipGetLastError();
+  }
   if (dtype == BF16)
     hipLaunchKernelGGL(rms_kernel<bf16_t>, dim3(blocks), dim3(256), 0, s, (const bf16_t*)x, weight, out, inverse,
                        rows, width, (float)eps);
@@ -406,7 +540,7 @@ int qutai_amd_rms_norm(const void* x, const float* weight, float* out, float* in
 }
 
 int64_t qutai_amd_rms_norm_workspace(int64_t rows, int64_t width) {
-  return rows <= 0 || width <= 0 ? 0 : ((rows + RC - 1) / RC) * width;
+  return rows <= 0 || width <= 0 ? 0 : ((rows + RCB - 1) / RCB) * width;
 }
 
 int qutai_amd_rms_norm_backward(const float* gradient, const void* x, const float* weight, const float* inverse,
@@ -420,6 +554,25 @@ int qutai_amd_rms_norm_backward(const float* gradient, const void* x, const floa
   const int64_t chunks = (rows + RC - 1) / RC;
   if (chunks > 65535) return QA_EINVAL;
   const dim3 grid((unsigned)((width + 255) / 256), (unsigned)chunks);
+  if (cols_path(gradient, width) && cols_path(x, width) && cols_path(weight, width) && cols_path(dx, width) &&
+      cols_path(partial, width)) {
+    const bool bf = dtype == BF16;
+    const int64_t groups = (rows + RCB - 1) / RCB;
+    switch (width / 256) {
+#define QA_RMSB(N)                                                                                                 \
+  case N:                                                                                                          \
+    if (bf) hipLaunchKernelGGL((rms_backward_cols_kernel<bf16_t, N>), dim3((unsigned)groups), dim3(256), 0, s,      \
+                               gradient, (const bf16_t*)x, weight, inverse, (bf16_t*)dx, partial, rows);            \
+    else hipLaunchKernelGGL((rms_backward_cols_kernel<float, N>), dim3((unsigned)groups), dim3(256), 0, s, gradient, \
+                            (const float*)x, weight, inverse, (float*)dx, partial, rows);                          \
+    break;
+      QA_RMSB(1) QA_RMSB(2) QA_RMSB(3) QA_RMSB(4) QA_RMSB(5) QA_RMSB(6) QA_RMSB(7) QA_RMSB(8)
+#undef QA_RMSB
+    }
+    hipLaunchKernelGGL(rms_dw_final_parts, dim3((unsigned)((width + 15) / 16)), dim3(256), 0, s, partial, dweight,
+                       groups, width);
+    return (int)hipGetLastError();
+  }
   if (dtype == BF16) {
     hipLaunchKernelGGL(rms_dx_kernel<bf16_t>, dim3(blocks), dim3(256), 0, s, gradient, (const bf16_t*)x, weight,
                        inverse, (bf16_t*)dx, rows, width);

@@ -61,6 +61,6 @@ def test_bindings_apply_without_a_device():
     # K chunks of 8192, four fp32 partial products
     assert size(1024, 32768, 2048, 1, 0, 0, 0, 0, 5, 5, 0) == 4 * 1024 * 2048 * 4 + 256
     assert size(4096, 4096, 4096, 1, 0, 0, 0, 0, 5, 5, 0) == 0  # a full round of tiles: no split
-    # RMSNorm backward partial sums: one row of floats per 64 rows
+    # RMSNorm backward partial sums: one row of floats per 16 rows
     rms = library.qutai_amd_rms_norm_workspace
-    assert rms(4096, 2048) == 64 * 2048 and rms(65, 8) == 2 * 8 and rms(0, 8) == 0
+    assert rms(4096, 2048) == 256 * 2048 and rms(65, 8) == 5 * 8 and rms(0, 8) == 0

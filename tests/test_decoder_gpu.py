@@ -50,7 +50,8 @@ def test_embedding_forward_and_backward(lm, dtype):
         lm.embedding(upload(table, "bfloat16"), ids, width)  # bf16 table: not the accumulation dtype
 
 
-@pytest.mark.parametrize("dtype,rows,width", [("float32", 37, 40), ("bfloat16", 300, 2048), ("float32", 4096, 2048)])
+@pytest.mark.parametrize("dtype,rows,width", [("float32", 37, 40), ("bfloat16", 300, 2048), ("float32", 4096, 2048),
+                                               ("bfloat16", 65, 768), ("float32", 129, 256), ("float32", 70, 2304)])
 def test_rms_norm_forward_and_backward(lm, dtype, rows, width):
     eps = 1e-5
     x = normal(112, rows * width, 2.0)
