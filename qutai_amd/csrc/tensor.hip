@@ -39,6 +39,29 @@ __global__ void cast_kernel(const void* src, void* dst, int64_t n, int s, int d)
   }
 }
 
+// fp32 <-> bf16 in 16-byte pieces (8 values per lane and step); the same
+// values as cast_kernel (RNE narrowing, exact widening)
+__global__ void cast_f32_bf16x8(const f32x4* src, u32x4* dst, int64_t n8) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += (int64_t)gridDim.x * blockDim.x) {
+    const f32x4 a = src[2 * i], b = src[2 * i + 1];
+    dst[i] = u32x4{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3]), pack_bf16x2(b[0], b[1]), pack_bf16x2(b[2], b[3])};
+  }
+}
+__global__ void cast_bf16_f32x8(const u32x4* src, f32x4* dst, int64_t n8) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += (int64_t)gridDim.x * blockDim.x) {
+    const u32x4 w = src[i];
+    dst[2 * i] = f32x4{__uint_as_float(w[0] << 16), __uint_as_float(w[0] & 0xffff0000u), __uint_as_float(w[1] << 16),
+                       __uint_as_float(w[1] & 0xffff0000u)};
+    dst[2 * i + 1] = f32x4{__uint_as_float(w[2] << 16), __uint_as_float(w[2] & 0xffff0000u),
+                           __uint_as_float(w[3] << 16), __uint_as_float(w[3] & 0xffff0000u)};
+  }
+}
+// out = a + b for fp32, 4 per lane and step
+__global__ void add_f32x4(const f32x4* a, const f32x4* b, f32x4* out, int64_t n4) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (int64_t)gridDim.x * blockDim.x)
+    out[i] = a[i] + b[i];
+}
+
 __global__ void fill_kernel(void* dst, int64_t n, double value, int d) {
   float f = (float)value;
   bf16_t h = f32_to_bf16(f);
@@ -504,8 +527,26 @@ int qutai_amd_cast(const void* src, void* dst, int64_t n, int src_dtype, int dst
   for (int d : {src_dtype, dst_dtype})
     if (!float_dtype(d) && d != I64) return QA_EINVAL;
   if (n == 0) return QA_OK;
-  hipLaunchKernelGGL(cast_kernel, dim3(grid_for(n)), dim3(THREADS), 0, (hipStream_t)stream, src, dst, n, src_dtype,
-                     dst_dtype);
+  hipStream_t s = (hipStream_t)stream;
+  int64_t head = 0;
+  const bool aligned = ((uintptr_t)src | (uintptr_t)dst) % 16 == 0;
+  if (aligned && src_dtype == F32 && dst_dtype == BF16) {
+    head = n / 8 * 8;
+    if (head)
+      hipLaunchKernelGGL(cast_f32_bf16x8, dim3(grid_for(head / 8)), dim3(THREADS), 0, s, (const f32x4*)src,
+                         (u32x4*)dst, head / 8);
+  } else if (aligned && src_dtype == BF16 && dst_dtype == F32) {
+    head = n / 8 * 8;
+    if (head)
+      hipLaunchKernelGGL(cast_bf16_f32x8, dim3(grid_for(head / 8)), dim3(THREADS), 0, s, (const u32x4*)src,
+                         (f32x4*)dst, head / 8);
+  }
+  if (head < n) {
+    const int64_t so = head * (src_dtype == BF16 ? 2 : src_dtype == F32 ? 4 : 8);
+    const int64_t d_o = head * (dst_dtype == BF16 ? 2 : dst_dtype == F32 ? 4 : 8);
+    hipLaunchKernelGGL(cast_kernel, dim3(grid_for(n - head)), dim3(THREADS), 0, s, (const char*)src + so,
+                       (char*)dst + d_o, n - head, src_dtype, dst_dtype);
+  }
   return (int)hipGetLastError();
 }
 
@@ -519,8 +560,18 @@ int qutai_amd_fill(void* dst, int64_t n, double value, int dtype, void* stream) 
 int qutai_amd_add(const void* left, const void* right, void* out, int64_t n, int dtype, void* stream) {
   if (n < 0 || !float_dtype(dtype)) return QA_EINVAL;
   if (n == 0) return QA_OK;
-  hipLaunchKernelGGL(add_kernel, dim3(grid_for(n)), dim3(THREADS), 0, (hipStream_t)stream, left, right, out, n,
-                     dtype);
+  int64_t head = 0;
+  if (dtype == F32 && ((uintptr_t)left | (uintptr_t)right | (uintptr_t)out) % 16 == 0) {
+    head = n / 4 * 4;
+    if (head)
+      hipLaunchKernelGGL(add_f32x4, dim3(grid_for(head / 4)), dim3(THREADS), 0, (hipStream_t)stream,
+                         (const f32x4*)left, (const f32x4*)right, (f32x4*)out, head / 4);
+  }
+  if (head < n) {
+    const int64_t off = head * (dtype == BF16 ? 2 : dtype == F32 ? 4 : 8);
+    hipLaunchKernelGGL(add_kernel, dim3(grid_for(n - head)), dim3(THREADS), 0, (hipStream_t)stream,
+                       (const char*)left + off, (const char*)right + off, (char*)out + off, n - head, dtype);
+  }
   return (int)hipGetLastError();
 }
 
