@@ -239,6 +239,15 @@ __global__ void silu_kernel(const T* x, const T* g, T* out, int64_t n, int backw
   }
 }
 
+// (x0, x1) at `at` rotated by the angle with sine s and cosine c, the
+// contractions spelled out so that every kernel rounds the same way
+template <class T>
+__device__ __forceinline__ void rotate_pair(const T* x, T* out, int64_t at, float s, float c) {
+  const float x0 = get<T>(x, at), x1 = get<T>(x, at + 1);
+  put<T>(out, at, fmaf(x0, c, -(x1 * s)));
+  put<T>(out, at + 1, fmaf(x0, s, x1 * c));
+}
+
 // rotary embedding of the pairs (2i, 2i+1) of [batch][time][heads][dim]:
 // angle (offset + t) * theta^(-d/dim), d = 2 (i mod dim/2); inverse rotates
 // back (lm.cu:55-59)
@@ -250,9 +259,25 @@ __global__ void rope_kernel(const T* x, T* out, int64_t pairs, int64_t time, int
     const float a = (float)(offset + t) * powf(theta, -(float)d / (float)dim) * (inverse ? -1.f : 1.f);
     float s, c;
     sincosf(a, &s, &c);
-    const float x0 = get<T>(x, at), x1 = get<T>(x, at + 1);
-    put<T>(out, at, x0 * c - x1 * s);
-    put<T>(out, at + 1, x0 * s + x1 * c);
+    rotate_pair<T>(x, out, at, s, c);
+  }
+}
+
+// The same rotation with the angle's sine and cosine computed once per
+// (position, pair) and applied to every head: one lane per (b t, pair),
+// looping over the heads (the angle does not depend on the head).
+template <class T>
+__global__ void rope_heads_kernel(const T* x, T* out, int64_t items, int64_t time, int64_t heads, int64_t dim,
+                                  float theta, int64_t offset, int inverse) {
+  const int64_t half = dim / 2;
+  GRID_STRIDE(i, items) {
+    const int64_t bt = i / half, p = i % half, d = 2 * p, t = bt % time;
+    const float a = (float)(offset + t) * powf(theta, -(float)d / (float)dim) * (inverse ? -1.f : 1.f);
+    float s, c;
+    sincosf(a, &s, &c);
+    for (int64_t h = 0; h < heads; h++) {
+      rotate_pair<T>(x, out, (bt * heads + h) * dim + d, s, c);
+    }
   }
 }
 
@@ -608,6 +633,16 @@ int qutai_amd_rope(const void* x, void* out, int64_t batch, int64_t time, int64_
   const int64_t pairs = batch * time * heads * dim / 2;
   if (pairs == 0) return QA_OK;
   hipStream_t s = (hipStream_t)stream;
+  if (heads > 1) {  // one angle per (position, pair), shared by the heads
+    const int64_t items = batch * time * dim / 2;
+    if (dtype == BF16)
+      hipLaunchKernelGGL(rope_heads_kernel<bf16_t>, dim3(blocks_for(items)), dim3(256), 0, s, (const bf16_t*)x,
+                         (bf16_t*)out, items, time, heads, dim, (float)theta, offset, inverse ? 1 : 0);
+    else
+      hipLaunchKernelGGL(rope_heads_kernel<float>, dim3(blocks_for(items)), dim3(256), 0, s, (const float*)x,
+                         (float*)out, items, time, heads, dim, (float)theta, offset, inverse ? 1 : 0);
+    return (int)hipGetLastError();
+  }
   if (dtype == BF16)
     hipLaunchKernelGGL(rope_kernel<bf16_t>, dim3(blocks_for(pairs)), dim3(256), 0, s, (const bf16_t*)x, (bf16_t*)out,
                        pairs, time, heads, dim, (float)theta, offset, inverse ? 1 : 0);

@@ -102,6 +102,15 @@ def test_rope_forward_inverse_and_offset(lm, dtype):
     assert ora.rel_frobenius(download(y), ref) <= tol
     back = lm.rope(y, batch, time, heads, dim, theta, offset=7, inverse=True)
     assert ora.rel_frobenius(download(back), stored(x, dtype)) <= (1e-5 if dtype == "float32" else 2e-2)
+    # the kernel that shares one angle per (position, pair) over the heads
+    # gives each head exactly what the one-head kernel gives it
+    got = np.frombuffer(y.to_array(), dtype=np.uint16 if dtype == "bfloat16" else np.float32)
+    got = got.reshape(batch, time, heads, dim)
+    for h in range(heads):
+        single = lm.rope(upload(x.reshape(batch, time, heads, dim)[:, :, h].copy(), dtype), batch, time, 1, dim, theta,
+                         offset=7)
+        want = np.frombuffer(single.to_array(), dtype=got.dtype).reshape(batch, time, dim)
+        assert np.array_equal(got[:, :, h], want)
 
 
 @pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
