@@ -38,7 +38,6 @@ namespace {
 constexpr int D = 64;          // head dimension
 constexpr int KB = 64;         // keys per block
 constexpr int TILE = KB * D;     // elements of one K (or V) stage
-constexpr uint32_t OOB = 0x80000000u;
 
 struct AttnArgs {
   const bf16_t* q;

@@ -24,11 +24,6 @@ __device__ __forceinline__ float wave_sum(float x) {
   for (int o = 32; o; o >>= 1) x += __shfl_xor(x, o);
   return x;
 }
-__device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-  for (int o = 32; o; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
-  return x;
-}
 
 constexpr int ROWS_PER_BLOCK = 4;  // one wave per row, 4 waves per workgroup
 

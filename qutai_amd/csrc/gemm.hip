@@ -278,8 +278,6 @@ int vec_out(const void* p, int64_t ldc, int64_t stride) {
   return (ldc % 4 == 0 && stride % 4 == 0) ? 1 : 0;
 }
 
-int esize_of(int dtype) { return dtype == QA_BF16 ? 2 : dtype == QA_F64 ? 8 : 4; }
-
 }  // namespace
 
 extern "C" {
