@@ -335,12 +335,13 @@ int qutai_amd_embedding(const float* weight, const int64_t* ids, void* out, int6
                         int out_dtype, void* stream);
 
 /* out[tokens[g]] = sum of gradient rows rows[offsets[g] .. offsets[g+1]) (input
- * order) for each of `groups` distinct tokens; other rows of out untouched.
- * Replaces `cuda_lm.embedding_backward` / `lm_embedding_backward`
- * (cuda_lm.py:96-123, cuda/lm.cu:32-38). */
+ * order) for each of `groups` distinct tokens, added to the old row when
+ * `accumulate` (a tied table's gradient that already holds the head's part);
+ * other rows of out untouched.  Replaces `cuda_lm.embedding_backward` /
+ * `lm_embedding_backward` (cuda_lm.py:96-123, cuda/lm.cu:32-38). */
 int qutai_amd_embedding_backward(const void* gradient, const int64_t* tokens, const int64_t* offsets,
                                  const int64_t* rows, float* out, int64_t groups, int64_t width, int dtype,
-                                 void* stream);
+                                 int accumulate, void* stream);
 
 /* inverse[r] = 1/sqrt(mean(x[r]^2) + eps), out = x * inverse * weight.
  * Replaces `cuda_lm.rms_norm` / `lm_rms` (cuda_lm.py:126-145, cuda/lm.cu:39-45). */

@@ -19,6 +19,7 @@ from random import Random
 from . import amd
 from .amd import AMDStorage, code
 from .amd_runtime import get_runtime
+from ..core.grad import DeferredGradient
 
 
 def normal(size, mean=0.0, std=1.0, *, seed=None, dtype="float32"):
@@ -471,16 +472,43 @@ def embedding_backward_index(ids):
                  for values in (array("q", tokens), offsets, array("q", order)))
 
 
-def embedding_backward(gradient, ids, count, width, *, index=None):
+def embedding_backward(gradient, ids, count, width, *, index=None, out=None):
     """Table gradient [count][width] (fp32): each token's gradient rows summed
     in input order (cuda_lm.py:96-123).  ``index`` is
-    ``embedding_backward_index(ids)`` when the caller made it earlier."""
-    result = amd.full(count * width, 0.0, dtype=_acc_dtype(gradient.dtype))
+    ``embedding_backward_index(ids)`` when the caller made it earlier; with
+    ``out`` (an fp32 [count][width] storage) the row sums are added into it in
+    place and it is returned."""
+    if out is None:
+        result = amd.full(count * width, 0.0, dtype=_acc_dtype(gradient.dtype))
+    elif out.dtype != "float32" or out.size != count * width:
+        raise ValueError("embedding_backward accumulates into an fp32 [count][width] storage")
+    else:
+        result = out
     if len(ids) and width:
         tokens, offsets, positions = embedding_backward_index(ids) if index is None else index
         result.runtime.call("qutai_amd_embedding_backward", gradient.ptr, tokens.ptr, offsets.ptr, positions.ptr,
-                            result.ptr, tokens.size, width, code(gradient.dtype))
+                            result.ptr, tokens.size, width, code(gradient.dtype), int(out is not None))
     return result
+
+
+class EmbeddingRowSums(DeferredGradient):
+    """The table gradient of an embedding lookup as a deferred contribution:
+    dense on demand, or its rows added in place into a gradient the backward
+    pass has just made (a tied embedding/head table), which skips filling a
+    [count][width] zero buffer and adding two whole tables."""
+
+    device = "amd"
+    dtype = "float32"
+
+    def __init__(self, gradient, ids, count, width, index):
+        self.gradient, self.ids, self.count, self.width, self.index = gradient, ids, count, width, index
+        self.size = count * width
+
+    def materialize(self):
+        return embedding_backward(self.gradient, self.ids, self.count, self.width, index=self.index)
+
+    def add_into(self, storage):
+        embedding_backward(self.gradient, self.ids, self.count, self.width, index=self.index, out=storage)
 
 
 def rms_norm(values, weight, width, eps):

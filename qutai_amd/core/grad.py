@@ -32,6 +32,24 @@ def take_owned(storage):
     return False
 
 
+class DeferredGradient:
+    """A gradient contribution a rule describes instead of materialising:
+    ``materialize()`` gives the dense storage, and ``add_into(storage)``
+    adds it in place into a gradient that this backward pass created (the
+    embedding table's row sums: a few rows of a [vocab][width] gradient).
+    Has ``device``, ``dtype`` and ``size`` like a storage."""
+
+    def materialize(self):
+        raise NotImplementedError
+
+    def add_into(self, storage):
+        raise NotImplementedError
+
+
+def _dense(contribution):
+    return contribution.materialize() if isinstance(contribution, DeferredGradient) else contribution
+
+
 def _topological_order(output):
     order, seen, pending = [], set(), [(output, False)]
     while pending:
@@ -62,7 +80,7 @@ def backward(output, gradient, *, retain_graph=True, leaf_sink=None):
         rule = tensor.backward_rule
         if rule is None:
             if leaf_sink is None:
-                leaves[tensor] = incoming
+                leaves[tensor] = _dense(incoming)
             else:
                 leaf_sink(tensor, incoming)
             continue
@@ -75,7 +93,8 @@ def backward(output, gradient, *, retain_graph=True, leaf_sink=None):
                 if leaf_sink is not None and parent.backward_rule is None:
                     leaf_sink(parent, contribution)
                 elif parent in gradients:
+                    contribution = _dense(contribution)
                     gradients[parent] = get_backend(contribution.device).add(gradients[parent], contribution)
                 else:
-                    gradients[parent] = contribution
+                    gradients[parent] = _dense(contribution)
     return leaves

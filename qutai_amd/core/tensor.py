@@ -136,7 +136,14 @@ class Tensor:
                 raise ValueError("output gradient shape differs from the Tensor's")
             seed = gradient.storage
 
+        created = set()  # leaves whose grad storage this pass made: no one else holds it
+
         def accumulate(tensor, values):
+            if isinstance(values, autograd.DeferredGradient):
+                if tensor.grad is not None and id(tensor) in created and values.dtype == tensor.dtype:
+                    values.add_into(tensor.grad.storage)
+                    return
+                values = autograd.owned(values.materialize())
             fresh = False
             if values.dtype != tensor.dtype:
                 values, fresh = transfer(values, tensor.device, tensor.dtype), True
@@ -145,6 +152,7 @@ class Tensor:
             elif not (fresh or autograd.take_owned(values)):
                 values = values.copy()
             tensor.grad = Tensor(values, shape=tensor.shape)
+            created.add(id(tensor))
 
         autograd.backward(self, seed, retain_graph=retain_graph, leaf_sink=accumulate)
 

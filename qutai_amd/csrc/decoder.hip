@@ -41,15 +41,17 @@ __global__ void embedding_kernel(const float* w, const int64_t* ids, T* out, int
 }
 
 // out[tokens[g]][f] = sum over the rows of group g (input order) of grad[row][f]
-// (lm.cu:32-38); rows of tokens that do not occur are not touched.
+// (lm.cu:32-38), added to the old value when accumulating; rows of tokens
+// that do not occur are not touched.
 template <class T>
 __global__ void embedding_grad_kernel(const T* g, const int64_t* tokens, const int64_t* offsets,
-                                      const int64_t* rows, float* out, int64_t n, int64_t width) {
+                                      const int64_t* rows, float* out, int64_t n, int64_t width, int accumulate) {
   GRID_STRIDE(i, n) {
     const int64_t group = i / width, f = i % width;
     float total = 0.f;
     for (int64_t p = offsets[group]; p < offsets[group + 1]; p++) total += get<T>(g, rows[p] * width + f);
-    out[tokens[group] * width + f] = total;
+    float* at = out + tokens[group] * width + f;
+    *at = accumulate ? *at + total : total;
   }
 }
 
@@ -515,17 +517,17 @@ int qutai_amd_embedding(const float* weight, const int64_t* ids, void* out, int6
 
 int qutai_amd_embedding_backward(const void* gradient, const int64_t* tokens, const int64_t* offsets,
                                  const int64_t* rows, float* out, int64_t groups, int64_t width, int dtype,
-                                 void* stream) {
+                                 int accumulate, void* stream) {
   if (groups < 0 || width < 0 || !act_dtype(dtype)) return QA_EINVAL;
   const int64_t n = groups * width;
   if (n == 0) return QA_OK;
   hipStream_t s = (hipStream_t)stream;
   if (dtype == BF16)
     hipLaunchKernelGGL(embedding_grad_kernel<bf16_t>, dim3(blocks_for(n)), dim3(256), 0, s, (const bf16_t*)gradient,
-                       tokens, offsets, rows, out, n, width);
+                       tokens, offsets, rows, out, n, width, accumulate ? 1 : 0);
   else
     hipLaunchKernelGGL(embedding_grad_kernel<float>, dim3(blocks_for(n)), dim3(256), 0, s, (const float*)gradient,
-                       tokens, offsets, rows, out, n, width);
+                       tokens, offsets, rows, out, n, width, accumulate ? 1 : 0);
   return (int)hipGetLastError();
 }
 

@@ -114,7 +114,7 @@ def embed(ids, weight, shape):
         # backward launches without a host transfer (which would wait for
         # every kernel queued before it)
         index = b.embedding_backward_index(ids)
-        result.backward_rule = lambda g: (owned(b.embedding_backward(g, ids, weight.shape[0], width, index=index)),)
+        result.backward_rule = lambda g: (b.EmbeddingRowSums(g, ids, weight.shape[0], width, index),)
     return result
 
 

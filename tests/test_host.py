@@ -222,3 +222,36 @@ def test_owned_gradient_marks_are_taken_once():
     assert owned(box) is box
     assert take_owned(box)
     assert not take_owned(box)
+
+
+def test_deferred_gradient_adds_in_place_only_into_this_pass_grad(fake_device):
+    """A DeferredGradient (the embedding table's row sums) is added in place
+    into a leaf gradient created by the same backward pass, and materialised
+    otherwise, so a grad kept from an earlier pass is never written
+    (core/grad.py, core/tensor.py)."""
+    from qutai_amd import Tensor
+    from qutai_amd.core.grad import DeferredGradient, owned, record
+
+    class Rows(DeferredGradient):
+        device, dtype, size = "fake", "float32", 3
+        added_in_place = 0
+
+        def materialize(self):
+            return FakeBackend.Store(np.array([0.0, 5.0, 0.0]), "float32")
+
+        def add_into(self, storage):
+            Rows.added_in_place += 1
+            storage.values[1] += 5.0
+
+    w = Tensor(FakeBackend.Store(np.zeros(3), "float32"), shape=(3,), requires_grad=True)
+    y = record(Tensor(FakeBackend.Store(np.zeros(1), "float32"), shape=()), (w, w),
+               lambda g: (owned(FakeBackend.Store(np.array([1.0, 1.0, 1.0]), "float32")), Rows()))
+    y.backward()
+    assert w.grad.storage.values.tolist() == [1.0, 6.0, 1.0] and Rows.added_in_place == 1
+    kept = w.grad.storage
+    # a second pass: the deferred part meets the grad of the first pass and is materialised
+    y2 = record(Tensor(FakeBackend.Store(np.zeros(1), "float32"), shape=()), (w,), lambda g: (Rows(),))
+    y2.backward()
+    assert Rows.added_in_place == 1
+    assert kept.values.tolist() == [1.0, 6.0, 1.0]
+    assert w.grad.storage.values.tolist() == [1.0, 11.0, 1.0]
