@@ -232,10 +232,11 @@ int qutai_amd_route_gather(const void* x, const int64_t* order, void* out, int64
  * Replaces `lm_pointer_table` + `lm_combine_all`
  * (src/qutai/backends/cuda/lm.cu:400-416, src/qutai/backends/cuda_lm.py:505-541).
  * weights may be NULL: unit weights, i.e. the sum over a token's slots (the
- * backward of the one-launch gather). */
+ * backward of the one-launch gather).  out_dtype is dtype, or QA_BF16 for
+ * fp32 expert rows (the token gradient rounded once from the fp32 sum). */
 int qutai_amd_combine(const void* expert_out, const float* weights, const int64_t* indices,
                       const int64_t* locations, const int64_t* offsets, void* y, int64_t rows, int64_t width,
-                      int64_t top_k, int dtype, void* stream);
+                      int64_t top_k, int dtype, int out_dtype, void* stream);
 
 /* Attention forward, fp32 math:
  *   out = softmax(scale * Q K^T [+ causal mask]) V  per (batch, head),

@@ -144,7 +144,7 @@ def combine_all(expert_rows, route, width):
     if result.size:
         result.runtime.call("qutai_amd_combine", expert_rows.ptr, route["weights"].ptr, route["indices"].ptr,
                             route["locations"].ptr, route["offsets"].ptr, result.ptr, route["rows"], width,
-                            route["top_k"], code(expert_rows.dtype))
+                            route["top_k"], code(expert_rows.dtype), code(expert_rows.dtype))
     return result
 
 
@@ -317,13 +317,16 @@ def combine_backward(gradient, outputs, weights, route, width):
     return (*grads, d_weights)
 
 
-def route_gather_backward_all(d_rows, route, width):
+def route_gather_backward_all(d_rows, route, width, *, out_dtype=None):
     """Token-row gradient of route_gather_all: the sum over each token's
-    slots of its expert-major rows (fp32 sum, one rounding)."""
-    out = AMDStorage(route["rows"] * width, d_rows.dtype)
+    slots of its expert-major rows (fp32 sum, one rounding to out_dtype:
+    the rows' dtype, or bf16 from fp32 rows)."""
+    out_dtype = d_rows.dtype if out_dtype is None else out_dtype
+    out = AMDStorage(route["rows"] * width, out_dtype)
     if out.size:
         out.runtime.call("qutai_amd_combine", d_rows.ptr, None, route["indices"].ptr, route["locations"].ptr,
-                         route["offsets"].ptr, out.ptr, route["rows"], width, route["top_k"], code(d_rows.dtype))
+                         route["offsets"].ptr, out.ptr, route["rows"], width, route["top_k"], code(d_rows.dtype),
+                         code(out_dtype))
     return out
 
 
@@ -367,7 +370,10 @@ def moe_experts_backward(gradient, route, saved, width, hidden, *, x_dtype, weig
         d_rows = repitch(d_rows, 1, capacity, wp, capacity, width)
         dw_gate, dw_up = (repitch(w, experts, hp, wp, hidden, width) for w in (dw_gate, dw_up))
         dw_down = repitch(dw_down, experts, wp, hp, width, hidden)
-    dx = _as_dtype(route_gather_backward_all(d_rows, route, width), x_dtype)
+    if x_dtype == "bfloat16":  # fp32 slot sums rounded once, straight to bf16
+        dx = route_gather_backward_all(d_rows, route, width, out_dtype="bfloat16")
+    else:
+        dx = _as_dtype(route_gather_backward_all(d_rows, route, width), x_dtype)
     return dx, d_weights, dw_gate, dw_up, dw_down
 
 

@@ -57,7 +57,7 @@ SIGNATURES = {
     "qutai_amd_silu_mul_backward": [_p, _p, _p, _p, _p, _i64, _i32, _p],
     "qutai_amd_route": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p],
     "qutai_amd_route_gather": [_p, _p, _p, _i64, _i64, _i32, _i32, _p],
-    "qutai_amd_combine": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p],
+    "qutai_amd_combine": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _p],
     "qutai_amd_gemm_grouped_k": [_p, _p, _p, _p, _i32, _i64, _i64, _i64, _i32, _i32, _i32, _p],
     "qutai_amd_combine_backward": [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p],
     "qutai_amd_route_backward": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p],

@@ -151,10 +151,11 @@ __global__ void gather_rows(const T* x, const int64_t* order, T* out, int64_t co
   }
 }
 
-// y[row] = sum over slots of w * expert row, fp32 sum in slot order.
-template <class T, int V>  // V values per thread
+// y[row] = sum over slots of w * expert row, fp32 sum in slot order, one
+// rounding to the output type U.
+template <class T, int V, class U = T>  // V values per thread
 __global__ void combine_kernel(const T* eo, const float* w, const int64_t* idx, const int64_t* loc,
-                               const int64_t* off, T* y, int64_t rows, int64_t width, int64_t top_k) {
+                               const int64_t* off, U* y, int64_t rows, int64_t width, int64_t top_k) {
   int64_t per_row = width / V;
   int64_t total = rows * per_row;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
@@ -176,7 +177,7 @@ __global__ void combine_kernel(const T* eo, const float* w, const int64_t* idx, 
     }
 #pragma unroll
     for (int v = 0; v < V; v++) {
-      if constexpr (sizeof(T) == 2) y[row * width + j + v] = f32_to_bf16(acc[v]);
+      if constexpr (sizeof(U) == 2) y[row * width + j + v] = f32_to_bf16(acc[v]);
       else y[row * width + j + v] = acc[v];
     }
   }
@@ -296,11 +297,23 @@ int qutai_amd_route_gather(const void* x, const int64_t* order, void* out, int64
 
 int qutai_amd_combine(const void* expert_out, const float* weights, const int64_t* indices,
                       const int64_t* locations, const int64_t* offsets, void* y, int64_t rows, int64_t width,
-                      int64_t top_k, int dtype, void* stream) {
+                      int64_t top_k, int dtype, int out_dtype, void* stream) {
   if (rows < 0 || width < 0 || top_k <= 0) return QA_EINVAL;
   if (dtype != F32 && dtype != BF16) return QA_EINVAL;
+  if (out_dtype != dtype && !(dtype == F32 && out_dtype == BF16)) return QA_EINVAL;
   if (rows * width == 0) return QA_OK;
   hipStream_t s = (hipStream_t)stream;
+  if (dtype == F32 && out_dtype == BF16) {  // fp32 rows summed straight into bf16 token rows
+    if (width % 4 == 0)
+      hipLaunchKernelGGL((combine_kernel<float, 4, bf16_t>), dim3(blocks_for(rows * width / 4)), dim3(256), 0, s,
+                         (const float*)expert_out, weights, indices, locations, offsets, (bf16_t*)y, rows, width,
+                         top_k);
+    else
+      hipLaunchKernelGGL((combine_kernel<float, 1, bf16_t>), dim3(blocks_for(rows * width)), dim3(256), 0, s,
+                         (const float*)expert_out, weights, indices, locations, offsets, (bf16_t*)y, rows, width,
+                         top_k);
+    return (int)hipGetLastError();
+  }
   if (dtype == BF16) {
     if (width % 8 == 0)
       hipLaunchKernelGGL((combine_kernel<bf16_t, 8>), dim3(blocks_for(rows * width / 8)), dim3(256), 0, s,

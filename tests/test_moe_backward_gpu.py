@@ -167,3 +167,18 @@ def test_sparse_moe_layer_forward_and_all_gradients(lm):
     assert ora.rel_frobenius(f64(layer.w_up.grad, wu.shape), rdwu) <= tol
     assert ora.rel_frobenius(f64(layer.w_down.grad, wd.shape), rdwd) <= tol
     assert sum(layer.last_counts) == tokens * top_k
+
+
+def test_gather_backward_rounds_fp32_slot_sums_once_to_bf16(lm):
+    """The token gradient of the gather: fp32 expert rows summed over each
+    token's slots straight into bf16 equals the fp32 sum rounded afterwards
+    (one rounding either way), bit for bit; ragged width too."""
+    from qutai_amd.backends import amd
+
+    for rows, width in ((700, 256), (97, 12)):
+        route = lm.routing(upload(normal(rows, rows * 8), "float32"), rows, 8, 2)
+        d_rows = upload(normal(rows + 1, route["capacity"] * width), "float32")
+        wide = lm.route_gather_backward_all(d_rows, route, width)
+        narrow = lm.route_gather_backward_all(d_rows, route, width, out_dtype="bfloat16")
+        assert narrow.dtype == "bfloat16"
+        assert narrow.to_array() == amd.from_storage(wide, dtype="bfloat16").to_array()
