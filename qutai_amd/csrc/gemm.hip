@@ -110,7 +110,10 @@ __global__ void splitk_reduce(const float* part, void* out, int64_t n, int64_t t
 //   N   : 256x64, 4 waves (N <= 64), W : 64x256, 4 waves (M <= 64)
 //   H   : 256x128, 8 waves 4x2 (64x64 per wave), BK 64, three-stage ring
 //         (grids of 256x256 tiles that would leave half the CUs idle)
-enum Tile { TILE_L8D2, TILE_L8R, TILE_L4D2, TILE_S, TILE_N, TILE_W, TILE_H, TILE_COUNT };
+//   T, U: 192x256 (8 waves 2x4, 96x64 per wave) and 256x192 (4x2, 64x96),
+//         BK 64, two-stage ring, bf16 only (a grid of 256x256 tiles just
+//         short of the CU count, e.g. 5632 x 2048: 176 tiles -> 240)
+enum Tile { TILE_L8D2, TILE_L8R, TILE_L4D2, TILE_S, TILE_N, TILE_W, TILE_H, TILE_T, TILE_U, TILE_COUNT };
 
 template <bool F32, bool TA, bool TB, int BM, int BN, int WM, int WN, int BK, int ST, bool DMA, bool SWIGLU = false>
 hipError_t launch_cfg(GemmArgs p, hipStream_t stream) {
@@ -135,6 +138,12 @@ hipError_t launch_tile(Tile tile, GemmArgs p, hipStream_t stream) {
     case TILE_N: return launch_cfg<F32, TA, TB, 256, 64, 4, 1, KB, 4, true>(p, stream);
     case TILE_W: return launch_cfg<F32, TA, TB, 64, 256, 1, 4, KB, 4, true>(p, stream);
     case TILE_H: return launch_cfg<F32, TA, TB, 256, 128, 4, 2, KR, 3, true>(p, stream);
+    case TILE_T:
+      if constexpr (F32) return launch_cfg<F32, TA, TB, 256, 256, 2, 4, KR, 2, true>(p, stream);
+      else return launch_cfg<F32, TA, TB, 192, 256, 2, 4, KR, 2, true>(p, stream);
+    case TILE_U:
+      if constexpr (F32) return launch_cfg<F32, TA, TB, 256, 256, 2, 4, KR, 2, true>(p, stream);
+      else return launch_cfg<F32, TA, TB, 256, 192, 4, 2, KR, 2, true>(p, stream);
     default: return launch_cfg<F32, TA, TB, 256, 256, 2, 4, KR, 2, true>(p, stream);
   }
 }
@@ -161,11 +170,11 @@ int64_t cu_count() {
 // Tile choice for an M x N output (batch of them) over K; thin outputs use
 // the 256x64 / 64x256 shapes.  QUTAI_AMD_GEMM_TILE=<L8D2|L8R|L4D2|S|N|W|H>
 // overrides the choice (tuning).
-Tile choose_tile(int64_t M, int64_t N, int64_t K, int64_t batch) {
+Tile choose_tile(int64_t M, int64_t N, int64_t K, int64_t batch, bool bf16) {
   static int forced = [] {
     const char* v = getenv("QUTAI_AMD_GEMM_TILE");
     if (!v) return -1;
-    const char* names[TILE_COUNT] = {"L8D2", "L8R", "L4D2", "S", "N", "W", "H"};
+    const char* names[TILE_COUNT] = {"L8D2", "L8R", "L4D2", "S", "N", "W", "H", "T", "U"};
     for (int i = 0; i < TILE_COUNT; i++)
       if (std::string(v) == names[i]) return i;
     return -1;
@@ -174,22 +183,28 @@ Tile choose_tile(int64_t M, int64_t N, int64_t K, int64_t batch) {
   if (N <= 64) return TILE_N;
   if (M <= 64) return TILE_W;
   if (K <= 128) return TILE_S;
-  // Wave-quantisation cost of the three large tiles, in units of one full
-  // round of 256x256 tiles over the CUs (per unit of K).  Measured on this
-  // GPU (bf16, 4096^3 and eight decoder / ragged shapes): a full round of
-  // 256x128 tiles (one per CU) costs 0.665, a full round of 128x128 tiles
-  // (two per CU) 0.70, and a partial round of at most one 128x128 tile per
-  // CU 0.5; a partial round of the others costs as much as a full one.  Ties
-  // (within 3%) go to 256x128, then 256x256.
+  // Wave-quantisation cost of the large tiles, in units of one full round of
+  // 256x256 tiles over the CUs (per unit of K).  Measured on this GPU (bf16,
+  // 4096^3 and the decoder / ragged shapes): a full round of 256x128 tiles
+  // (one per CU) costs 0.665, a full round of 128x128 tiles (two per CU)
+  // 0.70, and a partial round of at most one 128x128 tile per CU 0.5; a
+  // round of 192x256 / 256x192 tiles (bf16) 0.9; a partial round of the
+  // others costs as much as a full one.  Ties (within 3%) go to 256x128,
+  // then 256x192, 192x256, 256x256.
   const int64_t cus = cu_count();
+  auto rounds = [cus](int64_t tiles) { return (double)(tiles / cus + (tiles % cus ? 1 : 0)); };
   const int64_t mt = (M + 255) / 256, nt = (N + 255) / 256, ms = (M + 127) / 128, ns = (N + 127) / 128;
   const int64_t nl = mt * nt * batch, nh = mt * ns * batch, nsm = ms * ns * batch;
-  const double cost_l = (double)(nl / cus) + (nl % cus ? 1.0 : 0.0);
-  const double cost_h = 0.665 * (double)(nh / cus + (nh % cus ? 1 : 0));
+  const double cost_l = rounds(nl);
+  const double cost_h = 0.665 * rounds(nh);
   const int64_t rs = nsm % (2 * cus);
   const double cost_s = 0.70 * (double)(nsm / (2 * cus)) + (rs == 0 ? 0.0 : rs <= cus ? 0.5 : 0.70);
-  const double best = std::min(cost_l, std::min(cost_h, cost_s));
+  const double cost_t = bf16 ? 0.9 * rounds((M + 191) / 192 * nt * batch) : 1e30;
+  const double cost_u = bf16 ? 0.9 * rounds(mt * ((N + 191) / 192) * batch) : 1e30;
+  const double best = std::min({cost_l, cost_h, cost_s, cost_t, cost_u});
   if (cost_h <= best * 1.03) return TILE_H;
+  if (cost_u <= best * 1.03) return TILE_U;
+  if (cost_t <= best * 1.03) return TILE_T;
   if (cost_l <= best * 1.03) return TILE_L8D2;
   return TILE_S;
 }
@@ -208,6 +223,8 @@ int choose_split(int64_t rows, int64_t cols, int64_t inner, int64_t batch, Tile 
   int64_t bm = 256, bn = 256;
   if (tile == TILE_S) bm = bn = 128;
   else if (tile == TILE_H) bn = 128;
+  else if (tile == TILE_T) bm = 192;
+  else if (tile == TILE_U) bn = 192;
   else if (tile == TILE_N) bn = 64;
   else if (tile == TILE_W) bm = 64;
   const int64_t tiles = ((rows + bm - 1) / bm) * ((cols + bn - 1) / bn) * batch;
@@ -292,7 +309,7 @@ size_t qutai_amd_gemm_workspace_size(int64_t rows, int64_t inner, int64_t cols, 
   plan(rows, inner, cols, batch, left_stride, right_stride, transpose_left, transpose_right, a_dtype, b_dtype, bf16,
        (const void*)256, (const void*)256, &pa, &pb);
   int64_t chunk = 0;
-  const int splits = choose_split(rows, cols, inner, batch, choose_tile(rows, cols, inner, batch), &chunk);
+  const int splits = choose_split(rows, cols, inner, batch, choose_tile(rows, cols, inner, batch, bf16), &chunk);
   const size_t partial = splits > 1 ? split_bytes(rows, cols, batch, splits) : 0;
   if (!pa.copy && !pb.copy && !partial) return 0;
   return (pa.copy ? pa.bytes : 0) + (pb.copy ? pb.bytes : 0) + partial + 256;
@@ -326,7 +343,7 @@ int qutai_amd_gemm(const void* a, const void* b, void* out, int64_t rows, int64_
   Operand pa, pb;
   plan(rows, inner, cols, batch, left_stride, right_stride, transpose_left, transpose_right, a_dtype, b_dtype, bf16,
        a, b, &pa, &pb);
-  const Tile tile = choose_tile(rows, cols, inner, batch);
+  const Tile tile = choose_tile(rows, cols, inner, batch, bf16);
   int64_t chunk = 0;
   const int splits = inner > 0 ? choose_split(rows, cols, inner, batch, tile, &chunk) : 1;
   const size_t partial = splits > 1 ? split_bytes(rows, cols, batch, splits) : 0;
@@ -499,7 +516,7 @@ int qutai_amd_gemm_grouped_k(const void* a, const void* b, void* out, const int6
   p.alpha = 1.0f;
   int64_t es = dtype == QA_BF16 ? 2 : 4;
   if ((p.lda * 256 * es) >= (1ll << 31) || (p.ldb * 256 * es) >= (1ll << 31)) return QA_EINVAL;
-  Tile tile = choose_tile(rows, cols, total_k / groups + 1, groups);
+  Tile tile = choose_tile(rows, cols, total_k / groups + 1, groups, dtype == QA_BF16);
   hipError_t err = dtype == QA_F32 ? launch_mma<true>(tile, true, false, p, stream)
                                    : launch_mma<false>(tile, true, false, p, stream);
   return (int)err;

@@ -94,9 +94,13 @@ __device__ __forceinline__ int swz_k(int r) {
 // MN-major tile [BK][R] of bf16 read by ds_read_b64_tr_b16: 32 lanes read 4
 // consecutive k-rows x 64 bytes; shifting each of the 4 rows into its own
 // 64-byte quarter of a 256-byte bank window removes the 4-way conflict.
+// Rows of a multiple of 256 bytes (CR = 16, 32) all start in the same bank
+// and take four shifts; rows of 128 or 384 bytes (CR = 8, 24) already
+// alternate between the two halves of the window and take one shift per
+// row pair, which also keeps the XOR inside the 8-chunk groups of a row.
 template <int CR>
 __device__ __forceinline__ int swz_mn16(int k) {
-  return CR >= 16 ? (k & 3) * 4 : ((k >> 1) & 1) * 4;
+  return CR % 16 == 0 ? (k & 3) * 4 : ((k >> 1) & 1) * 4;
 }
 // MN-major tile of fp32 read with ds_read_b32: the two lane halves read
 // k-rows 8 apart; put them in different 128-byte bank halves.
@@ -613,9 +617,19 @@ struct GemmKernel {
           store_slab<1>(us, stage, ou, o.row0 + i * 32, lane, fast);
         }
       }
-    } else {
+    } else if constexpr ((FN & (FN - 1)) == 0) {
 #pragma unroll
       for (int i = 0; i < FM; i++) store_slab<FN>(acc[i], stage, o, o.row0 + i * 32, lane, fast);
+    } else {  // 96-wide wave tiles: one 32-column block at a time (whole rows per store)
+#pragma unroll
+      for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+          Out oj = o;
+          oj.col0 = o.col0 + 32 * j;
+          const f32x16 blk[1] = {acc[i][j]};
+          store_slab<1>(blk, stage, oj, o.row0 + i * 32, lane, fast);
+        }
     }
   }
 

@@ -1,0 +1,73 @@
+"""Every bf16 GEMM tile shape (256x256, 192x256, 256x192, 256x128, 128x128)
+sums K in the same order, in chunks of 64 through the same MFMA chain, so a
+tile forced with QUTAI_AMD_GEMM_TILE gives bit-identical output to any other
+for the same call: whole and ragged tiles, the four transpose forms, fp32 and
+bf16 output, accumulation and a strided batch.  The variable is read once per
+process, so each tile runs in a child process that writes its outputs to a
+file; the 256x256 outputs are also checked against the float64 oracle
+(bf16 storage within 1e-2 relative Frobenius error, the reference's bar)."""
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import reference as ora
+from tests.helpers import normal, stored
+
+pytestmark = pytest.mark.gpu
+
+ROOT = Path(__file__).resolve().parent.parent
+CASES = [(700, 320, 600, 1), (384, 256, 512, 1), (200, 130, 70, 3), (1024, 192, 768, 2)]
+
+CHILD = r"""
+import sys
+import numpy as np
+sys.path.insert(0, sys.argv[2])
+from qutai_amd.backends import amd
+from tests.helpers import download, normal, upload
+cases = eval(sys.argv[3])
+outs = {}
+for m, k, n, batch in cases:
+    a, b = normal(10 + m, batch * m * k), normal(20 + n, batch * k * n)
+    left, right = upload(a, "bfloat16"), upload(b, "bfloat16")
+    for ta in (False, True):
+        for tb in (False, True):
+            kw = dict(batch=batch, transpose_left=ta, transpose_right=tb)
+            for od in ("float32", "bfloat16"):
+                outs[f"{m}_{k}_{n}_{batch}_{ta:d}{tb:d}_{od}"] = download(amd.gemm(left, right, m, k, n, out_dtype=od, **kw))
+            acc = upload(normal(30 + m, batch * m * n), "bfloat16")
+            amd.gemm(left, right, m, k, n, out=acc, out_dtype="bfloat16", accumulate=True, **kw)
+            outs[f"{m}_{k}_{n}_{batch}_{ta:d}{tb:d}_acc"] = download(acc)
+np.savez(sys.argv[1], **outs)
+print("done", len(outs))
+"""
+
+
+def _run(tile, path):
+    env = dict(os.environ, QUTAI_AMD_GEMM_TILE=tile, QUTAI_AMD_SPLITK="1")
+    print(f"tile {tile}", flush=True)
+    out = subprocess.run([sys.executable, "-c", CHILD, str(path), str(ROOT), repr(CASES)], env=env,
+                         capture_output=True, text=True, timeout=110)
+    assert out.returncode == 0 and "done" in out.stdout, out.stderr[-2000:]
+    return np.load(path)
+
+
+def test_forced_tiles_are_bit_identical(tmp_path):
+    base = _run("L8D2", tmp_path / "L8D2.npz")
+    for m, k, n, batch in CASES:
+        a, b = normal(10 + m, batch * m * k), normal(20 + n, batch * k * n)
+        sa, sb = stored(a, "bfloat16"), stored(b, "bfloat16")
+        for ta in (False, True):
+            for tb in (False, True):
+                exact = np.concatenate([ora.gemm_f64(sa[i * m * k:(i + 1) * m * k], sb[i * k * n:(i + 1) * k * n],
+                                                     m, k, n, transpose_left=ta, transpose_right=tb).ravel()
+                                        for i in range(batch)])
+                got = base[f"{m}_{k}_{n}_{batch}_{ta:d}{tb:d}_float32"]
+                assert ora.rel_frobenius(got, exact) <= 1e-2, (m, k, n, batch, ta, tb)
+    for tile in ("T", "U", "H", "S"):
+        other = _run(tile, tmp_path / f"{tile}.npz")
+        for key in base.files:
+            assert np.array_equal(base[key], other[key]), (tile, key)
