@@ -170,7 +170,7 @@ int64_t cu_count() {
 // Tile choice for an M x N output (batch of them) over K; thin outputs use
 // the 256x64 / 64x256 shapes.  QUTAI_AMD_GEMM_TILE=<L8D2|L8R|L4D2|S|N|W|H>
 // overrides the choice (tuning).
-Tile choose_tile(int64_t M, int64_t N, int64_t K, int64_t batch, bool bf16) {
+int forced_tile() {
   static int forced = [] {
     const char* v = getenv("QUTAI_AMD_GEMM_TILE");
     if (!v) return -1;
@@ -179,7 +179,11 @@ Tile choose_tile(int64_t M, int64_t N, int64_t K, int64_t batch, bool bf16) {
       if (std::string(v) == names[i]) return i;
     return -1;
   }();
-  if (forced >= 0) return (Tile)forced;
+  return forced;
+}
+
+Tile choose_tile(int64_t M, int64_t N, int64_t K, int64_t batch, bool bf16) {
+  if (forced_tile() >= 0) return (Tile)forced_tile();
   if (N <= 64) return TILE_N;
   if (M <= 64) return TILE_W;
   if (K <= 128) return TILE_S;
@@ -219,7 +223,7 @@ size_t split_bytes(int64_t rows, int64_t cols, int64_t batch, int splits) {
   return ((size_t)splits * batch * rows * cols * 4 + 255) / 256 * 256;
 }
 
-int choose_split(int64_t rows, int64_t cols, int64_t inner, int64_t batch, Tile tile, int64_t* chunk) {
+int64_t tile_count(Tile tile, int64_t rows, int64_t cols, int64_t batch) {
   int64_t bm = 256, bn = 256;
   if (tile == TILE_S) bm = bn = 128;
   else if (tile == TILE_H) bn = 128;
@@ -227,12 +231,54 @@ int choose_split(int64_t rows, int64_t cols, int64_t inner, int64_t batch, Tile 
   else if (tile == TILE_U) bn = 192;
   else if (tile == TILE_N) bn = 64;
   else if (tile == TILE_W) bm = 64;
-  const int64_t tiles = ((rows + bm - 1) / bm) * ((cols + bn - 1) / bn) * batch;
-  const int64_t slots = (tile == TILE_S ? 2 : 1) * cu_count();
+  return ((rows + bm - 1) / bm) * ((cols + bn - 1) / bn) * batch;
+}
+
+// A plain product whose tiles fill at most a quarter of the tile slots over
+// K >= 4096 splits K.  For bf16 the tile and the split count are then chosen
+// together: each candidate (256x256, 256x128, 128x128) takes the most chunks
+// that fit its slots, at most 8 and at least 1024 of K each, and is priced as
+// its rounds of tiles over the chunk (the wave-quantisation costs of
+// choose_tile, a full 256x256 round being 113 us per 4096 of K on this GPU)
+// plus the partial sums' HBM traffic (s writes, s reads and one output write
+// of rows x cols fp32 at 5 TB/s).  Measured: the decoder head's dX (1024 x
+// 2048 outputs, K = 32768) takes 256x256 in 8 chunks, 158 -> 137 us; the
+// K/V projections' weight gradients (512 x 2048, K = 4096) take 128x128 in
+// 4 chunks, 28 -> 24 us.  The tile may change; a forced tile does not.
+int choose_split(int64_t rows, int64_t cols, int64_t inner, int64_t batch, Tile* tile, bool bf16, int64_t* chunk) {
+  const int64_t cus = cu_count();
+  const int64_t tiles = tile_count(*tile, rows, cols, batch);
+  const int64_t slots = (*tile == TILE_S ? 2 : 1) * cus;
   int64_t s = 1;
   const char* forced = getenv("QUTAI_AMD_SPLITK");
-  if (forced && atoi(forced) > 0) s = atoi(forced);
-  else if (batch == 1 && tiles * 4 <= slots && inner >= 4096) s = std::min<int64_t>(8, slots / tiles);
+  if (forced && atoi(forced) > 0) {
+    s = atoi(forced);
+  } else if (batch == 1 && tiles * 4 <= slots && inner >= 4096) {
+    s = std::min<int64_t>(8, slots / tiles);
+    if (bf16 && forced_tile() < 0) {
+      double best = 1e30;
+      for (Tile t : {TILE_L8D2, TILE_H, TILE_S}) {
+        const int64_t n = tile_count(t, rows, cols, 1), per = (t == TILE_S ? 2 : 1) * cus;
+        const int64_t st = std::max<int64_t>(1, std::min<int64_t>({8, per / n, inner / 1024}));
+        const int64_t units = n * st, r = (units + cus - 1) / cus;
+        double rounds;
+        if (t == TILE_L8D2) rounds = (double)r;
+        else if (t == TILE_H) rounds = 0.665 * (double)r;
+        else {
+          const int64_t rs = units % (2 * cus);
+          rounds = 0.70 * (double)(units / (2 * cus)) + (rs == 0 ? 0.0 : rs <= cus ? 0.5 : 0.70);
+        }
+        const double k_chunk = (double)((inner + st - 1) / st);
+        const double reduce_us = st > 1 ? (2.0 * st + 1) * rows * cols * 4 / 5.0e6 : 0.0;
+        const double cost = rounds * k_chunk * (113.0 / 4096) + reduce_us;
+        if (cost < best) {
+          best = cost;
+          *tile = t;
+          s = st;
+        }
+      }
+    }
+  }
   if (s <= 1 || inner < 128) return 1;
   const int64_t c = ((inner + s - 1) / s + 63) / 64 * 64;
   s = (inner + c - 1) / c;
@@ -309,7 +355,8 @@ size_t qutai_amd_gemm_workspace_size(int64_t rows, int64_t inner, int64_t cols, 
   plan(rows, inner, cols, batch, left_stride, right_stride, transpose_left, transpose_right, a_dtype, b_dtype, bf16,
        (const void*)256, (const void*)256, &pa, &pb);
   int64_t chunk = 0;
-  const int splits = choose_split(rows, cols, inner, batch, choose_tile(rows, cols, inner, batch, bf16), &chunk);
+  Tile tile = choose_tile(rows, cols, inner, batch, bf16);
+  const int splits = choose_split(rows, cols, inner, batch, &tile, bf16, &chunk);
   const size_t partial = splits > 1 ? split_bytes(rows, cols, batch, splits) : 0;
   if (!pa.copy && !pb.copy && !partial) return 0;
   return (pa.copy ? pa.bytes : 0) + (pb.copy ? pb.bytes : 0) + partial + 256;
@@ -343,9 +390,9 @@ int qutai_amd_gemm(const void* a, const void* b, void* out, int64_t rows, int64_
   Operand pa, pb;
   plan(rows, inner, cols, batch, left_stride, right_stride, transpose_left, transpose_right, a_dtype, b_dtype, bf16,
        a, b, &pa, &pb);
-  const Tile tile = choose_tile(rows, cols, inner, batch, bf16);
+  Tile tile = choose_tile(rows, cols, inner, batch, bf16);
   int64_t chunk = 0;
-  const int splits = inner > 0 ? choose_split(rows, cols, inner, batch, tile, &chunk) : 1;
+  const int splits = inner > 0 ? choose_split(rows, cols, inner, batch, &tile, bf16, &chunk) : 1;
   const size_t partial = splits > 1 ? split_bytes(rows, cols, batch, splits) : 0;
   float* part = nullptr;
   if (inner > 0 && (pa.copy || pb.copy || partial)) {

@@ -57,9 +57,13 @@ def test_bindings_apply_without_a_device():
     # autocast of two fp32 operands: both copied
     assert size(64, 64, 64, 1, 0, 0, 0, 0, 0, 0, 1) == 2 * 64 * 64 * 2 + 256
     # split-K: 1024 x 2048 outputs over K = 32768 fill a quarter of the
-    # 128x128-tile slots of 256 CUs (the count used without a device): four
-    # K chunks of 8192, four fp32 partial products
-    assert size(1024, 32768, 2048, 1, 0, 0, 0, 0, 5, 5, 0) == 4 * 1024 * 2048 * 4 + 256
+    # 128x128-tile slots of 256 CUs (the count used without a device); bf16
+    # then picks 256x256 tiles in eight K chunks of 4096 (32 tiles x 8 = one
+    # round): eight fp32 partial products; fp32 keeps 128x128 in four chunks
+    assert size(1024, 32768, 2048, 1, 0, 0, 0, 0, 5, 5, 0) == 8 * 1024 * 2048 * 4 + 256
+    assert size(1024, 32768, 2048, 1, 0, 0, 0, 0, 0, 0, 0) == 4 * 1024 * 2048 * 4 + 256
+    # K/V weight gradient shape: 128x128 tiles in four chunks of 1024
+    assert size(512, 4096, 2048, 1, 0, 0, 1, 0, 5, 5, 0) == 4 * 512 * 2048 * 4 + 256
     assert size(4096, 4096, 4096, 1, 0, 0, 0, 0, 5, 5, 0) == 0  # a full round of tiles: no split
     # RMSNorm backward partial sums: one row of floats per 16 rows
     rms = library.qutai_amd_rms_norm_workspace
