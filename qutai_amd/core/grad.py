@@ -36,7 +36,9 @@ class DeferredGradient:
     """A gradient contribution a rule describes instead of materialising:
     ``materialize()`` gives the dense storage, and ``add_into(storage)``
     adds it in place into a gradient that this backward pass created (the
-    embedding table's row sums: a few rows of a [vocab][width] gradient).
+    embedding table's row sums: a few rows of a [vocab][width] gradient; a
+    Linear's fp32 dX = G W, summed by the GEMM's accumulate epilogue).
+    ``add_into`` must give the same values as ``storage + materialize()``.
     Has ``device``, ``dtype`` and ``size`` like a storage."""
 
     def materialize(self):
@@ -71,6 +73,10 @@ def backward(output, gradient, *, retain_graph=True, leaf_sink=None):
     """Propagate ``gradient``; leaves go to ``leaf_sink`` (or a returned dict)."""
     order = _topological_order(output)
     gradients = {output: gradient}
+    # non-leaf gradients this loop allocated (a materialised deferred
+    # contribution or a sum): no rule holds them, so later deferred
+    # contributions may be added into them in place
+    fresh = set()
     leaves = {}
     while order:
         tensor = order.pop()
@@ -93,8 +99,16 @@ def backward(output, gradient, *, retain_graph=True, leaf_sink=None):
                 if leaf_sink is not None and parent.backward_rule is None:
                     leaf_sink(parent, contribution)
                 elif parent in gradients:
-                    contribution = _dense(contribution)
-                    gradients[parent] = get_backend(contribution.device).add(gradients[parent], contribution)
+                    existing = gradients[parent]
+                    if (isinstance(contribution, DeferredGradient) and parent in fresh
+                            and contribution.dtype == existing.dtype):
+                        contribution.add_into(existing)
+                    else:
+                        contribution = _dense(contribution)
+                        gradients[parent] = get_backend(contribution.device).add(existing, contribution)
+                        fresh.add(parent)
                 else:
+                    if isinstance(contribution, DeferredGradient):
+                        fresh.add(parent)
                     gradients[parent] = _dense(contribution)
     return leaves

@@ -18,7 +18,7 @@ from math import prod, sqrt
 
 from ..backends import amd, amd_lm
 from ..backends.precision import matmul_precision, set_matmul_precision
-from ..core.grad import owned, record
+from ..core.grad import DeferredGradient, owned, record
 from ..core.tensor import Tensor
 
 
@@ -79,12 +79,40 @@ def linear(x, weight):
 
     def backward(g):
         with set_matmul_precision(precision):
-            dx = b.gemm(g, ws, rows, out_features, inner, out_dtype=x.dtype) if x.requires_grad else None
+            dx = None
+            if x.requires_grad:
+                dx = (ProductGradient(b, g, ws, rows, out_features, inner, precision) if x.dtype == "float32"
+                      else b.gemm(g, ws, rows, out_features, inner, out_dtype=x.dtype))
             dw = (owned(b.gemm(g, xs, out_features, rows, inner, transpose_left=True, out_dtype=weight.dtype))
                   if weight.requires_grad else None)
         return dx, dw
 
     return record(Tensor(values, shape=(*x.shape[:-1], out_features)), (x, weight), backward)
+
+
+class ProductGradient(DeferredGradient):
+    """A Linear's fp32 input gradient dX = G W (rows x inner from G rows x
+    cols and W cols x inner), left for the backward pass to place: alone it
+    is one GEMM; when it meets another fp32 contribution to the same input
+    (the q, k and v projections of one normalised activation) the GEMM adds
+    into that gradient in its epilogue, round(old + product) once, the
+    value a separate fp32 add of the product gives, without the add's pass
+    over three rows x inner arrays."""
+
+    device, dtype = "amd", "float32"
+
+    def __init__(self, b, g, w, rows, cols, inner, precision):
+        self.b, self.g, self.w, self.rows, self.cols, self.inner = b, g, w, rows, cols, inner
+        self.precision, self.size = precision, rows * inner
+
+    def materialize(self):
+        with set_matmul_precision(self.precision):
+            return self.b.gemm(self.g, self.w, self.rows, self.cols, self.inner, out_dtype="float32")
+
+    def add_into(self, storage):
+        with set_matmul_precision(self.precision):
+            self.b.gemm(self.g, self.w, self.rows, self.cols, self.inner, out_dtype="float32", out=storage,
+                        accumulate=True)
 
 
 def residual_add(x, update):
@@ -168,8 +196,11 @@ def swiglu(x, w_gate, w_up):
         with set_matmul_precision(precision):
             dx = None
             if x.requires_grad:
-                dx = amd.add(b.gemm(dgate, gs, rows, hidden, inner, out_dtype=x.dtype),
-                             b.gemm(dup, us, rows, hidden, inner, out_dtype=x.dtype))
+                dx = b.gemm(dgate, gs, rows, hidden, inner, out_dtype=x.dtype)
+                if x.dtype == "float32":  # round(old + product) once: the fp32 add's value
+                    b.gemm(dup, us, rows, hidden, inner, out_dtype=x.dtype, out=dx, accumulate=True)
+                else:
+                    dx = amd.add(dx, b.gemm(dup, us, rows, hidden, inner, out_dtype=x.dtype))
             dwg = (owned(b.gemm(dgate, xs, hidden, rows, inner, transpose_left=True, out_dtype=w_gate.dtype))
                    if w_gate.requires_grad else None)
             dwu = (owned(b.gemm(dup, xs, hidden, rows, inner, transpose_left=True, out_dtype=w_up.dtype))

@@ -240,3 +240,31 @@ def test_residual_add_widened_equals_cast_then_add(base):
         y.backward(g)
         results.append([t.storage.to_array() for t in (y, x.grad, u.grad)])
     assert results[0] == results[1]
+
+
+
+@pytest.mark.parametrize("leaf", [True, False])
+def test_linear_input_gradients_sum_in_the_gemm(base, leaf):
+    """Two Linears of one fp32 activation under autocast (the k and v
+    projections): the second dX = G W is added by the GEMM's accumulate
+    epilogue into the first, for a leaf input (tensor.py) and for a
+    non-leaf one (the backward loop's fresh gradients).  Bit-exact against
+    the two products from separate GEMMs added in fp32 on the host (a + b
+    equals b + a, so the order the pass meets them in does not matter)."""
+    from qutai_amd import Tensor
+    from qutai_amd.backends.precision import set_matmul_precision
+    from qutai_amd.lm.layers import linear, scaled
+
+    rows, inner, out_features = 300, 256, 200
+    x0 = Tensor(upload(normal(41, rows * inner), "float32"), shape=(rows, inner), requires_grad=True)
+    w1, w2 = (Tensor(upload(normal(seed, out_features * inner, 0.05), "float32"), shape=(out_features, inner),
+                     requires_grad=True) for seed in (42, 43))
+    g = upload(normal(44, rows * out_features), "bfloat16")
+    with set_matmul_precision("bfloat16"):
+        x = x0 if leaf else scaled(x0, 2.0)
+        y = linear(x, w1) + linear(x, w2)
+        y.backward(Tensor(g, shape=y.shape))
+        a, b = (download(base.gemm(g, base.from_storage(w.storage, dtype="bfloat16"), rows, out_features, inner,
+                                   out_dtype="float32")).astype(np.float32) for w in (w1, w2))
+    want = (a + b) * np.float32(1.0 if leaf else 2.0)
+    assert np.array_equal(download(x0.grad.storage).astype(np.float32), want)
