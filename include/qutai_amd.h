@@ -355,10 +355,14 @@ int64_t qutai_amd_rms_norm_workspace(int64_t rows, int64_t width);
 /* dx = inverse * (g w - x inverse^2 mean(g w x)) (dx in the activation dtype),
  * dweight[j] = sum_r g x inverse (fp32, fixed-order chunked sum through
  * `partial`).  Replaces `cuda_lm.rms_norm_backward` / `lm_rms_dx` / `lm_rms_dw`
- * (cuda_lm.py:148-177, cuda/lm.cu:46-52). */
+ * (cuda_lm.py:148-177, cuda/lm.cu:46-52).  `residual` (NULL, or fp32 rows x
+ * width, not dx itself; QA_F32 only) is added to dx as it is stored:
+ * dx = residual + dx with one fp32 rounding, the value of a separate add (the
+ * residual stream's gradient summed with the norm's; no counterpart in the
+ * reference, whose autograd adds the two). */
 int qutai_amd_rms_norm_backward(const float* gradient, const void* x, const float* weight, const float* inverse,
-                                void* dx, float* dweight, float* partial, int64_t rows, int64_t width, int dtype,
-                                void* stream);
+                                const float* residual, void* dx, float* dweight, float* partial, int64_t rows,
+                                int64_t width, int dtype, void* stream);
 
 /* out = x sigmoid(x), or with backward = 1 out = g s (1 + x (1 - s)).
  * Replaces `cuda_lm.silu` / `silu_backward` (cuda_lm.py:180-207, cuda/lm.cu:54). */

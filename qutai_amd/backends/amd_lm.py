@@ -530,16 +530,24 @@ def rms_norm(values, weight, width, eps):
     return out, inverse
 
 
-def rms_norm_backward(gradient, values, weight, inverse, width):
-    """(dx in the activation dtype, dweight fp32) (cuda_lm.py:148-177)."""
+def rms_norm_backward(gradient, values, weight, inverse, width, residual=None):
+    """(dx in the activation dtype, dweight fp32) (cuda_lm.py:148-177).  With
+    ``residual`` (fp32 activations only) dx is residual + dx, added as dx is
+    stored: one fp32 rounding, the value of a separate add."""
     rows = values.size // width
     g = gradient if gradient.dtype == "float32" else amd.from_storage(gradient, dtype="float32")
+    if residual is not None and (values.dtype != "float32" or residual.dtype != "float32"
+                                 or residual.size != values.size):
+        raise ValueError("the residual gradient must be fp32 of the activation's size")
     dx, dw = AMDStorage(values.size, values.dtype), AMDStorage(width, weight.dtype)
     if rows:
         runtime = get_runtime()
         partial = AMDStorage(runtime.lib.qutai_amd_rms_norm_workspace(rows, width), "float32")
-        runtime.call("qutai_amd_rms_norm_backward", g.ptr, values.ptr, weight.ptr, inverse.ptr, dx.ptr, dw.ptr,
-                     partial.ptr, rows, width, code(values.dtype))
+        runtime.call("qutai_amd_rms_norm_backward", g.ptr, values.ptr, weight.ptr, inverse.ptr,
+                     None if residual is None else residual.ptr, dx.ptr, dw.ptr, partial.ptr, rows, width,
+                     code(values.dtype))
+    elif residual is not None:
+        dx = residual.copy()
     return dx, dw
 
 

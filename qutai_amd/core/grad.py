@@ -47,6 +47,15 @@ class DeferredGradient:
     def add_into(self, storage):
         raise NotImplementedError
 
+    def sum_with(self, existing, in_place):
+        """existing + this contribution.  ``in_place``: ``existing`` is a
+        gradient this pass allocated and no rule holds, so it may be
+        written; otherwise the sum goes to a new storage."""
+        if in_place:
+            self.add_into(existing)
+            return existing
+        return get_backend(existing.device).add(existing, self.materialize())
+
 
 def _dense(contribution):
     return contribution.materialize() if isinstance(contribution, DeferredGradient) else contribution
@@ -100,9 +109,9 @@ def backward(output, gradient, *, retain_graph=True, leaf_sink=None):
                     leaf_sink(parent, contribution)
                 elif parent in gradients:
                     existing = gradients[parent]
-                    if (isinstance(contribution, DeferredGradient) and parent in fresh
-                            and contribution.dtype == existing.dtype):
-                        contribution.add_into(existing)
+                    if isinstance(contribution, DeferredGradient) and contribution.dtype == existing.dtype:
+                        gradients[parent] = contribution.sum_with(existing, parent in fresh)
+                        fresh.add(parent)
                     else:
                         contribution = _dense(contribution)
                         gradients[parent] = get_backend(contribution.device).add(existing, contribution)

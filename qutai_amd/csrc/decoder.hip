@@ -166,8 +166,8 @@ __global__ void __launch_bounds__(256) rms_cols_kernel(const T* x, const float* 
 // into the workgroup's row of `partial` (rms_dw_final adds the chunks).
 template <class T, int NI>
 __global__ void __launch_bounds__(256) rms_backward_cols_kernel(const float* g, const T* x, const float* w,
-                                                                const float* inv, T* dx, float* partial,
-                                                                int64_t rows) {
+                                                                const float* inv, const float* residual, T* dx,
+                                                                float* partial, int64_t rows) {
   constexpr int W = 256 * NI;
   __shared__ f32x4 sums[4][W / 4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -191,6 +191,12 @@ __global__ void __launch_bounds__(256) rms_backward_cols_kernel(const float* g, 
     for (int i = 0; i < NI; i++) {
       acc[i] += gv[i] * xv[i] * scale;
       gv[i] = scale * (gv[i] * wv[i] - xv[i] * (scale * scale * projected));
+    }
+    if (residual) {  // fp32 only: dx = residual + dx, one rounding (may be dx itself)
+      f32x4 rv[NI];
+      load_cols<float, NI>(residual + r * W, lane, rv);
+#pragma unroll
+      for (int i = 0; i < NI; i++) gv[i] = rv[i] + gv[i];
     }
     store_cols<T, NI>(dx + r * W, lane, gv);
   }
@@ -566,9 +572,10 @@ int64_t qutai_amd_rms_norm_workspace(int64_t rows, int64_t width) {
 }
 
 int qutai_amd_rms_norm_backward(const float* gradient, const void* x, const float* weight, const float* inverse,
-                                void* dx, float* dweight, float* partial, int64_t rows, int64_t width, int dtype,
-                                void* stream) {
-  if (rows < 0 || width <= 0 || !act_dtype(dtype)) return QA_EINVAL;
+                                const float* residual, void* dx, float* dweight, float* partial, int64_t rows,
+                                int64_t width, int dtype, void* stream) {
+  if (rows < 0 || width <= 0 || !act_dtype(dtype) || (residual && (dtype != F32 || residual == dx)))
+    return QA_EINVAL;
   hipStream_t s = (hipStream_t)stream;
   if (rows == 0) return QA_OK;
   if (!partial) return QA_EWORKSPACE;
@@ -577,16 +584,16 @@ int qutai_amd_rms_norm_backward(const float* gradient, const void* x, const floa
   if (chunks > 65535) return QA_EINVAL;
   const dim3 grid((unsigned)((width + 255) / 256), (unsigned)chunks);
   if (cols_path(gradient, width) && cols_path(x, width) && cols_path(weight, width) && cols_path(dx, width) &&
-      cols_path(partial, width)) {
+      cols_path(partial, width) && (!residual || cols_path(residual, width))) {
     const bool bf = dtype == BF16;
     const int64_t groups = (rows + RCB - 1) / RCB;
     switch (width / 256) {
 #define QA_RMSB(N)                                                                                                 \
   case N:                                                                                                          \
     if (bf) hipLaunchKernelGGL((rms_backward_cols_kernel<bf16_t, N>), dim3((unsigned)groups), dim3(256), 0, s,      \
-                               gradient, (const bf16_t*)x, weight, inverse, (bf16_t*)dx, partial, rows);            \
+                               gradient, (const bf16_t*)x, weight, inverse, nullptr, (bf16_t*)dx, partial, rows);   \
     else hipLaunchKernelGGL((rms_backward_cols_kernel<float, N>), dim3((unsigned)groups), dim3(256), 0, s, gradient, \
-                            (const float*)x, weight, inverse, (float*)dx, partial, rows);                          \
+                            (const float*)x, weight, inverse, residual, (float*)dx, partial, rows);                \
     break;
       QA_RMSB(1) QA_RMSB(2) QA_RMSB(3) QA_RMSB(4) QA_RMSB(5) QA_RMSB(6) QA_RMSB(7) QA_RMSB(8)
 #undef QA_RMSB
@@ -603,6 +610,10 @@ int qutai_amd_rms_norm_backward(const float* gradient, const void* x, const floa
   } else {
     hipLaunchKernelGGL(rms_dx_kernel<float>, dim3(blocks), dim3(256), 0, s, gradient, (const float*)x, weight,
                        inverse, (float*)dx, rows, width);
+    if (residual) {
+      const int rc = qutai_amd_add(residual, dx, dx, rows * width, QA_F32, stream);
+      if (rc != QA_OK) return rc;
+    }
     hipLaunchKernelGGL(rms_dw_partial_kernel<float>, grid, dim3(256), 0, s, gradient, (const float*)x, inverse,
                        partial, rows, width);
   }

@@ -151,11 +151,66 @@ def rms_norm(x, weight, eps):
     b = backend(x)
     width = x.shape[-1]
     out, inverse = b.rms_norm(x.storage, weight.storage, width, eps)
+
     def backward(g):
+        if x.dtype == "float32" and x.requires_grad:
+            state = NormBackward(b, g, x.storage, weight.storage, inverse, width)
+            return NormInputGradient(state), NormWeightGradient(state)
         dx, dweight = b.rms_norm_backward(g, x.storage, weight.storage, inverse, width)
         return dx, owned(dweight)
 
     return record(Tensor(out, shape=x.shape), (x, weight), backward)
+
+
+class NormBackward:
+    """One RMSNorm backward kernel call (dx and dweight together), run when
+    the pass first asks for either: for dx summed with the residual stream's
+    gradient (the norm's input is also the residual connection's), the
+    kernel adds that gradient as it stores dx, the fp32 add's value without
+    the add's pass over three rows x width arrays."""
+
+    def __init__(self, b, g, x, weight, inverse, width):
+        self.args, self.dx, self.dweight = (b, g, x, weight, inverse, width), None, None
+
+    def run(self, residual=None):
+        b, g, x, weight, inverse, width = self.args
+        self.dx, self.dweight = b.rms_norm_backward(g, x, weight, inverse, width, residual=residual)
+        self.args = None
+        return self.dx
+
+
+class NormInputGradient(DeferredGradient):
+    device, dtype = "amd", "float32"
+
+    def __init__(self, state):
+        self.state, self.size = state, state.args[2].size
+
+    def materialize(self):
+        return self.state.run()
+
+    def add_into(self, storage):
+        amd_lm.add_into(storage, self.state.run())
+
+    def sum_with(self, existing, in_place):
+        return self.state.run(existing)
+
+
+class NormWeightGradient(DeferredGradient):
+    device = "amd"
+
+    def __init__(self, state):
+        self.state, self.size, self.dtype = state, state.args[3].size, state.args[3].dtype
+
+    def _get(self):
+        if self.state.dweight is None:
+            self.state.run()
+        return self.state.dweight
+
+    def materialize(self):
+        return owned(self._get())
+
+    def add_into(self, storage):
+        amd_lm.add_into(storage, self._get())
 
 
 def rope(x, heads, theta, offset=0):

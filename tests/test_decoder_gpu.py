@@ -268,3 +268,41 @@ def test_linear_input_gradients_sum_in_the_gemm(base, leaf):
                                    out_dtype="float32")).astype(np.float32) for w in (w1, w2))
     want = (a + b) * np.float32(1.0 if leaf else 2.0)
     assert np.array_equal(download(x0.grad.storage).astype(np.float32), want)
+
+
+@pytest.mark.parametrize("rows,width", [(300, 2048), (37, 100)])
+def test_rms_norm_backward_adds_the_residual(lm, rows, width):
+    """dx = residual + dx as the kernel stores it (the 16-byte column path at
+    width 2048, the generic path at 100): bit-exact against the plain dx
+    added to the residual in fp32 on the host; dweight unchanged."""
+    x, w = normal(51, rows * width), normal(52, width, 0.5) + 1.0
+    g, res = normal(53, rows * width), normal(54, rows * width)
+    xs, ws = upload(x, "float32"), upload(w, "float32")
+    _, inv = lm.rms_norm(xs, ws, width, 1e-5)
+    dx, dw = lm.rms_norm_backward(upload(g, "float32"), xs, ws, inv, width)
+    rx, rw = lm.rms_norm_backward(upload(g, "float32"), xs, ws, inv, width, residual=upload(res, "float32"))
+    assert np.array_equal(download(rx).astype(np.float32), res + download(dx).astype(np.float32))
+    assert np.array_equal(download(rw), download(dw))
+
+
+@pytest.mark.parametrize("leaf", [True, False])
+def test_norm_input_gradient_sums_with_the_residual(base, leaf):
+    """y = x + rms_norm(x): the backward pass sums the add's gradient G and
+    the norm's dx inside the norm kernel (non-leaf x) or adds dx into the
+    leaf's gradient; bit-exact against dx + G in fp32 on the host."""
+    from qutai_amd import Tensor
+    from qutai_amd.backends import amd_lm
+    from qutai_amd.lm.layers import rms_norm, scaled
+
+    rows, width = 64, 2048
+    x0 = Tensor(upload(normal(61, rows * width), "float32"), shape=(rows, width), requires_grad=True)
+    w = Tensor(upload(normal(62, width, 0.5) + 1.0, "float32"), shape=(width,), requires_grad=True)
+    g = normal(63, rows * width)
+    x = x0 if leaf else scaled(x0, 2.0)
+    y = x + rms_norm(x, w, 1e-5)
+    y.backward(Tensor(upload(g, "float32"), shape=y.shape))
+    _, inv = amd_lm.rms_norm(x.storage, w.storage, width, 1e-5)
+    dx, dw = amd_lm.rms_norm_backward(upload(g, "float32"), x.storage, w.storage, inv, width)
+    want = (g + download(dx).astype(np.float32)) * np.float32(1.0 if leaf else 2.0)
+    assert np.array_equal(download(x0.grad.storage).astype(np.float32), want)
+    assert np.array_equal(download(w.grad.storage), download(dw))
