@@ -306,3 +306,35 @@ def test_norm_input_gradient_sums_with_the_residual(base, leaf):
     want = (g + download(dx).astype(np.float32)) * np.float32(1.0 if leaf else 2.0)
     assert np.array_equal(download(x0.grad.storage).astype(np.float32), want)
     assert np.array_equal(download(w.grad.storage), download(dw))
+
+
+def test_head_kept_logits_equal_recomputed(monkeypatch):
+    """projection_loss keeps the forward's logit blocks for the backward when
+    they fit KEEP_LOGITS_BYTES: loss and both gradients bit-identical to the
+    recomputing form, and a second backward over the retained graph (the
+    kept blocks were overwritten by the first) adds the same gradients."""
+    from qutai_amd import Tensor
+    from qutai_amd.backends.precision import set_matmul_precision
+    from qutai_amd.lm import layers
+
+    batch, time, width, vocab = 2, 48, 256, 3000
+    labels = [[(7 * t + 3 * r) % vocab for t in range(time)] for r in range(batch)]
+    labels[0][5] = -100
+    results = []
+    for budget in (layers.KEEP_LOGITS_BYTES, 0):
+        monkeypatch.setattr(layers, "KEEP_LOGITS_BYTES", budget)
+        h = Tensor(upload(normal(71, batch * time * width), "float32"), shape=(batch, time, width),
+                   requires_grad=True)
+        w = Tensor(upload(normal(72, vocab * width, 0.05), "float32"), shape=(vocab, width), requires_grad=True)
+        with set_matmul_precision("bfloat16"):
+            loss = layers.projection_loss(h, w, labels, chunk_size=16)
+            loss.backward()
+            first = [download(t.grad.storage).copy() for t in (h, w)]
+            loss.backward()
+        second = [download(t.grad.storage) for t in (h, w)]
+        results.append((download(loss.storage), first))
+        for a, b2 in zip(first, second):
+            assert np.array_equal((a.astype(np.float32) * 2), b2.astype(np.float32))
+    assert np.array_equal(results[0][0], results[1][0])
+    for a, b2 in zip(results[0][1], results[1][1]):
+        assert np.array_equal(a, b2)
