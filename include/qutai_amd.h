@@ -33,6 +33,12 @@ extern "C" {
 #define QA_EINVAL (-1)     /* shapes, strides, dtypes or pointers rejected */
 #define QA_EWORKSPACE (-2) /* workspace missing or too small */
 
+/* The gcnArchName of HIP device `device` (e.g. "gfx950:sramecc+:xnack-"),
+ * NUL-terminated into name[size].  Replaces the compute-capability query of
+ * the reference runtime (src/qutai/backends/cuda_runtime.py:111-116, device
+ * attributes 75/76) that gates its kernels (src/qutai/backends/cuda.py:340-341). */
+int qutai_amd_device_arch(int device, char* name, size_t size);
+
 /* Batched GEMM: for z in [0, batch)
  *   out[z][m][n] (+)= sum_k A_z(m,k) * B_z(k,n)
  *   A_z(m,k) = transpose_left  ? a[z*left_stride  + k*rows + m] : a[z*left_stride  + m*inner + k]
@@ -185,6 +191,82 @@ int qutai_amd_transpose_last2(const void* x, void* out, int64_t batch, int64_t r
  * src/qutai/nn/layers.py:336 into the same pass. */
 int qutai_amd_softmax_rows(const void* x, void* out, int64_t rows, int64_t width, double scale, int dtype,
                            void* stream);
+
+/* Softmax of (scale * x) along the middle axis of x viewed as
+ * [outer][width][inner] (any axis of a row-major tensor).  inner == 1 is
+ * qutai_amd_softmax_rows; otherwise one lane per (outer, inner) column with
+ * coalesced passes (max, sum of exp, write).  fp32 math for fp32/bf16,
+ * fp64 for fp64.  Replaces `cuda.softmax` on any axis
+ * (src/qutai/backends/cuda.py:464-472) and its kernels `softmax_rows` /
+ * `softmax_forward` (src/qutai/backends/cuda/nn.cu:28-37, 67-76). */
+int qutai_amd_softmax(const void* x, void* out, int64_t outer, int64_t width, int64_t inner, double scale,
+                      int dtype, void* stream);
+
+/* Strided copy: for every coordinate c of the row-major index space dims[rank]
+ *   dst[sum_d c_d * dst_strides[d]] = src[sum_d c_d * src_strides[d]]
+ * (strides in elements of element_bytes = 2, 4 or 8; a source stride of 0
+ * broadcasts; rank <= 8).  dims and strides are host arrays.  Unit axes are
+ * dropped and axes contiguous on both sides merged before the launch; runs
+ * of the innermost axis move 16 bytes per lane when both sides allow it.
+ * One kernel for `cuda.broadcast` (src/qutai/backends/cuda.py:245-252),
+ * `cuda.transpose` (:255-262, any permutation), `cuda.concatenate`
+ * (:383-394) and `cuda.gather_slice` / `cuda.scatter_slice` (:229-242), all
+ * of which drive the reference's `broadcast` / `slice_copy` /
+ * `concatenate` kernels (src/qutai/backends/cuda/tensor.cu:49-54, 56-58,
+ * 67-69) with int64 metadata uploaded per call; here the metadata travels in
+ * the kernel arguments. */
+int qutai_amd_strided_copy(const void* src, void* dst, int rank, const int64_t* dims, const int64_t* src_strides,
+                           const int64_t* dst_strides, int element_bytes, void* stream);
+
+/* out = left (op) right element-wise, op 0 add, 1 subtract, 2 multiply,
+ * 3 divide; fp32 math for fp32/bf16 (one rounding), fp64 for fp64.  With
+ * zero_flag (device int32) the call first sets *zero_flag = 0 and a divide
+ * sets it to 1 when any divisor is zero (the caller reads it to raise
+ * ZeroDivisionError).  out may be left or right (in place).  Replaces
+ * `cuda.add/subtract/multiply/divide` and `add_into`
+ * (src/qutai/backends/cuda.py:171-189, 141-147) over the `binary` kernel
+ * (src/qutai/backends/cuda/tensor.cu:30). */
+int qutai_amd_binary(const void* left, const void* right, void* out, int64_t n, int op, int dtype, int* zero_flag,
+                     void* stream);
+
+/* out = f(x) element-wise (gradient = NULL) or g * f'(x) (gradient given):
+ * op 0 negate, 1 square, 2 x * factor, 3 relu, 4 relu backward, 5 gelu,
+ * 6 gelu backward, 7 exp, 8 log (sets *flag = 1 when some x <= 0), 9 tanh,
+ * 10 atan, 11 tanh backward, 12 atan backward, 13 x / factor.  fp32 math
+ * for fp32/bf16, fp64 for fp64; with flag the call first clears it.  out
+ * may be x (in place).  Replaces `cuda.divide_scalar`, `negate` ...
+ * `atan_backward` and `scale_into` (src/qutai/backends/cuda.py:157-168,
+ * 192-208, 150-154) over the `unary` kernel
+ * (src/qutai/backends/cuda/tensor.cu:31-46). */
+int qutai_amd_unary(const void* x, const void* gradient, void* out, int64_t n, int op, double factor, int dtype,
+                    int* flag, void* stream);
+
+/* out[o][j] = sum_c x[o][c][j] for x viewed as [outer][width][inner]
+ * (inner = 1: row sums; outer = inner = 1: the sum of everything), in fp32
+ * (fp64 for fp64) with one rounding.  Long sums are split into parts whose
+ * partial sums land in `workspace` and are added in part order, so results
+ * repeat bit for bit.  Replaces `cuda.sum` / `cuda.mean` / `cuda.unbroadcast`
+ * (src/qutai/backends/cuda.py:265-289) and the `reduce_sum` kernel
+ * (src/qutai/backends/cuda/tensor.cu:59-61), which sums each output in one
+ * thread. */
+int qutai_amd_reduce_sum(const void* x, void* out, int64_t outer, int64_t width, int64_t inner, int dtype,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* Bytes of workspace qutai_amd_reduce_sum needs (0 when one pass does). */
+size_t qutai_amd_reduce_sum_workspace_size(int64_t outer, int64_t width, int64_t inner, int dtype);
+
+/* out[i] = x[positions[i]] for n elements of element_bytes (positions:
+ * device int64).  Replaces `cuda.gather` (src/qutai/backends/cuda.py:211-215,
+ * kernel src/qutai/backends/cuda/tensor.cu:48). */
+int qutai_amd_gather(const void* x, const int64_t* positions, void* out, int64_t n, int element_bytes, void* stream);
+
+/* out[t] = sum of x[order[k]] for k in [start[t], start[t+1]), in k order, for
+ * t < size (start: size+1 device int64, order: device int64; the host groups
+ * every source index under its target position).  Deterministic form of
+ * `cuda.scatter` (src/qutai/backends/cuda.py:218-226, an atomicAdd kernel
+ * src/qutai/backends/cuda/tensor.cu:55). */
+int qutai_amd_scatter(const void* x, const int64_t* start, const int64_t* order, void* out, int64_t size, int dtype,
+                      void* stream);
 
 /* out = silu(gate) * up element-wise (fp32 math, one rounding to dtype).
  * Replaces `lm_silu` (src/qutai/backends/cuda/lm.cu:54) followed by the

@@ -18,7 +18,12 @@ Contents
     ``head_loss`` / ``head_gradient`` (cpu_lm.py:54-138, 323-371),
     ``attention`` / ``attention_backward``
     (cpu_lm.py:141-201), ``bf16`` (the RNE encoder of cuda.py:98-101 /
-    tests/test_bfloat16_storage.py:10-16);
+    tests/test_bfloat16_storage.py:10-16), and the generic tensor functions
+    ``broadcast`` (cpu.py:127-137), ``transpose`` (cpu.py:166-180),
+    ``reduce_sum`` (cpu.py:183-203), ``mean`` (cpu.py:206-215),
+    ``unbroadcast`` (cpu.py:218-228), ``concatenate`` (cpu.py:514-520),
+    ``gather`` / ``scatter`` (cpu.py:104-114), ``binary`` (cpu.py:122-124,
+    452-466) and ``unary`` (cpu.py:468-511);
   * ``gemm_f64``: the same float64 sequential-k GEMM compiled from
     ``oracle/gemm_f64.c`` (bit-identical to ``gemm``; used at sizes the
     Python loop cannot finish);
@@ -140,6 +145,132 @@ def softmax(values, shape, axis) -> list[float]:
         for index, weight in zip(indices, weights):
             result[index] = weight / total
     return result
+
+
+def _coordinates(shape):
+    from itertools import product as cartesian
+    return cartesian(*(range(size) for size in shape))
+
+
+def broadcast(values, shape, target) -> list[float]:
+    """cpu.broadcast (src/qutai/backends/cpu.py:127-137): every coordinate of
+    ``target`` reads the source element whose size-1 axes are pinned to 0."""
+    padded = (1,) * (len(target) - len(shape)) + tuple(shape)
+    steps = _strides(padded)
+    result = []
+    for coordinate in _coordinates(target):
+        offset = 0
+        for position, length, step in zip(coordinate, padded, steps):
+            if length != 1:
+                offset += position * step
+        result.append(values[offset])
+    return result
+
+
+def transpose(values, shape, axes=None) -> list[float]:
+    """cpu.transpose (src/qutai/backends/cpu.py:166-180): each source
+    element goes to its permuted coordinate."""
+    axes = tuple(reversed(range(len(shape)))) if axes is None else tuple(a % len(shape) for a in axes)
+    target = tuple(shape[a] for a in axes)
+    steps = _strides(target)
+    result = [0.0] * len(values)
+    for value, coordinate in zip(values, _coordinates(shape)):
+        result[sum(coordinate[a] * step for a, step in zip(axes, steps))] = value
+    return result
+
+
+def reduce_sum(values, shape=None, axis=None) -> list[float]:
+    """cpu.sum (src/qutai/backends/cpu.py:183-203): everything, or one axis
+    with the axis dropped; float64 additions in storage order."""
+    if axis is None:
+        total = 0.0
+        for value in values:
+            total += value
+        return [total]
+    axis %= len(shape)
+    target = tuple(shape[:axis]) + tuple(shape[axis + 1:])
+    steps = _strides(target)
+    result = [0.0] * prod(target)
+    for value, coordinate in zip(values, _coordinates(shape)):
+        kept = coordinate[:axis] + coordinate[axis + 1:]
+        result[sum(c * step for c, step in zip(kept, steps))] += value
+    return result
+
+
+def mean(values, shape=None, axis=None) -> list[float]:
+    """cpu.mean (src/qutai/backends/cpu.py:206-215)."""
+    count = len(values) if axis is None else shape[axis % len(shape)]
+    if not count:
+        raise ValueError("the mean of no elements is undefined")
+    return [total / count for total in reduce_sum(values, shape, axis)]
+
+
+def unbroadcast(values, shape, target) -> list[float]:
+    """cpu.unbroadcast (src/qutai/backends/cpu.py:218-228): sum every axis
+    that the target holds as 1, keeping it as 1."""
+    padded = (1,) * (len(shape) - len(target)) + tuple(target)
+    current = tuple(shape)
+    for axis, (length, original) in enumerate(zip(shape, padded)):
+        if original == 1 and length != 1:
+            values = reduce_sum(values, current, axis)
+            current = current[:axis] + (1,) + current[axis + 1:]
+    return list(values)
+
+
+def concatenate(values, shapes, axis=0) -> list[float]:
+    """cpu.concatenate (src/qutai/backends/cpu.py:514-520): for every outer
+    index, the pieces' blocks in order."""
+    axis %= len(shapes[0])
+    sizes = [prod(shape[axis:]) for shape in shapes]
+    return [value for outer in range(prod(shapes[0][:axis]))
+            for data, size in zip(values, sizes) for value in data[outer * size:(outer + 1) * size]]
+
+
+def gather(values, positions) -> list[float]:
+    """cpu.gather (src/qutai/backends/cpu.py:104-106)."""
+    return [values[position] for position in positions]
+
+
+def scatter(values, positions, size) -> list[float]:
+    """cpu.scatter (src/qutai/backends/cpu.py:109-114): additions in input order."""
+    result = [0.0] * size
+    for position, value in zip(positions, values):
+        result[position] += value
+    return result
+
+
+def binary(left, right, operation) -> list[float]:
+    """cpu.add / subtract / multiply / divide (src/qutai/backends/cpu.py:122-124,
+    452-466) for operation "add", "subtract", "multiply", "divide"."""
+    import operator
+    function = {"add": operator.add, "subtract": operator.sub, "multiply": operator.mul,
+                "divide": operator.truediv}[operation]
+    return [function(a, b) for a, b in zip(left, right)]
+
+
+def unary(values, operation, *, gradient=None, factor=None) -> list[float]:
+    """The element-wise functions of src/qutai/backends/cpu.py:468-511 (and
+    ``divide_scalar``, x / factor, of the CUDA path, cuda.py:192-195)."""
+    from math import atan, erf, pi, tanh
+    g = gradient if gradient is not None else [None] * len(values)
+    table = {
+        "negate": lambda x, _: -x,
+        "square": lambda x, _: x * x,
+        "scale": lambda x, _: x * factor,
+        "divide_scalar": lambda x, _: x / factor,
+        "relu": lambda x, _: max(x, 0.0),
+        "relu_backward": lambda x, d: d if x > 0 else 0.0,
+        "gelu": lambda x, _: x * (1 + erf(x / sqrt(2))) / 2,
+        "gelu_backward": lambda x, d: d * ((1 + erf(x / sqrt(2))) / 2 + x * exp(-x * x / 2) / sqrt(2 * pi)),
+        "exp": lambda x, _: exp(x),
+        "log": lambda x, _: log(x),
+        "tanh": lambda x, _: tanh(x),
+        "atan": lambda x, _: atan(x),
+        "tanh_backward": lambda x, d: d * (1 - tanh(x) ** 2),
+        "atan_backward": lambda x, d: d / (1 + x * x),
+    }
+    function = table[operation]
+    return [function(x, d) for x, d in zip(values, g)]
 
 
 def silu(values) -> list[float]:

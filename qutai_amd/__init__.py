@@ -5,6 +5,7 @@
 Importing the package does not touch the GPU.
 """
 from .backends.device import is_available, synchronize
-from .core.tensor import Tensor, matmul, sum
+from .core.tensor import Tensor, add, concatenate, divide, gelu, matmul, mean, multiply, relu, softmax, subtract, sum
 
-__all__ = ["Tensor", "matmul", "sum", "is_available", "synchronize"]
+__all__ = ["Tensor", "add", "concatenate", "divide", "gelu", "matmul", "mean", "multiply", "relu", "softmax",
+           "subtract", "sum", "is_available", "synchronize"]

@@ -11,16 +11,18 @@ library or the GPU is missing, the first device touch raises.
 """
 from __future__ import annotations
 
+import ctypes
 import struct
 from array import array
 from collections.abc import Iterable
 from itertools import product
-from math import isqrt, prod
+from builtins import sum as _add_up  # the module defines the reference's `sum`
+from math import prod
 
 from .amd_runtime import get_runtime
 from .precision import matmul_precision
 from .storage import Storage
-from ..core.shape import broadcast_shape, strides
+from ..core.shape import broadcast_shape, normalize_axis, strides, transpose_axes
 
 # dtype -> (array typecode, item size); the order gives the C-ABI dtype codes
 # (same table as src/qutai/backends/cuda.py:17).
@@ -272,8 +274,8 @@ def matmul(left, right, left_shape, right_shape):
     steps_a, steps_b = strides(a), strides(b)
     item = _TYPES[left.dtype][1]
     for index, coordinate in enumerate(product(*(range(n) for n in batches))):
-        offset_a = sum(p * steps_a[d] for d, p in enumerate(coordinate) if a[d] != 1)
-        offset_b = sum(p * steps_b[d] for d, p in enumerate(coordinate) if b[d] != 1)
+        offset_a = _add_up(p * steps_a[d] for d, p in enumerate(coordinate) if a[d] != 1)
+        offset_b = _add_up(p * steps_b[d] for d, p in enumerate(coordinate) if b[d] != 1)
         view_a = _View(left, offset_a, rows * inner)
         view_b = _View(right, offset_b, inner * columns)
         view_c = _View(result, index * rows * columns, rows * columns)
@@ -314,101 +316,420 @@ def add_widen(left: AMDStorage, right: AMDStorage) -> AMDStorage:
     return result
 
 
-def add(left: AMDStorage, right: AMDStorage) -> AMDStorage:
-    if (left.dtype, left.size) != (right.dtype, right.size):
-        raise ValueError("add needs equal dtype and size")
-    result = AMDStorage(left.size, left.dtype)
+_FLOATS = ("float32", "float64", "bfloat16")
+_MAX_RANK = 8
+
+
+def _item(dtype: str) -> int:
+    return _TYPES[dtype][1]
+
+
+def _copy_strided(source: AMDStorage, target: AMDStorage, dims, source_steps, target_steps, *, source_offset=0,
+                  target_offset=0) -> None:
+    """target[offset + c . target_steps] = source[offset + c . source_steps]
+    for every coordinate c of ``dims`` (one strided-copy launch)."""
+    dims = tuple(dims) or (1,)
+    source_steps = tuple(source_steps) or (1,)
+    target_steps = tuple(target_steps) or (1,)
+    if not prod(dims):
+        return
+    if len(dims) > _MAX_RANK:
+        raise ValueError(f"the amd device copies tensors of at most {_MAX_RANK} dimensions")
+    rank = len(dims)
+    array_type = ctypes.c_int64 * rank
+    item = _item(source.dtype)
+    get_runtime().call("qutai_amd_strided_copy", source.ptr + source_offset * item, target.ptr + target_offset * item,
+                       rank, array_type(*dims), array_type(*source_steps), array_type(*target_steps), item)
+
+
+def _span(shape, steps, offset) -> tuple[int, int]:
+    """Lowest and highest element a strided view of ``shape`` touches."""
+    low = high = offset
+    for size, step in zip(shape, steps):
+        if size > 1:
+            low += min(0, (size - 1) * step)
+            high += max(0, (size - 1) * step)
+    return low, high
+
+
+def broadcast(values: AMDStorage, shape, target) -> AMDStorage:
+    """``values`` of ``shape`` repeated to ``target`` (src/qutai/backends/cuda.py:245-252):
+    the same storage when the shapes agree, else a new one; size-1 axes
+    (and missing leading axes) are read with stride 0."""
+    shape, target = tuple(shape), tuple(target)
+    if shape == target:
+        return values
+    if len(shape) > len(target):
+        raise ValueError(f"shape {shape} cannot broadcast to {target}")
+    padded = (1,) * (len(target) - len(shape)) + shape
+    if any(n != 1 and n != t for n, t in zip(padded, target)):
+        raise ValueError(f"shape {shape} cannot broadcast to {target}")
+    if values.size != prod(shape):
+        raise ValueError("storage size does not match the broadcast source shape")
+    steps = tuple(0 if n == 1 else step for n, step in zip(padded, strides(padded)))
+    result = AMDStorage(prod(target), values.dtype)
+    _copy_strided(values, result, target, steps, strides(target))
+    return result
+
+
+def transpose(values: AMDStorage, shape, axes=None) -> AMDStorage:
+    """Any axis permutation (src/qutai/backends/cuda.py:255-262), reversed
+    axes when ``axes`` is None.  A swap of the last two axes runs through
+    32x32 LDS tiles (both sides coalesced); every other permutation is one
+    strided copy whose innermost runs stay 16-byte vectors when the last
+    axis does not move."""
+    shape = tuple(shape)
+    rank = len(shape)
+    order = transpose_axes(rank, axes)
+    if values.size != prod(shape):
+        raise ValueError("storage size does not match the shape")
+    target = tuple(shape[a] for a in order)
+    result = AMDStorage(values.size, values.dtype)
+    if not values.size:
+        return result
+    if rank >= 2 and order == tuple(range(rank - 2)) + (rank - 1, rank - 2):
+        result.runtime.call("qutai_amd_transpose_last2", values.ptr, result.ptr, prod(shape[:-2]), shape[-2],
+                            shape[-1], code(values.dtype))
+        return result
+    source_steps = strides(shape)
+    _copy_strided(values, result, target, tuple(source_steps[a] for a in order), strides(target))
+    return result
+
+
+def concatenate(values, shapes, axis=0) -> AMDStorage:
+    """Pieces joined along ``axis`` (src/qutai/backends/cuda.py:383-394): one
+    strided copy per piece into its column range of the [outer][total]
+    result."""
+    shapes = [tuple(shape) for shape in shapes]
+    if not values or len(values) != len(shapes):
+        raise ValueError("concatenate needs one shape per storage")
+    rank = len(shapes[0])
+    axis = normalize_axis(axis, rank)
+    if len({v.dtype for v in values}) != 1 or any(len(s) != rank for s in shapes):
+        raise ValueError("concatenate needs storages of one dtype and shapes of one rank")
+    if any(s[:axis] != shapes[0][:axis] or s[axis + 1:] != shapes[0][axis + 1:] for s in shapes):
+        raise ValueError("concatenate needs equal shapes outside the joined axis")
+    outer = prod(shapes[0][:axis])
+    sizes = [prod(shape[axis:]) for shape in shapes]
+    total = _add_up(sizes)
+    result = AMDStorage(outer * total, values[0].dtype)
+    start = 0
+    for data, size in zip(values, sizes):
+        if data.size != outer * size:
+            raise ValueError("storage size does not match its shape")
+        _copy_strided(data, result, (outer, size), (size, 1), (total, 1), target_offset=start)
+        start += size
+    return result
+
+
+def gather_slice(values: AMDStorage, shape, steps, offset) -> AMDStorage:
+    """Strided view read (src/qutai/backends/cuda.py:237-238): element c of
+    the result is values[offset + c . steps]."""
+    shape, steps = tuple(shape), tuple(steps)
+    low, high = _span(shape, steps, offset)
+    if prod(shape) and (low < 0 or high >= values.size):
+        raise IndexError("slice outside the storage")
+    result = AMDStorage(prod(shape), values.dtype)
+    _copy_strided(values, result, shape, steps, strides(shape), source_offset=offset)
+    return result
+
+
+def scatter_slice(values: AMDStorage, shape, steps, offset, size) -> AMDStorage:
+    """Inverse of ``gather_slice`` (src/qutai/backends/cuda.py:241-242): a
+    zero storage of ``size`` with ``values`` written at offset + c . steps."""
+    shape, steps = tuple(shape), tuple(steps)
+    if values.size != prod(shape):
+        raise ValueError("storage size does not match the slice shape")
+    low, high = _span(shape, steps, offset)
+    if prod(shape) and (low < 0 or high >= size):
+        raise IndexError("slice outside the storage")
+    result = full(size, 0.0, dtype=values.dtype)
+    _copy_strided(values, result, shape, strides(shape), steps, target_offset=offset)
+    return result
+
+
+def _positions(positions, limit: int):
+    index = positions if isinstance(positions, array) and positions.typecode == "q" else array("q", positions)
+    if index and (min(index) < 0 or max(index) >= limit):
+        raise IndexError("position outside the storage")
+    return storage(index, dtype="int64"), index
+
+
+def gather(values: AMDStorage, positions) -> AMDStorage:
+    """values[positions[i]] for each i (src/qutai/backends/cuda.py:211-215)."""
+    device_index, index = _positions(positions, values.size)
+    result = AMDStorage(len(index), values.dtype)
+    if len(index):
+        result.runtime.call("qutai_amd_gather", values.ptr, device_index.ptr, result.ptr, len(index),
+                            _item(values.dtype))
+    return result
+
+
+def scatter(values: AMDStorage, positions, size: int) -> AMDStorage:
+    """Zeros of ``size`` with values[i] added at positions[i]
+    (src/qutai/backends/cuda.py:218-226).  Repeated positions add up in
+    input order: the sources of every target are grouped on the host and
+    summed by one lane, so the result is deterministic."""
+    if values.dtype not in _FLOATS:
+        raise ValueError("scatter accumulates floating storages only")
+    index = positions if isinstance(positions, array) and positions.typecode == "q" else array("q", positions)
+    if len(index) != values.size:
+        raise ValueError("scatter needs one position per value")
+    if index and (min(index) < 0 or max(index) >= size):
+        raise IndexError("position outside the storage")
+    counts = [0] * (size + 1)
+    for position in index:
+        counts[position + 1] += 1
+    for t in range(size):
+        counts[t + 1] += counts[t]
+    order = sorted(range(len(index)), key=index.__getitem__)
+    start = storage(array("q", counts), dtype="int64")
+    sources = storage(array("q", order), dtype="int64") if order else None
+    result = AMDStorage(size, values.dtype)
+    if size:
+        result.runtime.call("qutai_amd_scatter", values.ptr, start.ptr, _p(sources), result.ptr, size,
+                            code(values.dtype))
+    return result
+
+
+# element-wise arithmetic (binary and unary op codes of qutai_amd_binary / qutai_amd_unary)
+_ADD, _SUBTRACT, _MULTIPLY, _DIVIDE = 0, 1, 2, 3
+(_NEGATE, _SQUARE, _SCALE, _RELU, _RELU_BACKWARD, _GELU, _GELU_BACKWARD, _EXP, _LOG, _TANH, _ATAN, _TANH_BACKWARD,
+ _ATAN_BACKWARD, _DIVIDE_SCALAR) = range(14)
+
+
+class _Flag:
+    """A device int32 that a kernel sets when it meets an invalid operand."""
+
+    def __init__(self):
+        self.runtime = get_runtime()
+        self.ptr = self.runtime.allocate(4)
+
+    def __del__(self):
+        if getattr(self, "ptr", 0):
+            self.runtime.free(self.ptr)
+            self.ptr = 0
+
+    def raised(self) -> bool:
+        value = array("i", [0])
+        self.runtime.download(self.ptr, value)
+        return bool(value[0])
+
+
+def _binary(left: AMDStorage, right: AMDStorage, operation: int, out: AMDStorage | None = None) -> AMDStorage:
+    if left.dtype == "int64":
+        raise ValueError("int64 index storages take no arithmetic")
+    if (left.size, left.dtype) != (right.size, right.dtype):
+        raise ValueError("element-wise operations need equal element counts and dtypes")
+    result = out if out is not None else AMDStorage(left.size, left.dtype)
+    flag = _Flag() if operation == _DIVIDE and left.size else None
     if left.size:
-        result.runtime.call("qutai_amd_add", left.ptr, right.ptr, result.ptr, left.size, code(left.dtype))
+        result.runtime.call("qutai_amd_binary", left.ptr, right.ptr, result.ptr, left.size, operation,
+                            code(left.dtype), _p(flag))
+    if flag is not None and flag.raised():
+        raise ZeroDivisionError("division by zero")
+    return result
+
+
+def _unary(values: AMDStorage, operation: int, factor: float = 0.0, gradient: AMDStorage | None = None,
+           out: AMDStorage | None = None) -> AMDStorage:
+    if values.dtype not in _FLOATS:
+        raise ValueError("element-wise functions take real floating storages")
+    if gradient is not None and (gradient.size, gradient.dtype) != (values.size, values.dtype):
+        raise ValueError("gradient and values need equal element counts and dtypes")
+    result = out if out is not None else AMDStorage(values.size, values.dtype)
+    flag = _Flag() if operation == _LOG and values.size else None
+    if values.size:
+        result.runtime.call("qutai_amd_unary", values.ptr, _p(gradient), result.ptr, values.size, operation,
+                            float(factor), code(values.dtype), _p(flag))
+    if flag is not None and flag.raised():
+        raise ValueError("the natural logarithm needs positive inputs")
+    return result
+
+
+def add(left: AMDStorage, right: AMDStorage) -> AMDStorage:
+    """left + right (src/qutai/backends/cuda.py:186)."""
+    return _binary(left, right, _ADD)
+
+
+def subtract(left: AMDStorage, right: AMDStorage) -> AMDStorage:
+    """left - right (src/qutai/backends/cuda.py:187)."""
+    return _binary(left, right, _SUBTRACT)
+
+
+def multiply(left: AMDStorage, right: AMDStorage) -> AMDStorage:
+    """left * right (src/qutai/backends/cuda.py:188)."""
+    return _binary(left, right, _MULTIPLY)
+
+
+def divide(left: AMDStorage, right: AMDStorage) -> AMDStorage:
+    """left / right; ZeroDivisionError when a divisor is zero, found on the
+    device and read back as the reference does (src/qutai/backends/cuda.py:189,
+    171-183)."""
+    return _binary(left, right, _DIVIDE)
+
+
+def add_into(target: AMDStorage, source: AMDStorage) -> None:
+    """target += source in place (src/qutai/backends/cuda.py:141-147)."""
+    if (target.device, target.dtype, target.size) != (source.device, source.dtype, source.size):
+        raise ValueError("add_into needs storages of one device, dtype and size")
+    if target.dtype == "int64":
+        raise ValueError("index storages take no gradient accumulation")
+    _binary(target, source, _ADD, out=target)
+
+
+def scale_into(values: AMDStorage, factor: float) -> None:
+    """values *= factor in place (src/qutai/backends/cuda.py:150-154)."""
+    if values.dtype == "int64":
+        raise ValueError("index storages take no scaling")
+    _unary(values, _SCALE, factor, out=values)
+
+
+def _real(value: float, dtype: str) -> float:
+    """``value`` as the kernel's arithmetic type sees it (fp32 for fp32/bf16)."""
+    return value if dtype == "float64" else struct.unpack("<f", struct.pack("<f", value))[0]
+
+
+def divide_scalar(values: AMDStorage, value: float) -> AMDStorage:
+    """values / value (src/qutai/backends/cuda.py:192-195); the divisor is
+    rounded to the arithmetic type first and a zero one raises
+    ZeroDivisionError on the host."""
+    divisor = _real(float(value), values.dtype)
+    if divisor == 0 and values.size:
+        raise ZeroDivisionError("division by zero")
+    return _unary(values, _DIVIDE_SCALAR, divisor)
+
+
+def negate(values):
+    return _unary(values, _NEGATE)
+
+
+def square(values):
+    return _unary(values, _SQUARE)
+
+
+def relu(values):
+    return _unary(values, _RELU)
+
+
+def relu_backward(gradient, values):
+    return _unary(values, _RELU_BACKWARD, gradient=gradient)
+
+
+def gelu(values):
+    return _unary(values, _GELU)
+
+
+def gelu_backward(gradient, values):
+    return _unary(values, _GELU_BACKWARD, gradient=gradient)
+
+
+def exp(values):
+    return _unary(values, _EXP)
+
+
+def log(values):
+    """Natural log; ValueError when some input is not positive
+    (src/qutai/backends/cuda.py:204, 157-168)."""
+    return _unary(values, _LOG)
+
+
+def tanh(values):
+    return _unary(values, _TANH)
+
+
+def atan(values):
+    return _unary(values, _ATAN)
+
+
+def tanh_backward(gradient, values):
+    return _unary(values, _TANH_BACKWARD, gradient=gradient)
+
+
+def atan_backward(gradient, values):
+    return _unary(values, _ATAN_BACKWARD, gradient=gradient)
+
+
+def add_widen(left: AMDStorage, right: AMDStorage) -> AMDStorage:
+    """fp32 left + bf16 right (exactly widened), fp32 result."""
+    if left.dtype != "float32" or right.dtype != "bfloat16" or left.size != right.size:
+        raise ValueError("add_widen takes float32 + bfloat16 storages of one size")
+    result = AMDStorage(left.size, "float32")
+    if left.size:
+        result.runtime.call("qutai_amd_add_widen", left.ptr, right.ptr, result.ptr, left.size)
     return result
 
 
 def scale(values: AMDStorage, factor: float) -> AMDStorage:
-    """values * factor (cuda.py:198)."""
+    """values * factor (src/qutai/backends/cuda.py:198)."""
     result = AMDStorage(values.size, values.dtype)
     if values.size:
         result.runtime.call("qutai_amd_scale", values.ptr, result.ptr, values.size, float(factor), code(values.dtype))
     return result
 
 
-def concatenate(values, shapes, axis=0) -> AMDStorage:
-    """Concatenation along ``axis`` (cuda.py:383-394): the pieces of every
-    outer index copied device to device, in order."""
-    rank = len(shapes[0])
-    axis = axis % rank
-    if len({v.dtype for v in values}) != 1 or any(len(s) != rank for s in shapes):
-        raise ValueError("concatenate needs storages of one dtype and shapes of one rank")
-    outer = prod(shapes[0][:axis])
-    sizes = [prod(shape[axis:]) for shape in shapes]
-    total = sum(sizes)
-    result = AMDStorage(outer * total, values[0].dtype)
-    item = _TYPES[values[0].dtype][1]
-    start = 0
-    for data, size in zip(values, sizes):
-        for o in range(outer):
-            if size:
-                result.runtime.copy(result.ptr + (o * total + start) * item, data.ptr + o * size * item, size * item)
-        start += size
-    return result
-
-
-def transpose(values: AMDStorage, shape, axes=None) -> AMDStorage:
-    """Axis permutation that swaps two adjacent axes: the last two (the form
-    the matmul gradient uses, src/qutai/core/operations/linalg.py:37-38) or
-    any other pair (the head split and merge of nn.MultiHeadAttention,
-    src/qutai/nn/layers.py:322-325, 354)."""
-    rank = len(shape)
-    axes = tuple(reversed(range(rank))) if axes is None else tuple(a % rank for a in axes)
-    if axes == tuple(range(rank)):
-        return values.copy()
-    swapped = [i for i in range(rank - 1) if axes[i] == i + 1 and axes[i + 1] == i]
-    if len(swapped) != 1 or any(axes[j] != j for j in range(rank) if j not in (swapped[0], swapped[0] + 1)):
-        raise NotImplementedError("amd transpose swaps two adjacent axes")
-    i = swapped[0]
-    if i < rank - 2:
-        result = AMDStorage(values.size, values.dtype)
-        if values.size:
-            result.runtime.call("qutai_amd_swap_axes", values.ptr, result.ptr, prod(shape[:i]), shape[i],
-                                shape[i + 1], prod(shape[i + 2:]), code(values.dtype))
+# reductions over one axis
+def _reduce(values: AMDStorage, outer: int, width: int, inner: int) -> AMDStorage:
+    result = AMDStorage(outer * inner, values.dtype)
+    if not result.size:
         return result
-    rows, cols = shape[-2], shape[-1]
-    batch = prod(shape[:-2])
-    result = AMDStorage(values.size, values.dtype)
-    if values.size:
-        result.runtime.call("qutai_amd_transpose_last2", values.ptr, result.ptr, batch, rows, cols,
-                            code(values.dtype))
+    runtime = get_runtime()
+    need = runtime.lib.qutai_amd_reduce_sum_workspace_size(outer, width, inner, code(values.dtype))
+    workspace = AMDStorage((need + 3) // 4, "float32") if need else None
+    runtime.call("qutai_amd_reduce_sum", values.ptr, result.ptr, outer, width, inner, code(values.dtype),
+                 _p(workspace), workspace.nbytes if workspace is not None else 0)
     return result
+
+
+def _axis_split(size: int, shape, axis) -> tuple[int, int, int]:
+    if axis is None:
+        return 1, size, 1
+    if shape is None:
+        raise ValueError("a sum over an axis needs the shape")
+    shape = tuple(shape)
+    axis = normalize_axis(axis, len(shape))
+    return prod(shape[:axis]), shape[axis], prod(shape[axis + 1:])
+
+
+def sum(values: AMDStorage, shape=None, axis=None) -> AMDStorage:  # noqa: A001 - the reference's name
+    """Sum of everything (axis None) or over one axis
+    (src/qutai/backends/cuda.py:265-274), fp32 accumulation (fp64 for fp64)."""
+    if values.dtype not in _FLOATS:
+        raise ValueError("sum takes real floating storages")
+    return _reduce(values, *_axis_split(values.size, shape, axis))
+
+
+def mean(values: AMDStorage, shape=None, axis=None) -> AMDStorage:
+    """Average over everything or one axis (src/qutai/backends/cuda.py:277-280)."""
+    count = _axis_split(values.size, shape, axis)[1]
+    if not count:
+        raise ValueError("the mean of no elements is undefined")
+    return scale(sum(values, shape, axis), 1 / count)
 
 
 def unbroadcast(values: AMDStorage, shape, target) -> AMDStorage:
-    """Sum a gradient of ``shape`` down to the broadcast source ``target``."""
+    """Sum a gradient of ``shape`` down to the broadcast source ``target``
+    (src/qutai/backends/cuda.py:283-289): every axis that ``target`` holds
+    as 1 (or lacks) is summed, keeping its place."""
     shape, target = tuple(shape), tuple(target)
     padded = (1,) * (len(shape) - len(target)) + target
     current, current_shape = values, shape
-    for axis in range(len(shape)):
-        if padded[axis] == 1 and current_shape[axis] != 1:
-            outer = prod(current_shape[:axis])
-            inner = prod(current_shape[axis + 1:])
-            reduced = AMDStorage(outer * inner, values.dtype)
-            if reduced.size:
-                reduced.runtime.call("qutai_amd_sum_middle", current.ptr, reduced.ptr, outer, current_shape[axis],
-                                     inner, code(values.dtype))
-            current = reduced
+    for axis, (length, original) in enumerate(zip(shape, padded)):
+        if original == 1 and length != 1:
+            current = sum(current, current_shape, axis)
             current_shape = current_shape[:axis] + (1,) + current_shape[axis + 1:]
-    return current if current is not values else values.copy()
+    return current
 
 
 def softmax(values: AMDStorage, shape, axis, *, scale: float = 1.0) -> AMDStorage:
-    """Stable softmax along the last axis (src/qutai/backends/cuda.py:464-472);
+    """Stable softmax along any axis (src/qutai/backends/cuda.py:464-472);
     ``scale`` multiplies the input first (the 1/sqrt(D) of attention scores)."""
-    axis %= len(shape)
-    if axis != len(shape) - 1:
-        raise NotImplementedError("amd softmax runs along the last axis")
-    width = shape[axis]
-    rows = values.size // width if width else 0
+    shape = tuple(shape)
+    axis = normalize_axis(axis, len(shape))
+    outer, width, inner = prod(shape[:axis]), shape[axis], prod(shape[axis + 1:])
     result = AMDStorage(values.size, values.dtype)
     if values.size:
-        result.runtime.call("qutai_amd_softmax_rows", values.ptr, result.ptr, rows, width, float(scale),
+        result.runtime.call("qutai_amd_softmax", values.ptr, result.ptr, outer, width, inner, float(scale),
                             code(values.dtype))
     return result
 
@@ -451,25 +772,14 @@ def add_rows(values: AMDStorage, bias: AMDStorage, rows: int, cols: int) -> AMDS
 
 def sum_rows(values: AMDStorage, rows: int, cols: int) -> AMDStorage:
     """Column sums of a [rows][cols] storage (gradient of a broadcast bias)."""
-    result = AMDStorage(cols, values.dtype)
-    if cols:
-        result.runtime.call("qutai_amd_sum_middle", values.ptr, result.ptr, 1, rows, cols, code(values.dtype))
-    return result
+    return _reduce(values, 1, rows, cols)
 
 
 def sum_all(values: AMDStorage) -> AMDStorage:
-    """Sum of all elements, in two parallel passes of about sqrt(n) each."""
-    n = values.size
-    if n == 0:
-        return full(1, 0.0, dtype=values.dtype)
-    width = max(1, isqrt(n))
-    while n % width:
-        width -= 1
-    partial = sum_rows(values, n // width, width)
-    return sum_rows(partial, width, 1) if width > 1 else partial
+    """Sum of all elements as a one-element storage."""
+    return _reduce(values, 1, values.size, 1)
 
 
 def broadcast_scalar(value: AMDStorage, size: int) -> AMDStorage:
     """A [size] storage holding the single element of ``value``."""
-    zeros = full(size, 0.0, dtype=value.dtype)
-    return add_rows(zeros, value, size, 1)
+    return broadcast(value, (1,), (size,))

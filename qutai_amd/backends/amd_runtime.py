@@ -26,7 +26,6 @@ LIBRARY = Path(__file__).resolve().parent.parent / "libqutai_amd.so"
 
 # hipDeviceAttribute_t values of ROCm 7 (hip_runtime_api.h)
 _ATTR_CC_MAJOR, _ATTR_CC_MINOR, _ATTR_CU_COUNT, _ATTR_CLOCK_KHZ = 23, 61, 63, 5
-_PROP_GCN_ARCH_OFFSET = 1160  # offsetof(hipDeviceProp_t (R0600), gcnArchName)
 _MEMCPY_H2D, _MEMCPY_D2H, _MEMCPY_D2D = 1, 2, 3
 _HIP_OOM = 2  # hipErrorOutOfMemory
 
@@ -79,9 +78,18 @@ SIGNATURES = {
     "qutai_amd_attention_bwd": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _i64, _i64, _i64, _i64, _i64, _i32,
                                 _i32, _f64, _i32, _p],
     "qutai_amd_attention_bwd_workspace_size": [_i64, _i64, _i64, _i64, _i64, _i32],
+    "qutai_amd_softmax": [_p, _p, _i64, _i64, _i64, _f64, _i32, _p],
+    "qutai_amd_strided_copy": [_p, _p, _i32, _p, _p, _p, _i32, _p],
+    "qutai_amd_binary": [_p, _p, _p, _i64, _i32, _i32, _p, _p],
+    "qutai_amd_unary": [_p, _p, _p, _i64, _i32, _f64, _i32, _p, _p],
+    "qutai_amd_reduce_sum": [_p, _p, _i64, _i64, _i64, _i32, _p, _sz, _p],
+    "qutai_amd_reduce_sum_workspace_size": [_i64, _i64, _i64, _i32],
+    "qutai_amd_gather": [_p, _p, _p, _i64, _i32, _p],
+    "qutai_amd_scatter": [_p, _p, _p, _p, _i64, _i32, _p],
+    "qutai_amd_device_arch": [_i32, ctypes.c_char_p, _sz],
 }
 RESTYPES = {"qutai_amd_gemm_workspace_size": _sz, "qutai_amd_rms_norm_workspace": _i64,
-            "qutai_amd_attention_bwd_workspace_size": _sz}
+            "qutai_amd_attention_bwd_workspace_size": _sz, "qutai_amd_reduce_sum_workspace_size": _sz}
 
 
 def _hip_library():
@@ -141,10 +149,9 @@ class Runtime:
         name = ctypes.create_string_buffer(256)
         self._check(self._device_name(name, len(name), self.device), "hipDeviceGetName")
         self.name = name.value.decode("utf8", "replace")
-        props = ctypes.create_string_buffer(8192)
-        self._check(self._device_props(props, self.device), "hipGetDeviceProperties")
-        arch = props.raw[_PROP_GCN_ARCH_OFFSET:_PROP_GCN_ARCH_OFFSET + 256].split(b"\0", 1)[0]
-        self.arch = arch.decode("ascii", "replace")
+        arch = ctypes.create_string_buffer(256)
+        self._check(self.lib.qutai_amd_device_arch(self.device, arch, len(arch)), "hipGetDeviceProperties")
+        self.arch = arch.value.decode("ascii", "replace")
         self.compute_capability = (self._attribute(_ATTR_CC_MAJOR), self._attribute(_ATTR_CC_MINOR))
         self.cu_count = self._attribute(_ATTR_CU_COUNT)
         self.clock_khz = self._attribute(_ATTR_CLOCK_KHZ)
@@ -178,7 +185,6 @@ class Runtime:
         self._device_count = bind("hipGetDeviceCount", [ctypes.POINTER(ctypes.c_int)])
         self._set_device = bind("hipSetDevice", [ctypes.c_int])
         self._device_name = bind("hipDeviceGetName", [ctypes.c_char_p, ctypes.c_int, ctypes.c_int])
-        self._device_props = bind("hipGetDevicePropertiesR0600", [vp, ctypes.c_int])
         self._device_attribute = bind("hipDeviceGetAttribute", [ctypes.POINTER(ctypes.c_int), ctypes.c_int,
                                                                 ctypes.c_int])
         self._driver_version = bind("hipDriverGetVersion", [ctypes.POINTER(ctypes.c_int)])

@@ -54,3 +54,31 @@ def broadcast_shape(left: tuple[int, ...], right: tuple[int, ...]) -> tuple[int,
 def strides(shape: tuple[int, ...]) -> tuple[int, ...]:
     """Contiguous strides in elements (src/qutai/core/shape.py:52-54)."""
     return tuple(prod(shape[axis + 1:]) for axis in range(len(shape)))
+
+
+def normalize_axis(axis: int, rank: int) -> int:
+    """Axis in [-rank, rank) as a non-negative index; ValueError otherwise
+    (src/qutai/core/shape.py:103-106)."""
+    if not -rank <= axis < rank:
+        raise ValueError(f"axis {axis} is out of range for {rank} dimensions")
+    return axis % rank
+
+
+def reduced_shape(shape: tuple[int, ...], axis: int | None = None, keepdims: bool = False) -> tuple[int, ...]:
+    """Shape after a reduction over ``axis`` (all axes when None)
+    (src/qutai/core/shape.py:109-114)."""
+    if axis is None:
+        return (1,) * len(shape) if keepdims else ()
+    axis = normalize_axis(axis, len(shape))
+    return shape[:axis] + ((1,) if keepdims else ()) + shape[axis + 1:]
+
+
+def transpose_axes(rank: int, axes=None) -> tuple[int, ...]:
+    """A full permutation of ``rank`` axes (reversed when None); ValueError
+    unless every axis appears once (src/qutai/core/shape.py:131-136)."""
+    if axes is None:
+        return tuple(range(rank - 1, -1, -1))
+    order = tuple(normalize_axis(axis, rank) for axis in axes)
+    if len(order) != rank or len(set(order)) != rank:
+        raise ValueError("a transpose needs every axis exactly once")
+    return order

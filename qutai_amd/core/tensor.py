@@ -1,15 +1,16 @@
 """Tensor front-end for the GEMM path (src/qutai/core/tensor.py:14-278).
 
-Only what the contraction path needs: construction from nested lists or a
-device storage, ``@`` / ``matmul`` with autograd, same-shape ``+`` and the
-broadcast bias add of ``nn.Linear``, ``sum``, ``to(dtype=)`` casts,
-``reshape``, last-two-axes ``transpose``, ``backward`` with leaf gradient
-accumulation, ``tolist`` / ``item`` reads.
+Construction from nested lists or a device storage, ``@`` / ``matmul``
+with autograd, broadcasting ``+ - * /`` (a scalar divisor divides in one
+kernel), negation, basic indexing, ``sum`` / ``mean`` over everything or
+one axis, ``softmax``, the element-wise functions of the reference Tensor,
+``to(dtype=)`` casts, ``reshape``, any ``transpose``, ``concatenate``,
+``backward`` with leaf gradient accumulation, ``tolist`` / ``item`` reads.
 """
 from __future__ import annotations
 
 from functools import partial
-from math import isqrt, prod
+from math import prod
 
 from ..backends.device import default_dtype, get_backend, transfer
 from ..backends.storage import Storage
@@ -71,32 +72,71 @@ class Tensor:
 
     def __add__(self, other):
         other = _as_tensor(other, self)
-        return _result(_add(self, other), (self, other))
+        return _result(operations.add(self, other), (self, other))
 
     def __radd__(self, other):
         other = _as_tensor(other, self)
-        return _result(_add(other, self), (other, self))
+        return _result(operations.add(other, self), (other, self))
 
-    def sum(self):
-        return _result(_sum(self), (self,))
+    def __sub__(self, other):
+        other = _as_tensor(other, self)
+        return _result(operations.subtract(self, other), (self, other))
+
+    def __rsub__(self, other):
+        other = _as_tensor(other, self)
+        return _result(operations.subtract(other, self), (other, self))
+
+    def __mul__(self, other):
+        other = _as_tensor(other, self)
+        return _result(operations.multiply(self, other), (self, other))
+
+    def __rmul__(self, other):
+        other = _as_tensor(other, self)
+        return _result(operations.multiply(other, self), (other, self))
+
+    def __truediv__(self, other):
+        if isinstance(other, (int, float)) and not isinstance(other, bool):
+            # a scalar divisor needs no broadcast tensor (src/qutai/core/tensor.py:119-121)
+            return _result(operations.divide_scalar(self, other), (self,))
+        other = _as_tensor(other, self)
+        return _result(operations.divide(self, other), (self, other))
+
+    def __rtruediv__(self, other):
+        other = _as_tensor(other, self)
+        return _result(operations.divide(other, self), (other, self))
+
+    def __neg__(self):
+        return _result(operations.negate(self), (self,))
+
+    def __getitem__(self, index):
+        return _result(operations.select(self, index), (self,))
+
+    def sum(self, axis=None, keepdims=False):
+        return _result(operations.sum(self, axis=axis, keepdims=keepdims), (self,))
+
+    def mean(self, axis=None, keepdims=False):
+        return _result(operations.mean(self, axis=axis, keepdims=keepdims), (self,))
+
+    def square(self):
+        return _result(operations.square(self), (self,))
+
+    def exp(self):
+        return _result(operations.exp(self), (self,))
+
+    def log(self):
+        return _result(operations.log(self), (self,))
+
+    def tanh(self):
+        return _result(operations.tanh(self), (self,))
+
+    def atan(self):
+        return _result(operations.atan(self), (self,))
 
     def reshape(self, shape):
-        shape = tuple(shape)
-        if -1 in shape:
-            known = prod(s for s in shape if s != -1)
-            shape = tuple(self.size // known if s == -1 else s for s in shape)
-        if prod(shape) != self.size:
-            raise ValueError("reshape must keep the element count")
-        return _result((self.storage.copy(), shape, lambda g: (g,)), (self,))
+        return _result(operations.reshape(self, shape), (self,))
 
     def transpose(self, axes=None):
-        rank = self.ndim
-        axes = tuple(reversed(range(rank))) if axes is None else tuple(a % rank for a in axes)
-        target = tuple(self.shape[a] for a in axes)
-        backend = get_backend(self.device)
-        values = backend.transpose(self.storage, self.shape, axes=axes)
-        inverse = tuple(axes.index(a) for a in range(rank))
-        return _result((values, target, lambda g: (backend.transpose(g, target, axes=inverse),)), (self,))
+        return _result(operations.transpose(self, axes), (self,))
 
     @property
     def T(self):
@@ -134,6 +174,8 @@ class Tensor:
             gradient = _as_tensor(gradient, self)
             if gradient.shape != self.shape:
                 raise ValueError("output gradient shape differs from the Tensor's")
+            if gradient.device != self.device or gradient.dtype != self.dtype:
+                raise ValueError("output gradient device and dtype must be the Tensor's")
             seed = gradient.storage
 
         created = set()  # leaves whose grad storage this pass made: no one else holds it
@@ -160,32 +202,6 @@ class Tensor:
         return f"Tensor({self.tolist()!r})"
 
 
-def _add(left, right):
-    """Same-shape add, or a bias broadcast over the leading axes (last axis equal)."""
-    backend = get_backend(left.storage, right.storage)
-    if left.shape == right.shape:
-        return backend.add(left.storage, right.storage), left.shape, lambda g: (g, g)
-    for big, small, swap in ((left, right, False), (right, left, True)):
-        if small.ndim == 1 and big.ndim >= 1 and big.shape[-1] == small.shape[0]:
-            cols = small.shape[0]
-            rows = big.size // cols if cols else 0
-            values = backend.add_rows(big.storage, small.storage, rows, cols)
-
-            def rule(g, rows=rows, cols=cols, swap=swap):
-                reduced = backend.sum_rows(g, rows, cols)
-                return (reduced, g) if swap else (g, reduced)
-
-            return values, big.shape, rule
-    raise ValueError(f"add supports equal shapes or a trailing-axis bias, got {left.shape} and {right.shape}")
-
-
-def _sum(x):
-    backend = get_backend(x.storage)
-    values = backend.sum_all(x.storage)
-    size = x.size
-    return values, (), lambda g: (backend.broadcast_scalar(g, size),)
-
-
 def _as_tensor(data, like=None):
     if isinstance(data, Tensor):
         if like is not None:
@@ -203,13 +219,64 @@ def _output(result, *inputs):
     return result if any(isinstance(data, Tensor) for data in inputs) else result.tolist()
 
 
+def _pair(left, right):
+    like = left if isinstance(left, Tensor) else right if isinstance(right, Tensor) else None
+    return _as_tensor(left, like), _as_tensor(right, like)
+
+
 def matmul(left, right):
     """Vector / matrix / batched product (src/qutai/core/tensor.py:275-278)."""
-    like = left if isinstance(left, Tensor) else right if isinstance(right, Tensor) else None
-    a, b = _as_tensor(left, like), _as_tensor(right, like)
+    a, b = _pair(left, right)
     return _output(a @ b, left, right)
 
 
-def sum(x):  # noqa: A001 - mirrors qutai.sum
+def add(left, right):
+    a, b = _pair(left, right)
+    return _output(a + b, left, right)
+
+
+def subtract(left, right):
+    a, b = _pair(left, right)
+    return _output(a - b, left, right)
+
+
+def multiply(left, right):
+    a, b = _pair(left, right)
+    return _output(a * b, left, right)
+
+
+def divide(left, right):
+    if isinstance(right, (int, float)) and not isinstance(right, bool):
+        return _output(_as_tensor(left) / right, left, right)
+    a, b = _pair(left, right)
+    return _output(a / b, left, right)
+
+
+def sum(x, axis=None, keepdims=False):  # noqa: A001 - mirrors qutai.sum
     tensor = _as_tensor(x)
-    return _output(tensor.sum(), x)
+    return _output(tensor.sum(axis, keepdims), x)
+
+
+def mean(x, axis=None, keepdims=False):
+    tensor = _as_tensor(x)
+    return _output(tensor.mean(axis, keepdims), x)
+
+
+def softmax(x, axis=-1):
+    tensor = _as_tensor(x)
+    return _output(_result(operations.softmax(tensor, axis), (tensor,)), x)
+
+
+def relu(x):
+    tensor = _as_tensor(x)
+    return _output(_result(operations.relu(tensor), (tensor,)), x)
+
+
+def gelu(x):
+    tensor = _as_tensor(x)
+    return _output(_result(operations.gelu(tensor), (tensor,)), x)
+
+
+def concatenate(tensors, axis=0):
+    items = tuple(_as_tensor(t, tensors[0] if isinstance(tensors[0], Tensor) else None) for t in tensors)
+    return _output(_result(operations.concatenate(items, axis), items), *tensors)

@@ -475,6 +475,9 @@ int qutai_amd_gemm_grouped(const void* a, const void* b, void* out, const int64_
   p.out_bf16 = out_dtype == QA_BF16;
   int64_t E = dtype == QA_BF16 ? 8 : 4;
   if ((uintptr_t)a % 16 || (uintptr_t)b % 16 || inner % E || p.ldb % E || expert_stride % E) return QA_EINVAL;
+  // a 256-row tile's operand range must fit the 31-bit buffer descriptor
+  const int64_t es = dtype == QA_BF16 ? 2 : 4;
+  if ((p.lda * 256 * es) >= (1ll << 31) || (p.ldb * 256 * es) >= (1ll << 31)) return QA_EINVAL;
   p.vec_c = vec_out(out, p.ldc, 0);
   p.offsets = offsets;
   p.groups = groups;

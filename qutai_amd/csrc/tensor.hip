@@ -2,6 +2,8 @@
 // fills, adds, batch reductions, last-two-axes transpose, row softmax and
 // SwiGLU's silu(gate) * up.  Reference counterparts are cited per entry
 // point in include/qutai_amd.h.
+#include <algorithm>
+
 #include "common.h"
 #include "qutai_amd.h"
 
@@ -412,6 +414,34 @@ __global__ void softmax_rows_f64(const double* x, double* out, int64_t rows, int
   for (int64_t at = tid; at < width; at += THREADS) yr[at] = exp(xr[at] * scale - peak) / total;
 }
 
+// Softmax along an axis that is not the last: x viewed as
+// [outer][width][inner], one lane per (o, j) column, consecutive lanes on
+// consecutive j so every pass over the axis is coalesced.  Three passes
+// (max, sum of exp, write), as the reference's softmax_forward
+// (src/qutai/backends/cuda/nn.cu:67-76), in fp32 (fp64 for fp64).
+template <class T, class R>
+__global__ void __launch_bounds__(THREADS) softmax_cols_kernel(const T* x, T* out, int64_t outer, int64_t width,
+                                                               int64_t inner, R scale) {
+  auto load = [&](int64_t i) -> R {
+    if constexpr (sizeof(T) == 2) return (R)bf16_to_f32(x[i]) * scale;
+    else return (R)x[i] * scale;
+  };
+  const int64_t total = outer * inner;
+  for (int64_t i = (int64_t)blockIdx.x * THREADS + threadIdx.x; i < total; i += (int64_t)gridDim.x * THREADS) {
+    const int64_t base = (i / inner) * width * inner + i % inner;
+    R peak = load(base);
+    for (int64_t c = 1; c < width; c++) peak = fmax(peak, load(base + c * inner));
+    R sum = 0;
+    for (int64_t c = 0; c < width; c++) sum += exp(load(base + c * inner) - peak);
+    const R inv = R(1) / sum;
+    for (int64_t c = 0; c < width; c++) {
+      const R v = exp(load(base + c * inner) - peak) * inv;
+      if constexpr (sizeof(T) == 2) out[base + c * inner] = f32_to_bf16((float)v);
+      else out[base + c * inner] = (T)v;
+    }
+  }
+}
+
 // silu(gate) * up with silu_f (common.h).  With bf16 storage the silu output
 // is itself a bf16 tensor before the multiply (two roundings), as in the
 // unfused SwiGLU of the reference.
@@ -686,6 +716,27 @@ int qutai_amd_softmax_rows(const void* x, void* out, int64_t rows, int64_t width
       hipLaunchKernelGGL((softmax_rows_kernel<bf16_t, 8>), dim3((unsigned)rows), dim3(THREADS), 0, s,
                          (const bf16_t*)x, (bf16_t*)out, rows, width, (float)scale);
   }
+  return (int)hipGetLastError();
+}
+
+int qutai_amd_softmax(const void* x, void* out, int64_t outer, int64_t width, int64_t inner, double scale,
+                      int dtype, void* stream) {
+  if (outer < 0 || width < 0 || inner < 1 || !float_dtype(dtype)) return QA_EINVAL;
+  if (inner == 1) return qutai_amd_softmax_rows(x, out, outer, width, scale, dtype, stream);
+  if (outer == 0 || width == 0) return QA_OK;
+  if (!x || !out) return QA_EINVAL;
+  const int64_t columns = outer * inner;
+  const unsigned blocks = (unsigned)std::min<int64_t>((columns + THREADS - 1) / THREADS, 65536);
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == F64)
+    hipLaunchKernelGGL((softmax_cols_kernel<double, double>), dim3(blocks), dim3(THREADS), 0, s, (const double*)x,
+                       (double*)out, outer, width, inner, scale);
+  else if (dtype == F32)
+    hipLaunchKernelGGL((softmax_cols_kernel<float, float>), dim3(blocks), dim3(THREADS), 0, s, (const float*)x,
+                       (float*)out, outer, width, inner, (float)scale);
+  else
+    hipLaunchKernelGGL((softmax_cols_kernel<bf16_t, float>), dim3(blocks), dim3(THREADS), 0, s, (const bf16_t*)x,
+                       (bf16_t*)out, outer, width, inner, (float)scale);
   return (int)hipGetLastError();
 }
 

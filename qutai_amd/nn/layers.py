@@ -11,7 +11,11 @@ sqrt(D)) V per head, optional causal mask.  The forward runs the fused
 attention kernels on the projections as they are ((batch, length, heads *
 dim) is the lm layout), so the length x length scores are never stored;
 ``weights`` materialises them (batched NT GEMM, mask, row softmax) like the
-reference.  Inference with a KV cache is not part of this path.
+reference.  ``MultiHeadAttention(..., cache=KVCache())`` runs causal
+inference over new positions only: their projections, the cached keys and
+values appended, the score product against every cached key with the
+causal mask shifted by the cached length, softmax and the value product, all
+with graph recording off (src/qutai/nn/layers.py:334-355).
 """
 from __future__ import annotations
 
@@ -19,8 +23,11 @@ from math import sqrt
 from random import Random
 
 from ..backends import amd, amd_lm
+from ..core import operations
+from ..core.context import set_recording
 from ..core.grad import record
-from ..core.tensor import Tensor, matmul
+from ..core.tensor import Tensor, _result, matmul
+from .cache import KVCache  # noqa: F401 - the reference exposes it beside the layers
 
 
 def _tensor(data, like):
@@ -28,10 +35,11 @@ def _tensor(data, like):
 
 
 def softmax(x, axis=-1, *, scale=1.0):
-    """softmax(scale * x) along the last axis, recorded (qutai.softmax,
-    src/qutai/core/operations/normalization.py:9-25)."""
+    """softmax(scale * x) along ``axis``, recorded (qutai.softmax,
+    src/qutai/core/operations/normalization.py:9-25); along the last axis
+    the scale is folded into the kernel and the backward is one fused pass."""
     if axis % x.ndim != x.ndim - 1:
-        raise NotImplementedError("amd softmax runs along the last axis")
+        return _result(operations.softmax(x if scale == 1.0 else x * scale, axis), (x,))
     if x.shape[-1] == 0:
         raise ValueError("softmax needs a non-empty axis")
     values = amd.softmax(x.storage, x.shape, -1, scale=scale)
@@ -118,9 +126,9 @@ class Attention:
 
     def _mix(self, q, k, v):
         """Per-head softmax(Q K^T / sqrt(D)) V, merged back to (batch, length,
-        features): the fused kernels up to 256 per head, beyond that the
-        score and value products."""
-        if q.shape[-1] // self.heads <= 256:
+        features): the fused kernels for bf16/fp32 up to 256 per head,
+        otherwise (fp64, larger heads) the score and value products."""
+        if q.shape[-1] // self.heads <= 256 and q.dtype in ("bfloat16", "float32"):
             return _attend(q, k, v, self.heads, self.causal)
         weights = self._probabilities(q, k)
         if self.heads == 1:
@@ -148,10 +156,24 @@ class MultiHeadAttention(Attention):
         self.output = Linear(features, features, seed=None if seed is None else seed + 3, device=device, dtype=dtype)
 
     def __call__(self, data, *, cache=None):
-        if cache is not None:
-            raise NotImplementedError("KV-cache inference is not part of the amd attention path")
-        tensor = self._input(data)
-        return self.output(self._mix(*(layer(tensor) for layer in (self.query, self.key, self.value))))
+        """Training/full forward through the fused kernels; with ``cache``
+        (causal only) inference over the new positions, recording off."""
+        if cache is not None and not self.causal:
+            raise ValueError("a KV cache serves causal attention inference only")
+        if cache is None:
+            tensor = self._input(data)
+            return self.output(self._mix(*(layer(tensor) for layer in (self.query, self.key, self.value))))
+        with set_recording(False):
+            tensor = self._input(data)
+            queries, keys, values = (self._split(layer(tensor)) for layer in (self.query, self.key, self.value))
+            keys, values = cache.update(keys, values)
+            length, total = queries.shape[2], keys.shape[2]
+            scores = matmul(queries, keys.transpose((0, 1, 3, 2)))
+            probabilities = softmax(causal_mask(scores, offset=total - length), -1,
+                                    scale=1 / sqrt(queries.shape[-1]))
+            mixed = matmul(probabilities, values)
+            batch, _, features = tensor.shape
+            return self.output(mixed.transpose((0, 2, 1, 3)).reshape((batch, length, features)))
 
     def parameters(self):
         return tuple(dict.fromkeys((*super().parameters(), *self.output.parameters())))

@@ -68,3 +68,42 @@ def test_bindings_apply_without_a_device():
     # RMSNorm backward partial sums: one row of floats per 16 rows
     rms = library.qutai_amd_rms_norm_workspace
     assert rms(4096, 2048) == 256 * 2048 and rms(65, 8) == 5 * 8 and rms(0, 8) == 0
+
+
+@pytest.mark.skipif(not LIBRARY.exists(), reason="libqutai_amd.so not built")
+def test_argument_checks_reject_before_any_device_call():
+    """Entry points validate on the host and return QA_EINVAL (-1) before
+    they launch anything, so these calls with stand-in pointers never reach
+    a device."""
+    from qutai_amd.backends import amd_runtime
+
+    library = amd_runtime.load_library()
+    fake = 1 << 20  # a 16-byte aligned stand-in address, never dereferenced
+    # grouped expert GEMM: a 256-row tile of a 2^23-wide bf16 operand spans
+    # 2^32 bytes, beyond the 31-bit buffer descriptor range
+    assert library.qutai_amd_gemm_grouped(fake, fake, fake, fake, 8, 512, 1 << 23, 64, 0, 1, 5, 5, 0, None) == -1
+    # strided copy: rank above 8, or an element size other than 2/4/8
+    dims = (ctypes.c_int64 * 9)(*([2] * 9))
+    assert library.qutai_amd_strided_copy(fake, fake, 9, dims, dims, dims, 4, None) == -1
+    assert library.qutai_amd_strided_copy(fake, fake, 1, dims, dims, dims, 3, None) == -1
+    # binary / unary op codes out of range; a backward without its gradient
+    assert library.qutai_amd_binary(fake, fake, fake, 8, 4, 0, None, None) == -1
+    assert library.qutai_amd_unary(fake, None, fake, 8, 14, 1.0, 0, None, None) == -1
+    assert library.qutai_amd_unary(fake, None, fake, 8, 4, 0.0, 0, None, None) == -1
+    # reduction over [outer][width][inner] needs inner >= 1 and a float dtype
+    assert library.qutai_amd_reduce_sum(fake, fake, 1, 8, 0, 0, None, 0, None) == -1
+    assert library.qutai_amd_reduce_sum(fake, fake, 1, 8, 1, 4, None, 0, None) == -1
+
+
+@pytest.mark.skipif(not LIBRARY.exists(), reason="libqutai_amd.so not built")
+def test_reduction_workspace_plan():
+    """Long sums split into parts whose fp32 partials need a workspace; short
+    or plentiful sums run in one pass."""
+    from qutai_amd.backends import amd_runtime
+
+    size = amd_runtime.load_library().qutai_amd_reduce_sum_workspace_size
+    assert size(4096, 2048, 1, 0) == 0  # 4096 rows: one wave per row is enough
+    assert size(1, 1 << 22, 1, 0) == 1024 * 4  # one long row: 1024 parts of 4096
+    assert size(1, 1 << 22, 1, 1) == 1024 * 8  # fp64 partials
+    assert size(1, 4096, 2048, 0) == 32 * 2048 * 4  # 2048 columns of 4096: 32 parts of 128
+    assert size(4, 100, 1, 0) == 0

@@ -68,12 +68,16 @@ class FakeBackend:
         return FakeBackend.Store(np.matmul(a, b), left.dtype)
 
     @staticmethod
-    def gemm(a, b, rows, inner, cols, *, batch=1, transpose_left=False, transpose_right=False, out_dtype=None,
-             **_):
-        A = a.values.reshape(batch, inner, rows).transpose(0, 2, 1) if transpose_left else a.values.reshape(
-            batch, rows, inner)
-        B = b.values.reshape(batch, cols, inner).transpose(0, 2, 1) if transpose_right else b.values.reshape(
-            batch, inner, cols)
+    def gemm(a, b, rows, inner, cols, *, batch=1, transpose_left=False, transpose_right=False, left_stride=None,
+             right_stride=None, out_dtype=None, **_):
+        def operand(values, stride, shape, dense):
+            stride = dense if stride is None else stride
+            return np.stack([values[z * stride:z * stride + dense].reshape(shape) for z in range(batch)])
+
+        A = operand(a.values, left_stride, (inner, rows) if transpose_left else (rows, inner), rows * inner)
+        B = operand(b.values, right_stride, (cols, inner) if transpose_right else (inner, cols), inner * cols)
+        A = A.transpose(0, 2, 1) if transpose_left else A
+        B = B.transpose(0, 2, 1) if transpose_right else B
         return FakeBackend.Store(A @ B, out_dtype or a.dtype)
 
     @staticmethod
@@ -90,12 +94,16 @@ class FakeBackend:
         return FakeBackend.Store(v, values.dtype)
 
     @staticmethod
-    def sum_all(values):
-        return FakeBackend.Store([values.values.sum()], values.dtype)
+    def sum(values, shape=None, axis=None):
+        if axis is None:
+            return FakeBackend.Store([values.values.sum()], values.dtype)
+        return FakeBackend.Store(values.values.reshape(shape).sum(axis=axis), values.dtype)
 
     @staticmethod
-    def broadcast_scalar(value, size):
-        return FakeBackend.Store(np.full(size, value.values[0]), value.dtype)
+    def broadcast(values, shape, target):
+        if tuple(shape) == tuple(target):
+            return values
+        return FakeBackend.Store(np.broadcast_to(values.values.reshape(shape), target).copy(), values.dtype)
 
 
 @pytest.fixture

@@ -62,8 +62,9 @@ def test_rows_are_probabilities_and_input_must_be_3d(amd):
                                         dtype="float32")).storage).reshape(2, 2, 5, 5)
     assert np.allclose(probs.sum(axis=-1), 1, atol=1e-6)
     assert (probs[..., np.triu_indices(5, 1)[0], np.triu_indices(5, 1)[1]] == 0).all()
-    with pytest.raises(NotImplementedError):
-        mha(Tensor([[[0.0] * 8]], device="amd", dtype="float32"), cache=object())
+    with pytest.raises(ValueError):  # a cache serves causal attention only (nn/layers.py:346)
+        nn.MultiHeadAttention(8, heads=2, seed=1)(Tensor([[[0.0] * 8]], device="amd", dtype="float32"),
+                                                   cache=nn.KVCache())
     with pytest.raises(ValueError):
         nn.MultiHeadAttention(8, heads=3)
 

@@ -522,3 +522,92 @@ def test_head_loss_and_gradient_closed_forms():
     g = ora.head_gradient(z, [1, 3], 2, vocab, [1.0], 1)
     for i in range(len(z)):
         assert g[i] == pytest.approx(_fd(lambda v: ora.head_loss(v, [1, 3], 2, vocab), z, i), rel=1e-6, abs=1e-9)
+
+
+# ---- generic tensor functions (broadcast, transpose, sums, element-wise) ---------------
+
+def test_generic_ops_golden_vectors():
+    # tests/test_operations.py:19-28 (broadcast arithmetic)
+    assert ora.binary([1, 2, 3, 4, 5, 6], ora.broadcast([10, 20, 30], (3,), (2, 3)), "add") == [11, 22, 33, 14, 25,
+                                                                                               36]
+    assert ora.binary(ora.broadcast([1, 2], (2, 1), (2, 3)), ora.broadcast([10, 20, 30], (3,), (2, 3)),
+                      "multiply") == [10, 20, 30, 20, 40, 60]
+    assert ora.binary(ora.broadcast([10], (), (2,)), [1, 2], "subtract") == [9, 8]
+    assert ora.binary([3, 8], [2, 4], "divide") == [1.5, 2]
+    assert ora.binary([1, 2, 3, 4], ora.broadcast([10, 20], (2,), (2, 1, 2)), "add") == [11, 22, 13, 24]
+    # tests/test_operations.py:30-33 (unary)
+    assert ora.unary([1, -2], "negate") == [-1, 2]
+    assert ora.unary([1, -2, 3, -4], "square") == [1, 4, 9, 16]
+    assert ora.unary([-2, 0, 3], "relu") == [0, 0, 3]
+    # tests/test_operations.py:35-40, 54-61 (transpose)
+    assert ora.transpose([1, 2, 3, 4, 5, 6], (2, 3)) == [1, 4, 2, 5, 3, 6]
+    assert ora.transpose(list(range(1, 13)), (2, 2, 3), (0, 2, 1)) == [1, 4, 2, 5, 3, 6, 7, 10, 8, 11, 9, 12]
+    # tests/test_operations.py:63-73 (reductions), :75-79 (empty axes)
+    data, shape = [1, 2, 3, 4, 5, 6], (2, 3)
+    assert ora.reduce_sum(data) == [21]
+    assert ora.reduce_sum(data, shape, 0) == [5, 7, 9]
+    assert ora.reduce_sum(data, shape, -1) == [6, 15]
+    assert ora.mean(data) == [3.5]
+    assert ora.mean(data, shape, 0) == [2.5, 3.5, 4.5]
+    assert ora.mean(data, shape, 1) == [2, 5]
+    assert ora.reduce_sum([]) == [0]
+    assert ora.reduce_sum([], (2, 0), 1) == [0, 0]
+    assert ora.mean([], (2, 0), 0) == []
+    with pytest.raises(ValueError):
+        ora.mean([], (2, 0), 1)
+    # tests/test_attention_cache.py:40-47 (append along the length axis)
+    keys = ora.concatenate(([1, 2, 3, 4], [5, 6, 7, 8]), ((2, 2, 1, 1), (2, 2, 1, 1)), axis=2)
+    assert keys == [1, 5, 2, 6, 3, 7, 4, 8]
+
+
+def test_generic_ops_against_numpy_and_closed_forms():
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((3, 4, 5))
+    flat = x.ravel().tolist()
+    for axes in ((2, 0, 1), (1, 2, 0), (0, 2, 1), None):
+        expected = np.transpose(x, axes).ravel()
+        got = ora.transpose(flat, x.shape, axes)
+        assert got == expected.tolist()
+        # the inverse permutation restores the input
+        order = tuple(reversed(range(3))) if axes is None else axes
+        inverse = tuple(order.index(a) for a in range(3))
+        assert ora.transpose(got, tuple(x.shape[a] for a in order), inverse) == flat
+    for axis in (0, 1, 2, -1):
+        np.testing.assert_allclose(ora.reduce_sum(flat, x.shape, axis), x.sum(axis=axis).ravel(), rtol=1e-13)
+    np.testing.assert_allclose(ora.broadcast([1.0, 2.0, 3.0, 4.0], (4, 1), (2, 4, 3)),
+                               np.broadcast_to(np.arange(1.0, 5.0).reshape(4, 1), (2, 4, 3)).ravel())
+    # unbroadcast(broadcast(v)) = v times the number of copies
+    source = rng.standard_normal((4, 1))
+    wide = ora.broadcast(source.ravel().tolist(), (4, 1), (2, 4, 3))
+    np.testing.assert_allclose(ora.unbroadcast(wide, (2, 4, 3), (4, 1)), 6 * source.ravel(), rtol=1e-13)
+    # scatter adds repeated positions; gather(scatter) over distinct positions is the identity
+    positions = [3, 0, 3, 1, 3]
+    values = [1.0, 2.0, 4.0, 8.0, 16.0]
+    expected = np.zeros(5)
+    np.add.at(expected, positions, values)
+    assert ora.scatter(values, positions, 5) == expected.tolist()
+    assert ora.gather(ora.scatter([5.0, 6.0], [4, 1], 5), [4, 1]) == [5.0, 6.0]
+    np.testing.assert_array_equal(ora.concatenate((flat[:20], flat[20:]), ((1, 4, 5), (2, 4, 5)), 0), flat)
+    a, b = x[:, :1], x[:, 1:]
+    np.testing.assert_array_equal(ora.concatenate((a.ravel().tolist(), b.ravel().tolist()), (a.shape, b.shape), 1),
+                                  flat)
+    # closed forms of the element-wise functions
+    assert ora.unary([0.0], "gelu") == [0.0] and ora.unary([0.0], "gelu_backward", gradient=[1.0]) == [0.5]
+    v = rng.standard_normal(7).tolist()
+    np.testing.assert_allclose(ora.unary(ora.unary(v, "exp"), "log"), v, rtol=1e-13, atol=1e-15)
+    np.testing.assert_allclose(ora.unary(v, "tanh_backward", gradient=[1.0] * 7), 1 - np.tanh(v) ** 2, rtol=1e-13)
+    np.testing.assert_allclose(ora.unary(v, "atan_backward", gradient=[2.0] * 7), 2 / (1 + np.square(v)),
+                               rtol=1e-13)
+    np.testing.assert_allclose(ora.unary(v, "divide_scalar", factor=4.0), np.array(v) / 4, rtol=0)
+    # gelu against its definition through the normal CDF: x * Phi(x)
+    from statistics import NormalDist
+    np.testing.assert_allclose(ora.unary(v, "gelu"), [t * NormalDist().cdf(t) for t in v], rtol=1e-12, atol=1e-15)
+    # gelu' from central differences of gelu
+    h = 1e-6
+    numeric = (np.array(ora.unary([t + h for t in v], "gelu")) - np.array(ora.unary([t - h for t in v], "gelu"))) / (
+        2 * h)
+    np.testing.assert_allclose(ora.unary(v, "gelu_backward", gradient=[1.0] * 7), numeric, rtol=1e-7, atol=1e-9)
+    # softmax over a middle axis against numpy
+    s = np.array(ora.softmax(flat, x.shape, 1)).reshape(x.shape)
+    e = np.exp(x - x.max(axis=1, keepdims=True))
+    np.testing.assert_allclose(s, e / e.sum(axis=1, keepdims=True), rtol=1e-13)
