@@ -32,6 +32,7 @@ extern "C" {
 #define QA_OK 0
 #define QA_EINVAL (-1)     /* shapes, strides, dtypes or pointers rejected */
 #define QA_EWORKSPACE (-2) /* workspace missing or too small */
+#define QA_ESCRATCH (-3)   /* needs more than the fixed scratch of qutai_amd_gemm_static */
 
 /* The gcnArchName of HIP device `device` (e.g. "gfx950:sramecc+:xnack-"),
  * NUL-terminated into name[size].  Replaces the compute-capability query of
@@ -60,6 +61,27 @@ int qutai_amd_gemm(const void* a, const void* b, void* out, int64_t rows, int64_
                    int64_t batch, int64_t left_stride, int64_t right_stride, int transpose_left,
                    int transpose_right, int a_dtype, int b_dtype, int out_dtype, int accumulate,
                    int bf16_compute, void* workspace, size_t workspace_bytes, void* stream);
+
+/* qutai_amd_gemm without a workspace argument and without any allocation:
+ * the workspace it needs (see qutai_amd_gemm_workspace_size) is a fixed
+ * array in device memory of qutai_amd_gemm_static_capacity() bytes
+ * (128 MiB) per GPU, held by the library until the process ends; the
+ * caller still passes inputs and output.  Results are bit-identical to
+ * qutai_amd_gemm (same kernels).  Returns QA_ESCRATCH when the operands need
+ * more workspace than that (e.g. fp32 operands into the bf16 path of more
+ * than 64 Mi elements together), before launching anything.  Every call on
+ * one GPU shares that GPU's array, so calls that overlap on one GPU (two
+ * streams, two host threads) race; calls in one stream are ordered.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc). */
+int qutai_amd_gemm_static(const void* a, const void* b, void* out, int64_t rows, int64_t inner, int64_t cols,
+                          int64_t batch, int64_t left_stride, int64_t right_stride, int transpose_left,
+                          int transpose_right, int a_dtype, int b_dtype, int out_dtype, int accumulate,
+                          int bf16_compute, void* stream);
+
+/* Bytes of device scratch behind qutai_amd_gemm_static (per GPU). */
+size_t qutai_amd_gemm_static_capacity(void);
 
 /* Bytes of workspace qutai_amd_gemm needs for these arguments with
  * 256-byte-aligned operands (0 when both operands are used in place).  An

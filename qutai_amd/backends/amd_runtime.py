@@ -29,7 +29,7 @@ _ATTR_CC_MAJOR, _ATTR_CC_MINOR, _ATTR_CU_COUNT, _ATTR_CLOCK_KHZ = 23, 61, 63, 5
 _MEMCPY_H2D, _MEMCPY_D2H, _MEMCPY_D2D = 1, 2, 3
 _HIP_OOM = 2  # hipErrorOutOfMemory
 
-QA_OK, QA_EINVAL, QA_EWORKSPACE = 0, -1, -2
+QA_OK, QA_EINVAL, QA_EWORKSPACE, QA_ESCRATCH = 0, -1, -2, -3
 
 _p, _i64, _i32, _f64, _sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_double, ctypes.c_size_t
 
@@ -87,9 +87,13 @@ SIGNATURES = {
     "qutai_amd_gather": [_p, _p, _p, _i64, _i32, _p],
     "qutai_amd_scatter": [_p, _p, _p, _p, _i64, _i32, _p],
     "qutai_amd_device_arch": [_i32, ctypes.c_char_p, _sz],
+    "qutai_amd_gemm_static": [_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32,
+                              _i32, _p],
+    "qutai_amd_gemm_static_capacity": [],
 }
 RESTYPES = {"qutai_amd_gemm_workspace_size": _sz, "qutai_amd_rms_norm_workspace": _i64,
-            "qutai_amd_attention_bwd_workspace_size": _sz, "qutai_amd_reduce_sum_workspace_size": _sz}
+            "qutai_amd_attention_bwd_workspace_size": _sz, "qutai_amd_reduce_sum_workspace_size": _sz,
+            "qutai_amd_gemm_static_capacity": _sz}
 
 
 def _hip_library():
@@ -356,6 +360,9 @@ class Runtime:
                 raise ValueError(f"{name}: arguments rejected by libqutai_amd")
             if status == QA_EWORKSPACE:
                 raise RuntimeError(f"{name}: workspace missing or too small")
+            if status == QA_ESCRATCH:
+                raise RuntimeError(f"{name}: the operands need more workspace than the fixed "
+                                   f"{self.lib.qutai_amd_gemm_static_capacity() >> 20} MiB device scratch")
             self._check(status, name)
             self.launches += 1
             if mfma:
