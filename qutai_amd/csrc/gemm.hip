@@ -107,13 +107,14 @@ __global__ void splitk_reduce(const float* part, void* out, int64_t n, int64_t t
 //   L8R : 256x256, 8 waves, same K step, register staging
 //   L4D2: 256x256, 4 waves (one per SIMD, 128x128 per wave), two-stage ring
 //   S   : 128x128, 4 waves, BK 32 / 16, four-stage ring (small grids, short K)
+//   S2  : 128x128, 4 waves, BK 32 / 16, two-stage ring (bf16, K <= 64: four per CU)
 //   N   : 256x64, 4 waves (N <= 64), W : 64x256, 4 waves (M <= 64)
 //   H   : 256x128, 8 waves 4x2 (64x64 per wave), BK 64, three-stage ring
 //         (grids of 256x256 tiles that would leave half the CUs idle)
 //   T, U: 192x256 (8 waves 2x4, 96x64 per wave) and 256x192 (4x2, 64x96),
 //         BK 64, two-stage ring, bf16 only (a grid of 256x256 tiles just
 //         short of the CU count, e.g. 5632 x 2048: 176 tiles -> 240)
-enum Tile { TILE_L8D2, TILE_L8R, TILE_L4D2, TILE_S, TILE_N, TILE_W, TILE_H, TILE_T, TILE_U, TILE_COUNT };
+enum Tile { TILE_L8D2, TILE_L8R, TILE_L4D2, TILE_S, TILE_N, TILE_W, TILE_H, TILE_T, TILE_U, TILE_S2, TILE_COUNT };
 
 template <bool F32, bool TA, bool TB, int BM, int BN, int WM, int WN, int BK, int ST, bool DMA, bool SWIGLU = false>
 hipError_t launch_cfg(GemmArgs p, hipStream_t stream) {
@@ -135,6 +136,7 @@ hipError_t launch_tile(Tile tile, GemmArgs p, hipStream_t stream) {
     case TILE_L8R: return launch_cfg<F32, TA, TB, 256, 256, 2, 4, KR, 2, false>(p, stream);
     case TILE_L4D2: return launch_cfg<F32, TA, TB, 256, 256, 2, 2, KR, 2, true>(p, stream);
     case TILE_S: return launch_cfg<F32, TA, TB, 128, 128, 2, 2, KB, 4, true>(p, stream);
+    case TILE_S2: return launch_cfg<F32, TA, TB, 128, 128, 2, 2, KB, 2, true>(p, stream);
     case TILE_N: return launch_cfg<F32, TA, TB, 256, 64, 4, 1, KB, 4, true>(p, stream);
     case TILE_W: return launch_cfg<F32, TA, TB, 64, 256, 1, 4, KB, 4, true>(p, stream);
     case TILE_H: return launch_cfg<F32, TA, TB, 256, 128, 4, 2, KR, 3, true>(p, stream);
@@ -174,7 +176,7 @@ int forced_tile() {
   static int forced = [] {
     const char* v = getenv("QUTAI_AMD_GEMM_TILE");
     if (!v) return -1;
-    const char* names[TILE_COUNT] = {"L8D2", "L8R", "L4D2", "S", "N", "W", "H", "T", "U"};
+    const char* names[TILE_COUNT] = {"L8D2", "L8R", "L4D2", "S", "N", "W", "H", "T", "U", "S2"};
     for (int i = 0; i < TILE_COUNT; i++)
       if (std::string(v) == names[i]) return i;
     return -1;
@@ -186,6 +188,11 @@ Tile choose_tile(int64_t M, int64_t N, int64_t K, int64_t batch, bool bf16) {
   if (forced_tile() >= 0) return (Tile)forced_tile();
   if (N <= 64) return TILE_N;
   if (M <= 64) return TILE_W;
+  // K <= 64 (bf16; the attention score product S = Q K^T with K = the head
+  // size) is bound by writing the output: a two-stage ring halves the LDS
+  // of the four-stage one, so four workgroups fit per CU instead of two
+  // (config 3's S product 336 -> 291 us)
+  if (bf16 && K <= 64) return TILE_S2;
   if (K <= 128) return TILE_S;
   // Wave-quantisation cost of the large tiles, in units of one full round of
   // 256x256 tiles over the CUs (per unit of K).  Measured on this GPU (bf16,

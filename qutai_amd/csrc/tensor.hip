@@ -3,6 +3,7 @@
 // SwiGLU's silu(gate) * up.  Reference counterparts are cited per entry
 // point in include/qutai_amd.h.
 #include <algorithm>
+#include <cstring>
 
 #include "common.h"
 #include "qutai_amd.h"
@@ -12,6 +13,15 @@ using namespace qa;
 namespace {
 
 constexpr int THREADS = 256;
+
+// fp32 -> bf16 on the host with the device rule (round to nearest even, a
+// NaN becomes (bits >> 16) | 0x40)
+uint32_t f32_to_bf16_host(float f) {
+  uint32_t bits;
+  memcpy(&bits, &f, 4);
+  if ((bits & 0x7fffffffu) > 0x7f800000u) return (bits >> 16) | 0x40u;
+  return (bits + 0x7fffu + ((bits >> 16) & 1u)) >> 16;
+}
 
 unsigned grid_for(int64_t n, int64_t per_thread = 1) {
   int64_t blocks = (n + THREADS * per_thread - 1) / (THREADS * per_thread);
@@ -62,6 +72,12 @@ __global__ void cast_bf16_f32x8(const u32x4* src, f32x4* dst, int64_t n8) {
 __global__ void add_f32x4(const f32x4* a, const f32x4* b, f32x4* out, int64_t n4) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (int64_t)gridDim.x * blockDim.x)
     out[i] = a[i] + b[i];
+}
+
+// 16 bytes per lane and step: the word pattern of one 16-byte piece
+__global__ void fill16_kernel(u32x4* dst, int64_t n16, u32x4 word) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += (int64_t)gridDim.x * blockDim.x)
+    global_store(dst + i, word);
 }
 
 __global__ void fill_kernel(void* dst, int64_t n, double value, int d) {
@@ -583,7 +599,36 @@ int qutai_amd_cast(const void* src, void* dst, int64_t n, int src_dtype, int dst
 int qutai_amd_fill(void* dst, int64_t n, double value, int dtype, void* stream) {
   if (n < 0 || (!float_dtype(dtype) && dtype != I64)) return QA_EINVAL;
   if (n == 0) return QA_OK;
-  hipLaunchKernelGGL(fill_kernel, dim3(grid_for(n)), dim3(THREADS), 0, (hipStream_t)stream, dst, n, value, dtype);
+  if (!dst) return QA_EINVAL;
+  hipStream_t s = (hipStream_t)stream;
+  const int es = dtype == BF16 ? 2 : dtype == F32 ? 4 : 8;
+  if ((uintptr_t)dst % 16 == 0 && n * es >= 16) {
+    // whole 16-byte pieces with one repeated word pattern, the rest element-wise
+    uint32_t w[4];
+    if (dtype == BF16) {
+      const uint32_t h = f32_to_bf16_host((float)value);
+      w[0] = w[1] = w[2] = w[3] = h | (h << 16);
+    } else if (dtype == F32) {
+      const float f = (float)value;
+      uint32_t u;
+      memcpy(&u, &f, 4);
+      w[0] = w[1] = w[2] = w[3] = u;
+    } else {
+      uint64_t u;
+      if (dtype == F64) memcpy(&u, &value, 8);
+      else { const int64_t iv = (int64_t)value; memcpy(&u, &iv, 8); }
+      w[0] = w[2] = (uint32_t)u;
+      w[1] = w[3] = (uint32_t)(u >> 32);
+    }
+    const int64_t n16 = n * es / 16, done = n16 * 16 / es;
+    hipLaunchKernelGGL(fill16_kernel, dim3(grid_for(n16)), dim3(THREADS), 0, s, (u32x4*)dst, n16,
+                       u32x4{w[0], w[1], w[2], w[3]});
+    if (done < n)
+      hipLaunchKernelGGL(fill_kernel, dim3(1), dim3(THREADS), 0, s, (void*)((char*)dst + done * es), n - done, value,
+                         dtype);
+    return (int)hipGetLastError();
+  }
+  hipLaunchKernelGGL(fill_kernel, dim3(grid_for(n)), dim3(THREADS), 0, s, dst, n, value, dtype);
   return (int)hipGetLastError();
 }
 
