@@ -105,10 +105,17 @@ size_t qutai_amd_gemm_workspace_size(int64_t rows, int64_t inner, int64_t cols, 
  * for both operands.  Replaces the per-expert loop of 3 `cuda_lm.gemm`
  * launches per expert in SparseMoE (src/qutai/lm/layers.py:395-397,
  * src/qutai/backends/cuda_lm.py:31-55) and the count download that sizes
- * them (cuda_lm.py:432-434). */
+ * them (cuda_lm.py:432-434).
+ * With `gather` (device, >= offsets[groups] int64 row indices, may be null)
+ * row i of the grouped block is row gather[i] of a, which then holds
+ * source_rows rows of `inner` values (source_rows * inner * element size
+ * below 2^31): the routed token gather (`route_gather`, cuda_lm.py:471-485)
+ * happens inside the operand copy.  An index outside [0, source_rows) reads
+ * zeros. */
 int qutai_amd_gemm_grouped(const void* a, const void* b, void* out, const int64_t* offsets, int groups,
                            int64_t max_rows, int64_t inner, int64_t cols, int64_t expert_stride,
-                           int transpose_right, int dtype, int out_dtype, int accumulate, void* stream);
+                           int transpose_right, int dtype, int out_dtype, int accumulate, const int64_t* gather,
+                           int64_t source_rows, void* stream);
 
 /* SwiGLU feed-forward input side in one GEMM (bf16 only):
  *   out = silu(a @ w_gate^T) * (a @ w_up^T)      [rows][hidden] bf16
@@ -123,10 +130,12 @@ int qutai_amd_gemm_grouped(const void* a, const void* b, void* out, const int64_
  * multiple of 8).  Replaces `silu(self.gate(x)) * self.up(x)` of the SwiGLU
  * block (src/qutai/lm/layers.py:310-311: two projections, lm_silu of
  * cuda/lm.cu:54 and the elementwise multiply), run per expert by SparseMoE
- * (lm/layers.py:395-397). */
+ * (lm/layers.py:395-397).  `gather` / source_rows (grouped calls only) read
+ * the rows through an index table as in qutai_amd_gemm_grouped. */
 int qutai_amd_gemm_swiglu(const void* a, const void* w_gate, const void* w_up, void* out, void* gate_out,
                           void* up_out, const int64_t* offsets, int groups, int64_t rows, int64_t inner,
-                          int64_t hidden, int64_t expert_stride, int dtype, void* stream);
+                          int64_t hidden, int64_t expert_stride, int dtype, const int64_t* gather,
+                          int64_t source_rows, void* stream);
 
 /* Element-wise dtype conversion of n values (fp32/fp64/bf16 among each
  * other; narrowing to bf16 rounds to nearest even).

@@ -165,15 +165,20 @@ def combine(outputs, weights, route, width):
 
 
 def grouped_gemm(rows_block, weight_stack, route, inner, cols, *, out_dtype="bfloat16", transpose_right=True,
-                 out=None, accumulate=False):
+                 out=None, accumulate=False, gather=False):
     """out[offsets[e]:offsets[e+1]] (+)= rows_block[offsets[e]:offsets[e+1]] @ op(W_e)
     for every expert in one launch, the row ranges read on the device.  With
     ``transpose_right`` W_e = weight_stack[e] is stored (cols, inner) and used
     transposed (the forward X W^T); without, it is stored (inner, cols) (the
-    backward dY W)."""
+    backward dY W).  With ``gather`` rows_block is the token matrix
+    [rows][inner] and the expert-major rows are read through ``order``
+    inside the GEMM (no gathered copy)."""
     experts = route["experts"]
     if weight_stack.size != experts * cols * inner or rows_block.dtype != weight_stack.dtype:
         raise ValueError("grouped_gemm needs [experts] weights of cols*inner values in the rows' dtype")
+    source = route["rows"] if gather else route["capacity"]
+    if rows_block.size != source * inner:
+        raise ValueError("grouped_gemm rows do not match the route (rows x inner, or capacity x inner)")
     if out is None:
         if accumulate:
             raise ValueError("accumulate needs out")
@@ -183,24 +188,29 @@ def grouped_gemm(rows_block, weight_stack, route, inner, cols, *, out_dtype="bfl
     if out.size:
         out.runtime.call("qutai_amd_gemm_grouped", rows_block.ptr, weight_stack.ptr, out.ptr, route["offsets"].ptr,
                          experts, route["capacity"], inner, cols, cols * inner, int(transpose_right),
-                         code(rows_block.dtype), code(out_dtype), int(accumulate), mfma=True)
+                         code(rows_block.dtype), code(out_dtype), int(accumulate),
+                         route["order"].ptr if gather else None, source if gather else 0, mfma=True)
     return out
 
 
-def swiglu_gemm(rows_block, w_gate, w_up, rows, inner, hidden, *, route=None, save=False):
+def swiglu_gemm(rows_block, w_gate, w_up, rows, inner, hidden, *, route=None, save=False, gather=False):
     """silu(rows_block @ W_gate^T) * (rows_block @ W_up^T) in one bf16 GEMM
     (qutai_amd_gemm_swiglu), with the unfused form's roundings.  With
     ``route`` the rows are grouped by expert and W_* are [experts][hidden][inner]
     stacks; without, one [hidden][inner] weight pair and ``rows`` rows.  With
-    ``save`` the bf16 gate and up products are returned too (for the
-    backward): (act, gate, up)."""
+    ``gather`` (grouped only) rows_block is the token matrix and the routed
+    rows are read through ``order`` inside the GEMM.  With ``save`` the bf16
+    gate and up products are returned too (for the backward): (act, gate, up)."""
     if route is not None:
         rows, groups = route["capacity"], route["experts"]
+    elif gather:
+        raise ValueError("swiglu_gemm gathers rows only for a route")
     else:
         groups = 1
+    source = route["rows"] if gather else rows
     if rows_block.dtype != "bfloat16" or {w_gate.dtype, w_up.dtype} != {"bfloat16"}:
         raise ValueError("swiglu_gemm runs bf16 operands")
-    if rows_block.size != rows * inner or w_gate.size != groups * hidden * inner or w_up.size != w_gate.size:
+    if rows_block.size != source * inner or w_gate.size != groups * hidden * inner or w_up.size != w_gate.size:
         raise ValueError("swiglu_gemm operand sizes do not match rows, inner and hidden")
     act = AMDStorage(rows * hidden, "bfloat16")
     gate = AMDStorage(rows * hidden, "bfloat16") if save else None
@@ -209,7 +219,8 @@ def swiglu_gemm(rows_block, w_gate, w_up, rows, inner, hidden, *, route=None, sa
         act.runtime.call("qutai_amd_gemm_swiglu", rows_block.ptr, w_gate.ptr, w_up.ptr, act.ptr,
                          gate.ptr if save else None, up.ptr if save else None,
                          route["offsets"].ptr if route is not None else None, groups, rows, inner, hidden,
-                         hidden * inner, code("bfloat16"), mfma=True)
+                         hidden * inner, code("bfloat16"), route["order"].ptr if gather else None,
+                         source if gather else 0, mfma=True)
     return (act, gate, up) if save else act
 
 
@@ -261,18 +272,22 @@ def moe_experts_forward(x, route, w_gate, w_up, w_down, width, hidden, *, save=F
     wp, hp = _pad8(width), _pad8(hidden)
     experts = route["experts"]
     wg, wu, wd = (_as_dtype(w, x.dtype) for w in (w_gate, w_up, w_down))
-    rows = route_gather_all(x, route, width)
+    # the forward alone reads the routed rows through `order` inside the
+    # GEMM; the backward's weight gradients need the gathered block itself
+    fused = not save and x.dtype in ("bfloat16", "float32")
+    rows = x if fused else route_gather_all(x, route, width)
     if (wp, hp) != (width, hidden):
         wg, wu = (repitch(w, experts, hidden, width, hp, wp) for w in (wg, wu))
         wd = repitch(wd, experts, width, hidden, wp, hp)
-        rows = repitch(rows, 1, route["capacity"], width, route["capacity"], wp)
+        rows = repitch(rows, 1, route["rows"] if fused else route["capacity"], width,
+                       route["rows"] if fused else route["capacity"], wp)
     if x.dtype == "bfloat16" and save:
         act, gate, up = swiglu_gemm(rows, wg, wu, 0, wp, hp, route=route, save=True)
     elif x.dtype == "bfloat16":
-        act, gate, up = swiglu_gemm(rows, wg, wu, 0, wp, hp, route=route), None, None
+        act, gate, up = swiglu_gemm(rows, wg, wu, 0, wp, hp, route=route, gather=fused), None, None
     else:
-        gate = grouped_gemm(rows, wg, route, wp, hp, out_dtype=x.dtype)
-        up = grouped_gemm(rows, wu, route, wp, hp, out_dtype=x.dtype)
+        gate = grouped_gemm(rows, wg, route, wp, hp, out_dtype=x.dtype, gather=fused)
+        up = grouped_gemm(rows, wu, route, wp, hp, out_dtype=x.dtype, gather=fused)
         act = silu_mul(gate, up)
     down = grouped_gemm(act, wd, route, hp, wp, out_dtype=x.dtype)
     if wp != width:

@@ -38,8 +38,8 @@ SIGNATURES = {
     "qutai_amd_gemm": [_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                        _p, _sz, _p],
     "qutai_amd_gemm_workspace_size": [_i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32],
-    "qutai_amd_gemm_grouped": [_p, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _p],
-    "qutai_amd_gemm_swiglu": [_p, _p, _p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _i32, _p],
+    "qutai_amd_gemm_grouped": [_p, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _p, _i64, _p],
+    "qutai_amd_gemm_swiglu": [_p, _p, _p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _i32, _p, _i64, _p],
     "qutai_amd_head_block_stats": [_p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _p],
     "qutai_amd_head_block_loss": [_p, _p, _p, _p, _i64, _p],
     "qutai_amd_head_block_gradient": [_p, _p, _p, _p, _i64, _i64, _i64, _f64, _i32, _p],

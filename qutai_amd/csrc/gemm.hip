@@ -230,6 +230,36 @@ size_t split_bytes(int64_t rows, int64_t cols, int64_t batch, int splits) {
   return ((size_t)splits * batch * rows * cols * 4 + 255) / 256 * 256;
 }
 
+// rows of an output tile (the M extent a grouped launch counts tiles in)
+int tile_rows(Tile tile) {
+  switch (tile) {
+    case TILE_S:
+    case TILE_S2: return 128;
+    case TILE_T: return 192;
+    case TILE_W: return 64;
+    default: return 256;
+  }
+}
+
+// Tile of a grouped (per-expert rows) launch: 256x64 for thin outputs, else
+// 256x256 or, for bf16, 256x192 when that takes fewer weighted rounds over
+// the CUs (a round of 256x192 tiles costs 0.9 of a 256x256 one, as in
+// choose_tile).  The M tile count is estimated as ceil(rows / 256) plus half
+// a partial tile per group.  The 256x128 / 128x128 tiles measured slower on
+// config 5's experts and are not considered.  Config 5's down product
+// (cols 2048): 256x192 109 us against 123 us for 256x256.
+Tile grouped_tile(int64_t rows, int64_t cols, int groups, bool bf16) {
+  if (forced_tile() >= 0) return (Tile)forced_tile();
+  if (cols <= 64) return TILE_N;
+  if (!bf16) return TILE_L8D2;
+  const int64_t cus = cu_count();
+  auto rounds = [cus](int64_t tiles) { return (double)(tiles / cus + (tiles % cus ? 1 : 0)); };
+  const int64_t tiles_m = (rows + 255) / 256 + groups / 2;
+  const double cost_l = rounds(tiles_m * ((cols + 255) / 256));
+  const double cost_u = 0.9 * rounds(tiles_m * ((cols + 191) / 192));
+  return cost_u < cost_l * 0.97 ? TILE_U : TILE_L8D2;
+}
+
 int64_t tile_count(Tile tile, int64_t rows, int64_t cols, int64_t batch) {
   int64_t bm = 256, bn = 256;
   if (tile == TILE_S) bm = bn = 128;
@@ -459,7 +489,8 @@ int qutai_amd_gemm(const void* a, const void* b, void* out, int64_t rows, int64_
 
 int qutai_amd_gemm_grouped(const void* a, const void* b, void* out, const int64_t* offsets, int groups,
                            int64_t max_rows, int64_t inner, int64_t cols, int64_t expert_stride,
-                           int transpose_right, int dtype, int out_dtype, int accumulate, void* stream_) {
+                           int transpose_right, int dtype, int out_dtype, int accumulate, const int64_t* gather,
+                           int64_t source_rows, void* stream_) {
   hipStream_t stream = (hipStream_t)stream_;
   if (groups <= 0 || max_rows < 0 || inner < 0 || cols < 0 || expert_stride < 0) return QA_EINVAL;
   if (dtype != QA_BF16 && dtype != QA_F32) return QA_EINVAL;
@@ -489,13 +520,15 @@ int qutai_amd_gemm_grouped(const void* a, const void* b, void* out, const int64_
   p.offsets = offsets;
   p.groups = groups;
   p.alpha = 1.0f;
-  // 256x256 tiles (256x64 for thin outputs): on config 5's experts the cost
-  // model's 256x128 / 128x128 picks measured slower (each group's last M tile
-  // is partial, which the model does not see).  The grid covers the upper
-  // bound sum ceil(n_g / BM) <= ceil(max_rows / BM) + groups of M tiles
-  // (tiles past the last group return at once).
-  const Tile tile = cols <= 64 ? TILE_N : TILE_L8D2;
-  const int bm = 256;
+  if (gather) {
+    // row offsets into a are 32-bit byte offsets of one buffer descriptor
+    if (source_rows < 0 || source_rows * inner * es >= (1ll << 31)) return QA_EINVAL;
+    p.a_rows = gather;
+    p.a_bytes = source_rows * inner * es;
+  }
+  Tile tile = grouped_tile(max_rows, cols, groups, dtype == QA_BF16);
+  if (gather && tile == TILE_L8R) tile = TILE_L8D2;  // gathered rows need the DMA ring
+  const int bm = tile_rows(tile);
   p.tiles_m = (int)((max_rows + bm - 1) / bm + groups);
   bool f32 = dtype == QA_F32;
   hipError_t err = f32 ? launch_mma<true>(tile, false, transpose_right, p, stream)
@@ -505,7 +538,8 @@ int qutai_amd_gemm_grouped(const void* a, const void* b, void* out, const int64_
 
 int qutai_amd_gemm_swiglu(const void* a, const void* w_gate, const void* w_up, void* out, void* gate_out,
                           void* up_out, const int64_t* offsets, int groups, int64_t rows, int64_t inner,
-                          int64_t hidden, int64_t expert_stride, int dtype, void* stream_) {
+                          int64_t hidden, int64_t expert_stride, int dtype, const int64_t* gather,
+                          int64_t source_rows, void* stream_) {
   hipStream_t stream = (hipStream_t)stream_;
   if (rows < 0 || inner < 0 || hidden < 0 || expert_stride < 0 || (offsets && groups <= 0)) return QA_EINVAL;
   if (dtype != QA_BF16) return QA_EINVAL;
@@ -535,6 +569,11 @@ int qutai_amd_gemm_swiglu(const void* a, const void* w_gate, const void* w_up, v
   p.vec_c = vec_out(out, p.ldc, 0);
   p.alpha = 1.0f;
   if ((p.lda * 256 * 2) >= (1ll << 31)) return QA_EINVAL;
+  if (gather) {
+    if (!offsets || source_rows < 0 || source_rows * inner * 2 >= (1ll << 31)) return QA_EINVAL;
+    p.a_rows = gather;
+    p.a_bytes = source_rows * inner * 2;
+  }
   if (offsets) {
     p.offsets = offsets;
     p.groups = groups;

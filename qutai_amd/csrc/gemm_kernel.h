@@ -50,6 +50,11 @@ struct GemmArgs {
   // of A (K-major, lda) and of out (ldc); its B operand is b + g*sb.
   const int64_t* offsets;
   int groups;
+  // Gathered rows (grouped mode, K-major A): when a_rows is set, row i of the
+  // grouped block is row a_rows[i] of A (a_bytes = A's size in bytes, every
+  // index below it), so a routed row set needs no copy of its own.
+  const int64_t* a_rows;
+  int64_t a_bytes;
   int tiles_m;            // M tiles in the grid (grouped: an upper bound)
   float alpha;            // scale applied to A@B before the epilogue
   // Grouped-K mode (group_k = 1, batch = groups): group g reduces over the K
@@ -347,6 +352,7 @@ struct GemmKernel {
     const T* B = reinterpret_cast<const T*>(p.b);
     const T* B2 = reinterpret_cast<const T*>(p.b2);
     int64_t M = p.M, row0 = 0, K = p.K;
+    const int64_t* gather = nullptr;  // grouped mode with a_rows: this group's row indices
     char* outp = reinterpret_cast<char*>(p.out);
     const int osize = p.out_bf16 ? 2 : 4;
     if (p.group_k) {
@@ -369,7 +375,8 @@ struct GemmKernel {
         before += nt;
       }
       if (g < 0) return;  // tile beyond the last group: nothing to do
-      A += lo * p.lda;
+      if (KA && p.a_rows) gather = p.a_rows + lo;
+      else A += lo * p.lda;
       B += (int64_t)g * p.sb;
       if constexpr (SWIGLU) B2 += (int64_t)g * p.sb;
       outp += lo * p.ldc * osize;
@@ -431,10 +438,16 @@ struct GemmKernel {
       for (int j = 0; j < JA; j++) {
         int q = (j * NW + wave) * 64 + lane, outer, c;
         TileA::coords(q, outer, c);
-        oa[j] = (uint32_t)(((int64_t)outer * lda + c * E) * (int64_t)sizeof(T));
         ka[j] = KA ? c * E : outer;
         va[j] = KA ? (row0 + outer < M) : (row0 + c * E < M);
+        // gathered rows: the row index comes from the table (read only for
+        // rows inside the group), the descriptor spans all of A
+        const int64_t src_row = KA && gather && va[j] ? gather[row0 + outer] : outer;
+        oa[j] = (uint32_t)((src_row * lda + c * E) * (int64_t)sizeof(T));
       }
+      // A's descriptor base at k0 is a_tile + k0 (K-major) or + k0 * lda
+      const T* a_tile = gather ? A : KA ? A + row0 * lda : A + row0;
+      const int64_t a_span = gather ? p.a_bytes : (int64_t)(KA ? BM * lda : BK * lda) * (int64_t)sizeof(T);
       bool up[JB];  // SWIGLU: instruction j copies up-weight rows
 #pragma unroll
       for (int j = 0; j < JB; j++) {
@@ -452,8 +465,7 @@ struct GemmKernel {
       char* base = reinterpret_cast<char*>(lds);
       // copies of one stage, optionally only instructions [first, last)
       auto issue_range = [&](int stage, int64_t k0, int first, int last) {
-        const u32x4 da = lds_rsrc(KA ? A + row0 * lda + k0 : A + k0 * lda + row0,
-                                  (int64_t)(KA ? BM * lda : BK * lda) * (int64_t)sizeof(T));
+        const u32x4 da = lds_rsrc(KA ? a_tile + k0 : a_tile + k0 * lda, a_span);
         const u32x4 db = lds_rsrc(KB ? B + col0 * ldb + k0 : B + k0 * ldb + col0,
                                   (int64_t)(KB ? BN * ldb : BK * ldb) * (int64_t)sizeof(T));
         const u32x4 db2 = SWIGLU ? lds_rsrc(B2 + col0 * ldb + k0, (int64_t)BN * ldb * (int64_t)sizeof(T)) : db;

@@ -81,7 +81,17 @@ def test_argument_checks_reject_before_any_device_call():
     fake = 1 << 20  # a 16-byte aligned stand-in address, never dereferenced
     # grouped expert GEMM: a 256-row tile of a 2^23-wide bf16 operand spans
     # 2^32 bytes, beyond the 31-bit buffer descriptor range
-    assert library.qutai_amd_gemm_grouped(fake, fake, fake, fake, 8, 512, 1 << 23, 64, 0, 1, 5, 5, 0, None) == -1
+    assert library.qutai_amd_gemm_grouped(fake, fake, fake, fake, 8, 512, 1 << 23, 64, 0, 1, 5, 5, 0, None, 0,
+                                          None) == -1
+    # gathered rows: the whole source matrix (2^19 rows of 2048 bf16 = 2^31
+    # bytes) must stay inside one descriptor's 31-bit range
+    assert library.qutai_amd_gemm_grouped(fake, fake, fake, fake, 8, 512, 2048, 64, 0, 1, 5, 5, 0, fake, 1 << 19,
+                                          None) == -1
+    assert library.qutai_amd_gemm_swiglu(fake, fake, fake, fake, None, None, fake, 8, 512, 2048, 64, 0, 5, fake,
+                                         1 << 19, None) == -1
+    # a gather needs the grouped form (offsets)
+    assert library.qutai_amd_gemm_swiglu(fake, fake, fake, fake, None, None, None, 1, 512, 2048, 64, 0, 5, fake,
+                                         16, None) == -1
     # strided copy: rank above 8, or an element size other than 2/4/8
     dims = (ctypes.c_int64 * 9)(*([2] * 9))
     assert library.qutai_amd_strided_copy(fake, fake, 9, dims, dims, dims, 4, None) == -1

@@ -79,6 +79,9 @@ def test_grouped_swiglu_matches_unfused_bit_for_bit(amd, lm, tokens, width, hidd
     assert np.array_equal(words(gate)[:used], words(gate_ref)[:used])
     assert np.array_equal(words(up)[:used], words(up_ref)[:used])
     assert np.array_equal(words(act)[:used], words(act_ref)[:used])
+    # rows read through the route's order inside the GEMM: the same values
+    act_g = lm.swiglu_gemm(xs, gs, us, 0, width, hidden, route=route, gather=True)
+    assert np.array_equal(words(act_g)[:used], words(act)[:used])
     # float64 check on every expert's first and last row
     offsets = download(route["offsets"]).astype(int).tolist()
     xr = stored(download(rows), "bfloat16").reshape(-1, width)
@@ -90,6 +93,28 @@ def test_grouped_swiglu_matches_unfused_bit_for_bit(amd, lm, tokens, width, hidd
         for r in sorted({lo, hi - 1}) if hi > lo else ():
             exact = reference_act(xr[r:r + 1], gr[e], ur[e])
             assert ora.rel_frobenius(got[r:r + 1], exact) <= BF16_TOL
+
+
+@pytest.mark.parametrize("dtype,tokens,width,cols,experts,top_k", [
+    ("bfloat16", 1500, 256, 200, 8, 2), ("bfloat16", 700, 1408, 2048, 8, 2), ("float32", 900, 132, 96, 4, 2),
+    ("bfloat16", 40, 64, 8, 16, 1)])
+def test_grouped_gemm_gather_equals_gathered_block(amd, lm, dtype, tokens, width, cols, experts, top_k):
+    """The grouped GEMM reading its rows through `order` (token gather inside
+    the operand copy) is bit-identical to the GEMM over the gathered block,
+    including experts with no rows and a partial last tile per expert."""
+    logits = normal(tokens + 3, tokens * experts)
+    route = lm.routing(upload(logits, "float32"), tokens, experts, top_k)
+    xs = upload(normal(tokens + 4, tokens * width), dtype)
+    ws = upload(normal(5, experts * cols * width, 0.1), dtype)
+    rows = lm.route_gather_all(xs, route, width)
+    used = int(download(route["offsets"])[-1]) * cols
+    for out_dtype in ("float32", dtype):
+        ref = download(lm.grouped_gemm(rows, ws, route, width, cols, out_dtype=out_dtype))
+        got = download(lm.grouped_gemm(xs, ws, route, width, cols, out_dtype=out_dtype, gather=True))
+        assert np.array_equal(got[:used], ref[:used]), out_dtype
+    if top_k > 1:
+        with pytest.raises(ValueError):  # the gathered form takes the token matrix
+            lm.grouped_gemm(rows, ws, route, width, cols, gather=True, out_dtype=dtype)
 
 
 def test_swiglu_rejects_unsupported_operands(amd, lm):
