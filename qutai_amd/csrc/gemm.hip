@@ -7,6 +7,7 @@
 #include <string>
 
 #include "gemm_kernel.h"
+#include "gemm_short.h"
 
 #include <algorithm>
 #include "qutai_amd.h"
@@ -17,6 +18,12 @@ namespace {
 
 template <class Kern>
 __global__ void __launch_bounds__(Kern::NT) gemm_entry(GemmArgs p) {
+  __shared__ __attribute__((aligned(16))) char smem[Kern::LDS_BYTES];
+  Kern::run(p, smem);
+}
+
+template <class Kern>
+__global__ void __launch_bounds__(Kern::NT) short_entry(ShortArgs p) {
   __shared__ __attribute__((aligned(16))) char smem[Kern::LDS_BYTES];
   Kern::run(p, smem);
 }
@@ -114,7 +121,10 @@ __global__ void splitk_reduce(const float* part, void* out, int64_t n, int64_t t
 //   T, U: 192x256 (8 waves 2x4, 96x64 per wave) and 256x192 (4x2, 64x96),
 //         BK 64, two-stage ring, bf16 only (a grid of 256x256 tiles just
 //         short of the CU count, e.g. 5632 x 2048: 176 tiles -> 240)
-enum Tile { TILE_L8D2, TILE_L8R, TILE_L4D2, TILE_S, TILE_N, TILE_W, TILE_H, TILE_T, TILE_U, TILE_S2, TILE_COUNT };
+//   R   : short-K row strips (gemm_short.h): bf16 NT with K <= 64, a 128-row
+//         block of A held in registers, 128-column chunks of B through a
+//         three-slot LDS ring, stores straight from the accumulators
+enum Tile { TILE_L8D2, TILE_L8R, TILE_L4D2, TILE_S, TILE_N, TILE_W, TILE_H, TILE_T, TILE_U, TILE_S2, TILE_R, TILE_COUNT };
 
 template <bool F32, bool TA, bool TB, int BM, int BN, int WM, int WN, int BK, int ST, bool DMA, bool SWIGLU = false>
 hipError_t launch_cfg(GemmArgs p, hipStream_t stream) {
@@ -170,13 +180,14 @@ int64_t cu_count() {
 }
 
 // Tile choice for an M x N output (batch of them) over K; thin outputs use
-// the 256x64 / 64x256 shapes.  QUTAI_AMD_GEMM_TILE=<L8D2|L8R|L4D2|S|N|W|H>
-// overrides the choice (tuning).
+// the 256x64 / 64x256 shapes.  QUTAI_AMD_GEMM_TILE=<L8D2|L8R|L4D2|S|N|W|H|T|U|S2|R>
+// overrides the choice (tuning and tests; R applies only where the short-K
+// strip kernel does, other calls then take L8D2).
 int forced_tile() {
   static int forced = [] {
     const char* v = getenv("QUTAI_AMD_GEMM_TILE");
     if (!v) return -1;
-    const char* names[TILE_COUNT] = {"L8D2", "L8R", "L4D2", "S", "N", "W", "H", "T", "U", "S2"};
+    const char* names[TILE_COUNT] = {"L8D2", "L8R", "L4D2", "S", "N", "W", "H", "T", "U", "S2", "R"};
     for (int i = 0; i < TILE_COUNT; i++)
       if (std::string(v) == names[i]) return i;
     return -1;
@@ -369,6 +380,48 @@ void launch_prepare(Operand& o, int src_dtype, bool bf16, char* ws, hipStream_t 
   o.ptr = ws;
 }
 
+// Short-K strip launch (tile R): the call's rows are K-major for both
+// operands (NT), K <= 64, bf16 output without accumulation, output rows
+// 16-byte aligned and N a multiple of 16 (every 16-byte store is inside or
+// wholly outside a row).  Each workgroup
+// sweeps `strip` 128-column chunks; strips shrink (halving) until the grid
+// holds at least 16 rounds of the two workgroups a CU runs at once.  Config
+// 3's score product (128 x 2048 x 2048, K 64): 208 us with one chunk per
+// workgroup, 181-185 us with 2, 4 or 8 (the rule gives 4), 200 us with 16.
+bool short_fits(const GemmArgs& p, bool bf16, bool ta, bool tb) {
+  return bf16 && !ta && tb && p.out_bf16 && !p.accumulate && p.K > 0 && p.K <= 64 && p.N % 16 == 0 &&
+         p.vec_c == 2 && p.ldc * 128 * 2 < (1ll << 31);
+}
+hipError_t launch_short(const GemmArgs& p, hipStream_t stream) {
+  ShortArgs s = {};
+  s.a = (const bf16_t*)p.a;
+  s.b = (const bf16_t*)p.b;
+  s.out = p.out;
+  s.M = p.M;
+  s.N = p.N;
+  s.K = p.K;
+  s.lda = p.lda;
+  s.ldb = p.ldb;
+  s.ldc = p.ldc;
+  s.sa = p.sa;
+  s.sb = p.sb;
+  s.sc = p.sc;
+  s.batch = p.batch;
+  s.alpha = p.alpha;
+  s.tiles_m = (int)((p.M + 127) / 128);
+  s.chunks = (int)((p.N + 127) / 128);
+  int strip = s.chunks;
+  const int64_t slots = 2 * cu_count();
+  while (strip > 1 && p.batch * s.tiles_m * ((s.chunks + strip - 1) / strip) < 16 * slots) strip = (strip + 1) / 2;
+  s.strip_chunks = strip;
+  s.strips = (s.chunks + strip - 1) / strip;
+  if (p.batch * s.tiles_m * s.strips > 0x7fffffff) return hipErrorInvalidValue;
+  typedef ShortKernel<3> Kern;
+  hipLaunchKernelGGL(short_entry<Kern>, dim3((unsigned)(p.batch * s.tiles_m * s.strips)), dim3(Kern::NT), 0, stream,
+                     s);
+  return hipGetLastError();
+}
+
 // 4-wide output stores need 4 | ldc, 4 | batch stride and an aligned base.
 // 2: every output row starts 16-byte aligned for both element sizes;
 // 1: 16-byte aligned fp32 rows / 8-byte aligned bf16 rows; 0: neither.
@@ -477,6 +530,9 @@ int qutai_amd_gemm(const void* a, const void* b, void* out, int64_t rows, int64_
     p.out_bf16 = 0;
     p.vec_c = vec_out(part, p.ldc, p.sc);
   }
+  if (!part && ((tile == TILE_S2 && forced_tile() < 0) || tile == TILE_R) &&
+      short_fits(p, bf16, transpose_left, transpose_right))
+    return (int)launch_short(p, stream);
   hipError_t err = bf16 ? launch_mma<false>(tile, transpose_left, transpose_right, p, stream)
                         : launch_mma<true>(tile, transpose_left, transpose_right, p, stream);
   if (err != hipSuccess || !part) return (int)err;

@@ -748,7 +748,7 @@ struct GemmKernel {
                       pack_bf16x2(b[2], b[3])};
       }
 #pragma unroll
-      for (int it = 0; it < ITERS; it++) global_store(dst + it * (64 / Q) * o.ldc, w[it]);
+      for (int it = 0; it < ITERS; it++) global_store_nt(dst + it * (64 / Q) * o.ldc, w[it]);
     } else if (fast) {
       constexpr int Q = W / 4, ITERS = 32 * Q / 64;
       static_assert(64 % Q == 0, "whole rows per store instruction");
@@ -765,7 +765,7 @@ struct GemmKernel {
         v[it] = o.accumulate ? v[it] + x : x;
       }
 #pragma unroll
-      for (int it = 0; it < ITERS; it++) global_store(dst + it * (64 / Q) * o.ldc, v[it]);
+      for (int it = 0; it < ITERS; it++) global_store_nt(dst + it * (64 / Q) * o.ldc, v[it]);
     } else {
       constexpr int Q = W / 4;  // float4 per staged row
       constexpr int ITERS = 32 * Q / 64;
