@@ -121,7 +121,12 @@ def attention_bmm(seed=2):
         p = amd.softmax(s, (b * h * t, t), -1, scale=d ** -0.5)
         amd.gemm(p, v, t, t, d, batch=b * h, out_dtype="bfloat16", out=o)
 
-    return step, 2 * 2.0 * b * h * t * t * d, {"batch": b, "heads": h, "seq": t, "head_dim": d, "storage": "bfloat16"}
+    # algorithmic HBM bytes of the three launches: S written (Q, K read),
+    # S read and P written, P read (V read, O written); bf16 throughout
+    scores, rows = b * h * t * t * 2, b * h * t * d * 2
+    hbm_bytes = (scores + 2 * rows) + 2 * scores + (scores + 2 * rows)
+    return step, 2 * 2.0 * b * h * t * t * d, {"batch": b, "heads": h, "seq": t, "head_dim": d, "storage": "bfloat16",
+                                               "hbm_bytes": hbm_bytes}
 
 
 def attention_fused(seed=2, causal=False):
@@ -385,6 +390,9 @@ def main():
         tflops = flops / (ms * 1e-3) / 1e12
         results[name] = {"ms": round(ms, 4), "wall_ms": round(wall_ms, 4), "tflops": round(tflops, 1),
                          "peak_frac": round(tflops / PEAK[kind], 4), "dtype": kind, **config}
+        if "hbm_bytes" in config:  # HBM-bound workloads: the fraction of the 8 TB/s roofline
+            rate = config["hbm_bytes"] / (ms * 1e-3)
+            results[name].update(hbm_tbps=round(rate / 1e12, 3), hbm_frac=round(rate / 1e9 / HBM_PEAK, 4))
         print(f"# {name}: {ms * 1e3:.1f} us/step  {tflops:.1f} TFLOP/s  ({100 * tflops / PEAK[kind]:.1f}% of "
               f"{kind} peak)", file=sys.stderr, flush=True)
         del fn

@@ -320,7 +320,8 @@ int qutai_amd_silu_mul_backward(const void* dy, const void* gate, const void* up
  * offsets [experts+1] (exclusive prefix sum of counts), order [rows*top_k]
  * (ids concatenated expert-major: order[offsets[e]+i] = ids[e][i]),
  * utilization [experts] (count / (rows*top_k)) and aux [1]
- * (experts * sum_{r,e} probs*utilization / rows).  capacity = rows * top_k.
+ * (experts * sum_{r,e} probs*utilization / rows).  capacity = rows * top_k
+ * (below 2^31, else QA_EINVAL).
  * Replaces `cuda_lm.routing` (src/qutai/backends/cuda_lm.py:368-449) and its
  * kernels lm_route, lm_route_pack, lm_route_util, lm_route_aux
  * (src/qutai/backends/cuda/lm.cu:345-387); selection follows the CPU

@@ -75,21 +75,32 @@ __global__ void __launch_bounds__(256) gemm_f64(const double* a, const double* b
 // for i < inner (converted to the compute type; fp32 -> bf16 rounds to
 // nearest even) and 0 in the padding up to `pitch`.  Used when an fp32
 // operand feeds the bf16 MFMA path (mixed inputs, autocast) or when the
-// operand's rows are not 16-byte aligned.
-__global__ void prepare_operand(const void* src, int src_bf16, void* dst, int dst_bf16, int64_t outer,
-                                int64_t inner, int64_t pitch, int64_t batches, int64_t stride) {
-  int64_t total = batches * outer * pitch;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
-    int64_t z = i / (outer * pitch), rest = i % (outer * pitch);
-    int64_t o = rest / pitch, c = rest % pitch;
-    float v = 0.f;
-    if (c < inner) {
-      int64_t at = z * stride + o * inner + c;
-      v = src_bf16 ? bf16_to_f32(((const bf16_t*)src)[at]) : ((const float*)src)[at];
-    }
-    if (dst_bf16) ((bf16_t*)dst)[i] = f32_to_bf16(v);
-    else ((float*)dst)[i] = v;
+// operand's rows are not 16-byte aligned.  One thread per 16-byte chunk of
+// the destination (E = 8 bf16 or 4 fp32 values; pitch is a multiple of E),
+// 32-bit index arithmetic (the host checks the sizes), element loads that
+// are contiguous across a wavefront and one 16-byte store.
+template <bool SRC_BF16, bool DST_BF16>
+__global__ void __launch_bounds__(256) prepare_operand(const void* src, void* dst, uint32_t rows, uint32_t outer,
+                                                       uint32_t inner, uint32_t pitch, int64_t stride) {
+  constexpr int E = DST_BF16 ? 8 : 4;
+  const uint32_t per_row = pitch / E;
+  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+  if (i >= rows * per_row) return;
+  const uint32_t r = i / per_row, c0 = (i - r * per_row) * E;
+  const uint32_t z = r / outer, o = r - z * outer;
+  const int64_t at = (int64_t)z * stride + (int64_t)o * inner + c0;
+  float v[E];
+#pragma unroll
+  for (int t = 0; t < E; t++) {
+    v[t] = 0.f;
+    if (c0 + t < inner) v[t] = SRC_BF16 ? bf16_to_f32(((const bf16_t*)src)[at + t]) : ((const float*)src)[at + t];
   }
+  char* d = (char*)dst + (int64_t)i * 16;
+  if constexpr (DST_BF16)
+    global_store(d, u32x4{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
+                          pack_bf16x2(v[6], v[7])});
+  else
+    global_store(d, f32x4{v[0], v[1], v[2], v[3]});
 }
 
 // Split-K reduction: out[b][e] = sum over s of part[b * splits + s][e] in
@@ -371,12 +382,25 @@ void plan(int64_t rows, int64_t inner, int64_t cols, int64_t batch, int64_t left
            : plan_operand(b, b_dtype, bf16, inner, cols, batch, right_stride);
 }
 
+// The re-layout's chunk count must fit the kernel's 32-bit indices.
+bool prepare_fits(const Operand& o) { return o.batches * o.outer * o.pitch < (1ll << 31); }
+
 void launch_prepare(Operand& o, int src_dtype, bool bf16, char* ws, hipStream_t stream) {
-  int64_t total = o.batches * o.outer * o.pitch;
-  unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 1 << 20);
-  hipLaunchKernelGGL(prepare_operand, dim3(blocks < 1 ? 1 : blocks), dim3(256), 0, stream, o.ptr,
-                     src_dtype == QA_BF16, (void*)ws, bf16 ? 1 : 0, o.outer, o.inner, o.pitch, o.batches,
-                     o.src_stride);
+  const int64_t rows = o.batches * o.outer, chunks = rows * o.pitch / (bf16 ? 8 : 4);
+  const dim3 grid((unsigned)((chunks + 255) / 256));
+  const uint32_t r = (uint32_t)rows, ou = (uint32_t)o.outer, in = (uint32_t)o.inner, pi = (uint32_t)o.pitch;
+  if (src_dtype == QA_BF16 && bf16)
+    hipLaunchKernelGGL((prepare_operand<true, true>), grid, dim3(256), 0, stream, o.ptr, (void*)ws, r, ou, in, pi,
+                       o.src_stride);
+  else if (bf16)
+    hipLaunchKernelGGL((prepare_operand<false, true>), grid, dim3(256), 0, stream, o.ptr, (void*)ws, r, ou, in, pi,
+                       o.src_stride);
+  else if (src_dtype == QA_BF16)
+    hipLaunchKernelGGL((prepare_operand<true, false>), grid, dim3(256), 0, stream, o.ptr, (void*)ws, r, ou, in, pi,
+                       o.src_stride);
+  else
+    hipLaunchKernelGGL((prepare_operand<false, false>), grid, dim3(256), 0, stream, o.ptr, (void*)ws, r, ou, in, pi,
+                       o.src_stride);
   o.ptr = ws;
 }
 
@@ -485,6 +509,7 @@ int qutai_amd_gemm(const void* a, const void* b, void* out, int64_t rows, int64_
   const int splits = inner > 0 ? choose_split(rows, cols, inner, batch, &tile, bf16, &chunk) : 1;
   const size_t partial = splits > 1 ? split_bytes(rows, cols, batch, splits) : 0;
   float* part = nullptr;
+  if (inner > 0 && ((pa.copy && !prepare_fits(pa)) || (pb.copy && !prepare_fits(pb)))) return QA_EINVAL;
   if (inner > 0 && (pa.copy || pb.copy || partial)) {
     size_t need = (pa.copy ? pa.bytes : 0) + (pb.copy ? pb.bytes : 0) + partial + 256;
     if (workspace == nullptr || workspace_bytes < need) return QA_EWORKSPACE;

@@ -40,6 +40,51 @@ __global__ void route_select(const float* scores, float* probs, float* weights, 
   for (int64_t slot = 0; slot < top_k; slot++) weights[r * top_k + slot] /= chosen;
 }
 
+// The same selection for up to 32 experts and top-8, the row held in
+// registers (the expression order of route_select, so the same bits).
+template <int E>
+__global__ void route_select_small(const float* scores, float* probs, float* weights, int64_t* indices, int64_t rows,
+                                   int experts, int top_k) {
+  int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  const float* s = scores + r * experts;
+  float x[E], p[E];
+#pragma unroll
+  for (int e = 0; e < E; e++) x[e] = e < experts ? s[e] : -INFINITY;
+  float peak = -INFINITY;
+#pragma unroll
+  for (int e = 0; e < E; e++)
+    if (e < experts) peak = fmaxf(peak, x[e]);
+  float total = 0.f;
+#pragma unroll
+  for (int e = 0; e < E; e++)
+    if (e < experts) total += expf(x[e] - peak);
+#pragma unroll
+  for (int e = 0; e < E; e++)
+    if (e < experts) {
+      p[e] = expf(x[e] - peak) / total;
+      probs[r * experts + e] = p[e];
+    }
+  uint32_t used = 0;
+  float w[8], chosen = 0.f;
+  for (int slot = 0; slot < top_k; slot++) {
+    int best = -1;
+    float bx = 0.f, bp = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; e++)
+      if (e < experts && !((used >> e) & 1u) && (best < 0 || x[e] > bx)) {
+        best = e;
+        bx = x[e];
+        bp = p[e];
+      }
+    used |= 1u << best;
+    indices[r * top_k + slot] = best;
+    w[slot] = bp;
+    chosen += bp;
+  }
+  for (int slot = 0; slot < top_k; slot++) weights[r * top_k + slot] = w[slot] / chosen;
+}
+
 // One workgroup per expert: stable compaction of the (token, slot)
 // assignments routed to it, in increasing assignment order.  The 16 waves
 // own contiguous segments of the assignments: one pass counts each
@@ -58,11 +103,22 @@ __global__ void __launch_bounds__(PACKW * 64) route_pack(const int64_t* indices,
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t seg = (n + PACKW - 1) / PACKW;
   const int64_t lo = min(n, wave * seg), hi = min(n, lo + seg);
+  // U rounds of 64 assignments per iteration: the loads are issued together
+  // (the loop is latency-bound otherwise)
+  constexpr int U = 8;
   int64_t count = 0, lower = 0;
-  for (int64_t at = lo + lane; at < hi; at += 64) {
-    const int64_t x = indices[at];
-    count += x == e;
-    lower += x < e;
+  for (int64_t start = lo; start < hi; start += 64 * U) {
+    int64_t x[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int64_t at = start + u * 64 + lane;
+      x[u] = at < hi ? indices[at] : experts;  // `experts`: neither e nor below it
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      count += x[u] == e;
+      lower += x[u] < e;
+    }
   }
   for (int o = 32; o > 0; o >>= 1) {
     count += __shfl_xor(count, o);
@@ -80,18 +136,29 @@ __global__ void __launch_bounds__(PACKW * 64) route_pack(const int64_t* indices,
     if (w < wave) written += seg_count[w];
   }
   const uint64_t below = (1ull << lane) - 1ull;
-  for (int64_t start = lo; start < hi; start += 64) {
-    const int64_t at = start + lane;
-    const bool sel = at < hi && indices[at] == e;
-    const uint64_t mask = __ballot(sel);
-    if (sel) {
-      const int64_t pos = written + __popcll(mask & below);
-      ids[e * n + pos] = at / top_k;
-      slots[e * n + pos] = at % top_k;
-      locations[at] = pos;
-      order[base + pos] = at / top_k;
+  for (int64_t start = lo; start < hi; start += 64 * U) {
+    int64_t x[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int64_t at = start + u * 64 + lane;
+      x[u] = at < hi ? indices[at] : experts;
     }
-    written += __popcll(mask);
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int64_t at = start + u * 64 + lane;
+      const bool sel = x[u] == e;
+      const uint64_t mask = __ballot(sel);
+      if (sel) {
+        const int64_t pos = written + __popcll(mask & below);
+        // n < 2^31 (checked by the host): 32-bit division
+        const uint32_t token = (uint32_t)at / (uint32_t)top_k, slot = (uint32_t)at - token * (uint32_t)top_k;
+        ids[e * n + pos] = token;
+        slots[e * n + pos] = slot;
+        locations[at] = pos;
+        order[base + pos] = token;
+      }
+      written += __popcll(mask);
+    }
   }
   if (tid == 0) {
     counts[e] = total;
@@ -102,7 +169,17 @@ __global__ void __launch_bounds__(PACKW * 64) route_pack(const int64_t* indices,
   // fixed-order tree), left in column[e] for route_stats
   const int64_t rows = n / top_k;
   float part = 0.f;
-  for (int64_t r = tid; r < rows; r += PACKW * 64) part += probs[r * experts + e];
+  for (int64_t r0 = tid; r0 < rows; r0 += U * PACKW * 64) {
+    float q[U];  // U loads in flight, summed in row order
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int64_t r = r0 + (int64_t)u * PACKW * 64;
+      q[u] = r < rows ? probs[r * experts + e] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++)
+      if (r0 + (int64_t)u * PACKW * 64 < rows) part += q[u];
+  }
   col_part[tid] = part;
   __syncthreads();
   for (int w = PACKW * 32; w > 0; w >>= 1) {
@@ -130,14 +207,29 @@ __global__ void __launch_bounds__(64) route_stats(const int64_t* counts, float* 
 }
 
 // Row gather / scatter in 16-byte pieces.
-__global__ void gather_rows16(const u32x4* x, const int64_t* order, u32x4* out, int64_t count, int64_t pieces,
-                              int backward) {
-  int64_t total = count * pieces;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
-    int64_t r = i / pieces, j = i % pieces;
-    int64_t src = order[r] * pieces + j;
-    if (backward) out[src] = x[i];
-    else out[i] = x[src];
+// One wavefront per gathered row (no per-element index division), 4 pieces
+// per lane in flight.
+__global__ void __launch_bounds__(256) gather_rows16(const u32x4* x, const int64_t* order, u32x4* out, int64_t count,
+                                                     int64_t pieces, int backward) {
+  constexpr int R = 4;
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= count) return;
+  const int64_t src = order[r];
+  const u32x4* from = backward ? x + r * pieces : x + src * pieces;
+  u32x4* to = backward ? out + src * pieces : out + r * pieces;
+  for (int64_t c0 = 0; c0 < pieces; c0 += 64 * R) {
+    u32x4 q[R];
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+      const int64_t c = c0 + i * 64 + lane;
+      if (c < pieces) q[i] = global_load<u32x4>(from + c);
+    }
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+      const int64_t c = c0 + i * 64 + lane;
+      if (c < pieces) global_store(to + c, q[i]);
+    }
   }
 }
 template <class T>
@@ -167,18 +259,105 @@ __global__ void combine_kernel(const T* eo, const float* w, const int64_t* idx, 
       int64_t at = row * top_k + s;
       float f = w ? w[at] : 1.f;
       const T* src = eo + (off[idx[at]] + loc[at]) * width + j;
+      float x[V];
+      if constexpr (V * sizeof(T) == 16) {  // one 16-byte load (rows and base 16-byte aligned)
+        const u32x4 q = global_load<u32x4>(src);
+        if constexpr (sizeof(T) == 2) {
+#pragma unroll
+          for (int h = 0; h < 4; h++) {
+            x[2 * h] = __uint_as_float(q[h] << 16);
+            x[2 * h + 1] = __uint_as_float(q[h] & 0xffff0000u);
+          }
+        } else {
+#pragma unroll
+          for (int h = 0; h < 4; h++) x[h] = __uint_as_float(q[h]);
+        }
+      } else {
+#pragma unroll
+        for (int v = 0; v < V; v++) {
+          if constexpr (sizeof(T) == 2) x[v] = bf16_to_f32(src[v]);
+          else x[v] = (float)src[v];
+        }
+      }
+#pragma unroll
+      for (int v = 0; v < V; v++) acc[v] += f * x[v];
+    }
+    U* dst = y + row * width + j;
+    if constexpr (sizeof(U) == 2 && V == 8) {
+      global_store(dst, u32x4{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]), pack_bf16x2(acc[4], acc[5]),
+                              pack_bf16x2(acc[6], acc[7])});
+    } else if constexpr (sizeof(U) == 2 && V == 4) {
+      global_store(dst, u32x2{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])});
+    } else {
 #pragma unroll
       for (int v = 0; v < V; v++) {
-        float x;
-        if constexpr (sizeof(T) == 2) x = bf16_to_f32(src[v]);
-        else x = (float)src[v];
-        acc[v] += f * x;
+        if constexpr (sizeof(U) == 2) dst[v] = f32_to_bf16(acc[v]);
+        else dst[v] = acc[v];
+      }
+    }
+  }
+}
+
+// The same combine with one wavefront per token row (16-byte chunks of
+// the expert rows, 4 chunks per lane and slot in flight at once): the
+// routing metadata is read once per row instead of once per chunk, and the
+// row's loads overlap instead of forming one dependent chain per chunk.
+// Same sums in the same order as combine_kernel.
+template <class T, class U>
+__global__ void __launch_bounds__(256) combine_rows_wave(const T* eo, const float* w, const int64_t* idx,
+                                                         const int64_t* loc, const int64_t* off, U* y, int64_t rows,
+                                                         int64_t width, int64_t top_k) {
+  constexpr int V = 16 / sizeof(T), R = 4;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t chunks = width / V;
+  for (int64_t c0 = 0; c0 < chunks; c0 += 64 * R) {
+    float acc[R][V];
+#pragma unroll
+    for (int i = 0; i < R; i++)
+#pragma unroll
+      for (int v = 0; v < V; v++) acc[i][v] = 0.f;
+    for (int64_t s = 0; s < top_k; s++) {
+      const int64_t at = row * top_k + s;
+      const float f = w ? w[at] : 1.f;
+      const T* src = eo + (off[idx[at]] + loc[at]) * width;
+      u32x4 q[R];
+#pragma unroll
+      for (int i = 0; i < R; i++) {
+        const int64_t c = c0 + i * 64 + lane;
+        q[i] = c < chunks ? global_load<u32x4>(src + c * V) : u32x4{0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int i = 0; i < R; i++) {
+        float x[V];
+        if constexpr (sizeof(T) == 2) {
+#pragma unroll
+          for (int h = 0; h < 4; h++) {
+            x[2 * h] = __uint_as_float(q[i][h] << 16);
+            x[2 * h + 1] = __uint_as_float(q[i][h] & 0xffff0000u);
+          }
+        } else {
+#pragma unroll
+          for (int h = 0; h < 4; h++) x[h] = __uint_as_float(q[i][h]);
+        }
+#pragma unroll
+        for (int v = 0; v < V; v++) acc[i][v] += f * x[v];
       }
     }
 #pragma unroll
-    for (int v = 0; v < V; v++) {
-      if constexpr (sizeof(U) == 2) y[row * width + j + v] = f32_to_bf16(acc[v]);
-      else y[row * width + j + v] = acc[v];
+    for (int i = 0; i < R; i++) {
+      const int64_t c = c0 + i * 64 + lane;
+      if (c >= chunks) continue;
+      U* dst = y + row * width + c * V;
+      if constexpr (sizeof(U) == 2 && V == 8) {
+        global_store(dst, u32x4{pack_bf16x2(acc[i][0], acc[i][1]), pack_bf16x2(acc[i][2], acc[i][3]),
+                                pack_bf16x2(acc[i][4], acc[i][5]), pack_bf16x2(acc[i][6], acc[i][7])});
+      } else if constexpr (sizeof(U) == 2) {
+        global_store(dst, u32x2{pack_bf16x2(acc[i][0], acc[i][1]), pack_bf16x2(acc[i][2], acc[i][3])});
+      } else {
+        global_store(dst, f32x4{acc[i][0], acc[i][1], acc[i][2], acc[i][3]});
+      }
     }
   }
 }
@@ -259,8 +438,14 @@ int qutai_amd_route(const float* scores, float* probs, float* weights, int64_t* 
   if (rows < 0 || experts <= 0 || top_k <= 0 || top_k > experts) return QA_EINVAL;
   hipStream_t s = (hipStream_t)stream;
   int64_t n = rows * top_k;
-  if (experts > 0x7fffffff) return QA_EINVAL;
-  if (rows > 0)
+  if (experts > 0x7fffffff || n >= (1ll << 31)) return QA_EINVAL;
+  if (rows > 0 && experts <= 8 && top_k <= 8)
+    hipLaunchKernelGGL(route_select_small<8>, dim3(blocks_for(rows)), dim3(256), 0, s, scores, probs, weights, indices,
+                       rows, (int)experts, (int)top_k);
+  else if (rows > 0 && experts <= 32 && top_k <= 8)
+    hipLaunchKernelGGL(route_select_small<32>, dim3(blocks_for(rows)), dim3(256), 0, s, scores, probs, weights,
+                       indices, rows, (int)experts, (int)top_k);
+  else if (rows > 0)
     hipLaunchKernelGGL(route_select, dim3(blocks_for(rows)), dim3(256), 0, s, scores, probs, weights, indices, rows,
                        experts, top_k);
   hipLaunchKernelGGL(route_pack, dim3((unsigned)experts), dim3(PACKW * 64), 0, s, indices, counts, ids, slots,
@@ -280,7 +465,8 @@ int qutai_amd_route_gather(const void* x, const int64_t* order, void* out, int64
   bool vec = (width * es) % 16 == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)out % 16 == 0;
   if (vec) {
     int64_t pieces = width * es / 16;
-    hipLaunchKernelGGL(gather_rows16, dim3(blocks_for(count * pieces)), dim3(256), 0, s, (const u32x4*)x, order,
+    if ((count + 3) / 4 > 0x7fffffff) return QA_EINVAL;
+    hipLaunchKernelGGL(gather_rows16, dim3((unsigned)((count + 3) / 4)), dim3(256), 0, s, (const u32x4*)x, order,
                        (u32x4*)out, count, pieces, backward);
   } else if (dtype == BF16) {
     hipLaunchKernelGGL(gather_rows<bf16_t>, dim3(blocks_for(count * width)), dim3(256), 0, s, (const bf16_t*)x,
@@ -303,8 +489,30 @@ int qutai_amd_combine(const void* expert_out, const float* weights, const int64_
   if (out_dtype != dtype && !(dtype == F32 && out_dtype == BF16)) return QA_EINVAL;
   if (rows * width == 0) return QA_OK;
   hipStream_t s = (hipStream_t)stream;
+  // vector paths: 16-byte loads of expert rows, 16- / 8-byte stores
+  const bool aligned = (uintptr_t)expert_out % 16 == 0 && (uintptr_t)y % 16 == 0;
+  const unsigned wave_blocks = (unsigned)((rows + 3) / 4);
+  if ((rows + 3) / 4 <= 0x7fffffff && aligned) {
+    if (dtype == BF16 && width % 8 == 0) {
+      hipLaunchKernelGGL((combine_rows_wave<bf16_t, bf16_t>), dim3(wave_blocks), dim3(256), 0, s,
+                         (const bf16_t*)expert_out, weights, indices, locations, offsets, (bf16_t*)y, rows, width,
+                         top_k);
+      return (int)hipGetLastError();
+    }
+    if (dtype == F32 && width % 4 == 0) {
+      if (out_dtype == BF16)
+        hipLaunchKernelGGL((combine_rows_wave<float, bf16_t>), dim3(wave_blocks), dim3(256), 0, s,
+                           (const float*)expert_out, weights, indices, locations, offsets, (bf16_t*)y, rows, width,
+                           top_k);
+      else
+        hipLaunchKernelGGL((combine_rows_wave<float, float>), dim3(wave_blocks), dim3(256), 0, s,
+                           (const float*)expert_out, weights, indices, locations, offsets, (float*)y, rows, width,
+                           top_k);
+      return (int)hipGetLastError();
+    }
+  }
   if (dtype == F32 && out_dtype == BF16) {  // fp32 rows summed straight into bf16 token rows
-    if (width % 4 == 0)
+    if (width % 4 == 0 && aligned)
       hipLaunchKernelGGL((combine_kernel<float, 4, bf16_t>), dim3(blocks_for(rows * width / 4)), dim3(256), 0, s,
                          (const float*)expert_out, weights, indices, locations, offsets, (bf16_t*)y, rows, width,
                          top_k);
@@ -315,7 +523,7 @@ int qutai_amd_combine(const void* expert_out, const float* weights, const int64_
     return (int)hipGetLastError();
   }
   if (dtype == BF16) {
-    if (width % 8 == 0)
+    if (width % 8 == 0 && aligned)
       hipLaunchKernelGGL((combine_kernel<bf16_t, 8>), dim3(blocks_for(rows * width / 8)), dim3(256), 0, s,
                          (const bf16_t*)expert_out, weights, indices, locations, offsets, (bf16_t*)y, rows, width,
                          top_k);
@@ -324,7 +532,7 @@ int qutai_amd_combine(const void* expert_out, const float* weights, const int64_
                          (const bf16_t*)expert_out, weights, indices, locations, offsets, (bf16_t*)y, rows, width,
                          top_k);
   } else {
-    if (width % 4 == 0)
+    if (width % 4 == 0 && aligned)
       hipLaunchKernelGGL((combine_kernel<float, 4>), dim3(blocks_for(rows * width / 4)), dim3(256), 0, s,
                          (const float*)expert_out, weights, indices, locations, offsets, (float*)y, rows, width,
                          top_k);

@@ -32,10 +32,11 @@ sys.path.insert(0, sys.argv[2])
 from qutai_amd.backends import amd
 from tests.helpers import download, normal, upload
 cases = eval(sys.argv[3])
+dtype = sys.argv[4] if len(sys.argv) > 4 else "bfloat16"
 outs = {}
 for m, k, n, batch in cases:
     a, b = normal(10 + m, batch * m * k), normal(20 + n, batch * k * n)
-    left, right = upload(a, "bfloat16"), upload(b, "bfloat16")
+    left, right = upload(a, dtype), upload(b, dtype)
     for ta in (False, True):
         for tb in (False, True):
             kw = dict(batch=batch, transpose_left=ta, transpose_right=tb)
@@ -44,15 +45,22 @@ for m, k, n, batch in cases:
             acc = upload(normal(30 + m, batch * m * n), "bfloat16")
             amd.gemm(left, right, m, k, n, out=acc, out_dtype="bfloat16", accumulate=True, **kw)
             outs[f"{m}_{k}_{n}_{batch}_{ta:d}{tb:d}_acc"] = download(acc)
+# large outputs (the ragged config-2 shape) are compared through a CRC of
+# their bytes instead of the values themselves
+import zlib
+outs = {k: (np.array([zlib.crc32(v.tobytes())]) if v.size > (1 << 22) else v) for k, v in outs.items()}
 np.savez(sys.argv[1], **outs)
 print("done", len(outs))
 """
 
 
-def _run(tile, path):
-    env = dict(os.environ, QUTAI_AMD_GEMM_TILE=tile, QUTAI_AMD_SPLITK="1")
-    print(f"tile {tile}", flush=True)
-    out = subprocess.run([sys.executable, "-c", CHILD, str(path), str(ROOT), repr(CASES)], env=env,
+def _run(tile, path, cases=CASES, dtype="bfloat16"):
+    env = dict(os.environ, QUTAI_AMD_SPLITK="1")
+    env.pop("QUTAI_AMD_GEMM_TILE", None)
+    if tile:
+        env["QUTAI_AMD_GEMM_TILE"] = tile
+    print(f"tile {tile or 'default'} {dtype}", flush=True)
+    out = subprocess.run([sys.executable, "-c", CHILD, str(path), str(ROOT), repr(cases), dtype], env=env,
                          capture_output=True, text=True, timeout=110)
     assert out.returncode == 0 and "done" in out.stdout, out.stderr[-2000:]
     return np.load(path)
@@ -74,3 +82,4 @@ def test_forced_tiles_are_bit_identical(tmp_path):
         other = _run(tile, tmp_path / f"{tile}.npz")
         for key in base.files:
             assert np.array_equal(base[key], other[key]), (tile, key)
+
