@@ -1,0 +1,332 @@
+"""Host model of the GEMM kernels' memory addressing (CPU only).
+
+Every operand load of the MFMA GEMM kernels is a 16-byte buffer load whose
+address is a descriptor base plus a per-lane byte offset; a load that the
+kernel decides is outside the matrix gets the offset 0x80000000, beyond the
+descriptor's range, and reads zeros.  Whether the remaining loads stay inside
+the operand's allocation rests on host-side invariants (16-byte aligned K-major
+rows, zero-padded re-layouts, split-K chunks of a multiple of 64, ...), not on
+the descriptor range, which starts at the tile's first row and may extend past
+the allocation.  This module restates, with numpy, the offsets the kernels
+compute -- per tile, K step, copy instruction and lane -- so that tests can
+check over randomised shapes that every issued load and every store lies
+inside its allocation.
+
+Restated from qutai_amd/csrc/gemm_kernel.h (tile scheduling and operand
+bases 342-404, descriptor bases 418-425 and 466-471, DMA lane offsets
+430-465, register-staging offsets 523-545, epilogue 590-660 and 711-770) and
+qutai_amd/csrc/gemm_short.h (copies 91-101, output offsets 104-112 and
+176-186); the host's operand re-layout rule (plan_operand), split-K chunking
+(choose_split) and grouped grid from qutai_amd/csrc/gemm.hip.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+
+OOB = 0x80000000
+RANGE_CAP = 0x7FFFFFF0
+
+
+@dataclass(frozen=True)
+class Config:
+    """One kernel configuration: GemmKernel<F32, TA, TB, BM, BN, WM, WN, BK, STAGES, DMA, SWIGLU>."""
+    name: str
+    bm: int
+    bn: int
+    wm: int
+    wn: int
+    bk: int
+    stages: int
+    dma: bool = True
+    swiglu: bool = False
+
+
+def tile_configs(f32: bool) -> list[Config]:
+    """The tile table of launch_tile (gemm.hip): K per stage 64/32 (bf16/fp32)
+    for the two- and three-stage rings, 32/16 for the four-stage ones; T and U
+    are 256x256 for fp32."""
+    kb, kr = (16, 32) if f32 else (32, 64)
+    table = [Config("L8D2", 256, 256, 2, 4, kr, 2), Config("L8R", 256, 256, 2, 4, kr, 2, dma=False),
+             Config("L4D2", 256, 256, 2, 2, kr, 2), Config("S", 128, 128, 2, 2, kb, 4),
+             Config("S2", 128, 128, 2, 2, kb, 2), Config("N", 256, 64, 4, 1, kb, 4),
+             Config("W", 64, 256, 1, 4, kb, 4), Config("H", 256, 128, 4, 2, kr, 3)]
+    if f32:
+        table += [Config("T", 256, 256, 2, 4, kr, 2), Config("U", 256, 256, 2, 4, kr, 2)]
+    else:
+        table += [Config("T", 192, 256, 2, 4, kr, 2), Config("U", 256, 192, 4, 2, kr, 2)]
+    return table
+
+
+SWIGLU = Config("SWIGLU", 256, 256, 2, 4, 64, 2, swiglu=True)
+
+
+# ---- LDS chunk maps (OperandTile::coords) -------------------------------------------
+
+def _swz_k(ck: int, r: np.ndarray) -> np.ndarray:
+    return (r ^ (r >> 3)) & 7 if ck == 8 else ((r >> 1) ^ (r >> 3)) & 3
+
+
+def _swz_mn(f32: bool, cr: int, k: np.ndarray) -> np.ndarray:
+    if f32:
+        return ((k >> 3) & 1) * 8
+    return (k & 3) * 4 if cr % 16 == 0 else ((k >> 1) & 1) * 4
+
+
+def chunk_coords(f32: bool, kmajor: bool, rows: int, bk: int, q: np.ndarray):
+    """(outer, logical chunk) of physical chunk q of a [rows][bk] (K-major) or
+    [bk][rows] (MN-major) operand stage."""
+    e = 4 if f32 else 8
+    if kmajor:
+        ck = bk // e
+        outer = q // ck
+        return outer, (q % ck) ^ _swz_k(ck, outer)
+    cr = rows // e
+    outer = q // cr
+    return outer, (q % cr) ^ _swz_mn(f32, cr, outer)
+
+
+@dataclass
+class Operand:
+    """An operand as the kernel sees it: element strides and the allocation
+    (in elements) that its loads must stay inside."""
+    ld: int
+    batch_stride: int
+    alloc: int
+
+
+class Violation(AssertionError):
+    pass
+
+
+def _check(what: str, lo: np.ndarray, hi: np.ndarray, alloc_bytes: int):
+    """Byte ranges [lo, hi) must lie in [0, alloc_bytes)."""
+    if lo.size == 0:
+        return
+    if lo.min() < 0 or hi.max() > alloc_bytes:
+        bad = np.flatnonzero((lo < 0) | (hi > alloc_bytes))[0]
+        raise Violation(f"{what}: access [{lo.flat[bad]}, {hi.flat[bad]}) outside [0, {alloc_bytes})")
+
+
+def operand_loads(cfg: Config, f32: bool, kmajor: bool, rows_tile: int, base_elem: int, row0: int, rows: int,
+                  k_len: int, ld: int, alloc: int, what: str, gather: np.ndarray | None = None,
+                  swiglu_up: bool = False):
+    """Every load of one operand over one tile's K loop: base_elem is the
+    operand pointer after the mode's adjustments (in elements), row0 the
+    tile's first row (A) / column (B), rows the operand's valid extent (M or
+    N), k_len the K range.  gather (grouped A, K-major): row i of the tile's
+    group is row gather[row0 + i] of the operand, the descriptor spans the
+    whole allocation."""
+    e, es = (4, 4) if f32 else (8, 2)
+    nt = 64 * cfg.wm * cfg.wn
+    chunks = rows_tile * cfg.bk // e
+    if cfg.dma:
+        q = np.arange(chunks)  # physical chunk (j * NW + wave) * 64 + lane
+        outer, c = chunk_coords(f32, kmajor, rows_tile, cfg.bk, q)
+    else:  # register staging: thread idx = tid + i * NT walks the chunks row by row
+        idx = np.arange(chunks)
+        per = cfg.bk // e if kmajor else rows_tile // e
+        outer, c = idx // per, idx % per
+    if cfg.swiglu and what.startswith("B"):
+        # tile row `outer` is row (outer / 64) * 32 + outer % 32 of the gate
+        # or up weight (the same offsets for both, each its own descriptor)
+        outer = ((outer >> 6) << 5) + (outer & 31)
+    kidx = c * e if kmajor else outer
+    valid = (row0 + outer < rows) if kmajor else (row0 + c * e < rows)
+    if gather is not None:
+        src = np.where(valid, gather[np.minimum(row0 + outer, gather.size - 1)], outer)
+        off = (src * ld + c * e) * es
+    else:
+        off = (outer * ld + c * e) * es
+    nk = (k_len + cfg.bk - 1) // cfg.bk
+    for kt in range(nk):
+        k0 = kt * cfg.bk
+        krem = k_len - k0
+        if gather is not None:
+            tile_elem = base_elem + k0
+            span = alloc * es
+        else:
+            tile_elem = base_elem + (row0 * ld + k0 if kmajor else k0 * ld + row0)
+            span = (rows_tile * ld if kmajor else cfg.bk * ld) * es
+        rng = min(span, RANGE_CAP)
+        issued = valid & (kidx < krem)
+        offs = np.where(issued, off, OOB)
+        hit = offs + 16 <= rng  # the load reads memory (else zeros)
+        if np.any(issued & ~hit):
+            raise Violation(f"{what}: an in-matrix chunk falls outside the descriptor range")
+        lo = tile_elem * es + offs[hit]
+        _check(f"{what} load", lo, lo + 16, alloc * es)
+
+
+def output_stores(cfg: Config, f32_out: bool, out_elem: int, row0: int, col0: int, m: int, n: int, ldc: int,
+                  alloc: int, vec: int, what: str = "C"):
+    """Element ranges the epilogue writes for one tile (store_slab / write4):
+    the straight-line path for a whole in-range wave tile with aligned rows,
+    else per 4 columns with row < M and col < N checks."""
+    es = 4 if f32_out else 2
+    tm = cfg.bm // cfg.wm
+    bno = cfg.bn // 2 if cfg.swiglu else cfg.bn
+    tw = bno // cfg.wn
+    for wm in range(cfg.wm):
+        for wn in range(cfg.wn):
+            r0, c0 = row0 + wm * tm, col0 + wn * tw
+            fast = vec >= (1 if f32_out else 2) and r0 + tm <= m and c0 + tw <= n
+            if fast:
+                rows = np.arange(r0, r0 + tm)
+                lo = (out_elem + rows * ldc + c0) * es
+                _check(f"{what} store (fast)", lo, lo + tw * es, alloc * es)
+            else:
+                rows = np.arange(r0, min(r0 + tm, m))
+                if rows.size == 0 or c0 >= n:
+                    continue
+                last = min(c0 + tw, n)
+                lo = (out_elem + rows * ldc + c0) * es
+                _check(f"{what} store", lo, lo + (last - c0) * es, alloc * es)
+
+
+def plan_operand(inner: int, outer: int, batch: int, stride: int, f32_compute: bool, aligned_base: bool = True):
+    """plan_operand (gemm.hip): rows of `inner` elements are used in place when
+    16-byte aligned (inner a multiple of E, batch stride too), else re-laid out
+    into a zero-padded pitch.  Returns (ld, batch stride, allocation) as the
+    kernel sees the operand."""
+    e = 4 if f32_compute else 8
+    alloc = (batch - 1) * stride + outer * inner if stride else outer * inner
+    if aligned_base and inner % e == 0 and (batch <= 1 or stride % e == 0):
+        return Operand(inner, stride, alloc)
+    pitch = (inner + e - 1) // e * e
+    batches = 1 if stride == 0 or batch <= 1 else batch
+    return Operand(pitch, 0 if stride == 0 else outer * pitch, batches * outer * pitch)
+
+
+def split_chunk(inner: int, splits: int) -> tuple[int, int]:
+    """choose_split's chunking: chunks of a multiple of 64 elements."""
+    c = ((inner + splits - 1) // splits + 63) // 64 * 64
+    return (inner + c - 1) // c, c
+
+
+def plain_gemm(cfg: Config, f32: bool, m: int, k: int, n: int, batch: int, ta: bool, tb: bool,
+               broadcast_a: bool = False, broadcast_b: bool = False, splits: int = 1, out_f32: bool = True):
+    """All loads and stores of one qutai_amd_gemm call on tile `cfg`
+    (batched, broadcast operands, optional split-K into fp32 partials)."""
+    pa = plan_operand(m if ta else k, k if ta else m, batch, 0 if broadcast_a else m * k, f32)
+    pb = plan_operand(k if tb else n, n if tb else k, batch, 0 if broadcast_b else k * n, f32)
+    ka, kb = not ta, tb
+    chunk = k
+    if splits > 1:
+        splits, chunk = split_chunk(k, splits)
+        out_f32 = True
+    tiles_m, tiles_n = (m + cfg.bm - 1) // cfg.bm, (n + cfg.bn - 1) // cfg.bn
+    out_alloc = splits * batch * m * n
+    vec = 2 if n % 8 == 0 else 1 if n % 4 == 0 else 0
+    for z in range(batch * splits):
+        prod, s = divmod(z, splits)
+        k_lo = s * chunk
+        k_len = min(k, k_lo + chunk) - k_lo
+        a_base = prod * pa.batch_stride + k_lo * (1 if ka else pa.ld)
+        b_base = prod * pb.batch_stride + k_lo * (1 if kb else pb.ld)
+        for tm in range(tiles_m):
+            for tn in range(tiles_n):
+                operand_loads(cfg, f32, ka, cfg.bm, a_base, tm * cfg.bm, m, k_len, pa.ld, pa.alloc, "A")
+                operand_loads(cfg, f32, kb, cfg.bn, b_base, tn * cfg.bn, n, k_len, pb.ld, pb.alloc, "B")
+                output_stores(cfg, out_f32, z * m * n, tm * cfg.bm, tn * cfg.bn, m, n, n, out_alloc, vec)
+
+
+def grouped_gemm(cfg: Config, f32: bool, counts: list[int], inner: int, cols: int, transpose_right: bool,
+                 gather: np.ndarray | None = None, source_rows: int = 0):
+    """qutai_amd_gemm_grouped (and the SwiGLU form with cfg = SWIGLU): group g
+    owns rows [offsets[g], offsets[g+1]) of A (or, with gather, the rows
+    gather[offsets[g]:...] of a source_rows-row A) and of out; its B is
+    b + g * expert_stride."""
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    capacity = int(offsets[-1])
+    groups = len(counts)
+    es_in = 4 if f32 else 2
+    ldb = inner if transpose_right else cols
+    expert_stride = cols * inner
+    a_alloc = (source_rows if gather is not None else capacity) * inner
+    b_alloc = groups * expert_stride
+    bno = cfg.bn // 2 if cfg.swiglu else cfg.bn
+    tiles_n = (cols + bno - 1) // bno
+    vec = 2 if cols % 8 == 0 else 1 if cols % 4 == 0 else 0
+    # the entry point's own checks (QA_EINVAL otherwise): 16-byte rows
+    e = 4 if f32 else 8
+    if inner % e or ldb % e or (inner * 256 * es_in) >= 2 ** 31 or (ldb * 256 * es_in) >= 2 ** 31:
+        raise ValueError("rejected by qutai_amd_gemm_grouped")
+    for g in range(groups):
+        lo, hi = int(offsets[g]), int(offsets[g + 1])
+        rows = hi - lo
+        for tm in range((rows + cfg.bm - 1) // cfg.bm):
+            row0 = tm * cfg.bm
+            if gather is not None:
+                operand_loads(cfg, f32, True, cfg.bm, 0, row0, rows, inner, inner, a_alloc, "A",
+                              gather=gather[lo:hi])
+            else:
+                operand_loads(cfg, f32, True, cfg.bm, lo * inner, row0, rows, inner, inner, a_alloc, "A")
+            for tn in range(tiles_n):
+                col0 = tn * bno
+                if cfg.swiglu:  # gate and up weights: one 32-row block each in turn
+                    for up in (False, True):
+                        operand_loads(cfg, f32, True, cfg.bn, g * expert_stride, col0, cols, inner, ldb, b_alloc,
+                                      "B" + ("up" if up else "gate"), swiglu_up=up)
+                else:
+                    operand_loads(cfg, f32, transpose_right, cfg.bn, g * expert_stride, col0, cols, inner, ldb,
+                                  b_alloc, "B")
+                output_stores(cfg, False, lo * cols, row0, col0, rows, cols, cols, capacity * cols, vec)
+
+
+def grouped_k_gemm(cfg: Config, f32: bool, counts: list[int], rows: int, cols: int):
+    """qutai_amd_gemm_grouped_k: out[g] = A_g^T B_g over the K rows
+    [offsets[g], offsets[g+1]) of a [capacity][rows] and b [capacity][cols]
+    (A and B MN-major, ta = 1, tb = 0)."""
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    capacity = int(offsets[-1])
+    pa = plan_operand(rows, capacity, 1, 0, f32)
+    pb = plan_operand(cols, capacity, 1, 0, f32)
+    tiles_m, tiles_n = (rows + cfg.bm - 1) // cfg.bm, (cols + cfg.bn - 1) // cfg.bn
+    vec = 2 if cols % 8 == 0 else 1 if cols % 4 == 0 else 0
+    for g in range(len(counts)):
+        k_lo, k_hi = int(offsets[g]), int(offsets[g + 1])
+        for tm in range(tiles_m):
+            for tn in range(tiles_n):
+                operand_loads(cfg, f32, False, cfg.bm, k_lo * pa.ld, tm * cfg.bm, rows, k_hi - k_lo, pa.ld,
+                              pa.alloc, "A")
+                operand_loads(cfg, f32, False, cfg.bn, k_lo * pb.ld, tn * cfg.bn, cols, k_hi - k_lo, pb.ld,
+                              pb.alloc, "B")
+                output_stores(cfg, True, g * rows * cols, tm * cfg.bm, tn * cfg.bn, rows, cols, cols,
+                              len(counts) * rows * cols, vec)
+
+
+def short_strip(m: int, k: int, n: int, batch: int, strip: int):
+    """The short-K strip kernel (gemm_short.h): A block [128][64] and B chunks
+    through descriptors starting at the block's / chunk's first row with a
+    128-row range; output 16-byte stores at row offsets inside the tile's
+    existing rows and columns below N (N a multiple of 16)."""
+    assert k <= 64 and n % 16 == 0
+    pa = plan_operand(k, m, batch, m * k, False)
+    pb = plan_operand(k, n, batch, n * k, False)
+    cfg = Config("R", 128, 128, 2, 2, 64, 3)
+    tiles_m, chunks = (m + 127) // 128, (n + 127) // 128
+    lane = np.arange(64)
+    for z in range(batch):
+        for tm in range(tiles_m):
+            row0 = tm * 128
+            # copy(): offsets (row * ld + chunk * 8) * 2 from A + row0 * lda
+            operand_loads(cfg, False, True, 128, z * pa.batch_stride, row0, m, k, pa.ld, pa.alloc, "A")
+            rows_here = min(128, m - row0)
+            orange = min(rows_here * n * 2, RANGE_CAP)
+            obase = (z * m * n + row0 * n) * 2
+            for c in range(chunks):
+                n0 = c * 128
+                operand_loads(cfg, False, True, 128, z * pb.batch_stride, n0, n, k, pb.ld, pb.alloc, "B")
+                for wm in range(2):
+                    for wn in range(2):
+                        for fm in range(2):
+                            for it in range(4):
+                                idx = it * 64 + lane
+                                r, q = idx >> 3, idx & 7
+                                col = n0 + wn * 64 + 8 * q
+                                off = np.where(col < n, ((wm * 64 + fm * 32 + r) * n + col) * 2, OOB)
+                                hit = off + 16 <= orange
+                                lo = obase + off[hit]
+                                _check("C store (strip)", lo, lo + 16, batch * m * n * 2)
