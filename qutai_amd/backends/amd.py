@@ -159,6 +159,25 @@ def storage(values: Iterable = (), *, dtype: str = "float64") -> AMDStorage:
     return result
 
 
+# The storage class under the name the reference's serialization and
+# checkpoint code spells `cuda.CUDAStorage` (core/serialization.py:69,
+# lm/checkpoint.py:89): constructor (size, dtype), `ptr`, `nbytes`, `runtime`.
+storage_class = AMDStorage
+
+
+def normal(size: int, mean: float = 0.0, std: float = 1.0, *, seed=None, dtype: str = "float32") -> AMDStorage:
+    """N(mean, std) values (cuda.normal, src/qutai/backends/cuda.py:297-302,
+    called by nn Dropout, nn/layers.py:87): drawn on the host with
+    Random(seed).gauss, as the CPU path draws them (cpu_lm.py:6-8), and
+    uploaded once."""
+    if dtype not in ("float32", "float64"):
+        raise ValueError("normal draws float32 or float64 values")
+    from random import Random
+
+    draw = Random(seed)
+    return storage(array("d", (draw.gauss(mean, std) for _ in range(size))), dtype=dtype)
+
+
 def full(size: int, value: float = 0.0, *, dtype: str = "float64") -> AMDStorage:
     result = AMDStorage(size, dtype)
     if size:

@@ -33,6 +33,9 @@ LM = ["add_into", "attention", "attention_backward", "combine", "combine_backwar
       "embedding_backward", "gemm", "head_gradient", "head_loss", "head_rows", "head_rows_backward",
       "normal", "prepare_labels", "rms_norm", "rms_norm_backward", "rope", "route_gather", "route_gather_backward",
       "routing", "routing_backward", "silu", "silu_backward", "take"]
+# direct module calls `cuda.<name>` / `cuda_lm.<name>` of those callers
+DIRECT = {"nn/layers.py:87-88": ["normal", "full", "relu_backward"]}
+DIRECT_LM = {"core/operations/transforms.py:19,44": ["embedding", "embedding_backward"]}
 # generic functions of those files that are off the contraction path: batch
 # and layer normalisation and argmax (classification / sampling)
 OFF_PATH = {"batch_norm2d", "batch_norm2d_backward", "channel_stats", "layer_norm", "layer_norm_backward", "argmax",
@@ -63,6 +66,15 @@ def test_generic_functions_exported(where):
     assert not missing, f"{where}: amd lacks {missing}"
 
 
+def test_direct_module_calls_exported():
+    for where, names in DIRECT.items():
+        assert all(callable(getattr(amd, n, None)) for n in names), where
+    for where, names in DIRECT_LM.items():
+        assert all(callable(getattr(amd_lm, n, None)) for n in names), where
+    # the storage class the serialization / checkpoint code constructs
+    assert amd.storage_class is amd.AMDStorage
+
+
 def test_lm_functions_exported():
     missing = [name for name in LM if not callable(getattr(amd_lm, name, None))]
     assert not missing, missing
@@ -90,4 +102,8 @@ def test_lists_cover_the_reference_callers():
                                                                                lm_text))
     listed = {name for names in GENERIC.values() for name in names}
     assert found - OFF_PATH <= listed, sorted(found - OFF_PATH - listed)
+    for table, module in ((DIRECT, "cuda"), (DIRECT_LM, "cuda_lm")):
+        for where, names in table.items():
+            text = (REFERENCE / where.split(":")[0]).read_text(encoding="utf8")
+            assert set(re.findall(rf"\b{module}\.([a-z_]+)\(", text)) <= set(names), where
     assert lm_found <= set(LM) | listed, sorted(lm_found - set(LM) - listed)

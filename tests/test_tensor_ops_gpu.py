@@ -385,3 +385,14 @@ def test_cached_attention_fp32_against_float64_oracle(amd):
     expected = mixed @ weight["output"]
     assert ora.rel_frobenius(got, expected) <= 1e-5
     assert math.isfinite(float(got.sum()))
+
+
+def test_normal_draws_are_seeded(amd):
+    """cuda.normal's role for nn Dropout (nn/layers.py:87): N(mean, std)
+    values, the same values for the same seed."""
+    a = download(amd.normal(20000, 2.0, 0.5, seed=3, dtype="float32"))
+    b = download(amd.normal(20000, 2.0, 0.5, seed=3, dtype="float32"))
+    assert np.array_equal(a, b)
+    assert abs(a.mean() - 2.0) < 0.02 and abs(a.std() - 0.5) < 0.02
+    with pytest.raises(ValueError):
+        amd.normal(4, dtype="int64")
