@@ -484,9 +484,10 @@ def vocab_block(chunk_size, rows, vocab):
 
 
 KEEP_LOGITS_BYTES = 2 << 30
+KEEP_LOGITS_CHUNKS = 4
 
 
-def projection_loss(hidden, weight, labels, chunk_size, *, prepared_labels=None):
+def projection_loss(hidden, weight, labels, chunk_size, *, prepared_labels=None, keep_logits=None):
     """Mean next-token cross entropy of hidden (batch, time, width) against
     the tied (vocab, width) weight; labels -100 are ignored
     (src/qutai/lm/layers.py:194-257).  As in the reference at most
@@ -498,12 +499,16 @@ def projection_loss(hidden, weight, labels, chunk_size, *, prepared_labels=None)
     of the weight gradient with one GEMM over all rows (no read-modify-write
     of the whole gradient per chunk), while dX accumulates in fp32.
 
-    When all rows x vocab logits fit KEEP_LOGITS_BYTES and a backward can
-    follow, the forward's blocks are kept and the first backward turns them
-    into the gradient in place instead of recomputing them (the same values:
-    the GEMM is deterministic); a second backward over a retained graph
-    recomputes.  The reference's chunking bounds memory on small GPUs; on a
-    288 GB one the config-4 head keeps 268 MB and skips four 137-GFLOP GEMMs."""
+    With ``keep_logits`` (default: when the rows are at most
+    KEEP_LOGITS_CHUNKS x chunk_size -- the caller's chunk still bounds the
+    memory, to that factor -- and all rows x vocab logits fit
+    KEEP_LOGITS_BYTES) and a backward to follow, the forward's blocks are
+    kept and the first backward turns them into the gradient in place instead
+    of recomputing them (the same values: the GEMM is deterministic); the
+    graph holds them until then, and a second backward over a retained graph
+    recomputes.  ``keep_logits=False`` restores the reference's bound of
+    chunk_size x vocab logits.  The config-4 head (4096 rows, chunk 1024)
+    keeps 268 MB and skips four 137-GFLOP GEMMs."""
     b = backend(hidden)
     _, time, width = hidden.shape
     vocab = weight.shape[0]
@@ -529,8 +534,9 @@ def projection_loss(hidden, weight, labels, chunk_size, *, prepared_labels=None)
                       out_dtype=out_dtype)
 
     esize = 2 if out_dtype == "bfloat16" else 4
-    keep = (is_recording() and (hidden.requires_grad or weight.requires_grad)
-            and rows * vocab * esize <= KEEP_LOGITS_BYTES)
+    if keep_logits is None:
+        keep_logits = rows <= KEEP_LOGITS_CHUNKS * chunk_size and rows * vocab * esize <= KEEP_LOGITS_BYTES
+    keep = is_recording() and (hidden.requires_grad or weight.requires_grad) and bool(keep_logits)
     kept = {}
     for c0 in range(0, vocab, block):
         cols = min(block, vocab - c0)

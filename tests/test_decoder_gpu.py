@@ -308,9 +308,9 @@ def test_norm_input_gradient_sums_with_the_residual(base, leaf):
     assert np.array_equal(download(w.grad.storage), download(dw))
 
 
-def test_head_kept_logits_equal_recomputed(monkeypatch):
-    """projection_loss keeps the forward's logit blocks for the backward when
-    they fit KEEP_LOGITS_BYTES: loss and both gradients bit-identical to the
+def test_head_kept_logits_equal_recomputed():
+    """projection_loss keeps the forward's logit blocks for the backward
+    (keep_logits=True): loss and both gradients bit-identical to the
     recomputing form, and a second backward over the retained graph (the
     kept blocks were overwritten by the first) adds the same gradients."""
     from qutai_amd import Tensor
@@ -321,13 +321,12 @@ def test_head_kept_logits_equal_recomputed(monkeypatch):
     labels = [[(7 * t + 3 * r) % vocab for t in range(time)] for r in range(batch)]
     labels[0][5] = -100
     results = []
-    for budget in (layers.KEEP_LOGITS_BYTES, 0):
-        monkeypatch.setattr(layers, "KEEP_LOGITS_BYTES", budget)
+    for keep in (True, False):
         h = Tensor(upload(normal(71, batch * time * width), "float32"), shape=(batch, time, width),
                    requires_grad=True)
         w = Tensor(upload(normal(72, vocab * width, 0.05), "float32"), shape=(vocab, width), requires_grad=True)
         with set_matmul_precision("bfloat16"):
-            loss = layers.projection_loss(h, w, labels, chunk_size=16)
+            loss = layers.projection_loss(h, w, labels, chunk_size=16, keep_logits=keep)
             loss.backward()
             first = [download(t.grad.storage).copy() for t in (h, w)]
             loss.backward()
@@ -338,3 +337,30 @@ def test_head_kept_logits_equal_recomputed(monkeypatch):
     assert np.array_equal(results[0][0], results[1][0])
     for a, b2 in zip(results[0][1], results[1][1]):
         assert np.array_equal(a, b2)
+
+
+def test_head_small_chunk_bounds_forward_memory():
+    """The caller's chunk_size still bounds the loss head's memory: with 2048
+    prediction rows and chunk 64 the logits are not kept (32 MB of fp32
+    logits in all), and the forward's peak stays near one 1 MB block; asking
+    for keep_logits=True holds all of them until the backward."""
+    from qutai_amd import Tensor
+    from qutai_amd.backends import amd
+    from qutai_amd.lm import layers
+
+    batch, time, width, vocab = 2, 1025, 64, 4096
+    labels = [[(5 * t + r) % vocab for t in range(time)] for r in range(batch)]
+    h = Tensor(upload(normal(81, batch * time * width), "float32"), shape=(batch, time, width), requires_grad=True)
+    w = Tensor(upload(normal(82, vocab * width, 0.05), "float32"), shape=(vocab, width), requires_grad=True)
+    full = batch * (time - 1) * vocab * 4
+    growth = {}
+    for keep in (None, True):
+        amd.synchronize()
+        base = amd.memory_stats()["allocated_bytes"]
+        amd.reset_peak_memory_stats()
+        loss = layers.projection_loss(h, w, labels, chunk_size=64, keep_logits=keep)
+        amd.synchronize()
+        growth[keep] = amd.memory_stats()["peak_allocated_bytes"] - base
+        del loss
+    assert growth[None] < full // 4, growth
+    assert growth[True] >= full, growth
