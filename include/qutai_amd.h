@@ -328,8 +328,15 @@ int qutai_amd_silu_mul_backward(const void* dy, const void* gate, const void* up
  * oracle `cpu_lm.routing` (src/qutai/backends/cpu_lm.py:204-242). */
 int qutai_amd_route(const float* scores, float* probs, float* weights, int64_t* indices, int64_t* counts,
                     int64_t* ids, int64_t* slots, int64_t* locations, int64_t* offsets, int64_t* order,
-                    float* utilization, float* aux, int64_t rows, int64_t experts, int64_t top_k,
-                    void* stream);
+                    float* utilization, float* aux, int64_t rows, int64_t experts, int64_t top_k, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+/* Device workspace bytes for qutai_amd_route's chunked path (up to 32
+ * experts and top-8: three launches over chunks of 256 tokens, no per-expert
+ * pass over all assignments); 0 when that path does not apply.  With a smaller
+ * or NULL workspace qutai_amd_route runs its one-workgroup-per-expert pack.
+ * Same outputs either way (the aux loss up to fp32 summation order). */
+size_t qutai_amd_route_workspace_size(int64_t rows, int64_t experts, int64_t top_k);
 
 /* out[r] = x[order[r]] for r in [0, count): gathers the token rows of all
  * experts into one expert-major block (width values per row).  backward != 0

@@ -58,6 +58,11 @@ def silu_mul_backward(gradient, gate, up):
     return dgate, dup
 
 
+def _route_workspace_bytes(runtime, rows, experts, top_k):
+    """Workspace of the chunked routing path (0: the per-expert pack)."""
+    return runtime.lib.qutai_amd_route_workspace_size(rows, experts, top_k)
+
+
 def routing(scores, rows, experts, top_k, *, download_counts=True):
     """Router softmax, top-k selection and stable per-expert packing.
 
@@ -87,8 +92,11 @@ def routing(scores, rows, experts, top_k, *, download_counts=True):
     utilization = AMDStorage(experts, "float32")
     aux = AMDStorage(1, "float32")
     runtime = get_runtime()
+    need = _route_workspace_bytes(runtime, rows, experts, top_k)
+    workspace = AMDStorage((need + 3) // 4, "float32") if need else None
     runtime.call("qutai_amd_route", scores.ptr, probs.ptr, weights.ptr, indices.ptr, counts.ptr, ids.ptr, slots.ptr,
-                 locations.ptr, offsets.ptr, order.ptr, utilization.ptr, aux.ptr, rows, experts, top_k)
+                 locations.ptr, offsets.ptr, order.ptr, utilization.ptr, aux.ptr, rows, experts, top_k,
+                 workspace.ptr if workspace else None, need)
     host_counts = tuple(counts.to_array().tolist()) if download_counts else None
     return dict(probs=probs, weights=weights, indices=indices, counts=host_counts, count_buffer=counts, ids=ids,
                 slots=slots, locations=locations, offsets=offsets, order=order, utilization=utilization, aux=aux,

@@ -54,7 +54,8 @@ SIGNATURES = {
     "qutai_amd_softmax_rows": [_p, _p, _i64, _i64, _f64, _i32, _p],
     "qutai_amd_silu_mul": [_p, _p, _p, _i64, _i32, _p],
     "qutai_amd_silu_mul_backward": [_p, _p, _p, _p, _p, _i64, _i32, _p],
-    "qutai_amd_route": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p],
+    "qutai_amd_route": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _sz, _p],
+    "qutai_amd_route_workspace_size": [_i64, _i64, _i64],
     "qutai_amd_route_gather": [_p, _p, _p, _i64, _i64, _i32, _i32, _p],
     "qutai_amd_combine": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _p],
     "qutai_amd_gemm_grouped_k": [_p, _p, _p, _p, _i32, _i64, _i64, _i64, _i32, _i32, _i32, _p],
@@ -93,7 +94,7 @@ SIGNATURES = {
 }
 RESTYPES = {"qutai_amd_gemm_workspace_size": _sz, "qutai_amd_rms_norm_workspace": _i64,
             "qutai_amd_attention_bwd_workspace_size": _sz, "qutai_amd_reduce_sum_workspace_size": _sz,
-            "qutai_amd_gemm_static_capacity": _sz}
+            "qutai_amd_gemm_static_capacity": _sz, "qutai_amd_route_workspace_size": _sz}
 
 
 def _hip_library():

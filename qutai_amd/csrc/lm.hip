@@ -40,49 +40,180 @@ __global__ void route_select(const float* scores, float* probs, float* weights, 
   for (int64_t slot = 0; slot < top_k; slot++) weights[r * top_k + slot] /= chosen;
 }
 
-// The same selection for up to 32 experts and top-8, the row held in
-// registers (the expression order of route_select, so the same bits).
+// Routing for up to 32 experts and top-8 in three launches over chunks of
+// 256 tokens (one thread per token), all deterministic and without atomics:
+//   route_select_small  the selection of route_select with the row in
+//                       registers (same expressions, so the same bits), plus
+//                       the chunk's per-expert assignment counts and
+//                       probability column sums (fixed shuffle tree, waves
+//                       added in order);
+//   route_scan          one workgroup: per expert the exclusive prefix of the
+//                       chunk counts (each chunk's first position in the
+//                       expert's list), counts, offsets, utilization and the
+//                       aux loss from the column sums (chunk order);
+//   route_scatter       per chunk: a token's rank among the chunk's tokens
+//                       routed to the same expert (one ballot per expert; a
+//                       token's slots have distinct experts), so positions are
+//                       stable in (token, slot) order like route_pack's.
+constexpr int RCHUNK = 256;
+
 template <int E>
-__global__ void route_select_small(const float* scores, float* probs, float* weights, int64_t* indices, int64_t rows,
-                                   int experts, int top_k) {
-  int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (r >= rows) return;
-  const float* s = scores + r * experts;
+__global__ void __launch_bounds__(RCHUNK) route_select_small(const float* scores, float* probs, float* weights,
+                                                             int64_t* indices, int64_t rows, int experts, int top_k,
+                                                             int* chunk_counts, float* chunk_cols) {
+  __shared__ int hist[RCHUNK / 64][E];
+  __shared__ float cols[RCHUNK / 64][E];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t r = (int64_t)blockIdx.x * RCHUNK + threadIdx.x;
+  const bool valid = r < rows;
   float x[E], p[E];
 #pragma unroll
-  for (int e = 0; e < E; e++) x[e] = e < experts ? s[e] : -INFINITY;
-  float peak = -INFINITY;
-#pragma unroll
-  for (int e = 0; e < E; e++)
-    if (e < experts) peak = fmaxf(peak, x[e]);
-  float total = 0.f;
-#pragma unroll
-  for (int e = 0; e < E; e++)
-    if (e < experts) total += expf(x[e] - peak);
-#pragma unroll
-  for (int e = 0; e < E; e++)
-    if (e < experts) {
-      p[e] = expf(x[e] - peak) / total;
-      probs[r * experts + e] = p[e];
-    }
+  for (int e = 0; e < E; e++) {
+    x[e] = valid && e < experts ? scores[r * experts + e] : -INFINITY;
+    p[e] = 0.f;
+  }
   uint32_t used = 0;
-  float w[8], chosen = 0.f;
-  for (int slot = 0; slot < top_k; slot++) {
-    int best = -1;
-    float bx = 0.f, bp = 0.f;
+  if (valid) {
+    float peak = -INFINITY;
 #pragma unroll
     for (int e = 0; e < E; e++)
-      if (e < experts && !((used >> e) & 1u) && (best < 0 || x[e] > bx)) {
-        best = e;
-        bx = x[e];
-        bp = p[e];
+      if (e < experts) peak = fmaxf(peak, x[e]);
+    float total = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; e++)
+      if (e < experts) total += expf(x[e] - peak);
+#pragma unroll
+    for (int e = 0; e < E; e++)
+      if (e < experts) {
+        p[e] = expf(x[e] - peak) / total;
+        probs[r * experts + e] = p[e];
       }
-    used |= 1u << best;
-    indices[r * top_k + slot] = best;
-    w[slot] = bp;
-    chosen += bp;
+    float w[8], chosen = 0.f;
+    for (int slot = 0; slot < top_k; slot++) {
+      int best = -1;
+      float bx = 0.f, bp = 0.f;
+#pragma unroll
+      for (int e = 0; e < E; e++)
+        if (e < experts && !((used >> e) & 1u) && (best < 0 || x[e] > bx)) {
+          best = e;
+          bx = x[e];
+          bp = p[e];
+        }
+      used |= 1u << best;
+      indices[r * top_k + slot] = best;
+      w[slot] = bp;
+      chosen += bp;
+    }
+    for (int slot = 0; slot < top_k; slot++) weights[r * top_k + slot] = w[slot] / chosen;
   }
-  for (int slot = 0; slot < top_k; slot++) weights[r * top_k + slot] = w[slot] / chosen;
+  if (!chunk_counts) return;
+#pragma unroll
+  for (int e = 0; e < E; e++) {
+    if (e >= experts) break;
+    const uint64_t m = __ballot((used >> e) & 1u);
+    float c = p[e];
+    for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o);
+    if (lane == 0) {
+      hist[wave][e] = __popcll(m);
+      cols[wave][e] = c;
+    }
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < experts) {
+    const int e = threadIdx.x;
+    int count = 0;
+    float col = 0.f;
+    for (int w = 0; w < RCHUNK / 64; w++) {
+      count += hist[w][e];
+      col += cols[w][e];
+    }
+    chunk_counts[(int64_t)blockIdx.x * experts + e] = count;
+    chunk_cols[(int64_t)blockIdx.x * experts + e] = col;
+  }
+}
+
+__global__ void __launch_bounds__(1024) route_scan(const int* chunk_counts, const float* chunk_cols, int* chunk_base,
+                                                   int64_t chunks, int experts, int64_t* counts, int64_t* offsets,
+                                                   float* utilization, float* aux, int64_t rows, int64_t n) {
+  __shared__ int64_t total[32];
+  __shared__ float colsum[32];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int e = wave; e < experts; e += 16) {
+    int64_t running = 0;
+    float col = 0.f;
+    for (int64_t c0 = 0; c0 < chunks; c0 += 64) {
+      const int64_t c = c0 + lane;
+      const int v = c < chunks ? chunk_counts[c * experts + e] : 0;
+      int incl = v;
+      for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(incl, o);
+        if (lane >= o) incl += t;
+      }
+      if (c < chunks) chunk_base[c * experts + e] = (int)(running + incl - v);
+      running += __shfl(incl, 63);
+      float f = c < chunks ? chunk_cols[c * experts + e] : 0.f;
+      for (int o = 32; o > 0; o >>= 1) f += __shfl_xor(f, o);
+      col += f;
+    }
+    if (lane == 0) {
+      total[e] = running;
+      colsum[e] = col;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int64_t start = 0;
+    float sum = 0.f;
+    for (int e = 0; e < experts; e++) {
+      counts[e] = total[e];
+      offsets[e] = start;
+      start += total[e];
+      const float u = (float)total[e] / (float)n;
+      utilization[e] = u;
+      sum += u * colsum[e];
+    }
+    offsets[experts] = n;
+    aux[0] = (float)experts * sum / (float)rows;
+  }
+}
+
+template <int E>
+__global__ void __launch_bounds__(RCHUNK) route_scatter(const int64_t* indices, const int* chunk_base,
+                                                        const int64_t* offsets, int64_t* ids, int64_t* slots,
+                                                        int64_t* locations, int64_t* order, int64_t rows, int experts,
+                                                        int top_k, int64_t n) {
+  __shared__ int wcount[RCHUNK / 64][E];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t r = (int64_t)blockIdx.x * RCHUNK + threadIdx.x;
+  const bool valid = r < rows;
+  int idx[8];
+  uint32_t used = 0;
+  for (int s = 0; s < top_k; s++) {
+    idx[s] = valid ? (int)indices[r * top_k + s] : 0;
+    if (valid) used |= 1u << idx[s];
+  }
+  int rank[8];
+  const uint64_t below = (1ull << lane) - 1ull;
+#pragma unroll
+  for (int e = 0; e < E; e++) {
+    if (e >= experts) break;
+    const uint64_t m = __ballot((used >> e) & 1u);
+    if (lane == 0) wcount[wave][e] = __popcll(m);
+    for (int s = 0; s < top_k; s++)
+      if (valid && idx[s] == e) rank[s] = __popcll(m & below);
+  }
+  __syncthreads();
+  if (!valid) return;
+  for (int s = 0; s < top_k; s++) {
+    const int e = idx[s];
+    int pos = chunk_base[(int64_t)blockIdx.x * experts + e] + rank[s];
+    for (int w = 0; w < wave; w++) pos += wcount[w][e];
+    const int64_t at = r * top_k + s;
+    ids[e * n + pos] = r;
+    slots[e * n + pos] = s;
+    locations[at] = pos;
+    order[offsets[e] + pos] = r;
+  }
 }
 
 // One workgroup per expert: stable compaction of the (token, slot)
@@ -432,19 +563,52 @@ unsigned blocks_for(int64_t n) {
 
 extern "C" {
 
+size_t qutai_amd_route_workspace_size(int64_t rows, int64_t experts, int64_t top_k) {
+  if (rows <= 0 || experts <= 0 || experts > 32 || top_k <= 0 || top_k > 8) return 0;
+  const int64_t chunks = (rows + RCHUNK - 1) / RCHUNK;
+  return (size_t)(chunks * experts * 3 * 4 + 256);
+}
+
 int qutai_amd_route(const float* scores, float* probs, float* weights, int64_t* indices, int64_t* counts,
                     int64_t* ids, int64_t* slots, int64_t* locations, int64_t* offsets, int64_t* order,
-                    float* utilization, float* aux, int64_t rows, int64_t experts, int64_t top_k, void* stream) {
+                    float* utilization, float* aux, int64_t rows, int64_t experts, int64_t top_k, void* workspace,
+                    size_t workspace_bytes, void* stream) {
   if (rows < 0 || experts <= 0 || top_k <= 0 || top_k > experts) return QA_EINVAL;
   hipStream_t s = (hipStream_t)stream;
   int64_t n = rows * top_k;
   if (experts > 0x7fffffff || n >= (1ll << 31)) return QA_EINVAL;
+  const size_t need = qutai_amd_route_workspace_size(rows, experts, top_k);
+  if (need && workspace && workspace_bytes >= need) {
+    // chunked path: select + chunk counts, scan, scatter
+    const int64_t chunks = (rows + RCHUNK - 1) / RCHUNK;
+    if (chunks > 0x7fffffff) return QA_EINVAL;
+    int* chunk_counts = (int*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
+    float* chunk_cols = (float*)(chunk_counts + chunks * experts);
+    int* chunk_base = (int*)(chunk_cols + chunks * experts);
+    const int e32 = (int)experts, k32 = (int)top_k;
+    if (experts <= 8) {
+      hipLaunchKernelGGL(route_select_small<8>, dim3((unsigned)chunks), dim3(RCHUNK), 0, s, scores, probs, weights,
+                         indices, rows, e32, k32, chunk_counts, chunk_cols);
+    } else {
+      hipLaunchKernelGGL(route_select_small<32>, dim3((unsigned)chunks), dim3(RCHUNK), 0, s, scores, probs, weights,
+                         indices, rows, e32, k32, chunk_counts, chunk_cols);
+    }
+    hipLaunchKernelGGL(route_scan, dim3(1), dim3(1024), 0, s, chunk_counts, chunk_cols, chunk_base, chunks, e32,
+                       counts, offsets, utilization, aux, rows, n);
+    if (experts <= 8)
+      hipLaunchKernelGGL(route_scatter<8>, dim3((unsigned)chunks), dim3(RCHUNK), 0, s, indices, chunk_base, offsets,
+                         ids, slots, locations, order, rows, e32, k32, n);
+    else
+      hipLaunchKernelGGL(route_scatter<32>, dim3((unsigned)chunks), dim3(RCHUNK), 0, s, indices, chunk_base, offsets,
+                         ids, slots, locations, order, rows, e32, k32, n);
+    return (int)hipGetLastError();
+  }
   if (rows > 0 && experts <= 8 && top_k <= 8)
-    hipLaunchKernelGGL(route_select_small<8>, dim3(blocks_for(rows)), dim3(256), 0, s, scores, probs, weights, indices,
-                       rows, (int)experts, (int)top_k);
+    hipLaunchKernelGGL(route_select_small<8>, dim3((unsigned)((rows + RCHUNK - 1) / RCHUNK)), dim3(RCHUNK), 0, s,
+                       scores, probs, weights, indices, rows, (int)experts, (int)top_k, nullptr, nullptr);
   else if (rows > 0 && experts <= 32 && top_k <= 8)
-    hipLaunchKernelGGL(route_select_small<32>, dim3(blocks_for(rows)), dim3(256), 0, s, scores, probs, weights,
-                       indices, rows, (int)experts, (int)top_k);
+    hipLaunchKernelGGL(route_select_small<32>, dim3((unsigned)((rows + RCHUNK - 1) / RCHUNK)), dim3(RCHUNK), 0, s,
+                       scores, probs, weights, indices, rows, (int)experts, (int)top_k, nullptr, nullptr);
   else if (rows > 0)
     hipLaunchKernelGGL(route_select, dim3(blocks_for(rows)), dim3(256), 0, s, scores, probs, weights, indices, rows,
                        experts, top_k);

@@ -72,6 +72,27 @@ def c5_route(amd, lm):
     return logits, route, reference
 
 
+@pytest.mark.parametrize("rows,experts,top_k", [(8192, 8, 2), (1000, 32, 8), (300, 5, 3), (257, 16, 1), (1, 3, 3)])
+def test_routing_chunked_and_per_expert_paths_agree(amd, lm, monkeypatch, rows, experts, top_k):
+    """The chunked routing (select + chunk counts, scan, scatter) and the
+    one-workgroup-per-expert pack give the same indices, lists, positions,
+    counts, offsets, weights and utilization bit for bit; the aux loss sums
+    the probability columns in another order (fp32)."""
+    logits = upload(normal(rows + experts, rows * experts), "float32")
+    chunked = lm.routing(logits, rows, experts, top_k)
+    monkeypatch.setattr(lm, "_route_workspace_bytes", lambda *args: 0)
+    packed = lm.routing(logits, rows, experts, top_k)
+    for key in ("indices", "ids", "slots", "locations", "offsets", "order", "probs", "weights", "utilization"):
+        a, b = download(chunked[key]), download(packed[key])
+        if key in ("ids", "slots"):  # only each expert's first count_e entries are defined
+            a, b = a.reshape(experts, -1), b.reshape(experts, -1)
+            a = np.concatenate([a[e, :c] for e, c in enumerate(chunked["counts"])])
+            b = np.concatenate([b[e, :c] for e, c in enumerate(packed["counts"])])
+        assert np.array_equal(a, b), key
+    assert chunked["counts"] == packed["counts"]
+    assert download(chunked["aux"])[0] == pytest.approx(download(packed["aux"])[0], rel=1e-6)
+
+
 def test_config5_routing_indices_bit_exact(amd, lm):
     logits, route, reference = c5_route(amd, lm)
     rows, experts, top_k = 8192, 8, 2
