@@ -390,7 +390,7 @@ __global__ void __launch_bounds__(256) softmax_rows_wave(const T* x, T* out, int
     if (at < chunks) {
 #pragma unroll
       for (int e = 0; e < V; e++) v[c][e] *= inv;
-      yr[at] = pack(v[c]);
+      global_store_nt(yr + at, pack(v[c]));
     }
   }
   for (int at = lane + 64 * CH; at < chunks; at += 64) {
@@ -398,7 +398,7 @@ __global__ void __launch_bounds__(256) softmax_rows_wave(const T* x, T* out, int
     unpack(xr[at], f);
 #pragma unroll
     for (int e = 0; e < V; e++) f[e] = __expf(f[e] - peak) * inv;
-    yr[at] = pack(f);
+    global_store_nt(yr + at, pack(f));
   }
 }
 
