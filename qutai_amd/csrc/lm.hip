@@ -529,6 +529,72 @@ __global__ void __launch_bounds__(256) combine_backward_kernel(const T* dy, cons
   if (lane == 0) dw[at] = dot;
 }
 
+// The same backward with 16-byte chunks (width a multiple of 16 / size(T),
+// 16-byte aligned rows): a lane takes 4 chunks per round, their loads in
+// flight together; the dot product sums each lane's chunks in order, then
+// the fixed shuffle tree.
+template <class T>
+__global__ void __launch_bounds__(256) combine_backward_vec(const T* dy, const T* eo, const float* w,
+                                                            const int64_t* idx, const int64_t* loc,
+                                                            const int64_t* off, T* deo, float* dw, int64_t pairs,
+                                                            int64_t width, int64_t top_k) {
+  constexpr int V = 16 / sizeof(T), R = 4;
+  const int lane = threadIdx.x & 63;
+  const int64_t at = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (at >= pairs) return;  // whole wave
+  const int64_t row = at / top_k, pos = off[idx[at]] + loc[at];
+  const float f = w[at];
+  const u32x4* g = reinterpret_cast<const u32x4*>(dy + row * width);
+  const u32x4* x = reinterpret_cast<const u32x4*>(eo + pos * width);
+  u32x4* d = reinterpret_cast<u32x4*>(deo + pos * width);
+  const int64_t chunks = width / V;
+  float dot = 0.f;
+  auto unpack = [](const u32x4& q, float (&v)[V]) {
+    if constexpr (sizeof(T) == 2) {
+#pragma unroll
+      for (int h = 0; h < 4; h++) {
+        v[2 * h] = __uint_as_float(q[h] << 16);
+        v[2 * h + 1] = __uint_as_float(q[h] & 0xffff0000u);
+      }
+    } else {
+#pragma unroll
+      for (int h = 0; h < 4; h++) v[h] = __uint_as_float(q[h]);
+    }
+  };
+  for (int64_t c0 = 0; c0 < chunks; c0 += 64 * R) {
+    u32x4 qg[R], qx[R];
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+      const int64_t c = c0 + i * 64 + lane;
+      if (c < chunks) {
+        qg[i] = global_load<u32x4>(g + c);
+        qx[i] = global_load<u32x4>(x + c);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+      const int64_t c = c0 + i * 64 + lane;
+      if (c >= chunks) continue;
+      float gv[V], xv[V];
+      unpack(qg[i], gv);
+      unpack(qx[i], xv);
+      u32x4 out;
+      if constexpr (sizeof(T) == 2) {
+#pragma unroll
+        for (int h = 0; h < 4; h++) out[h] = pack_bf16x2(gv[2 * h] * f, gv[2 * h + 1] * f);
+      } else {
+#pragma unroll
+        for (int h = 0; h < 4; h++) out[h] = __float_as_uint(gv[h] * f);
+      }
+      global_store(d + c, out);
+#pragma unroll
+      for (int v = 0; v < V; v++) dot += gv[v] * xv[v];
+    }
+  }
+  for (int o = 32; o > 0; o >>= 1) dot += __shfl_xor(dot, o);
+  if (lane == 0) dw[at] = dot;
+}
+
 // Gradient of the router logits (cpu_lm.routing_backward,
 // src/qutai/backends/cpu_lm.py:245-276), one thread per token row:
 //   weights: out[e_s] = w_s (g_s - sum_t g_t w_t) for the selected experts;
@@ -718,6 +784,23 @@ int qutai_amd_combine_backward(const void* dy, const void* expert_out, const flo
   if (pairs == 0) return QA_OK;
   const unsigned blocks = (unsigned)((pairs + 3) / 4);
   hipStream_t s = (hipStream_t)stream;
+  {
+    const int64_t es = dtype == BF16 ? 2 : 4;
+    const bool vec = (width * es) % 16 == 0 && (uintptr_t)dy % 16 == 0 && (uintptr_t)expert_out % 16 == 0 &&
+                     (uintptr_t)d_expert_out % 16 == 0;
+    if (vec && dtype == BF16) {
+      hipLaunchKernelGGL(combine_backward_vec<bf16_t>, dim3(blocks), dim3(256), 0, s, (const bf16_t*)dy,
+                         (const bf16_t*)expert_out, weights, indices, locations, offsets, (bf16_t*)d_expert_out,
+                         d_weights, pairs, width, top_k);
+      return (int)hipGetLastError();
+    }
+    if (vec) {
+      hipLaunchKernelGGL(combine_backward_vec<float>, dim3(blocks), dim3(256), 0, s, (const float*)dy,
+                         (const float*)expert_out, weights, indices, locations, offsets, (float*)d_expert_out,
+                         d_weights, pairs, width, top_k);
+      return (int)hipGetLastError();
+    }
+  }
   if (dtype == BF16)
     hipLaunchKernelGGL(combine_backward_kernel<bf16_t>, dim3(blocks), dim3(256), 0, s, (const bf16_t*)dy,
                        (const bf16_t*)expert_out, weights, indices, locations, offsets, (bf16_t*)d_expert_out,

@@ -38,8 +38,9 @@ def test_routing_backward_weights_and_aux(lm):
 
 
 @pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
-def test_combine_backward_all_and_reference_shape(lm, dtype):
-    rows, experts, top_k, width = 517, 5, 3, 64
+@pytest.mark.parametrize("width", [64, 36, 2048])  # 16-byte rows (vector kernel) and not (element kernel)
+def test_combine_backward_all_and_reference_shape(lm, dtype, width):
+    rows, experts, top_k = 517, 5, 3
     scores = [((row * 37 + expert * 11) % 101) / 13 for row in range(rows) for expert in range(experts)]
     route = lm.routing(upload(np.array(scores, dtype=np.float32), "float32"), rows, experts, top_k)
     reference = ora.routing([float(np.float32(s)) for s in scores], rows, experts, top_k)
