@@ -89,13 +89,24 @@ __global__ void __launch_bounds__(256) prepare_operand(const void* src, void* ds
   const uint32_t r = i / per_row, c0 = (i - r * per_row) * E;
   const uint32_t z = r / outer, o = r - z * outer;
   const int64_t at = (int64_t)z * stride + (int64_t)o * inner + c0;
+  char* d = (char*)dst + (int64_t)i * 16;
+  if constexpr (SRC_BF16 && DST_BF16) {
+    if (c0 + E <= inner) {
+      // a whole chunk inside the row: one 16-byte load at the element's own
+      // (2-byte) alignment -- unaligned global loads are enabled on this
+      // platform, and the compiler emits the same for an unaligned memcpy
+      u32x4 w;
+      __builtin_memcpy(&w, (const char*)src + at * 2, 16);
+      global_store(d, w);
+      return;
+    }
+  }
   float v[E];
 #pragma unroll
   for (int t = 0; t < E; t++) {
     v[t] = 0.f;
     if (c0 + t < inner) v[t] = SRC_BF16 ? bf16_to_f32(((const bf16_t*)src)[at + t]) : ((const float*)src)[at + t];
   }
-  char* d = (char*)dst + (int64_t)i * 16;
   if constexpr (DST_BF16)
     global_store(d, u32x4{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
                           pack_bf16x2(v[6], v[7])});

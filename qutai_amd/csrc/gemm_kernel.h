@@ -666,8 +666,11 @@ struct GemmKernel {
     int64_t at = row * o.ldc + col;
     if (o.bf16) {
       gbf16* q = (gbf16*)(o.ptr) + at;
-      if (o.vec && col + 4 <= o.N) {
-        typedef __attribute__((address_space(1))) u32x2 gu2;
+      if (col + 4 <= o.N) {
+        // four whole columns: one 8-byte access; rows with an odd pitch give
+        // 2-byte alignment only, which unaligned global accesses accept
+        typedef unsigned u32x2a2 __attribute__((ext_vector_type(2), aligned(2)));
+        typedef __attribute__((address_space(1))) u32x2a2 gu2;
         if (o.accumulate) {
           u32x2 old = *(const gu2*)q;
           v[0] += __uint_as_float(old[0] << 16);
@@ -688,10 +691,20 @@ struct GemmKernel {
       }
     } else {
       gf32* q = (gf32*)(o.ptr) + at;
-      if (o.vec && col + 4 <= o.N) {
+      if (col + 4 <= o.N) {
+        // four whole columns: one 16-byte store; rows whose pitch is not a
+        // multiple of 4 elements only give 4-byte alignment, which the
+        // vector store accepts (global accesses need dword alignment only)
         typedef __attribute__((address_space(1))) f32x4 gf4;
-        if (o.accumulate) v += *(const gf4*)q;
-        *(gf4*)q = v;
+        typedef float f32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+        typedef __attribute__((address_space(1))) f32x4a4 gf4a4;
+        if (o.vec) {
+          if (o.accumulate) v += *(const gf4*)q;
+          *(gf4*)q = v;
+        } else {
+          if (o.accumulate) v += *(const gf4a4*)q;
+          *(gf4a4*)q = v;
+        }
       } else {
 #pragma unroll
         for (int t = 0; t < 4; t++) {

@@ -56,6 +56,8 @@ def test_cast_random_bit_patterns_bit_exact():
     (512, 256, 384, False, True),
     (300, 100, 260, False, False),   # ragged tiles: bounds-checked epilogue
     (300, 100, 262, True, False),    # odd pitch: 4-byte bf16 rows
+    (300, 100, 261, False, False),   # odd element pitch: 2-byte bf16 rows, 4-byte fp32 rows
+    (129, 64, 257, False, True),
 ])
 def test_gemm_bf16_output_is_rounded_fp32_output(m, k, n, ta, tb):
     from qutai_amd.backends import amd
@@ -71,7 +73,7 @@ def test_gemm_bf16_output_is_rounded_fp32_output(m, k, n, ta, tb):
     assert np.array_equal(got, want)
 
 
-@pytest.mark.parametrize("m,k,n", [(512, 256, 384), (300, 100, 264)])
+@pytest.mark.parametrize("m,k,n", [(512, 256, 384), (300, 100, 264), (300, 100, 261)])
 def test_gemm_accumulate_adds_old_value_before_one_rounding(m, k, n):
     """out = round(old + A@B) (gemm.cu:25-32) on whole tiles (straight-line
     epilogue) and ragged tiles: bit-exact against the fp32 product of the
