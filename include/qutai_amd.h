@@ -174,6 +174,15 @@ int qutai_amd_scale(const void* x, void* out, int64_t n, double factor, int dtyp
 int qutai_amd_repitch(const void* src, void* dst, int64_t batches, int64_t src_rows, int64_t src_cols,
                       int64_t dst_rows, int64_t dst_cols, int dtype, void* stream);
 
+/* dst[r][0:width] = src[r][0:width] for `rows` rows with row pitches src_row
+ * and dst_row (elements, >= width; fp32 or bf16, bits copied): a column slice
+ * of a row-major matrix moved to or from a contiguous block -- the v columns
+ * of the stacked q/k/v projection output and the v gradient's place in the
+ * stacked gradient (the GQA block, src/qutai/lm/layers.py:317-350, whose
+ * separate `Projection` outputs need no such copy). */
+int qutai_amd_copy_rows(const void* src, int64_t src_row, void* dst, int64_t dst_row, int64_t rows, int64_t width,
+                        int dtype, void* stream);
+
 /* Softmax backward along rows: out = scale * p * (g - rowsum(g * p)), p the
  * softmax of (scale * x) (fp32 math; fp32/fp64/bf16 storage).  Replaces
  * `_softmax_backward` (src/qutai/core/operations/normalization.py:18-25), the
@@ -495,6 +504,16 @@ int qutai_amd_silu(const void* x, const void* gradient, void* out, int64_t n, in
  * Replaces `cuda_lm.rope` / `lm_rope` (cuda_lm.py:210-226, cuda/lm.cu:55-59). */
 int qutai_amd_rope(const void* x, void* out, int64_t batch, int64_t time, int64_t heads, int64_t dim, double theta,
                    int64_t offset, int inverse, int dtype, void* stream);
+
+/* The same rotation where a position's heads*dim values sit x_row (out_row)
+ * elements after the previous position's (>= heads*dim): RoPE read from, or
+ * written into, a column slice of a wider row-major matrix -- the q and k
+ * columns of the stacked q/k/v projection output [rows][dq + 2 dkv], which
+ * replaces the three `Projection` calls ahead of `rope` in the reference's
+ * GQA block (src/qutai/lm/layers.py:317-350, cuda_lm.py:210-226). */
+int qutai_amd_rope_rows(const void* x, void* out, int64_t batch, int64_t time, int64_t heads, int64_t dim,
+                        double theta, int64_t offset, int inverse, int64_t x_row, int64_t out_row, int dtype,
+                        void* stream);
 
 /* The rows start .. start+count of the (time-1) prediction positions of every
  * sequence of a [.][time][width] block (backward = 1: add them back into it).

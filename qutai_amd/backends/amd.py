@@ -196,6 +196,19 @@ def from_storage(values: Storage, *, dtype: str) -> AMDStorage:
     return result
 
 
+def cast_into(target: AMDStorage, source: AMDStorage) -> None:
+    """``target`` (e.g. a view into a larger block) receives ``source``'s values
+    in its own dtype: the conversion of ``from_storage`` without a new
+    allocation."""
+    if target.device != "amd" or source.device != "amd" or target.size != source.size:
+        raise ValueError("cast_into needs two amd storages of one element count")
+    if target.dtype == source.dtype:
+        copy_into(target, source)
+    elif source.size:
+        target.runtime.call("qutai_amd_cast", source.ptr, target.ptr, source.size, code(source.dtype),
+                            code(target.dtype))
+
+
 def copy_into(target: AMDStorage, source: AMDStorage) -> None:
     if (target.device, target.dtype, target.size) != (source.device, source.dtype, source.size):
         raise ValueError("copy needs the same device, dtype and element count")

@@ -17,7 +17,7 @@ from functools import partial
 from random import Random
 
 from . import amd
-from .amd import AMDStorage, code
+from .amd import _TYPES, AMDStorage, code
 from .amd_runtime import get_runtime
 from ..core.grad import DeferredGradient
 
@@ -590,13 +590,52 @@ def silu_backward(gradient, values):
     return out
 
 
-def rope(values, batch, time, heads, dim, theta, offset=0, inverse=False):
-    """Rotary embedding of [batch][time][heads][dim] (cuda_lm.py:210-226)."""
-    result = AMDStorage(values.size, values.dtype)
-    if result.size:
-        result.runtime.call("qutai_amd_rope", values.ptr, result.ptr, batch, time, heads, dim, float(theta), offset,
-                            int(bool(inverse)), code(values.dtype))
-    return result
+def rope(values, batch, time, heads, dim, theta, offset=0, inverse=False, *, column=0, row=None, out=None,
+         out_column=0, out_row=None):
+    """Rotary embedding of [batch][time][heads][dim] (cuda_lm.py:210-226).
+    ``values`` may be a wider matrix of ``row`` elements per position whose
+    columns column .. column + heads*dim are rotated; the result goes to a new
+    contiguous block, or into columns out_column .. of ``out`` (``out_row``
+    elements per position)."""
+    width = heads * dim
+    row = width if row is None else row
+    positions = batch * time
+    if column < 0 or row < width or column + width > row or values.size < positions * row:
+        raise ValueError("rope columns outside the source rows")
+    if out is None:
+        if out_column or out_row not in (None, width):
+            raise ValueError("a new rope result is contiguous")
+        out, out_row = AMDStorage(positions * width, values.dtype), width
+    else:
+        out_row = width if out_row is None else out_row
+        if out.dtype != values.dtype or out_column < 0 or out_row < width or out_column + width > out_row \
+                or out.size < positions * out_row:
+            raise ValueError("rope output columns outside the target rows")
+    if positions * width:
+        item = _TYPES[values.dtype][1]
+        out.runtime.call("qutai_amd_rope_rows", values.ptr + column * item, out.ptr + out_column * item, batch, time,
+                         heads, dim, float(theta), offset, int(bool(inverse)), row, out_row, code(values.dtype))
+    return out
+
+
+def copy_rows(source, rows, width, *, column=0, row=None, out=None, out_column=0, out_row=None):
+    """Columns column .. column + width of the ``rows`` rows of ``source``
+    (``row`` elements each) into a new contiguous [rows][width] block, or into
+    columns out_column .. of ``out`` (``out_row`` elements per row)."""
+    row = width if row is None else row
+    if column < 0 or row < width or column + width > row or source.size < rows * row:
+        raise ValueError("copied columns outside the source rows")
+    if out is None:
+        out, out_column, out_row = AMDStorage(rows * width, source.dtype), 0, width
+    else:
+        out_row = width if out_row is None else out_row
+        if out.dtype != source.dtype or out_column < 0 or out_column + width > out_row or out.size < rows * out_row:
+            raise ValueError("copied columns outside the target rows")
+    if rows * width:
+        item = _TYPES[source.dtype][1]
+        out.runtime.call("qutai_amd_copy_rows", source.ptr + column * item, row, out.ptr + out_column * item, out_row,
+                         rows, width, code(source.dtype))
+    return out
 
 
 def head_rows(values, start, count, width, time):

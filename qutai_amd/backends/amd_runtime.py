@@ -63,6 +63,7 @@ SIGNATURES = {
     "qutai_amd_route_backward": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p],
     "qutai_amd_scale": [_p, _p, _i64, _f64, _i32, _p],
     "qutai_amd_repitch": [_p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _p],
+    "qutai_amd_copy_rows": [_p, _i64, _p, _i64, _i64, _i64, _i32, _p],
     "qutai_amd_softmax_backward": [_p, _p, _p, _i64, _i64, _f64, _i32, _p],
     "qutai_amd_causal_mask": [_p, _p, _i64, _i64, _i64, _i64, _i32, _p],
     "qutai_amd_embedding": [_p, _p, _p, _i64, _i64, _i32, _p],
@@ -72,6 +73,7 @@ SIGNATURES = {
     "qutai_amd_rms_norm_backward": [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p],
     "qutai_amd_silu": [_p, _p, _p, _i64, _i32, _i32, _p],
     "qutai_amd_rope": [_p, _p, _i64, _i64, _i64, _i64, _f64, _i64, _i32, _i32, _p],
+    "qutai_amd_rope_rows": [_p, _p, _i64, _i64, _i64, _i64, _f64, _i64, _i32, _i64, _i64, _i32, _p],
     "qutai_amd_head_rows": [_p, _p, _i64, _i64, _i64, _i64, _i32, _i32, _p],
     "qutai_amd_head_loss": [_p, _p, _p, _i64, _i64, _i32, _p],
     "qutai_amd_head_gradient": [_p, _p, _p, _i64, _i64, _f64, _i32, _p],

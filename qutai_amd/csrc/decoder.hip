@@ -245,24 +245,27 @@ __global__ void silu_kernel(const T* x, const T* g, T* out, int64_t n, int backw
 // (x0, x1) at `at` rotated by the angle with sine s and cosine c, the
 // contractions spelled out so that every kernel rounds the same way
 template <class T>
-__device__ __forceinline__ void rotate_pair(const T* x, T* out, int64_t at, float s, float c) {
+__device__ __forceinline__ void rotate_pair(const T* x, T* out, int64_t at, int64_t to, float s, float c) {
   const float x0 = get<T>(x, at), x1 = get<T>(x, at + 1);
-  put<T>(out, at, fmaf(x0, c, -(x1 * s)));
-  put<T>(out, at + 1, fmaf(x0, s, x1 * c));
+  put<T>(out, to, fmaf(x0, c, -(x1 * s)));
+  put<T>(out, to + 1, fmaf(x0, s, x1 * c));
 }
 
 // rotary embedding of the pairs (2i, 2i+1) of [batch][time][heads][dim]:
 // angle (offset + t) * theta^(-d/dim), d = 2 (i mod dim/2); inverse rotates
-// back (lm.cu:55-59)
+// back (lm.cu:55-59).  A position's heads*dim values start x_row (out_row)
+// elements after the previous position's: heads*dim for a contiguous block,
+// more for a column slice of a wider matrix.
 template <class T>
 __global__ void rope_kernel(const T* x, T* out, int64_t pairs, int64_t time, int64_t heads, int64_t dim, float theta,
-                            int64_t offset, int inverse) {
+                            int64_t offset, int inverse, int64_t x_row, int64_t out_row) {
+  const int64_t per = heads * (dim / 2);
   GRID_STRIDE(i, pairs) {
-    const int64_t at = 2 * i, d = (i % (dim / 2)) * 2, t = (i / (heads * (dim / 2))) % time;
+    const int64_t bt = i / per, within = 2 * (i % per), d = (i % (dim / 2)) * 2, t = bt % time;
     const float a = (float)(offset + t) * powf(theta, -(float)d / (float)dim) * (inverse ? -1.f : 1.f);
     float s, c;
     sincosf(a, &s, &c);
-    rotate_pair<T>(x, out, at, s, c);
+    rotate_pair<T>(x, out, bt * x_row + within, bt * out_row + within, s, c);
   }
 }
 
@@ -271,7 +274,7 @@ __global__ void rope_kernel(const T* x, T* out, int64_t pairs, int64_t time, int
 // looping over the heads (the angle does not depend on the head).
 template <class T>
 __global__ void rope_heads_kernel(const T* x, T* out, int64_t items, int64_t time, int64_t heads, int64_t dim,
-                                  float theta, int64_t offset, int inverse) {
+                                  float theta, int64_t offset, int inverse, int64_t x_row, int64_t out_row) {
   const int64_t half = dim / 2;
   GRID_STRIDE(i, items) {
     const int64_t bt = i / half, p = i % half, d = 2 * p, t = bt % time;
@@ -279,7 +282,7 @@ __global__ void rope_heads_kernel(const T* x, T* out, int64_t items, int64_t tim
     float s, c;
     sincosf(a, &s, &c);
     for (int64_t h = 0; h < heads; h++) {
-      rotate_pair<T>(x, out, (bt * heads + h) * dim + d, s, c);
+      rotate_pair<T>(x, out, bt * x_row + h * dim + d, bt * out_row + h * dim + d, s, c);
     }
   }
 }
@@ -635,9 +638,11 @@ int qutai_amd_silu(const void* x, const void* gradient, void* out, int64_t n, in
   return (int)hipGetLastError();
 }
 
-int qutai_amd_rope(const void* x, void* out, int64_t batch, int64_t time, int64_t heads, int64_t dim, double theta,
-                   int64_t offset, int inverse, int dtype, void* stream) {
+int qutai_amd_rope_rows(const void* x, void* out, int64_t batch, int64_t time, int64_t heads, int64_t dim,
+                        double theta, int64_t offset, int inverse, int64_t x_row, int64_t out_row, int dtype,
+                        void* stream) {
   if (batch < 0 || time < 0 || heads < 0 || dim <= 0 || dim % 2 || !act_dtype(dtype)) return QA_EINVAL;
+  if (x_row < heads * dim || out_row < heads * dim) return QA_EINVAL;
   const int64_t pairs = batch * time * heads * dim / 2;
   if (pairs == 0) return QA_OK;
   hipStream_t s = (hipStream_t)stream;
@@ -645,19 +650,25 @@ int qutai_amd_rope(const void* x, void* out, int64_t batch, int64_t time, int64_
     const int64_t items = batch * time * dim / 2;
     if (dtype == BF16)
       hipLaunchKernelGGL(rope_heads_kernel<bf16_t>, dim3(blocks_for(items)), dim3(256), 0, s, (const bf16_t*)x,
-                         (bf16_t*)out, items, time, heads, dim, (float)theta, offset, inverse ? 1 : 0);
+                         (bf16_t*)out, items, time, heads, dim, (float)theta, offset, inverse ? 1 : 0, x_row, out_row);
     else
       hipLaunchKernelGGL(rope_heads_kernel<float>, dim3(blocks_for(items)), dim3(256), 0, s, (const float*)x,
-                         (float*)out, items, time, heads, dim, (float)theta, offset, inverse ? 1 : 0);
+                         (float*)out, items, time, heads, dim, (float)theta, offset, inverse ? 1 : 0, x_row, out_row);
     return (int)hipGetLastError();
   }
   if (dtype == BF16)
     hipLaunchKernelGGL(rope_kernel<bf16_t>, dim3(blocks_for(pairs)), dim3(256), 0, s, (const bf16_t*)x, (bf16_t*)out,
-                       pairs, time, heads, dim, (float)theta, offset, inverse ? 1 : 0);
+                       pairs, time, heads, dim, (float)theta, offset, inverse ? 1 : 0, x_row, out_row);
   else
     hipLaunchKernelGGL(rope_kernel<float>, dim3(blocks_for(pairs)), dim3(256), 0, s, (const float*)x, (float*)out,
-                       pairs, time, heads, dim, (float)theta, offset, inverse ? 1 : 0);
+                       pairs, time, heads, dim, (float)theta, offset, inverse ? 1 : 0, x_row, out_row);
   return (int)hipGetLastError();
+}
+
+int qutai_amd_rope(const void* x, void* out, int64_t batch, int64_t time, int64_t heads, int64_t dim, double theta,
+                   int64_t offset, int inverse, int dtype, void* stream) {
+  return qutai_amd_rope_rows(x, out, batch, time, heads, dim, theta, offset, inverse, heads * dim, heads * dim, dtype,
+                             stream);
 }
 
 int qutai_amd_head_rows(const void* x, void* out, int64_t count, int64_t start, int64_t width, int64_t time,

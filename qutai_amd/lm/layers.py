@@ -405,6 +405,9 @@ class GQA:
         self.heads, self.kv_heads, self.theta = config.n_heads, config.n_kv_heads, config.rope_theta
 
     def __call__(self, x):
+        weights = (self.q.weight, self.k.weight, self.v.weight)
+        if _stacked_qkv(x, *weights):
+            return self.out(gqa_attention(x, *weights, self.heads, self.kv_heads, self.theta))
         q = rope(self.q(x), self.heads, self.theta)
         k = rope(self.k(x), self.kv_heads, self.theta)
         return self.out(attention(q, k, self.v(x), self.heads, self.kv_heads))
@@ -601,6 +604,71 @@ def attention(q, k, v, heads, kv_heads):
     out, lse = b.attention(q.storage, k.storage, v.storage, *dims)
     return record(Tensor(out, shape=q.shape), (q, k, v),
                   lambda g: b.attention_backward(g, q.storage, k.storage, v.storage, out, lse, *dims))
+
+
+def _stacked_qkv(x, wq, wk, wv):
+    """True when GQA's three projections can run as one GEMM: amd tensors on
+    the bf16 path with bf16 projection outputs, one weight dtype."""
+    if x.device != "amd" or x.ndim != 3 or any(w.device != "amd" or w.ndim != 2 for w in (wq, wk, wv)):
+        return False
+    if not (wq.dtype == wk.dtype == wv.dtype) or wk.shape != wv.shape:
+        return False
+    if wq.shape[1] != x.shape[-1] or wk.shape[1] != x.shape[-1]:
+        return False
+    return _bf16_path(x, wq) and activation_dtype(x, wq) == "bfloat16"
+
+
+def gqa_attention(x, wq, wk, wv, heads, kv_heads, theta):
+    """RoPE(x Wq^T), RoPE(x Wk^T), x Wv^T and causal grouped-query attention
+    as one recorded op: GQA up to its out projection (src/qutai/lm/layers.py:
+    317-350 with rope 108-116 and attention 119-130) on the bf16 path.  The
+    three projections are one GEMM against the stacked weight [Wq; Wk; Wv]
+    (dq + 2 dkv rows, cast to bf16 into one block); RoPE reads the q and k
+    columns of that product in place and v's columns are copied out.  The
+    backward stacks dq, dk, dv the same way, so the input gradient is one GEMM
+    over K = dq + 2 dkv and the weight gradients are the row blocks of one
+    GEMM.  The forward values are those of the separate projections (every
+    output element sums K in the same order whatever the tile); the input
+    gradient sums its three terms in one accumulator where the separate
+    projections add three rounded products."""
+    b = backend(x)
+    batch, time, width = x.shape
+    rows = batch * time
+    dq, dkv = wq.shape[0], wk.shape[0]
+    total = dq + 2 * dkv
+    head = dq // heads
+    precision = matmul_precision()
+    xs = _bf16_input(x)
+    ws = amd.AMDStorage(total * width, "bfloat16")
+    for w, start in ((wq, 0), (wk, dq), (wv, dq + dkv)):
+        amd.cast_into(amd.view(ws, start * width, w.size), w.storage)
+    qkv = b.gemm(xs, ws, rows, width, total, transpose_right=True, out_dtype="bfloat16")
+    q = b.rope(qkv, batch, time, heads, head, theta, row=total)
+    k = b.rope(qkv, batch, time, kv_heads, head, theta, column=dq, row=total)
+    v = b.copy_rows(qkv, rows, dkv, column=dq + dkv, row=total)
+    del qkv
+    dims = (batch, time, heads, kv_heads, head)
+    out, lse = b.attention(q, k, v, *dims)
+
+    def backward(g):
+        with set_matmul_precision(precision):
+            gq, gk, gv = b.attention_backward(g, q, k, v, out, lse, *dims)
+            d = amd.AMDStorage(rows * total, gq.dtype)
+            b.rope(gq, batch, time, heads, head, theta, inverse=True, out=d, out_row=total)
+            b.rope(gk, batch, time, kv_heads, head, theta, inverse=True, out=d, out_column=dq, out_row=total)
+            b.copy_rows(gv, rows, dkv, out=d, out_column=dq + dkv, out_row=total)
+            dx = None
+            if x.requires_grad:
+                dx = (ProductGradient(b, d, ws, rows, total, width, precision) if x.dtype == "float32"
+                      else b.gemm(d, ws, rows, total, width, out_dtype=x.dtype))
+            dws = (None, None, None)
+            if wq.requires_grad or wk.requires_grad or wv.requires_grad:
+                dw = b.gemm(d, xs, total, rows, width, transpose_left=True, out_dtype=wq.dtype)
+                dws = tuple(owned(amd.view(dw, start * width, w.size)) if w.requires_grad else None
+                            for w, start in ((wq, 0), (wk, dq), (wv, dq + dkv)))
+        return (dx, *dws)
+
+    return record(Tensor(out, shape=(batch, time, dq)), (x, wq, wk, wv), backward)
 
 
 def attention_fused(q, k, v, *, scale=None, causal=False):

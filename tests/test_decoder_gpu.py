@@ -270,6 +270,90 @@ def test_linear_input_gradients_sum_in_the_gemm(base, leaf):
     assert np.array_equal(download(x0.grad.storage).astype(np.float32), want)
 
 
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_rope_and_copy_on_column_slices(lm, dtype):
+    """RoPE reading the q / k columns of a stacked [positions][dq + 2 dkv]
+    matrix and writing into such columns gives the bits of RoPE on the
+    contiguous slice, leaving the other columns alone; copy_rows moves a
+    column slice exactly.  Column ranges outside the rows are rejected."""
+    batch, time, dq, dkv, theta = 2, 19, 256, 128, 10000.0
+    total, positions = dq + 2 * dkv, batch * time
+    words = np.uint16 if dtype == "bfloat16" else np.float32
+    x = normal(131, positions * total).reshape(positions, total)
+    stacked = upload(x, dtype)
+    host = np.frombuffer(stacked.to_array(), dtype=words).reshape(positions, total)
+    for column, width, heads in ((0, dq, 4), (dq, dkv, 2)):
+        got = lm.rope(stacked, batch, time, heads, 64, theta, column=column, row=total)
+        want = lm.rope(upload(x[:, column:column + width].copy(), dtype), batch, time, heads, 64, theta)
+        assert np.array_equal(np.frombuffer(got.to_array(), dtype=words), np.frombuffer(want.to_array(), dtype=words))
+        # the inverse written back into the same columns of another stacked block
+        target = upload(np.zeros((positions, total)), dtype)
+        lm.rope(got, batch, time, heads, 64, theta, inverse=True, out=target, out_column=column, out_row=total)
+        back = np.frombuffer(target.to_array(), dtype=words).reshape(positions, total)
+        plain = lm.rope(want, batch, time, heads, 64, theta, inverse=True)
+        assert np.array_equal(back[:, column:column + width],
+                              np.frombuffer(plain.to_array(), dtype=words).reshape(positions, width))
+        assert not back[:, :column].any() and not back[:, column + width:].any()
+    v = lm.copy_rows(stacked, positions, dkv, column=dq + dkv, row=total)
+    assert np.array_equal(np.frombuffer(v.to_array(), dtype=words).reshape(positions, dkv), host[:, dq + dkv:])
+    target = upload(np.zeros((positions, total)), dtype)
+    lm.copy_rows(v, positions, dkv, out=target, out_column=dq, out_row=total)
+    back = np.frombuffer(target.to_array(), dtype=words).reshape(positions, total)
+    assert np.array_equal(back[:, dq:dq + dkv], host[:, dq + dkv:]) and not back[:, :dq].any()
+    # odd widths and pitches take the element path
+    odd = lm.copy_rows(stacked, positions, 37, column=3, row=total)
+    assert np.array_equal(np.frombuffer(odd.to_array(), dtype=words).reshape(positions, 37), host[:, 3:40])
+    with pytest.raises(ValueError):
+        lm.rope(stacked, batch, time, heads, 64, theta, column=total - 64, row=total)
+    with pytest.raises(ValueError):
+        lm.copy_rows(stacked, positions, dkv, column=total - dkv + 1, row=total)
+
+
+@pytest.mark.parametrize("x_dtype", ["float32", "bfloat16"])
+def test_stacked_qkv_attention_matches_separate_projections(base, x_dtype):
+    """GQA's q/k/v projections as one GEMM on the stacked weight (bf16 path,
+    fp32 master weights under autocast): the attention output is bit-identical
+    to the separate projections + RoPE + attention, the weight gradients are
+    bit-identical (each is its own row block of one product summed over the
+    same rows in the same order), and the input gradient, which sums its three
+    terms in one accumulator instead of two rounded additions, agrees to fp32
+    rounding."""
+    from qutai_amd import Tensor
+    from qutai_amd.backends.precision import set_matmul_precision
+    from qutai_amd.lm.layers import attention, gqa_attention, linear, rope
+
+    batch, time, heads, kv_heads, width, theta = 2, 128, 4, 2, 192, 10000.0
+    dq, dkv = heads * 64, kv_heads * 64
+    x = Tensor(upload(normal(71, batch * time * width), x_dtype), shape=(batch, time, width), requires_grad=True)
+    ws = [Tensor(upload(normal(72 + i, rows * width, 0.05), "float32"), shape=(rows, width), requires_grad=True)
+          for i, rows in enumerate((dq, dkv, dkv))]
+    g = Tensor(upload(normal(75, batch * time * dq), "bfloat16"), shape=(batch, time, dq))
+    results = []
+    with set_matmul_precision("bfloat16"):
+        for fused in (True, False):
+            for t in (x, *ws):
+                t.grad = None
+            if fused:
+                y = gqa_attention(x, *ws, heads, kv_heads, theta)
+            else:
+                q = rope(linear(x, ws[0]), heads, theta)
+                k = rope(linear(x, ws[1]), kv_heads, theta)
+                y = attention(q, k, linear(x, ws[2]), heads, kv_heads)
+            y.backward(g)
+            words = np.uint16 if x_dtype == "bfloat16" else np.float32
+            results.append((np.frombuffer(y.storage.to_array(), dtype=np.uint16).copy(),
+                            [download(w.grad.storage) for w in ws],
+                            np.frombuffer(x.grad.storage.to_array(), dtype=words).copy()))
+    (y1, dw1, dx1), (y2, dw2, dx2) = results
+    assert np.array_equal(y1, y2)
+    for a, b in zip(dw1, dw2):
+        assert np.array_equal(a, b)
+    if x_dtype == "float32":
+        assert ora.rel_frobenius(dx1.astype(np.float64), dx2.astype(np.float64)) <= 1e-6
+    else:
+        assert ora.rel_frobenius(ora.bf16_values(dx1), ora.bf16_values(dx2)) <= 1e-2
+
+
 @pytest.mark.parametrize("rows,width", [(300, 2048), (37, 100)])
 def test_rms_norm_backward_adds_the_residual(lm, rows, width):
     """dx = residual + dx as the kernel stores it (the 16-byte column path at
