@@ -117,6 +117,21 @@ int qutai_amd_gemm_grouped(const void* a, const void* b, void* out, const int64_
                            int transpose_right, int dtype, int out_dtype, int accumulate, const int64_t* gather,
                            int64_t source_rows, void* stream);
 
+/* Two grouped products summed in one accumulator:
+ *   out_g (+)= a_g @ B_g + a_tail_g @ Btail_g
+ * with a / a_tail [offsets[groups]][inner] and b / b_tail laid out as in
+ * qutai_amd_gemm_grouped (same expert_stride and orientation), i.e. one
+ * grouped product over K = 2 * inner whose first half reads (a, b) and
+ * second half (a_tail, b_tail); inner a multiple of 64.  Replaces the two
+ * input-gradient products of a SwiGLU expert, dX = dGate W_gate + dUp W_up
+ * (src/qutai/lm/layers.py:291-314 under the SparseMoE expert loop 395-397,
+ * each a `cuda_lm.gemm`, cuda_lm.py:31-55), which otherwise write and re-read
+ * an fp32 [rows][cols] partial between the two. */
+int qutai_amd_gemm_grouped_pair(const void* a, const void* a_tail, const void* b, const void* b_tail, void* out,
+                                const int64_t* offsets, int groups, int64_t max_rows, int64_t inner, int64_t cols,
+                                int64_t expert_stride, int transpose_right, int dtype, int out_dtype, int accumulate,
+                                void* stream);
+
 /* SwiGLU feed-forward input side in one GEMM (bf16 only):
  *   out = silu(a @ w_gate^T) * (a @ w_up^T)      [rows][hidden] bf16
  * with the roundings of the unfused form: both products rounded to bf16,
@@ -173,15 +188,6 @@ int qutai_amd_scale(const void* x, void* out, int64_t n, double factor, int dtyp
  * test models use d_model 8, d_expert 6, tests/test_lm_decoder.py:18-31). */
 int qutai_amd_repitch(const void* src, void* dst, int64_t batches, int64_t src_rows, int64_t src_cols,
                       int64_t dst_rows, int64_t dst_cols, int dtype, void* stream);
-
-/* dst[r][0:width] = src[r][0:width] for `rows` rows with row pitches src_row
- * and dst_row (elements, >= width; fp32 or bf16, bits copied): a column slice
- * of a row-major matrix moved to or from a contiguous block -- the v columns
- * of the stacked q/k/v projection output and the v gradient's place in the
- * stacked gradient (the GQA block, src/qutai/lm/layers.py:317-350, whose
- * separate `Projection` outputs need no such copy). */
-int qutai_amd_copy_rows(const void* src, int64_t src_row, void* dst, int64_t dst_row, int64_t rows, int64_t width,
-                        int dtype, void* stream);
 
 /* Softmax backward along rows: out = scale * p * (g - rowsum(g * p)), p the
  * softmax of (scale * x) (fp32 math; fp32/fp64/bf16 storage).  Replaces

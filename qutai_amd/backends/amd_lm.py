@@ -201,6 +201,28 @@ def grouped_gemm(rows_block, weight_stack, route, inner, cols, *, out_dtype="bfl
     return out
 
 
+def grouped_gemm_pair(rows_block, rows_tail, weight_stack, weight_tail, route, inner, cols, *,
+                      out_dtype="float32", transpose_right=False):
+    """out[offsets[e]:offsets[e+1]] = rows_block[..] @ op(W_e) + rows_tail[..] @ op(Wtail_e)
+    in one launch and one accumulator (qutai_amd_gemm_grouped_pair): the two
+    products of grouped_gemm summed over K = 2 * inner without an fp32
+    partial in between; inner a multiple of 64."""
+    experts = route["experts"]
+    for block, stack in ((rows_block, weight_stack), (rows_tail, weight_tail)):
+        if stack.size != experts * cols * inner or block.dtype != stack.dtype or block.dtype != rows_block.dtype:
+            raise ValueError("grouped_gemm_pair needs [experts] weights of cols*inner values in the rows' dtype")
+        if block.size != route["capacity"] * inner:
+            raise ValueError("grouped_gemm_pair rows must be capacity x inner")
+    if inner % 64:
+        raise ValueError("grouped_gemm_pair joins its two halves at a multiple of 64")
+    out = AMDStorage(route["capacity"] * cols, out_dtype)
+    if out.size:
+        out.runtime.call("qutai_amd_gemm_grouped_pair", rows_block.ptr, rows_tail.ptr, weight_stack.ptr,
+                         weight_tail.ptr, out.ptr, route["offsets"].ptr, experts, route["capacity"], inner, cols,
+                         cols * inner, int(transpose_right), code(rows_block.dtype), code(out_dtype), 0, mfma=True)
+    return out
+
+
 def swiglu_gemm(rows_block, w_gate, w_up, rows, inner, hidden, *, route=None, save=False, gather=False):
     """silu(rows_block @ W_gate^T) * (rows_block @ W_up^T) in one bf16 GEMM
     (qutai_amd_gemm_swiglu), with the unfused form's roundings.  With
@@ -384,9 +406,12 @@ def moe_experts_backward(gradient, route, saved, width, hidden, *, x_dtype, weig
     d_act = grouped_gemm(d_down, saved["w_down"], route, wp, hp, out_dtype=dt, transpose_right=False)
     dw_down = grouped_gemm_k(d_down, saved["act"], route, wp, hp, out_dtype=weight_dtype)
     d_gate, d_up = silu_mul_backward(d_act, saved["gate"], saved["up"])
-    d_rows = grouped_gemm(d_gate, saved["w_gate"], route, hp, wp, out_dtype="float32", transpose_right=False)
-    grouped_gemm(d_up, saved["w_up"], route, hp, wp, out_dtype="float32", transpose_right=False, out=d_rows,
-                 accumulate=True)
+    if hp % 64 == 0:  # dGate W_gate + dUp W_up in one accumulator
+        d_rows = grouped_gemm_pair(d_gate, d_up, saved["w_gate"], saved["w_up"], route, hp, wp)
+    else:
+        d_rows = grouped_gemm(d_gate, saved["w_gate"], route, hp, wp, out_dtype="float32", transpose_right=False)
+        grouped_gemm(d_up, saved["w_up"], route, hp, wp, out_dtype="float32", transpose_right=False, out=d_rows,
+                     accumulate=True)
     dw_gate = grouped_gemm_k(d_gate, saved["rows"], route, hp, wp, out_dtype=weight_dtype)
     dw_up = grouped_gemm_k(d_up, saved["rows"], route, hp, wp, out_dtype=weight_dtype)
     if (wp, hp) != (width, hidden):
@@ -631,10 +656,8 @@ def copy_rows(source, rows, width, *, column=0, row=None, out=None, out_column=0
         out_row = width if out_row is None else out_row
         if out.dtype != source.dtype or out_column < 0 or out_column + width > out_row or out.size < rows * out_row:
             raise ValueError("copied columns outside the target rows")
-    if rows * width:
-        item = _TYPES[source.dtype][1]
-        out.runtime.call("qutai_amd_copy_rows", source.ptr + column * item, row, out.ptr + out_column * item, out_row,
-                         rows, width, code(source.dtype))
+    amd._copy_strided(source, out, (rows, width), (row, 1), (out_row, 1), source_offset=column,
+                      target_offset=out_column)
     return out
 
 

@@ -39,6 +39,8 @@ SIGNATURES = {
                        _p, _sz, _p],
     "qutai_amd_gemm_workspace_size": [_i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32],
     "qutai_amd_gemm_grouped": [_p, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _p, _i64, _p],
+    "qutai_amd_gemm_grouped_pair": [_p, _p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32,
+                                    _p],
     "qutai_amd_gemm_swiglu": [_p, _p, _p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _i32, _p, _i64, _p],
     "qutai_amd_head_block_stats": [_p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _p],
     "qutai_amd_head_block_loss": [_p, _p, _p, _p, _i64, _p],
@@ -63,7 +65,6 @@ SIGNATURES = {
     "qutai_amd_route_backward": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p],
     "qutai_amd_scale": [_p, _p, _i64, _f64, _i32, _p],
     "qutai_amd_repitch": [_p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _p],
-    "qutai_amd_copy_rows": [_p, _i64, _p, _i64, _i64, _i64, _i32, _p],
     "qutai_amd_softmax_backward": [_p, _p, _p, _i64, _i64, _f64, _i32, _p],
     "qutai_amd_causal_mask": [_p, _p, _i64, _i64, _i64, _i64, _i32, _p],
     "qutai_amd_embedding": [_p, _p, _p, _i64, _i64, _i32, _p],

@@ -628,6 +628,54 @@ int qutai_amd_gemm_grouped(const void* a, const void* b, void* out, const int64_
   return (int)err;
 }
 
+int qutai_amd_gemm_grouped_pair(const void* a, const void* a_tail, const void* b, const void* b_tail, void* out,
+                                const int64_t* offsets, int groups, int64_t max_rows, int64_t inner, int64_t cols,
+                                int64_t expert_stride, int transpose_right, int dtype, int out_dtype, int accumulate,
+                                void* stream_) {
+  hipStream_t stream = (hipStream_t)stream_;
+  if (groups <= 0 || max_rows < 0 || inner < 0 || cols < 0 || expert_stride < 0) return QA_EINVAL;
+  if (dtype != QA_BF16 && dtype != QA_F32) return QA_EINVAL;
+  if (out_dtype != QA_F32 && out_dtype != QA_BF16) return QA_EINVAL;
+  if (!offsets || !out) return QA_EINVAL;
+  // the join must fall on a K step of every tile configuration (64 / 32)
+  if (inner % 64) return QA_EINVAL;
+  if (max_rows == 0 || cols == 0) return QA_OK;
+  if (inner == 0) return QA_EINVAL;
+  GemmArgs p = {};
+  p.a = a;
+  p.b = b;
+  p.a_tail = a_tail;
+  p.b_tail = b_tail;
+  p.k_head = inner;
+  p.out = out;
+  p.M = max_rows;
+  p.N = cols;
+  p.K = 2 * inner;
+  p.lda = inner;
+  p.ldb = transpose_right ? inner : cols;
+  p.ldc = cols;
+  p.sb = expert_stride;
+  p.batch = 1;
+  p.accumulate = accumulate ? 1 : 0;
+  p.out_bf16 = out_dtype == QA_BF16;
+  const int64_t E = dtype == QA_BF16 ? 8 : 4;
+  for (const void* q : {a, a_tail, b, b_tail})
+    if (!q || (uintptr_t)q % 16) return QA_EINVAL;
+  if (p.ldb % E || expert_stride % E) return QA_EINVAL;
+  const int64_t es = dtype == QA_BF16 ? 2 : 4;
+  if ((p.lda * 256 * es) >= (1ll << 31) || (p.ldb * 256 * es) >= (1ll << 31)) return QA_EINVAL;
+  p.vec_c = vec_out(out, p.ldc, 0);
+  p.offsets = offsets;
+  p.groups = groups;
+  p.alpha = 1.0f;
+  Tile tile = grouped_tile(max_rows, cols, groups, dtype == QA_BF16);
+  const int bm = tile_rows(tile);
+  p.tiles_m = (int)((max_rows + bm - 1) / bm + groups);
+  hipError_t err = dtype == QA_F32 ? launch_mma<true>(tile, false, transpose_right, p, stream)
+                                   : launch_mma<false>(tile, false, transpose_right, p, stream);
+  return (int)err;
+}
+
 int qutai_amd_gemm_swiglu(const void* a, const void* w_gate, const void* w_up, void* out, void* gate_out,
                           void* up_out, const int64_t* offsets, int groups, int64_t rows, int64_t inner,
                           int64_t hidden, int64_t expert_stride, int dtype, const int64_t* gather,

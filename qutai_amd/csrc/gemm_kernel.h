@@ -55,6 +55,14 @@ struct GemmArgs {
   // index below it), so a routed row set needs no copy of its own.
   const int64_t* a_rows;
   int64_t a_bytes;
+  // Two K segments (k_head > 0; grouped mode without gathered rows): the
+  // reduction runs over k < k_head from a and b, then over k_head <= k < K
+  // from a_tail and b_tail at k - k_head (same leading dimensions and group
+  // stride), in one accumulator: out = a op(b) + a_tail op(b_tail).  k_head
+  // is a multiple of 64, so no K step straddles the join.
+  const void* a_tail;
+  const void* b_tail;
+  int64_t k_head;
   int tiles_m;            // M tiles in the grid (grouped: an upper bound)
   float alpha;            // scale applied to A@B before the epilogue
   // Grouped-K mode (group_k = 1, batch = groups): group g reduces over the K
@@ -351,6 +359,8 @@ struct GemmKernel {
     const T* A = reinterpret_cast<const T*>(p.a);
     const T* B = reinterpret_cast<const T*>(p.b);
     const T* B2 = reinterpret_cast<const T*>(p.b2);
+    const T* A_tail = reinterpret_cast<const T*>(p.a_tail);  // second K segment (k_head > 0)
+    const T* B_tail = reinterpret_cast<const T*>(p.b_tail);
     int64_t M = p.M, row0 = 0, K = p.K;
     const int64_t* gather = nullptr;  // grouped mode with a_rows: this group's row indices
     char* outp = reinterpret_cast<char*>(p.out);
@@ -378,6 +388,10 @@ struct GemmKernel {
       if (KA && p.a_rows) gather = p.a_rows + lo;
       else A += lo * p.lda;
       B += (int64_t)g * p.sb;
+      if (p.k_head > 0) {
+        A_tail += lo * p.lda;
+        B_tail += (int64_t)g * p.sb;
+      }
       if constexpr (SWIGLU) B2 += (int64_t)g * p.sb;
       outp += lo * p.ldc * osize;
       M = hi - lo;
@@ -396,6 +410,9 @@ struct GemmKernel {
     }
     A = uniform_ptr(A);
     B = uniform_ptr(B);
+    A_tail = uniform_ptr(A_tail);
+    B_tail = uniform_ptr(B_tail);
+    const int64_t k_head = uniform64(p.k_head);
     if constexpr (SWIGLU) B2 = uniform_ptr(B2);
     outp = uniform_ptr(outp);
     M = uniform64(M);
@@ -416,11 +433,17 @@ struct GemmKernel {
     const int nk = (int)((K + BK - 1) / BK);
     // descriptor of one operand for the K step starting at k0
     auto desc_a = [&](int64_t k0) {
-      return rsrc(KA ? A + row0 * lda + k0 : A + k0 * lda + row0,
+      const bool tail = k_head > 0 && k0 >= k_head;
+      const T* a = tail ? A_tail : A;
+      if (tail) k0 -= k_head;
+      return rsrc(KA ? a + row0 * lda + k0 : a + k0 * lda + row0,
                   (int64_t)(KA ? BM * lda : BK * lda) * (int64_t)sizeof(T));
     };
     auto desc_b = [&](int64_t k0) {
-      return rsrc(KB ? B + col0 * ldb + k0 : B + k0 * ldb + col0,
+      const bool tail = k_head > 0 && k0 >= k_head;
+      const T* b = tail ? B_tail : B;
+      if (tail) k0 -= k_head;
+      return rsrc(KB ? b + col0 * ldb + k0 : b + k0 * ldb + col0,
                   (int64_t)(KB ? BN * ldb : BK * ldb) * (int64_t)sizeof(T));
     };
 
@@ -447,6 +470,7 @@ struct GemmKernel {
       }
       // A's descriptor base at k0 is a_tile + k0 (K-major) or + k0 * lda
       const T* a_tile = gather ? A : KA ? A + row0 * lda : A + row0;
+      const T* a_tail_tile = KA ? A_tail + row0 * lda : A_tail + row0;
       const int64_t a_span = gather ? p.a_bytes : (int64_t)(KA ? BM * lda : BK * lda) * (int64_t)sizeof(T);
       bool up[JB];  // SWIGLU: instruction j copies up-weight rows
 #pragma unroll
@@ -465,8 +489,13 @@ struct GemmKernel {
       char* base = reinterpret_cast<char*>(lds);
       // copies of one stage, optionally only instructions [first, last)
       auto issue_range = [&](int stage, int64_t k0, int first, int last) {
-        const u32x4 da = lds_rsrc(KA ? a_tile + k0 : a_tile + k0 * lda, a_span);
-        const u32x4 db = lds_rsrc(KB ? B + col0 * ldb + k0 : B + k0 * ldb + col0,
+        // the second K segment reads a_tail / b_tail at k0 - k_head
+        const bool tail = k_head > 0 && k0 >= k_head;
+        const int64_t kk = tail ? k0 - k_head : k0;
+        const T* at = tail ? a_tail_tile : a_tile;
+        const T* bt = tail ? B_tail : B;
+        const u32x4 da = lds_rsrc(KA ? at + kk : at + kk * lda, a_span);
+        const u32x4 db = lds_rsrc(KB ? bt + col0 * ldb + kk : bt + kk * ldb + col0,
                                   (int64_t)(KB ? BN * ldb : BK * ldb) * (int64_t)sizeof(T));
         const u32x4 db2 = SWIGLU ? lds_rsrc(B2 + col0 * ldb + k0, (int64_t)BN * ldb * (int64_t)sizeof(T)) : db;
         const int64_t krem = K - k0;

@@ -117,27 +117,6 @@ __global__ void repitch_kernel(const void* src, void* dst, int64_t batches, int6
   }
 }
 
-// dst[r * dst_row + c] = src[r * src_row + c] for c < width bytes: rows of a
-// column slice copied between matrices of different pitches (all in bytes).
-// With every row start and the width 16-byte aligned, one 16-byte chunk per
-// thread; otherwise one 2-byte element per thread.
-__global__ void copy_rows16(const char* src, int64_t src_row, char* dst, int64_t dst_row, int64_t rows,
-                            int64_t chunks) {
-  const int64_t total = rows * chunks;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t r = i / chunks, c = (i - r * chunks) * 16;
-    global_store(dst + r * dst_row + c, global_load<u32x4>(src + r * src_row + c));
-  }
-}
-__global__ void copy_rows2(const char* src, int64_t src_row, char* dst, int64_t dst_row, int64_t rows,
-                           int64_t halves) {
-  const int64_t total = rows * halves;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t r = i / halves, c = (i - r * halves) * 2;
-    *(uint16_t*)(dst + r * dst_row + c) = *(const uint16_t*)(src + r * src_row + c);
-  }
-}
-
 // Softmax backward along rows, one wave per row: dx = scale * p * (g - sum(g p))
 // (the gradient rule of qutai.softmax with the input scaled by `scale`).
 __device__ __forceinline__ float ld_any(const void* p, int64_t i, int d) {
@@ -703,24 +682,6 @@ int qutai_amd_repitch(const void* src, void* dst, int64_t batches, int64_t src_r
   if (!src || !dst) return QA_EINVAL;
   hipLaunchKernelGGL(repitch_kernel, dim3(grid_for(n)), dim3(THREADS), 0, (hipStream_t)stream, src, dst, batches,
                      src_rows, src_cols, dst_rows, dst_cols, dtype == BF16 ? 2 : 4);
-  return (int)hipGetLastError();
-}
-
-int qutai_amd_copy_rows(const void* src, int64_t src_row, void* dst, int64_t dst_row, int64_t rows, int64_t width,
-                        int dtype, void* stream) {
-  if (rows < 0 || width < 0 || src_row < width || dst_row < width) return QA_EINVAL;
-  if (dtype != BF16 && dtype != F32) return QA_EINVAL;
-  if (rows * width == 0) return QA_OK;
-  if (!src || !dst) return QA_EINVAL;
-  const int64_t es = dtype == BF16 ? 2 : 4, bytes = width * es;
-  const bool vec = (uintptr_t)src % 16 == 0 && (uintptr_t)dst % 16 == 0 && (src_row * es) % 16 == 0 &&
-                   (dst_row * es) % 16 == 0 && bytes % 16 == 0;
-  if (vec)
-    hipLaunchKernelGGL(copy_rows16, dim3(grid_for(rows * (bytes / 16))), dim3(THREADS), 0, (hipStream_t)stream,
-                       (const char*)src, src_row * es, (char*)dst, dst_row * es, rows, bytes / 16);
-  else
-    hipLaunchKernelGGL(copy_rows2, dim3(grid_for(rows * (bytes / 2))), dim3(THREADS), 0, (hipStream_t)stream,
-                       (const char*)src, src_row * es, (char*)dst, dst_row * es, rows, bytes / 2);
   return (int)hipGetLastError();
 }
 

@@ -17,7 +17,8 @@ bases 342-404, descriptor bases 418-425 and 466-471, DMA lane offsets
 430-465, register-staging offsets 523-545, epilogue 590-660 and 711-770) and
 qutai_amd/csrc/gemm_short.h (copies 91-101, output offsets 104-112 and
 176-186); the host's operand re-layout rule (plan_operand), split-K chunking
-(choose_split) and grouped grid from qutai_amd/csrc/gemm.hip.
+(choose_split), grouped grid and the pair form's K join from
+qutai_amd/csrc/gemm.hip.
 """
 from __future__ import annotations
 
@@ -273,6 +274,18 @@ def grouped_gemm(cfg: Config, f32: bool, counts: list[int], inner: int, cols: in
                     operand_loads(cfg, f32, transpose_right, cfg.bn, g * expert_stride, col0, cols, inner, ldb,
                                   b_alloc, "B")
                 output_stores(cfg, False, lo * cols, row0, col0, rows, cols, cols, capacity * cols, vec)
+
+
+def grouped_pair_gemm(cfg: Config, f32: bool, counts: list[int], inner: int, cols: int, transpose_right: bool):
+    """qutai_amd_gemm_grouped_pair: one grouped product over K = 2 inner whose
+    steps below inner read (a, b) and the rest (a_tail, b_tail) at k - inner,
+    two allocations per side of the grouped shapes.  inner is a multiple of 64
+    (the entry point's check), so every step of the first half is whole and
+    each half's loads are those of a grouped product over K = inner."""
+    if inner % 64 or inner == 0:
+        raise ValueError("rejected by qutai_amd_gemm_grouped_pair")
+    for _ in ("head", "tail"):
+        grouped_gemm(cfg, f32, counts, inner, cols, transpose_right)
 
 
 def grouped_k_gemm(cfg: Config, f32: bool, counts: list[int], rows: int, cols: int):

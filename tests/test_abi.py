@@ -89,6 +89,9 @@ def test_argument_checks_reject_before_any_device_call():
                                           None) == -1
     assert library.qutai_amd_gemm_swiglu(fake, fake, fake, fake, None, None, fake, 8, 512, 2048, 64, 0, 5, fake,
                                          1 << 19, None) == -1
+    # the pair form joins its two K halves at a multiple of 64
+    assert library.qutai_amd_gemm_grouped_pair(fake, fake, fake, fake, fake, fake, 8, 512, 96, 64, 0, 0, 5, 0, 0,
+                                               None) == -1
     # a gather needs the grouped form (offsets)
     assert library.qutai_amd_gemm_swiglu(fake, fake, fake, fake, None, None, None, 1, 512, 2048, 64, 0, 5, fake,
                                          16, None) == -1

@@ -100,6 +100,19 @@ def test_grouped_products_stay_in_bounds(f32):
         gm.grouped_gemm(cfg, f32, counts, inner, cols, True, gather=order, source_rows=tokens)
 
 
+@pytest.mark.parametrize("f32", [False, True])
+def test_grouped_pair_products_stay_in_bounds(f32):
+    rng = np.random.default_rng(SEED + 13 + f32)
+    for cfg in [c for c in gm.tile_configs(f32) if c.name in ("L8D2", "U", "N")]:
+        counts = _counts(rng, 4, int(rng.integers(1, 700)))
+        inner = 64 * int(rng.integers(1, 12))
+        cols = 8 * int(rng.integers(1, 60))
+        gm.grouped_pair_gemm(cfg, f32, counts, inner, cols, False)
+        gm.grouped_pair_gemm(cfg, f32, counts, inner, cols, True)
+        with pytest.raises(ValueError):
+            gm.grouped_pair_gemm(cfg, f32, counts, inner + 8, cols, False)
+
+
 def test_swiglu_grouped_and_plain_stay_in_bounds():
     rng = np.random.default_rng(SEED + 11)
     for _ in range(3):

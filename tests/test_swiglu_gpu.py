@@ -117,6 +117,50 @@ def test_grouped_gemm_gather_equals_gathered_block(amd, lm, dtype, tokens, width
             lm.grouped_gemm(rows, ws, route, width, cols, gather=True, out_dtype=dtype)
 
 
+@pytest.mark.parametrize("dtype,tokens,inner,cols,experts,transpose_right", [
+    ("bfloat16", 1500, 128, 200, 8, False), ("bfloat16", 700, 1408, 2048, 8, False),
+    ("bfloat16", 600, 64, 96, 4, True), ("float32", 900, 192, 96, 4, False)])
+def test_grouped_gemm_pair_sums_two_products(amd, lm, dtype, tokens, inner, cols, experts, transpose_right):
+    """One grouped launch over K = 2 inner summing a b + a_tail b_tail: with
+    either half zero it is bit-identical to the other half's grouped GEMM
+    (pins both halves' addressing), and with both it matches the two fp32
+    products added on the host to fp32 rounding and the float64 product of
+    the stored operands."""
+    logits = normal(tokens + 7, tokens * experts)
+    route = lm.routing(upload(logits, "float32"), tokens, experts, 2)
+    capacity = route["capacity"]
+    used = int(download(route["offsets"])[-1])
+    a, a_tail = (upload(normal(seed, capacity * inner), dtype) for seed in (11, 12))
+    b, b_tail = (upload(normal(seed, experts * cols * inner, 0.1), dtype) for seed in (13, 14))
+    zero = upload(np.zeros(capacity * inner), dtype)
+    kw = dict(out_dtype="float32", transpose_right=transpose_right)
+    head = download(lm.grouped_gemm(a, b, route, inner, cols, **kw))[:used * cols]
+    tail = download(lm.grouped_gemm(a_tail, b_tail, route, inner, cols, **kw))[:used * cols]
+    only_head = download(lm.grouped_gemm_pair(a, zero, b, b_tail, route, inner, cols, **kw))[:used * cols]
+    only_tail = download(lm.grouped_gemm_pair(zero, a_tail, b, b_tail, route, inner, cols, **kw))[:used * cols]
+    assert np.array_equal(only_head, head) and np.array_equal(only_tail, tail)
+    both = download(lm.grouped_gemm_pair(a, a_tail, b, b_tail, route, inner, cols, **kw))[:used * cols]
+    summed = head.astype(np.float32) + tail.astype(np.float32)
+    assert ora.rel_frobenius(both, summed) <= 1e-6
+    # float64 product of the stored values for the first expert's rows
+    offsets = download(route["offsets"])
+    lo, hi = int(offsets[0]), int(offsets[1])
+    host = {name: ora.bf16_values(np.frombuffer(t.to_array(), dtype=np.uint16)) if dtype == "bfloat16"
+            else np.frombuffer(t.to_array(), dtype=np.float32).astype(np.float64)
+            for name, t in (("a", a), ("at", a_tail), ("b", b), ("bt", b_tail))}
+    shape = (cols, inner) if transpose_right else (inner, cols)
+    w0, wt0 = host["b"][:cols * inner].reshape(shape), host["bt"][:cols * inner].reshape(shape)
+    if transpose_right:
+        w0, wt0 = w0.T, wt0.T
+    exact = host["a"].reshape(capacity, inner)[lo:hi] @ w0 + host["at"].reshape(capacity, inner)[lo:hi] @ wt0
+    got = both.reshape(used, cols)[lo:hi]
+    assert ora.rel_frobenius(got, exact) <= 1e-5
+    with pytest.raises(ValueError):  # the join must fall on a multiple of 64
+        lm.grouped_gemm_pair(upload(normal(1, capacity * 72), dtype), upload(normal(2, capacity * 72), dtype),
+                             upload(normal(3, experts * cols * 72), dtype), upload(normal(4, experts * cols * 72), dtype),
+                             route, 72, cols, **kw)
+
+
 def test_swiglu_rejects_unsupported_operands(amd, lm):
     x = upload(normal(0, 16 * 12), "bfloat16")
     w = upload(normal(1, 8 * 12), "bfloat16")
