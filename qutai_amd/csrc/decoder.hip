@@ -287,6 +287,66 @@ __global__ void rope_heads_kernel(const T* x, T* out, int64_t items, int64_t tim
   }
 }
 
+// The same rotation with 16-byte accesses: a lane takes the P = 16 /
+// (2 sizeof(T)) consecutive pairs of one position that share a 16-byte chunk
+// (their angles computed once, with the expressions above, so the bits are
+// the same) in up to HB heads, whose chunks it loads together before
+// rotating and storing them.  Bases and row pitches 16-byte aligned, dim a
+// multiple of 2P.
+constexpr int ROPE_HB = 8;
+template <class T>
+__global__ void rope_heads_vec(const T* x, T* out, int64_t items, int64_t time, int64_t heads, int64_t dim,
+                               float theta, int64_t offset, int inverse, int64_t x_row, int64_t out_row) {
+  constexpr int P = 16 / (2 * (int)sizeof(T));
+  const int64_t groups = dim / (2 * P), blocks = (heads + ROPE_HB - 1) / ROPE_HB;
+  GRID_STRIDE(i, items) {
+    const int64_t g = i % groups, hb = (i / groups) % blocks, bt = i / (groups * blocks), t = bt % time;
+    float s[P], c[P];
+#pragma unroll
+    for (int q = 0; q < P; q++) {
+      const int64_t d = 2 * (g * P + q);
+      const float a = (float)(offset + t) * powf(theta, -(float)d / (float)dim) * (inverse ? -1.f : 1.f);
+      sincosf(a, &s[q], &c[q]);
+    }
+    const int64_t h0 = hb * ROPE_HB;
+    const int n = (int)(heads - h0 < ROPE_HB ? heads - h0 : ROPE_HB);
+    const T* src = x + bt * x_row + h0 * dim + 2 * g * P;
+    T* dst = out + bt * out_row + h0 * dim + 2 * g * P;
+    u32x4 w[ROPE_HB];
+#pragma unroll
+    for (int h = 0; h < ROPE_HB; h++)
+      if (h < n) w[h] = global_load<u32x4>(src + h * dim);
+#pragma unroll
+    for (int h = 0; h < ROPE_HB; h++) {
+      if (h >= n) break;
+      float v[2 * P];
+      if constexpr (sizeof(T) == 2) {
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] = __uint_as_float(((w[h][k >> 1] >> (16 * (k & 1))) & 0xffffu) << 16);
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; k++) v[k] = __uint_as_float(w[h][k]);
+      }
+      float y[2 * P];
+#pragma unroll
+      for (int q = 0; q < P; q++) {
+        y[2 * q] = fmaf(v[2 * q], c[q], -(v[2 * q + 1] * s[q]));
+        y[2 * q + 1] = fmaf(v[2 * q], s[q], v[2 * q + 1] * c[q]);
+      }
+      u32x4 r;
+      if constexpr (sizeof(T) == 2) {
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+          r[k] = (uint32_t)f32_to_bf16(y[2 * k]) | ((uint32_t)f32_to_bf16(y[2 * k + 1]) << 16);
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; k++) r[k] = __float_as_uint(y[k]);
+      }
+      global_store(dst + h * dim, r);
+    }
+  }
+}
+
 // rows start.. of the (time-1)-long prediction positions of every sequence
 // (lm.cu:425-427); backward adds the rows back into the [.. time ..] layout
 template <class T>
@@ -647,6 +707,20 @@ int qutai_amd_rope_rows(const void* x, void* out, int64_t batch, int64_t time, i
   if (pairs == 0) return QA_OK;
   hipStream_t s = (hipStream_t)stream;
   if (heads > 1) {  // one angle per (position, pair), shared by the heads
+    const int64_t es = dtype == BF16 ? 2 : 4, P = 16 / (2 * es);
+    if (dim % (2 * P) == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)out % 16 == 0 && (x_row * es) % 16 == 0 &&
+        (out_row * es) % 16 == 0) {
+      const int64_t items = batch * time * (dim / (2 * P)) * ((heads + ROPE_HB - 1) / ROPE_HB);
+      if (dtype == BF16)
+        hipLaunchKernelGGL(rope_heads_vec<bf16_t>, dim3(blocks_for(items)), dim3(256), 0, s, (const bf16_t*)x,
+                           (bf16_t*)out, items, time, heads, dim, (float)theta, offset, inverse ? 1 : 0, x_row,
+                           out_row);
+      else
+        hipLaunchKernelGGL(rope_heads_vec<float>, dim3(blocks_for(items)), dim3(256), 0, s, (const float*)x,
+                           (float*)out, items, time, heads, dim, (float)theta, offset, inverse ? 1 : 0, x_row,
+                           out_row);
+      return (int)hipGetLastError();
+    }
     const int64_t items = batch * time * dim / 2;
     if (dtype == BF16)
       hipLaunchKernelGGL(rope_heads_kernel<bf16_t>, dim3(blocks_for(items)), dim3(256), 0, s, (const bf16_t*)x,
