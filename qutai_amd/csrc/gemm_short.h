@@ -5,8 +5,10 @@
 //
 // Such a product writes one output element per 2K FLOPs, so it is bound by
 // the output stream and by how fast short-lived tiles can be fed.  One
-// workgroup keeps a 128-row block of A in registers and sweeps a strip of N
-// in 128-column chunks:
+// workgroup keeps a 128-row block of A in registers and sweeps its strip of
+// N: every strips-th 128-column chunk (strip, strip + strips, ...), so the
+// workgroups of a row block write neighbouring chunks of the same rows at
+// the same time:
 //  * the B chunks move HBM/L2 -> LDS with direct-to-LDS buffer loads into a
 //    SLOTS-deep ring, SLOTS - 1 chunks ahead of the MFMAs;
 //  * the MFMAs compute the transposed block (B rows as the first operand), so
@@ -74,8 +76,10 @@ struct ShortKernel {
     const int strip = pid % p.strips, tm = (pid / p.strips) % p.tiles_m;
     const int64_t bz = pid / (p.strips * p.tiles_m);
     const int64_t row0 = (int64_t)tm * BM;
-    const int first = strip * p.strip_chunks;
-    const int nc = uniform32(min(p.strip_chunks, p.chunks - first));
+    // this strip's chunks are strip, strip + strips, ...: the workgroups of
+    // one row block (consecutive ids, one XCD) write neighbouring 128-column
+    // chunks of the same rows at the same time
+    const int nc = uniform32((p.chunks - strip + p.strips - 1) / p.strips);
     const int64_t K = p.K;
 
     const bf16_t* A = uniform_ptr(p.a + bz * p.sa + row0 * p.lda);
@@ -97,7 +101,7 @@ struct ShortKernel {
       }
     };
     auto copy_b = [&](int c) {  // chunk c of the strip into its ring slot
-      const int64_t n0 = (int64_t)(first + c) * BN;
+      const int64_t n0 = (int64_t)(strip + c * p.strips) * BN;
       copy(uniform_ptr(B + n0 * p.ldb), p.ldb, p.N - n0, ring + (c % SLOTS) * TILE_BYTES);
     };
 
@@ -153,7 +157,7 @@ struct ShortKernel {
       // One 32-row block at a time: the lane-half swap gives each lane 8
       // consecutive columns (16 bytes), staged in LDS and read back as whole
       // 128-byte row segments, so every streaming store writes full lines.
-      const int64_t n0 = (int64_t)(first + c) * BN + wn * 64;
+      const int64_t n0 = (int64_t)(strip + c * p.strips) * BN + wn * 64;
 #pragma unroll
       for (int fm = 0; fm < 2; fm++) {
 #pragma unroll

@@ -320,6 +320,11 @@ def short_strip(m: int, k: int, n: int, batch: int, strip: int):
     pb = plan_operand(k, n, batch, n * k, False)
     cfg = Config("R", 128, 128, 2, 2, 64, 3)
     tiles_m, chunks = (m + 127) // 128, (n + 127) // 128
+    # strip s sweeps chunks s, s + strips, ... (strips = ceil(chunks / strip)):
+    # every chunk belongs to exactly one strip
+    strips = (chunks + strip - 1) // strip
+    covered = sorted(s + c * strips for s in range(strips) for c in range((chunks - s + strips - 1) // strips))
+    assert covered == list(range(chunks))
     lane = np.arange(64)
     for z in range(batch):
         for tm in range(tiles_m):
