@@ -348,6 +348,11 @@ int choose_split(int64_t rows, int64_t cols, int64_t inner, int64_t batch, Tile*
         }
       }
     }
+  } else if (batch == 1 && (*tile == TILE_N || *tile == TILE_W) && tiles * 4 <= cus && inner >= 1024) {
+    // a thin output (<= 64 columns or rows) over a few 256-wide blocks, e.g.
+    // a router's logits: K chunks of at least 256 put the idle CUs to work
+    // (8192 x 2048 x 8 logits of an 8-expert router: 32 workgroups -> 256)
+    s = std::min<int64_t>({8, cus / tiles, inner / 256});
   }
   if (s <= 1 || inner < 128) return 1;
   const int64_t c = ((inner + s - 1) / s + 63) / 64 * 64;

@@ -65,7 +65,7 @@ def test_plain_and_batched_products_stay_in_bounds(f32):
 @pytest.mark.parametrize("splits", [2, 3, 7])
 def test_split_k_chunks_stay_in_bounds(splits):
     rng = np.random.default_rng(SEED + splits)
-    for cfg in [c for c in gm.tile_configs(False) if c.name in ("L8D2", "H", "S")]:
+    for cfg in [c for c in gm.tile_configs(False) if c.name in ("L8D2", "H", "S", "N", "W")]:
         for _ in range(2):
             m, n = (int(v) for v in rng.integers(1, 400, size=2))
             k = int(rng.integers(129, 3000))

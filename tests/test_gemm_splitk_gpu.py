@@ -86,3 +86,22 @@ def test_decoder_head_shape_splits_by_itself(amd, dtype):
     exact = ora.gemm_f64(stored(a, dtype), stored(b, dtype), m, k, n, row_list=rows)
     assert ora.rel_frobenius(got[rows], exact) <= FP32_TOL
     assert np.isfinite(got).all()
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+@pytest.mark.parametrize("m,k,n,tb", [(8192, 2048, 8, True), (2000, 1500, 40, False), (48, 3000, 1024, False)])
+def test_thin_outputs_split_by_themselves(amd, dtype, m, k, n, tb):
+    """A router-shaped product (8192 x 2048 x 8, X W^T) and other thin outputs
+    over few 256-wide blocks take K chunks without being forced: the
+    workspace asks for fp32 partials, and every row matches the oracle."""
+    runtime = amd.get_runtime()
+    code = 0 if dtype == "float32" else 5
+    ws = runtime.lib.qutai_amd_gemm_workspace_size(m, k, n, 1, 0, 0, 0, int(tb), code, code, 0)
+    assert ws >= 2 * m * n * 4
+    a, b = normal(40 + n, m * k), normal(50 + n, k * n)
+    got = download(amd.gemm(upload(a, dtype), upload(b, dtype), m, k, n, transpose_right=tb)).reshape(m, n)
+    exact = ora.gemm_f64(stored(a, dtype), stored(b, dtype), m, k, n, transpose_right=tb)
+    assert ora.rel_frobenius(got, exact) <= FP32_TOL
+    rounded = download(amd.gemm(upload(a, dtype), upload(b, dtype), m, k, n, transpose_right=tb,
+                                out_dtype="bfloat16")).reshape(m, n)
+    assert ora.rel_frobenius(rounded, exact) <= BF16_TOL
