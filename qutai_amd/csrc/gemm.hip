@@ -116,17 +116,115 @@ __global__ void __launch_bounds__(256) prepare_operand(const void* src, void* ds
 
 // Split-K reduction: out[b][e] = sum over s of part[b * splits + s][e] in
 // order s = 0, 1, ... (fp32), plus the old output when accumulating, one
-// rounding to the output type.
+// rounding to the output type.  The partials hold rows of `cols` elements;
+// out's rows are `ldc` apart (a column window of a wider output).
 __global__ void splitk_reduce(const float* part, void* out, int64_t n, int64_t total, int splits, int accumulate,
-                              int out_bf16) {
+                              int out_bf16, int64_t cols, int64_t ldc) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
     const int64_t b = i / n, e = i - b * n;
     const float* src = part + b * splits * n + e;
     float acc = 0.f;
     for (int s = 0; s < splits; s++) acc += src[s * n];
-    if (accumulate) acc += out_bf16 ? bf16_to_f32(((const bf16_t*)out)[i]) : ((const float*)out)[i];
-    if (out_bf16) ((bf16_t*)out)[i] = f32_to_bf16(acc);
-    else ((float*)out)[i] = acc;
+    const int64_t row = e / cols, at = (b * (n / cols) + row) * ldc + (e - row * cols);
+    if (accumulate) acc += out_bf16 ? bf16_to_f32(((const bf16_t*)out)[at]) : ((const float*)out)[at];
+    if (out_bf16) ((bf16_t*)out)[at] = f32_to_bf16(acc);
+    else ((float*)out)[at] = acc;
+  }
+}
+
+// Column remainder of at most 8 columns with a K-major A (the last r
+// columns of a 256 q + r wide product), in two small launches:
+// gather_columns copies B's r columns once into a compact fp32 block
+// [r][pitch] (zero beyond K; every workgroup of the second launch would
+// otherwise fetch the same scattered elements, one cache line each, at the
+// same time), then remainder_columns computes one output row per wave:
+// 16-byte A loads and the matching column values spread over the lanes,
+// fp32 sums per lane in K order and a fixed xor tree over the lanes, then
+// the GEMM epilogue's accumulate and rounding.  Planned operands only: A's
+// rows are 16-byte aligned and zero-padded to its pitch, so no 16-byte chunk
+// crosses the allocation; `pitch` is K rounded up to 8.
+template <bool BF16, bool KB>
+__global__ void __launch_bounds__(256) gather_columns(const void* b, float* cols, int64_t K, int64_t ldb, int r,
+                                                      int64_t pitch) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= r * pitch) return;
+  const int64_t j = t / pitch, k = t - j * pitch;
+  float v = 0.f;
+  if (k < K) {
+    const int64_t at = KB ? j * ldb + k : k * ldb + j;
+    v = BF16 ? bf16_to_f32(((const bf16_t*)b)[at]) : ((const float*)b)[at];
+  }
+  cols[t] = v;
+}
+
+constexpr int RWAVES = 4, RROWS = 4;  // waves per workgroup, rows per wave
+template <bool BF16>
+__global__ void __launch_bounds__(64 * RWAVES) remainder_columns(const void* a, const float* cols, void* out,
+                                                                 int64_t M, int64_t K, int64_t lda, int64_t pitch,
+                                                                 int64_t ldc, int r, int out_bf16, int accumulate) {
+  constexpr int E = BF16 ? 8 : 4;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t row0 = ((int64_t)blockIdx.x * RWAVES + wave) * RROWS;
+  float acc[RROWS][8];
+#pragma unroll
+  for (int i = 0; i < RROWS; i++)
+#pragma unroll
+    for (int j = 0; j < 8; j++) acc[i][j] = 0.f;
+  for (int64_t c = lane; c * E < K; c += 64) {
+    u32x4 w[RROWS];
+#pragma unroll
+    for (int i = 0; i < RROWS; i++) {
+      const int64_t m = row0 + i;
+      w[i] = u32x4{0u, 0u, 0u, 0u};
+      if (m < M) w[i] = *(const u32x4*)((const char*)a + (m * lda + c * E) * (BF16 ? 2 : 4));
+    }
+    float bv[8][E];
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+#pragma unroll
+      for (int e = 0; e < E; e += 4) {
+        f32x4 v = {0.f, 0.f, 0.f, 0.f};
+        if (j < r) v = *(const f32x4*)(cols + j * pitch + c * E + e);
+        bv[j][e] = v[0];
+        bv[j][e + 1] = v[1];
+        bv[j][e + 2] = v[2];
+        bv[j][e + 3] = v[3];
+      }
+#pragma unroll
+    for (int i = 0; i < RROWS; i++) {
+      float x[E];
+      if constexpr (BF16) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          x[2 * q] = __uint_as_float(w[i][q] << 16);
+          x[2 * q + 1] = __uint_as_float(w[i][q] & 0xffff0000u);
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; q++) x[q] = __uint_as_float(w[i][q]);
+      }
+#pragma unroll
+      for (int e = 0; e < E; e++)
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+          if (j < r) acc[i][j] = __builtin_fmaf(x[e], bv[j][e], acc[i][j]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < RROWS; i++) {
+    const int64_t m = row0 + i;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      if (j >= r) break;
+      float v = acc[i][j];
+      for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+      if (lane == j && m < M) {
+        const int64_t at = m * ldc + j;
+        if (accumulate) v += out_bf16 ? bf16_to_f32(((const bf16_t*)out)[at]) : ((const float*)out)[at];
+        if (out_bf16) ((bf16_t*)out)[at] = f32_to_bf16(v);
+        else ((float*)out)[at] = v;
+      }
+    }
   }
 }
 
@@ -217,6 +315,8 @@ int forced_tile() {
   return forced;
 }
 
+Tile pick_tile(int64_t M, int64_t N, int64_t batch, bool bf16, double* cost);
+
 Tile choose_tile(int64_t M, int64_t N, int64_t K, int64_t batch, bool bf16) {
   if (forced_tile() >= 0) return (Tile)forced_tile();
   if (N <= 64) return TILE_N;
@@ -235,6 +335,12 @@ Tile choose_tile(int64_t M, int64_t N, int64_t K, int64_t batch, bool bf16) {
   // round of 192x256 / 256x192 tiles (bf16) 0.9; a partial round of the
   // others costs as much as a full one.  Ties (within 3%) go to 256x128,
   // then 256x192, 192x256, 256x256.
+  return pick_tile(M, N, batch, bf16, nullptr);
+}
+
+// The large-tile choice of choose_tile and its cost (rounds of 256x256 tiles
+// over the CUs, per unit of K).
+Tile pick_tile(int64_t M, int64_t N, int64_t batch, bool bf16, double* cost) {
   const int64_t cus = cu_count();
   auto rounds = [cus](int64_t tiles) { return (double)(tiles / cus + (tiles % cus ? 1 : 0)); };
   const int64_t mt = (M + 255) / 256, nt = (N + 255) / 256, ms = (M + 127) / 128, ns = (N + 127) / 128;
@@ -246,11 +352,32 @@ Tile choose_tile(int64_t M, int64_t N, int64_t K, int64_t batch, bool bf16) {
   const double cost_t = bf16 ? 0.9 * rounds((M + 191) / 192 * nt * batch) : 1e30;
   const double cost_u = bf16 ? 0.9 * rounds(mt * ((N + 191) / 192) * batch) : 1e30;
   const double best = std::min({cost_l, cost_h, cost_s, cost_t, cost_u});
-  if (cost_h <= best * 1.03) return TILE_H;
-  if (cost_u <= best * 1.03) return TILE_U;
-  if (cost_t <= best * 1.03) return TILE_T;
-  if (cost_l <= best * 1.03) return TILE_L8D2;
-  return TILE_S;
+  Tile pick = TILE_S;
+  double chosen = cost_s;
+  if (cost_h <= best * 1.03) pick = TILE_H, chosen = cost_h;
+  else if (cost_u <= best * 1.03) pick = TILE_U, chosen = cost_u;
+  else if (cost_t <= best * 1.03) pick = TILE_T, chosen = cost_t;
+  else if (cost_l <= best * 1.03) pick = TILE_L8D2, chosen = cost_l;
+  if (cost) *cost = chosen;
+  return pick;
+}
+
+// Column remainder: an output N = 256 q + r wide with 0 < r <= 64, whose last
+// r columns cost the large tiles about a round of their own (4095 x 4097:
+// 272 tiles of 256x256 or 352 of 256x192 for 256 CUs), runs as two launches:
+// the first 256 q columns on the large tiles and the last r on the thin
+// 256x64 tile, which splits K when its tiles fill few CUs (priced at 0.3 of a
+// round).  Returns the first launch's width, or 0 for one launch.  Each
+// output element still sums K through the same MFMA chain (split K sums its
+// chunks in order), so results stay bit-repeatable.
+int64_t column_split(int64_t M, int64_t N, int64_t K, int64_t batch, bool bf16) {
+  if (forced_tile() >= 0 || batch != 1 || M <= 64 || K <= 128 || N < 512) return 0;
+  const int64_t r = N % 256;
+  if (r == 0 || r > 64) return 0;
+  double full = 0.0, main = 0.0;
+  pick_tile(M, N, 1, bf16, &full);
+  pick_tile(M, N - r, 1, bf16, &main);
+  return main + 0.3 < full * 0.97 ? N - r : 0;
 }
 
 // Split-K for plain products whose tiles fill at most a quarter of the CU
@@ -348,11 +475,13 @@ int choose_split(int64_t rows, int64_t cols, int64_t inner, int64_t batch, Tile*
         }
       }
     }
-  } else if (batch == 1 && (*tile == TILE_N || *tile == TILE_W) && tiles * 4 <= cus && inner >= 1024) {
+  } else if (batch == 1 && (*tile == TILE_N || *tile == TILE_W) && tiles * 4 <= cus && inner >= 512) {
     // a thin output (<= 64 columns or rows) over a few 256-wide blocks, e.g.
-    // a router's logits: K chunks of at least 256 put the idle CUs to work
-    // (8192 x 2048 x 8 logits of an 8-expert router: 32 workgroups -> 256)
-    s = std::min<int64_t>({8, cus / tiles, inner / 256});
+    // a router's logits or a column remainder: latency-bound tiles, so K
+    // chunks down to 64 (up to 16 of them) put the idle CUs to work
+    // (8192 x 2048 x 8 logits of an 8-expert router: 32 workgroups -> 256;
+    // the last column of 4095 x 1000 x 4097: 16 -> 256)
+    s = std::min<int64_t>({16, cus / tiles, (inner + 63) / 64});
   }
   if (s <= 1 || inner < 128) return 1;
   const int64_t c = ((inner + s - 1) / s + 63) / 64 * 64;
@@ -471,6 +600,39 @@ int vec_out(const void* p, int64_t ldc, int64_t stride) {
   return (ldc % 4 == 0 && stride % 4 == 0) ? 1 : 0;
 }
 
+// One launch of a plain product over output columns [c0, c0 + n): its tile,
+// K chunks and fp32 partial bytes.
+struct Window {
+  int64_t c0, n;
+  Tile tile;
+  int splits;
+  int64_t chunk;
+  size_t partial;
+  bool rows_kernel;  // remainder_columns instead of a tile
+};
+
+// The launches of a plain product: one window over every column or, with a
+// column remainder (column_split), the large-tile columns and the rest: up
+// to 8 columns of a K-major A on remainder_columns (one launch, no partial
+// sums), wider remainders on the thin tile.
+int plan_windows(int64_t rows, int64_t inner, int64_t cols, int64_t batch, bool bf16, int transpose_left,
+                 Window (&w)[2]) {
+  const int64_t main_cols = inner > 0 ? column_split(rows, cols, inner, batch, bf16) : 0;
+  const int count = main_cols ? 2 : 1;
+  for (int i = 0; i < count; i++) {
+    Window& x = w[i];
+    x.c0 = i == 0 ? 0 : main_cols;
+    x.n = count == 1 ? cols : i == 0 ? main_cols : cols - main_cols;
+    x.rows_kernel = i == 1 && x.n <= 8 && !transpose_left;
+    x.tile = choose_tile(rows, x.n, inner, batch, bf16);
+    x.chunk = 0;
+    x.splits = inner > 0 && !x.rows_kernel ? choose_split(rows, x.n, inner, batch, &x.tile, bf16, &x.chunk) : 1;
+    x.partial = x.splits > 1 ? split_bytes(rows, x.n, batch, x.splits) : 0;
+    if (x.rows_kernel) x.partial = ((size_t)x.n * ((inner + 7) / 8 * 8) * 4 + 255) / 256 * 256;  // compact columns
+  }
+  return count;
+}
+
 }  // namespace
 
 extern "C" {
@@ -484,10 +646,10 @@ size_t qutai_amd_gemm_workspace_size(int64_t rows, int64_t inner, int64_t cols, 
   // 256-byte aligned pointers: only dtype and row alignment decide
   plan(rows, inner, cols, batch, left_stride, right_stride, transpose_left, transpose_right, a_dtype, b_dtype, bf16,
        (const void*)256, (const void*)256, &pa, &pb);
-  int64_t chunk = 0;
-  Tile tile = choose_tile(rows, cols, inner, batch, bf16);
-  const int splits = choose_split(rows, cols, inner, batch, &tile, bf16, &chunk);
-  const size_t partial = splits > 1 ? split_bytes(rows, cols, batch, splits) : 0;
+  Window w[2];
+  const int count = plan_windows(rows, inner, cols, batch, bf16, transpose_left, w);
+  size_t partial = 0;
+  for (int i = 0; i < count; i++) partial += w[i].partial;
   if (!pa.copy && !pb.copy && !partial) return 0;
   return (pa.copy ? pa.bytes : 0) + (pb.copy ? pb.bytes : 0) + partial + 256;
 }
@@ -520,11 +682,11 @@ int qutai_amd_gemm(const void* a, const void* b, void* out, int64_t rows, int64_
   Operand pa, pb;
   plan(rows, inner, cols, batch, left_stride, right_stride, transpose_left, transpose_right, a_dtype, b_dtype, bf16,
        a, b, &pa, &pb);
-  Tile tile = choose_tile(rows, cols, inner, batch, bf16);
-  int64_t chunk = 0;
-  const int splits = inner > 0 ? choose_split(rows, cols, inner, batch, &tile, bf16, &chunk) : 1;
-  const size_t partial = splits > 1 ? split_bytes(rows, cols, batch, splits) : 0;
-  float* part = nullptr;
+  Window w[2];
+  const int count = plan_windows(rows, inner, cols, batch, bf16, transpose_left, w);
+  size_t partial = 0;
+  for (int i = 0; i < count; i++) partial += w[i].partial;
+  char* part = nullptr;
   if (inner > 0 && ((pa.copy && !prepare_fits(pa)) || (pb.copy && !prepare_fits(pb)))) return QA_EINVAL;
   if (inner > 0 && (pa.copy || pb.copy || partial)) {
     size_t need = (pa.copy ? pa.bytes : 0) + (pb.copy ? pb.bytes : 0) + partial + 256;
@@ -538,7 +700,7 @@ int qutai_amd_gemm(const void* a, const void* b, void* out, int64_t rows, int64_
       launch_prepare(pb, b_dtype, bf16, ws, stream);
       ws += pb.bytes;
     }
-    if (partial) part = (float*)ws;
+    if (partial) part = ws;
   }
   GemmArgs p = {};
   p.a = pa.ptr;
@@ -561,27 +723,78 @@ int qutai_amd_gemm(const void* a, const void* b, void* out, int64_t rows, int64_
   // buffer descriptors address at most 2^31 bytes per K step
   int64_t es = bf16 ? 2 : 4;
   if ((p.lda * 256 * es) >= (1ll << 31) || (p.ldb * 256 * es) >= (1ll << 31)) return QA_EINVAL;
-  if (part) {
-    // fp32 partials of each K chunk, then the ordered sum into `out`
-    p.out = part;
-    p.k_split = splits;
-    p.k_chunk = chunk;
-    p.batch = batch * splits;
-    p.accumulate = 0;
-    p.out_bf16 = 0;
-    p.vec_c = vec_out(part, p.ldc, p.sc);
+  const int osize = out_dtype == QA_BF16 ? 2 : 4;
+  for (int i = 0; i < count; i++) {
+    const Window& x = w[i];
+    GemmArgs q = p;
+    // the window's columns: B's rows (K-major) or columns from c0, out's
+    // columns from c0 at the full row pitch
+    q.N = x.n;
+    q.b = (const char*)pb.ptr + x.c0 * (transpose_right ? pb.ld : 1) * es;
+    char* window_out = (char*)out + x.c0 * osize;
+    q.out = window_out;
+    q.vec_c = vec_out(window_out, q.ldc, q.sc);
+    float* window_part = nullptr;
+    if (x.partial && !x.rows_kernel) {
+      // fp32 partials of each K chunk ([rows][n] each), then the ordered sum
+      window_part = (float*)part;
+      part += x.partial;
+      q.out = window_part;
+      q.ldc = x.n;
+      q.sc = rows * x.n;
+      q.k_split = x.splits;
+      q.k_chunk = x.chunk;
+      q.batch = batch * x.splits;
+      q.accumulate = 0;
+      q.out_bf16 = 0;
+      q.vec_c = vec_out(window_part, q.ldc, q.sc);
+    }
+    if (x.rows_kernel) {
+      // B's columns into the compact block (the window's workspace), then rows
+      float* cols_ws = (float*)part;
+      part += x.partial;
+      const int64_t pitch = (inner + 7) / 8 * 8;
+      const unsigned gblocks = (unsigned)((x.n * pitch + 255) / 256);
+      if (bf16 && transpose_right)
+        hipLaunchKernelGGL((gather_columns<true, true>), dim3(gblocks), dim3(256), 0, stream, q.b, cols_ws, inner,
+                           q.ldb, (int)x.n, pitch);
+      else if (bf16)
+        hipLaunchKernelGGL((gather_columns<true, false>), dim3(gblocks), dim3(256), 0, stream, q.b, cols_ws, inner,
+                           q.ldb, (int)x.n, pitch);
+      else if (transpose_right)
+        hipLaunchKernelGGL((gather_columns<false, true>), dim3(gblocks), dim3(256), 0, stream, q.b, cols_ws, inner,
+                           q.ldb, (int)x.n, pitch);
+      else
+        hipLaunchKernelGGL((gather_columns<false, false>), dim3(gblocks), dim3(256), 0, stream, q.b, cols_ws, inner,
+                           q.ldb, (int)x.n, pitch);
+      const unsigned blocks = (unsigned)((rows + RWAVES * RROWS - 1) / (RWAVES * RROWS));
+      const int bf = out_dtype == QA_BF16 ? 1 : 0, acc = accumulate ? 1 : 0;
+      if (bf16)
+        hipLaunchKernelGGL((remainder_columns<true>), dim3(blocks), dim3(64 * RWAVES), 0, stream, q.a, cols_ws,
+                           (void*)window_out, rows, inner, q.lda, pitch, q.ldc, (int)x.n, bf, acc);
+      else
+        hipLaunchKernelGGL((remainder_columns<false>), dim3(blocks), dim3(64 * RWAVES), 0, stream, q.a, cols_ws,
+                           (void*)window_out, rows, inner, q.lda, pitch, q.ldc, (int)x.n, bf, acc);
+      const hipError_t err = hipGetLastError();
+      if (err != hipSuccess) return (int)err;
+      continue;
+    }
+    if (!window_part && count == 1 && ((x.tile == TILE_S2 && forced_tile() < 0) || x.tile == TILE_R) &&
+        short_fits(q, bf16, transpose_left, transpose_right))
+      return (int)launch_short(q, stream);
+    hipError_t err = bf16 ? launch_mma<false>(x.tile, transpose_left, transpose_right, q, stream)
+                          : launch_mma<true>(x.tile, transpose_left, transpose_right, q, stream);
+    if (err != hipSuccess) return (int)err;
+    if (!window_part) continue;
+    const int64_t total = batch * rows * x.n;
+    const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 1 << 20);
+    hipLaunchKernelGGL(splitk_reduce, dim3(blocks), dim3(256), 0, stream, (const float*)window_part,
+                       (void*)window_out, rows * x.n, total, x.splits, accumulate ? 1 : 0,
+                       out_dtype == QA_BF16 ? 1 : 0, x.n, cols);
+    err = hipGetLastError();
+    if (err != hipSuccess) return (int)err;
   }
-  if (!part && ((tile == TILE_S2 && forced_tile() < 0) || tile == TILE_R) &&
-      short_fits(p, bf16, transpose_left, transpose_right))
-    return (int)launch_short(p, stream);
-  hipError_t err = bf16 ? launch_mma<false>(tile, transpose_left, transpose_right, p, stream)
-                        : launch_mma<true>(tile, transpose_left, transpose_right, p, stream);
-  if (err != hipSuccess || !part) return (int)err;
-  const int64_t total = batch * rows * cols;
-  const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 1 << 20);
-  hipLaunchKernelGGL(splitk_reduce, dim3(blocks), dim3(256), 0, stream, (const float*)part, out, rows * cols, total,
-                     splits, accumulate ? 1 : 0, out_dtype == QA_BF16 ? 1 : 0);
-  return (int)hipGetLastError();
+  return QA_OK;
 }
 
 int qutai_amd_gemm_grouped(const void* a, const void* b, void* out, const int64_t* offsets, int groups,

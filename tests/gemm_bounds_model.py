@@ -233,6 +233,63 @@ def plain_gemm(cfg: Config, f32: bool, m: int, k: int, n: int, batch: int, ta: b
                 output_stores(cfg, out_f32, z * m * n, tm * cfg.bm, tn * cfg.bn, m, n, n, out_alloc, vec)
 
 
+
+def window_gemm(cfg: Config, f32: bool, m: int, k: int, n: int, c0: int, width: int, ta: bool, tb: bool,
+                splits: int = 1, out_f32: bool = True):
+    """One column window [c0, c0 + width) of a plain product (the column
+    remainder's two launches, column_split / plan_windows): B from its c0-th
+    column (row when K-major), out from column c0 at the full pitch n; with
+    split K the fp32 partials are [m][width] each."""
+    pa = plan_operand(m if ta else k, k if ta else m, 1, m * k, f32)
+    pb = plan_operand(k if tb else n, n if tb else k, 1, k * n, f32)
+    ka, kb = not ta, tb
+    chunk = k
+    if splits > 1:
+        splits, chunk = split_chunk(k, splits)
+    b_shift = c0 * (pb.ld if kb else 1)
+    tiles_m, tiles_n = (m + cfg.bm - 1) // cfg.bm, (width + cfg.bn - 1) // cfg.bn
+    for s in range(splits):
+        k_lo = s * chunk
+        k_len = min(k, k_lo + chunk) - k_lo
+        a_base = k_lo * (1 if ka else pa.ld)
+        b_base = b_shift + k_lo * (1 if kb else pb.ld)
+        for tm in range(tiles_m):
+            for tn in range(tiles_n):
+                operand_loads(cfg, f32, ka, cfg.bm, a_base, tm * cfg.bm, m, k_len, pa.ld, pa.alloc, "A")
+                operand_loads(cfg, f32, kb, cfg.bn, b_base, tn * cfg.bn, width, k_len, pb.ld, pb.alloc, "B")
+                if splits > 1:
+                    vec = 2 if width % 8 == 0 else 1 if width % 4 == 0 else 0
+                    output_stores(cfg, True, s * m * width, tm * cfg.bm, tn * cfg.bn, m, width, width,
+                                  splits * m * width, vec, "partial")
+                else:
+                    vec = 2 if n % 8 == 0 else 1 if n % 4 == 0 else 0
+                    output_stores(cfg, out_f32, c0, tm * cfg.bm, tn * cfg.bn, m, width, n, m * n, vec)
+
+
+def remainder_rows(f32: bool, m: int, k: int, n: int, c0: int, width: int, tb: bool):
+    """gather_columns + remainder_columns (gemm.hip): the last `width` <= 8
+    columns of a plain product with a K-major A.  The gather reads B's
+    elements (k, c0 + j) for k < K, j < width into a [width][pitch] block
+    (pitch = K rounded up to 8); each wave row m < M reads A's row in 16-byte
+    chunks c * E < K and the block's matching values; out's (m, c0 + j) at
+    pitch n."""
+    e, es = (4, 4) if f32 else (8, 2)
+    pa = plan_operand(k, m, 1, m * k, f32)
+    pb = plan_operand(k if tb else n, n if tb else k, 1, k * n, f32)
+    pitch = (k + 7) // 8 * 8
+    kk = np.arange(k)[:, None]
+    j = np.arange(width)[None, :]
+    at = ((c0 + j) * pb.ld + kk) if tb else (kk * pb.ld + c0 + j)
+    _check("remainder B load", at.ravel() * es, at.ravel() * es + es, pb.alloc * es)
+    chunks = np.arange((k + e - 1) // e)
+    lo = ((np.arange(m)[:, None] * pa.ld + chunks[None, :] * e) * es).ravel()
+    _check("remainder A load", lo, lo + 16, pa.alloc * es)
+    lo = ((np.arange(width)[:, None] * pitch + chunks[None, :] * e) * 4).ravel()
+    _check("remainder column load", lo, lo + e * 4, width * pitch * 4)
+    at = (np.arange(m)[:, None] * n + c0 + j).ravel()
+    _check("remainder store", at * 4, at * 4 + 4, m * n * 4)
+
+
 def grouped_gemm(cfg: Config, f32: bool, counts: list[int], inner: int, cols: int, transpose_right: bool,
                  gather: np.ndarray | None = None, source_rows: int = 0):
     """qutai_amd_gemm_grouped (and the SwiGLU form with cfg = SWIGLU): group g

@@ -74,6 +74,30 @@ def test_split_k_chunks_stay_in_bounds(splits):
                     gm.plain_gemm(cfg, False, m, k, n, 1, ta, tb, splits=splits)
 
 
+
+def test_column_windows_stay_in_bounds():
+    """The two launches of a column remainder (N = 256 q + r, r <= 64): the
+    first 256 q columns on the large tiles, the last r on the thin tile with
+    and without split K, over odd row pitches and both transpose forms."""
+    rng = np.random.default_rng(SEED + 101)
+    for f32 in (False, True):
+        big = [c for c in gm.tile_configs(f32) if c.name in ("L8D2", "H", "S", "T", "U")]
+        thin = [c for c in gm.tile_configs(f32) if c.name == "N"]
+        for _ in range(3):
+            m = int(rng.integers(65, 700))
+            k = int(rng.integers(129, 1200))
+            q, r = int(rng.integers(2, 4)), int(rng.choice([1, 3, 8, int(rng.integers(9, 65))]))
+            n = 256 * q + r
+            for ta in (False, True):
+                for tb in (False, True):
+                    for cfg in big:
+                        gm.window_gemm(cfg, f32, m, k, n, 0, n - r, ta, tb)
+                    for cfg in thin:
+                        for splits in (1, 3, 6, 16):
+                            gm.window_gemm(cfg, f32, m, k, n, n - r, r, ta, tb, splits=splits)
+                    if not ta and r <= 8:
+                        gm.remainder_rows(f32, m, k, n, n - r, r, tb)
+
 def _counts(rng, groups, total):
     cuts = np.sort(rng.integers(0, total + 1, size=groups - 1))
     counts = np.diff(np.concatenate([[0], cuts, [total]])).tolist()
