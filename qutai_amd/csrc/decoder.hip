@@ -569,6 +569,35 @@ __global__ void __launch_bounds__(HEAD_THREADS) head_block_gradient_kernel(T* lo
   }
 }
 
+// The same with 16-byte chunks: one workgroup per selected row (the row
+// index arithmetic once per row), rows of whole chunks and aligned bases.
+// The backward add is the elementwise one (fp32 sum, one rounding).
+template <class T>
+__global__ void __launch_bounds__(256) head_rows_vec(const T* x, T* out, int64_t start, int64_t width, int64_t time,
+                                                     int backward) {
+  constexpr int V = 16 / (int)sizeof(T);
+  const int64_t i = blockIdx.x, row = start + i;
+  const int64_t at = (row / (time - 1)) * time + row % (time - 1);
+  const T* src = x + (backward ? i : at) * width;
+  T* dst = out + (backward ? at : i) * width;
+  for (int64_t c = (int64_t)threadIdx.x * V; c < width; c += 256 * V) {
+    if (!backward) {
+      *(uint4*)(dst + c) = *(const uint4*)(src + c);
+      continue;
+    }
+    float a[8], b[8];
+    load_chunk<T>(src + c, a);
+    load_chunk<T>(dst + c, b);
+#pragma unroll
+    for (int e = 0; e < V; e++) b[e] += a[e];
+    if constexpr (sizeof(T) == 2)
+      *(uint4*)(dst + c) = make_uint4(pack_bf16x2(b[0], b[1]), pack_bf16x2(b[2], b[3]), pack_bf16x2(b[4], b[5]),
+                                      pack_bf16x2(b[6], b[7]));
+    else
+      *(float4*)(dst + c) = make_float4(b[0], b[1], b[2], b[3]);
+  }
+}
+
 bool act_dtype(int d) { return d == F32 || d == BF16; }
 
 // rows of whole 256-column groups, at most 2048 wide, 16-byte aligned base
@@ -767,6 +796,16 @@ int qutai_amd_head_rows(const void* x, void* out, int64_t count, int64_t start, 
   const int64_t n = count * width;
   if (n == 0) return QA_OK;
   hipStream_t s = (hipStream_t)stream;
+  const int per = dtype == BF16 ? 8 : 4;
+  if (width % per == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)out % 16 == 0 && count <= 0x7fffffff) {
+    if (dtype == BF16)
+      hipLaunchKernelGGL(head_rows_vec<bf16_t>, dim3((unsigned)count), dim3(256), 0, s, (const bf16_t*)x,
+                         (bf16_t*)out, start, width, time, backward ? 1 : 0);
+    else
+      hipLaunchKernelGGL(head_rows_vec<float>, dim3((unsigned)count), dim3(256), 0, s, (const float*)x, (float*)out,
+                         start, width, time, backward ? 1 : 0);
+    return (int)hipGetLastError();
+  }
   if (dtype == BF16)
     hipLaunchKernelGGL(head_rows_kernel<bf16_t>, dim3(blocks_for(n)), dim3(256), 0, s, (const bf16_t*)x,
                        (bf16_t*)out, n, start, width, time, backward ? 1 : 0);

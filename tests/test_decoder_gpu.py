@@ -114,21 +114,23 @@ def test_rope_forward_inverse_and_offset(lm, dtype):
 
 
 @pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
-def test_head_rows_and_backward(lm, dtype):
-    batch, time, width = 3, 6, 8
+@pytest.mark.parametrize("width", [8, 13, 2048])  # 16-byte chunks per row (8, 2048) or elementwise (13)
+def test_head_rows_and_backward(lm, dtype, width):
+    batch, time = 3, 6
     h = normal(118, batch * time * width)
     rows = batch * (time - 1)
     got = download(lm.head_rows(upload(h, dtype), 4, 9, width, time))
     assert got.tobytes() == stored(np.array(ora.head_rows(stored(h, dtype).tolist(), 4, 9, width, time)),
                                    dtype).astype(np.float32).tobytes()
     g = normal(119, 9 * width)
-    from qutai_amd.backends import amd
-
-    target = amd.full(batch * time * width, 0.0, dtype=dtype)
+    start = normal(117, batch * time * width)
+    target = upload(start, dtype)
     lm.head_rows_backward(target, upload(g, dtype), 4, 9, width, time)
-    expected = [0.0] * (batch * time * width)
-    ora.head_rows_backward(expected, stored(g, dtype).tolist(), 4, 9, width, time)
-    assert np.array_equal(download(target), stored(np.array(expected), dtype))
+    added = [0.0] * (batch * time * width)
+    ora.head_rows_backward(added, stored(g, dtype).tolist(), 4, 9, width, time)
+    # one fp32 addition per element (zero where no row lands), then the storage rounding
+    sums = stored(start, dtype).astype(np.float32) + np.array(added, dtype=np.float32)
+    assert np.array_equal(download(target), stored(sums, dtype))
     assert rows == 15
 
 
