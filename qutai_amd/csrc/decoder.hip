@@ -55,6 +55,56 @@ __global__ void embedding_grad_kernel(const T* g, const int64_t* tokens, const i
   }
 }
 
+// The same two with 4 features per thread (16-byte table rows and fp32
+// gradient rows, 8-byte bf16 rows): one workgroup per token row / per
+// group, the index arithmetic once per row.  Same sums in the same order.
+template <class T>
+__global__ void __launch_bounds__(256) embedding_rows(const float* w, const int64_t* ids, T* out, int64_t width) {
+  const int64_t r = blockIdx.x;
+  const float* src = w + ids[r] * width;
+  T* dst = out + r * width;
+  for (int64_t c = (int64_t)threadIdx.x * 4; c < width; c += 1024) {
+    const float4 v = *(const float4*)(src + c);
+    if constexpr (sizeof(T) == 2)
+      *(uint2*)(dst + c) = make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
+    else
+      *(float4*)(dst + c) = v;
+  }
+}
+
+template <class T>
+__global__ void __launch_bounds__(256) embedding_grad_rows(const T* g, const int64_t* tokens, const int64_t* offsets,
+                                                           const int64_t* rows, float* out, int64_t width,
+                                                           int accumulate) {
+  const int64_t group = blockIdx.x, p0 = offsets[group], p1 = offsets[group + 1];
+  float* dst = out + tokens[group] * width;
+  for (int64_t c = (int64_t)threadIdx.x * 4; c < width; c += 1024) {
+    float t[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int64_t p = p0; p < p1; p++) {
+      const T* src = g + rows[p] * width + c;
+      float v[4];
+      if constexpr (sizeof(T) == 2) {
+        const uint2 raw = *(const uint2*)src;
+        v[0] = __uint_as_float(raw.x << 16);
+        v[1] = __uint_as_float(raw.x & 0xffff0000u);
+        v[2] = __uint_as_float(raw.y << 16);
+        v[3] = __uint_as_float(raw.y & 0xffff0000u);
+      } else {
+        const float4 x = *(const float4*)src;
+        v[0] = x.x, v[1] = x.y, v[2] = x.z, v[3] = x.w;
+      }
+#pragma unroll
+      for (int e = 0; e < 4; e++) t[e] += v[e];
+    }
+    float4 o = make_float4(t[0], t[1], t[2], t[3]);
+    if (accumulate) {
+      const float4 old = *(const float4*)(dst + c);
+      o = make_float4(old.x + t[0], old.y + t[1], old.z + t[2], old.w + t[3]);
+    }
+    *(float4*)(dst + c) = o;
+  }
+}
+
 // RMSNorm forward, one wave per row: inv = 1/sqrt(mean(x^2) + eps),
 // out = x * inv * w (fp32 out and inv, lm.cu:39-45)
 template <class T>
@@ -620,6 +670,15 @@ int qutai_amd_embedding(const float* weight, const int64_t* ids, void* out, int6
   const int64_t n = count * width;
   if (n == 0) return QA_OK;
   hipStream_t s = (hipStream_t)stream;
+  if (width % 4 == 0 && (uintptr_t)weight % 16 == 0 && (uintptr_t)out % 16 == 0 && count <= 0x7fffffff) {
+    if (out_dtype == BF16)
+      hipLaunchKernelGGL(embedding_rows<bf16_t>, dim3((unsigned)count), dim3(256), 0, s, weight, ids, (bf16_t*)out,
+                         width);
+    else
+      hipLaunchKernelGGL(embedding_rows<float>, dim3((unsigned)count), dim3(256), 0, s, weight, ids, (float*)out,
+                         width);
+    return (int)hipGetLastError();
+  }
   if (out_dtype == BF16)
     hipLaunchKernelGGL(embedding_kernel<bf16_t>, dim3(blocks_for(n)), dim3(256), 0, s, weight, ids, (bf16_t*)out, n,
                        width);
@@ -636,6 +695,15 @@ int qutai_amd_embedding_backward(const void* gradient, const int64_t* tokens, co
   const int64_t n = groups * width;
   if (n == 0) return QA_OK;
   hipStream_t s = (hipStream_t)stream;
+  if (width % 4 == 0 && (uintptr_t)gradient % 16 == 0 && (uintptr_t)out % 16 == 0 && groups <= 0x7fffffff) {
+    if (dtype == BF16)
+      hipLaunchKernelGGL(embedding_grad_rows<bf16_t>, dim3((unsigned)groups), dim3(256), 0, s,
+                         (const bf16_t*)gradient, tokens, offsets, rows, out, width, accumulate ? 1 : 0);
+    else
+      hipLaunchKernelGGL(embedding_grad_rows<float>, dim3((unsigned)groups), dim3(256), 0, s, (const float*)gradient,
+                         tokens, offsets, rows, out, width, accumulate ? 1 : 0);
+    return (int)hipGetLastError();
+  }
   if (dtype == BF16)
     hipLaunchKernelGGL(embedding_grad_kernel<bf16_t>, dim3(blocks_for(n)), dim3(256), 0, s, (const bf16_t*)gradient,
                        tokens, offsets, rows, out, n, width, accumulate ? 1 : 0);

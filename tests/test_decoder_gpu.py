@@ -34,8 +34,9 @@ def base():
 
 
 @pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
-def test_embedding_forward_and_backward(lm, dtype):
-    vocab, width = 37, 24
+@pytest.mark.parametrize("width", [24, 27, 2048])  # 4 features per thread (24, 2048) or elementwise (27)
+def test_embedding_forward_and_backward(lm, dtype, width):
+    vocab = 37
     table = normal(110, vocab * width)
     ids = [Random(1).randrange(vocab) for _ in range(200)]
     out = lm.embedding(upload(table, "float32"), ids, width, out_dtype=dtype)
@@ -46,6 +47,11 @@ def test_embedding_forward_and_backward(lm, dtype):
     assert grad.dtype == "float32"
     reference = ora.embedding_backward(stored(g, dtype).tolist(), ids, vocab, width)
     assert ora.rel_frobenius(download(grad), reference) <= FP32_TOL
+    # the sums go in place into an existing table gradient: old + row sums
+    start = normal(112, vocab * width)
+    into = upload(start, "float32")
+    assert lm.embedding_backward(upload(g, dtype), ids, vocab, width, out=into) is into
+    assert np.array_equal(download(into), start + download(grad))
     with pytest.raises(ValueError):
         lm.embedding(upload(table, "bfloat16"), ids, width)  # bf16 table: not the accumulation dtype
 
