@@ -354,7 +354,9 @@ class SparseMoE:
         def backward(g):
             dx, dw, dwg, dwu, dwd = b.moe_experts_backward(g, route, saved, self.width, self.hidden,
                                                            x_dtype=x.dtype, weight_dtype=weight_dtype)
-            return dx, dw, owned(dwg), owned(dwu), owned(dwd)
+            # every one is a storage this backward just made (dx: the routed
+            # rows summed back into token order)
+            return owned(dx), dw, owned(dwg), owned(dwu), owned(dwd)
 
         result = record(Tensor(values, shape=x.shape), (x, weights, self.w_gate, self.w_up, self.w_down), backward)
         return result, aux
