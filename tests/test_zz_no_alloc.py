@@ -54,6 +54,10 @@ CASES = {
     # aligned bf16 operands: used in place, no scratch
     "in_place": [dict(shape=(512, 768, 1024), dtype="bfloat16", transpose_right=True),
                  dict(shape=(128, 256, 64), dtype="bfloat16")],
+    # column remainders: the row kernel's compact B columns (4097 = 16 x 256 + 1)
+    # and the thin tile's K-chunk partials (8232 = 32 x 256 + 40) in the scratch
+    "columns": [dict(shape=(4095, 1000, 4097), dtype="bfloat16"),
+                dict(shape=(2048, 640, 8232), dtype="bfloat16")],
     # fp32 true-fp32 path with a split K
     "fp32_split": [dict(shape=(1024, 16384, 1024), dtype="float32"),
                    dict(shape=(256, 8192, 256), dtype="float32")],
