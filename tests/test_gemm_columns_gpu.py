@@ -81,3 +81,27 @@ def test_remainder_matches_oracle(amd, m, k, n, dtype):
     amd.gemm(left, right, m, k, n, out=out, accumulate=True)
     expected = start.reshape(m, n)[rows].astype(np.float64) + exact
     assert ora.rel_frobenius(download(out).reshape(m, n)[rows], expected) <= FP32_TOL
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, True)])
+def test_remainder_mixed_inputs_autocast_and_bf16_accumulate(amd, ta, tb):
+    """The remainder windows with fp32 A and bf16 B (mixed inputs take the bf16
+    path: A is narrowed, B re-laid out first), the transpose forms the two
+    remainder kernels take (row kernel for K-major A, thin tile otherwise),
+    and a bf16 output accumulated in place: old + product rounded once."""
+    m, k, n = 4095, 1000, 4097
+    a, b = normal(90, m * k, k ** -0.5), normal(91, k * n, k ** -0.5)
+    left, right = upload(a, "float32"), upload(b, "bfloat16")
+    sa, sb = stored(a, "bfloat16"), stored(b, "bfloat16")  # the bf16 path rounds A once
+    rows = sorted({0, 17, m // 3, m - 1, *np.random.default_rng(10).choice(m, 8, replace=False).tolist()})
+    exact = ora.gemm_f64(sa, sb, m, k, n, transpose_left=ta, transpose_right=tb, row_list=rows)
+    got = download(amd.gemm(left, right, m, k, n, transpose_left=ta, transpose_right=tb)).reshape(m, n)
+    assert ora.rel_frobenius(got[rows], exact) <= FP32_TOL
+    assert ora.rel_frobenius(got[rows][:, n - 1:], exact[:, n - 1:]) <= FP32_TOL
+    start = normal(92, m * n)
+    out = upload(start, "bfloat16")
+    amd.gemm(left, right, m, k, n, out=out, accumulate=True, out_dtype="bfloat16", transpose_left=ta,
+             transpose_right=tb)
+    fp32 = got.astype(np.float32)
+    want = stored(stored(start, "bfloat16").reshape(m, n).astype(np.float32) + fp32, "bfloat16")
+    assert np.array_equal(download(out).reshape(m, n), want)
