@@ -485,6 +485,15 @@ int qutai_amd_embedding_backward(const void* gradient, const int64_t* tokens, co
 int qutai_amd_rms_norm(const void* x, const float* weight, float* out, float* inverse, int64_t rows, int64_t width,
                        double eps, int dtype, void* stream);
 
+/* qutai_amd_rms_norm that also stores out rounded to bf16 (RNE, the cast
+ * kernel's rounding) into out_bf16 when it is not null: the copy the
+ * bf16-path products of the normalised activation take under autocast
+ * (the reference rounds the fp32 norm output when its Linear runs in bf16,
+ * lm/layers.py:20-28 with 88-96), written by the norm instead of a separate
+ * cast pass.  Same fp32 outputs as qutai_amd_rms_norm. */
+int qutai_amd_rms_norm_bf16(const void* x, const float* weight, float* out, void* out_bf16, float* inverse,
+                            int64_t rows, int64_t width, double eps, int dtype, void* stream);
+
 /* Floats of the `partial` workspace qutai_amd_rms_norm_backward needs. */
 int64_t qutai_amd_rms_norm_workspace(int64_t rows, int64_t width);
 

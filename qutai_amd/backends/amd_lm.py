@@ -565,17 +565,20 @@ class EmbeddingRowSums(DeferredGradient):
         embedding_backward(self.gradient, self.ids, self.count, self.width, index=self.index, out=storage)
 
 
-def rms_norm(values, weight, width, eps):
-    """(out, inverse) of RMSNorm over rows of width (cuda_lm.py:126-145); both fp32."""
+def rms_norm(values, weight, width, eps, *, bf16_copy=False):
+    """(out, inverse) of RMSNorm over rows of width (cuda_lm.py:126-145); both
+    fp32.  With ``bf16_copy`` also out rounded to bf16 (the copy the bf16
+    path's products take), written by the same kernel: (out, inverse, copy)."""
     acc = _acc_dtype(values.dtype)
     if weight.dtype != acc or weight.size != width:
         raise ValueError("rms_norm needs an fp32 weight of width values")
     rows = values.size // width
     out, inverse = AMDStorage(values.size, acc), AMDStorage(rows, acc)
+    copy = AMDStorage(values.size, "bfloat16") if bf16_copy else None
     if rows:
-        out.runtime.call("qutai_amd_rms_norm", values.ptr, weight.ptr, out.ptr, inverse.ptr, rows, width, float(eps),
-                         code(values.dtype))
-    return out, inverse
+        out.runtime.call("qutai_amd_rms_norm_bf16", values.ptr, weight.ptr, out.ptr, None if copy is None else copy.ptr,
+                         inverse.ptr, rows, width, float(eps), code(values.dtype))
+    return (out, inverse, copy) if bf16_copy else (out, inverse)
 
 
 def rms_norm_backward(gradient, values, weight, inverse, width, residual=None):

@@ -70,6 +70,7 @@ SIGNATURES = {
     "qutai_amd_embedding": [_p, _p, _p, _i64, _i64, _i32, _p],
     "qutai_amd_embedding_backward": [_p, _p, _p, _p, _p, _i64, _i64, _i32, _i32, _p],
     "qutai_amd_rms_norm": [_p, _p, _p, _p, _i64, _i64, _f64, _i32, _p],
+    "qutai_amd_rms_norm_bf16": [_p, _p, _p, _p, _p, _i64, _i64, _f64, _i32, _p],
     "qutai_amd_rms_norm_workspace": [_i64, _i64],
     "qutai_amd_rms_norm_backward": [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p],
     "qutai_amd_silu": [_p, _p, _p, _i64, _i32, _i32, _p],

@@ -109,7 +109,7 @@ __global__ void __launch_bounds__(256) embedding_grad_rows(const T* g, const int
 // out = x * inv * w (fp32 out and inv, lm.cu:39-45)
 template <class T>
 __global__ void __launch_bounds__(256) rms_kernel(const T* x, const float* w, float* out, float* inv, int64_t rows,
-                                                  int64_t width, float eps) {
+                                                  int64_t width, float eps, bf16_t* out16) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
   if (row >= rows) return;
@@ -121,7 +121,11 @@ __global__ void __launch_bounds__(256) rms_kernel(const T* x, const float* w, fl
   }
   const float scale = 1.f / sqrtf(wave_sum(total) / (float)width + eps);
   if (lane == 0) inv[row] = scale;
-  for (int64_t j = lane; j < width; j += 64) out[row * width + j] = get<T>(xr, j) * scale * w[j];
+  for (int64_t j = lane; j < width; j += 64) {
+    const float y = get<T>(xr, j) * scale * w[j];
+    out[row * width + j] = y;
+    if (out16) out16[row * width + j] = f32_to_bf16(y);
+  }
 }
 
 // dx = inv * (g w - x inv^2 mean(g w x)), one wave per row (lm.cu:46-51)
@@ -192,7 +196,7 @@ __device__ __forceinline__ void store_cols(T* row, int lane, const f32x4 (&v)[NI
 
 template <class T, int NI>
 __global__ void __launch_bounds__(256) rms_cols_kernel(const T* x, const float* w, float* out, float* inv,
-                                                       int64_t rows, float eps) {
+                                                       int64_t rows, float eps, bf16_t* out16) {
   constexpr int W = 256 * NI;
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
@@ -208,6 +212,8 @@ __global__ void __launch_bounds__(256) rms_cols_kernel(const T* x, const float* 
 #pragma unroll
   for (int i = 0; i < NI; i++) v[i] = v[i] * scale * wv[i];
   store_cols<float, NI>(out + row * W, lane, v);
+  // the bf16 copy of the bf16-path products (the cast kernel's rounding)
+  if (out16) store_cols<bf16_t, NI>(out16 + row * W, lane, v);
 }
 
 // Backward in one pass over g and x: a workgroup takes RCB rows (wave k the
@@ -715,19 +721,26 @@ int qutai_amd_embedding_backward(const void* gradient, const int64_t* tokens, co
 
 int qutai_amd_rms_norm(const void* x, const float* weight, float* out, float* inverse, int64_t rows, int64_t width,
                        double eps, int dtype, void* stream) {
+  return qutai_amd_rms_norm_bf16(x, weight, out, nullptr, inverse, rows, width, eps, dtype, stream);
+}
+
+int qutai_amd_rms_norm_bf16(const void* x, const float* weight, float* out, void* out_bf16, float* inverse,
+                            int64_t rows, int64_t width, double eps, int dtype, void* stream) {
   if (rows < 0 || width <= 0 || !act_dtype(dtype)) return QA_EINVAL;
   if (rows == 0) return QA_OK;
   const unsigned blocks = (unsigned)((rows + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK);
   hipStream_t s = (hipStream_t)stream;
-  if (cols_path(x, width) && cols_path(weight, width) && cols_path(out, width)) {
+  bf16_t* out16 = (bf16_t*)out_bf16;
+  if (cols_path(x, width) && cols_path(weight, width) && cols_path(out, width) &&
+      (!out16 || (uintptr_t)out16 % 8 == 0)) {
     const bool bf = dtype == BF16;
     switch (width / 256) {
 #define QA_RMS(N)                                                                                                   \
   case N:                                                                                                           \
     if (bf) hipLaunchKernelGGL((rms_cols_kernel<bf16_t, N>), dim3(blocks), dim3(256), 0, s, (const bf16_t*)x, weight, \
-                               out, inverse, rows, (float)eps);                                                     \
+                               out, inverse, rows, (float)eps, out16);                                              \
     else hipLaunchKernelGGL((rms_cols_kernel<float, N>), dim3(blocks), dim3(256), 0, s, (const float*)x, weight, out,   \
-                            inverse, rows, (float)eps);                                                             \
+                            inverse, rows, (float)eps, out16);                                                      \
     break;
       QA_RMS(1) QA_RMS(2) QA_RMS(3) QA_RMS(4) QA_RMS(5) QA_RMS(6) QA_RMS(7) QA_RMS(8)
 #undef QA_RMS
@@ -736,10 +749,10 @@ int qutai_amd_rms_norm(const void* x, const float* weight, float* out, float* in
   }
   if (dtype == BF16)
     hipLaunchKernelGGL(rms_kernel<bf16_t>, dim3(blocks), dim3(256), 0, s, (const bf16_t*)x, weight, out, inverse,
-                       rows, width, (float)eps);
+                       rows, width, (float)eps, out16);
   else
     hipLaunchKernelGGL(rms_kernel<float>, dim3(blocks), dim3(256), 0, s, (const float*)x, weight, out, inverse, rows,
-                       width, (float)eps);
+                       width, (float)eps, out16);
   return (int)hipGetLastError();
 }
 

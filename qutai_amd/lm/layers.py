@@ -148,10 +148,17 @@ def embed(ids, weight, shape):
 
 
 def rms_norm(x, weight, eps):
-    """RMSNorm over the last axis, fp32 output (src/qutai/lm/layers.py:88-96)."""
+    """RMSNorm over the last axis, fp32 output (src/qutai/lm/layers.py:88-96).
+    Under autocast the following projections round this output to bf16: the
+    norm kernel writes that copy too and it becomes the output's cached bf16
+    input (_bf16_input), in place of a separate cast pass."""
     b = backend(x)
     width = x.shape[-1]
-    out, inverse = b.rms_norm(x.storage, weight.storage, width, eps)
+    copy = None
+    if matmul_precision() == "bfloat16":
+        out, inverse, copy = b.rms_norm(x.storage, weight.storage, width, eps, bf16_copy=True)
+    else:
+        out, inverse = b.rms_norm(x.storage, weight.storage, width, eps)
 
     def backward(g):
         if x.dtype == "float32" and x.requires_grad:
@@ -160,7 +167,10 @@ def rms_norm(x, weight, eps):
         dx, dweight = b.rms_norm_backward(g, x.storage, weight.storage, inverse, width)
         return dx, owned(dweight)
 
-    return record(Tensor(out, shape=x.shape), (x, weight), backward)
+    result = record(Tensor(out, shape=x.shape), (x, weight), backward)
+    if copy is not None:
+        result._bf16_input = (out, copy)
+    return result
 
 
 class NormBackward:

@@ -58,7 +58,7 @@ def test_embedding_forward_and_backward(lm, dtype, width):
 
 @pytest.mark.parametrize("dtype,rows,width", [("float32", 37, 40), ("bfloat16", 300, 2048), ("float32", 4096, 2048),
                                                ("bfloat16", 65, 768), ("float32", 129, 256), ("float32", 70, 2304)])
-def test_rms_norm_forward_and_backward(lm, dtype, rows, width):
+def test_rms_norm_forward_and_backward(lm, base, dtype, rows, width):
     eps = 1e-5
     x = normal(112, rows * width, 2.0)
     w = (1 + 0.1 * normal(113, width)).astype(np.float32)
@@ -72,6 +72,13 @@ def test_rms_norm_forward_and_backward(lm, dtype, rows, width):
     ref_out, ref_inv = ora.rms_norm(sub_x, ws, width, eps)
     assert ora.rel_frobenius(download(out).reshape(rows, width)[sample], np.array(ref_out).reshape(-1, width)) <= FP32_TOL
     assert ora.rel_frobenius(download(inv)[sample], ref_inv) <= FP32_TOL
+    # the bf16 companion output: same fp32 results, and the copy is the cast
+    # kernel's rounding of them bit for bit
+    out2, inv2, copy = lm.rms_norm(upload(x, dtype), upload(w, "float32"), width, eps, bf16_copy=True)
+    assert np.array_equal(download(out2), download(out)) and np.array_equal(download(inv2), download(inv))
+    assert copy.dtype == "bfloat16"
+    assert np.array_equal(np.frombuffer(copy.to_array(), np.uint16),
+                          np.frombuffer(base.from_storage(out, dtype="bfloat16").to_array(), np.uint16))
     dx, dw = lm.rms_norm_backward(upload(g, "float32"), upload(x, dtype), upload(w, "float32"), inv, width)
     assert (dx.dtype, dw.dtype) == (dtype, "float32")
     gs = g.astype(np.float64).reshape(rows, width)
