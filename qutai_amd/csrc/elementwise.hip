@@ -213,7 +213,16 @@ __global__ void __launch_bounds__(THREADS) row_sum_kernel(const T* __restrict__ 
   const int64_t lo = part * span, hi = lo + span < width ? lo + span : width;
   const T* p = x + row * width;
   R s = R(0);
-  for (int64_t c = lo + lane; c < hi; c += 64) s += widen(p[c]);
+  // eight loads in flight, added in the same order as one at a time
+  int64_t c = lo + lane;
+  for (; c + 7 * 64 < hi; c += 8 * 64) {
+    T v[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) v[u] = p[c + u * 64];
+#pragma unroll
+    for (int u = 0; u < 8; u++) s += widen(v[u]);
+  }
+  for (; c < hi; c += 64) s += widen(p[c]);
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
   if (lane == 0) {
