@@ -277,8 +277,18 @@ __global__ void __launch_bounds__(256) rms_dw_final_parts(const float* partial, 
   const int64_t j = (int64_t)blockIdx.x * 16 + col;
   const int64_t per = (chunks + 15) / 16, c0 = k * per, c1 = min(chunks, c0 + per);
   float total = 0.f;
-  if (j < width)
-    for (int64_t c = c0; c < c1; c++) total += partial[c * width + j];
+  if (j < width) {
+    // eight loads in flight, added in chunk order
+    int64_t c = c0;
+    for (; c + 7 < c1; c += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) v[u] = partial[(c + u) * width + j];
+#pragma unroll
+      for (int u = 0; u < 8; u++) total += v[u];
+    }
+    for (; c < c1; c++) total += partial[c * width + j];
+  }
   part[k][col] = total;
   __syncthreads();
   if (k == 0 && j < width) {
