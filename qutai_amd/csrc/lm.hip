@@ -438,7 +438,8 @@ template <class T, class U>
 __global__ void __launch_bounds__(256) combine_rows_wave(const T* eo, const float* w, const int64_t* idx,
                                                          const int64_t* loc, const int64_t* off, U* y, int64_t rows,
                                                          int64_t width, int64_t top_k) {
-  constexpr int V = 16 / sizeof(T), R = 4;
+  // fp32 rows hold half the values per 16-byte chunk: twice the chunks in flight
+  constexpr int V = 16 / sizeof(T), R = sizeof(T) == 4 ? 8 : 4;
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
