@@ -7,6 +7,7 @@
 #include <string>
 
 #include "gemm_kernel.h"
+#include "gemm_pingpong.h"
 #include "gemm_short.h"
 
 #include <algorithm>
@@ -18,6 +19,12 @@ namespace {
 
 template <class Kern>
 __global__ void __launch_bounds__(Kern::NT) gemm_entry(GemmArgs p) {
+  __shared__ __attribute__((aligned(16))) char smem[Kern::LDS_BYTES];
+  Kern::run(p, smem);
+}
+
+template <class Kern>
+__global__ void __launch_bounds__(Kern::NT) pingpong_entry(GemmArgs p) {
   __shared__ __attribute__((aligned(16))) char smem[Kern::LDS_BYTES];
   Kern::run(p, smem);
 }
@@ -244,7 +251,8 @@ __global__ void __launch_bounds__(64 * RWAVES) remainder_columns(const void* a, 
 //   R   : short-K row strips (gemm_short.h): bf16 NT with K <= 64, a 128-row
 //         block of A held in registers, 128-column chunks of B through a
 //         three-slot LDS ring, stores straight from the accumulators
-enum Tile { TILE_L8D2, TILE_L8R, TILE_L4D2, TILE_S, TILE_N, TILE_W, TILE_H, TILE_T, TILE_U, TILE_S2, TILE_R, TILE_COUNT };
+enum Tile { TILE_L8D2, TILE_L8R, TILE_L4D2, TILE_S, TILE_N, TILE_W, TILE_H, TILE_T, TILE_U, TILE_S2, TILE_R, TILE_P,
+            TILE_COUNT };
 
 template <bool F32, bool TA, bool TB, int BM, int BN, int WM, int WN, int BK, int ST, bool DMA, bool SWIGLU = false>
 hipError_t launch_cfg(GemmArgs p, hipStream_t stream) {
@@ -258,11 +266,36 @@ hipError_t launch_cfg(GemmArgs p, hipStream_t stream) {
   return hipGetLastError();
 }
 
+int forced_tile();
+
+// Tile P: the ping-pong kernel (gemm_pingpong.h) for plain bf16 products
+// with K a multiple of 64; other calls take L8D2, whose results it matches
+// bit for bit.  Unforced, a 256x256 choice in the NN, NT and TT forms runs
+// it (1-3% faster on 4096^3 and 8192-class shapes; TN is equal or 1% slower
+// and keeps GemmKernel).
+bool pingpong_fits(const GemmArgs& p) {
+  return p.K > 0 && p.K % 64 == 0 && p.groups == 0 && p.k_split <= 1 && p.k_head == 0 && !p.group_k;
+}
+template <bool TA, bool TB>
+hipError_t launch_pingpong(GemmArgs p, hipStream_t stream) {
+  typedef PingPong<TA, TB> Kern;
+  p.tiles_m = (int)((p.M + 255) / 256);
+  const int64_t blocks = (int64_t)p.tiles_m * ((p.N + 255) / 256) * p.batch;
+  if (blocks <= 0) return hipSuccess;
+  if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(pingpong_entry<Kern>, dim3((unsigned)blocks), dim3(Kern::NT), 0, stream, p);
+  return hipGetLastError();
+}
+
 template <bool F32, bool TA, bool TB>
 hipError_t launch_tile(Tile tile, GemmArgs p, hipStream_t stream) {
   constexpr int KB = F32 ? 16 : 32;  // K per stage of the four-stage rings
   constexpr int KR = F32 ? 32 : 64;  // K per stage of the two-stage rings
   switch (tile) {
+    case TILE_P:
+      if constexpr (!F32)
+        if (pingpong_fits(p)) return launch_pingpong<TA, TB>(p, stream);
+      return launch_cfg<F32, TA, TB, 256, 256, 2, 4, KR, 2, true>(p, stream);
     case TILE_L8R: return launch_cfg<F32, TA, TB, 256, 256, 2, 4, KR, 2, false>(p, stream);
     case TILE_L4D2: return launch_cfg<F32, TA, TB, 256, 256, 2, 2, KR, 2, true>(p, stream);
     case TILE_S: return launch_cfg<F32, TA, TB, 128, 128, 2, 2, KB, 4, true>(p, stream);
@@ -276,7 +309,11 @@ hipError_t launch_tile(Tile tile, GemmArgs p, hipStream_t stream) {
     case TILE_U:
       if constexpr (F32) return launch_cfg<F32, TA, TB, 256, 256, 2, 4, KR, 2, true>(p, stream);
       else return launch_cfg<F32, TA, TB, 256, 192, 4, 2, KR, 2, true>(p, stream);
-    default: return launch_cfg<F32, TA, TB, 256, 256, 2, 4, KR, 2, true>(p, stream);
+    default:
+      // the ping-pong kernel where it measured faster (bit-identical results)
+      if constexpr (!F32 && !(TA && !TB))
+        if (forced_tile() < 0 && pingpong_fits(p)) return launch_pingpong<TA, TB>(p, stream);
+      return launch_cfg<F32, TA, TB, 256, 256, 2, 4, KR, 2, true>(p, stream);
   }
 }
 
@@ -307,7 +344,7 @@ int forced_tile() {
   static int forced = [] {
     const char* v = getenv("QUTAI_AMD_GEMM_TILE");
     if (!v) return -1;
-    const char* names[TILE_COUNT] = {"L8D2", "L8R", "L4D2", "S", "N", "W", "H", "T", "U", "S2", "R"};
+    const char* names[TILE_COUNT] = {"L8D2", "L8R", "L4D2", "S", "N", "W", "H", "T", "U", "S2", "R", "P"};
     for (int i = 0; i < TILE_COUNT; i++)
       if (std::string(v) == names[i]) return i;
     return -1;

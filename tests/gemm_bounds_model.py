@@ -405,3 +405,95 @@ def short_strip(m: int, k: int, n: int, batch: int, strip: int):
                                 hit = off + 16 <= orange
                                 lo = obase + off[hit]
                                 _check("C store (strip)", lo, lo + 16, batch * m * n * 2)
+
+
+# ---- ping-pong kernel (gemm_pingpong.h) ------------------------------------------------
+
+PINGPONG = Config("P", 256, 256, 2, 4, 64, 2)
+
+
+def _pingpong_lane(kmajor: bool, ld: int, w4: int, parity: int) -> np.ndarray:
+    """PingPong::kmajor_lane / mnmajor_lane: byte offset of each lane of copy
+    instruction j (parity j % 2) of wave w4 from the instruction's base."""
+    lane = np.arange(64)
+    if kmajor:
+        row = 8 * w4 + (lane >> 3)
+        c = (lane & 7) ^ (((lane >> 3) ^ (4 * parity + w4)) & 7)
+    else:
+        row = 2 * w4 + (lane >> 5)
+        c = (lane & 31) ^ ((row & 3) * 4)
+    return (row * ld + c * 8) * 2
+
+
+def pingpong_operand(kmajor: bool, base_elem: int, o0: int, ext: int, k: int, ld: int, alloc: int, what: str,
+                     range_rule: str = "end"):
+    """Every copy of one operand over one tile's K loop in the ping-pong
+    kernel: instruction j of wave w4 at step kt has descriptor base
+    tile + kk + j * step (elements; step = 32 rows K-major, 8 k-rows
+    MN-major) and range = bytes from the step's first element to the
+    end of the operand's last chunk (range_rule "end", the kernel's: K-major
+    rows end at K, a multiple of 64; MN-major rows at the extent rounded up to
+    8, which the host's zero-padded re-layout guarantees), minus j * step,
+    clamped to [0, RANGE_CAP].  Checks (1) every lane that reads memory
+    reads inside the allocation, (2) every chunk of the matrix (row < ext,
+    k < K) is read, not zeroed, and lands at the LDS position whose
+    OperandTile coordinates are its own, and (3) the 32 instructions of a
+    step fill each 16-byte chunk of the 32 KiB slot exactly once.
+    range_rule "tile" (a planted mistake for the tests) spans the tile's
+    256 rows instead of ending at the operand; "exact" ends MN-major rows at
+    the extent itself, which cuts the last chunk of a ragged extent."""
+    es = 2
+    if k % 64 or k <= 0:
+        raise ValueError("the ping-pong kernel needs K a positive multiple of 64")
+    end = (ext - o0 - 1) * ld + k if kmajor else (k - 1) * ld + (ext + 7) // 8 * 8 - o0
+    step_elems = 32 * ld if kmajor else 8 * ld
+    tile = base_elem + (o0 * ld if kmajor else o0)
+    lane = np.arange(64)
+    for kt in range(k // 64):
+        k0 = kt * 64
+        kk = k0 if kmajor else k0 * ld
+        if range_rule == "end":
+            r0 = min(max((end - kk) * es, 0), RANGE_CAP)
+        elif range_rule == "exact":
+            r0 = min(max(((ext - o0 - 1) * ld + k if kmajor else (k - 1) * ld + ext - o0) - kk, 0) * es, RANGE_CAP)
+        else:
+            r0 = min((256 * ld if kmajor else 64 * ld) * es, RANGE_CAP)
+        filled = np.zeros(256 * 64 // 8, dtype=np.int64)
+        for w4 in range(4):
+            for j in range(8):
+                off = _pingpong_lane(kmajor, ld, w4, j & 1)
+                rng = max(r0 - j * step_elems * es, 0)
+                hit = off + 16 <= rng
+                lo = (tile + kk + j * step_elems) * es + off[hit]
+                _check(f"{what} copy", lo, lo + 16, alloc * es)
+                # the element each lane fetches and where it lands in LDS
+                q = (4 * j + w4) * 64 + lane
+                outer, c = chunk_coords(False, kmajor, 256, 64, q)
+                filled[q] += 1
+                if kmajor:
+                    src_outer, src_c = 32 * j + 8 * w4 + (lane >> 3), (off // es - (8 * w4 + (lane >> 3)) * ld) // 8
+                else:
+                    src_outer, src_c = 8 * j + 2 * w4 + (lane >> 5), (off // es - (2 * w4 + (lane >> 5)) * ld) // 8
+                if not (np.array_equal(src_outer, outer) and np.array_equal(src_c, c)):
+                    raise Violation(f"{what}: copy lands at the wrong LDS chunk")
+                row_ok = (o0 + outer < ext) if kmajor else (o0 + c * 8 < ext)
+                if np.any(row_ok & ~hit):
+                    raise Violation(f"{what}: a chunk of the matrix falls outside the copy descriptor")
+        if not np.all(filled == 1):
+            raise Violation(f"{what}: LDS slot not filled exactly once")
+
+
+def pingpong_gemm(m: int, k: int, n: int, batch: int, ta: bool, tb: bool, broadcast_a: bool = False,
+                  broadcast_b: bool = False, range_rule: str = "end", out_f32: bool = False):
+    """All copies and stores of one qutai_amd_gemm call on the ping-pong
+    kernel (bf16, K a multiple of 64, batched or broadcast operands)."""
+    pa = plan_operand(m if ta else k, k if ta else m, batch, 0 if broadcast_a else m * k, False)
+    pb = plan_operand(k if tb else n, n if tb else k, batch, 0 if broadcast_b else k * n, False)
+    tiles_m, tiles_n = (m + 255) // 256, (n + 255) // 256
+    vec = 2 if n % 8 == 0 else 1 if n % 4 == 0 else 0
+    for z in range(batch):
+        for tm in range(tiles_m):
+            for tn in range(tiles_n):
+                pingpong_operand(not ta, z * pa.batch_stride, tm * 256, m, k, pa.ld, pa.alloc, "A", range_rule)
+                pingpong_operand(tb, z * pb.batch_stride, tn * 256, n, k, pb.ld, pb.alloc, "B", range_rule)
+                output_stores(PINGPONG, out_f32, z * m * n, tm * 256, tn * 256, m, n, n, batch * m * n, vec)

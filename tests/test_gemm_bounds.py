@@ -168,3 +168,37 @@ def test_short_k_strips_stay_in_bounds():
         k = int(rng.integers(1, 65))
         n = 16 * int(rng.integers(1, 70))
         gm.short_strip(m, k, n, int(rng.integers(1, 3)), 4)
+
+
+def test_pingpong_copies_stay_in_bounds():
+    """The ping-pong kernel's copies (descriptor per instruction, range up to
+    the operand's end): ragged M and N in every transpose form, odd pitches
+    that force the re-layout, broadcast batches; each step fills its LDS
+    slot exactly once at OperandTile's coordinates."""
+    rng = np.random.default_rng(SEED + 99)
+    shapes = [(257, 64, 129), (300, 128, 31), (1, 64, 1), (520, 192, 300)]
+    shapes += [(int(rng.integers(1, 600)), 64 * int(rng.integers(1, 5)), int(rng.integers(1, 600))) for _ in range(3)]
+    for m, k, n in shapes:
+        for ta in (False, True):
+            for tb in (False, True):
+                gm.pingpong_gemm(m, k, n, 1, ta, tb)
+    gm.pingpong_gemm(130, 128, 70, 3, False, True, broadcast_a=True)
+    gm.pingpong_gemm(70, 64, 130, 2, True, False, broadcast_b=True)
+
+
+def test_model_reports_a_pingpong_range_past_the_operand():
+    """A planted mistake: copy descriptors that span the tile's 256 rows
+    instead of ending at the operand read past the allocation in a ragged
+    last tile."""
+    gm.pingpong_gemm(300, 64, 40, 1, False, True)
+    with pytest.raises(gm.Violation):
+        gm.pingpong_gemm(300, 64, 40, 1, False, True, range_rule="tile")
+
+
+def test_model_reports_a_cut_last_chunk():
+    """A planted mistake: an MN-major range that ends at the extent (129
+    columns, re-laid out to a pitch of 136) cuts the chunk of columns
+    128-135 in the last k-row, so column 128 would read zero."""
+    gm.pingpong_gemm(64, 64, 129, 1, False, False)
+    with pytest.raises(gm.Violation):
+        gm.pingpong_gemm(64, 64, 129, 1, False, False, range_rule="exact")

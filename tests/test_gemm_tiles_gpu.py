@@ -1,6 +1,7 @@
 """Every bf16 GEMM tile shape (256x256, 192x256, 256x192, 256x128, 128x128 with
-a four- or two-stage ring, and the short-K row strips of NT products with
-K <= 64 and N a multiple of 16)
+a four- or two-stage ring, the 256x256 ping-pong kernel for K a multiple of
+64, and the short-K row strips of NT products with K <= 64 and N a multiple
+of 16)
 sums K in the same order, in chunks of 64 through the same MFMA chain, so a
 tile forced with QUTAI_AMD_GEMM_TILE gives bit-identical output to any other
 for the same call: whole and ragged tiles, the four transpose forms, fp32 and
@@ -23,7 +24,7 @@ pytestmark = pytest.mark.gpu
 
 ROOT = Path(__file__).resolve().parent.parent
 CASES = [(700, 320, 600, 1), (384, 256, 512, 1), (200, 130, 70, 3), (1024, 192, 768, 2), (700, 64, 600, 2),
-         (129, 40, 257, 1), (320, 64, 1040, 3), (129, 24, 144, 2), (64, 8, 2064, 1)]
+         (129, 40, 257, 1), (320, 64, 1040, 3), (129, 24, 144, 2), (64, 8, 2064, 1), (129, 128, 70, 2)]
 
 CHILD = r"""
 import sys
@@ -78,7 +79,7 @@ def test_forced_tiles_are_bit_identical(tmp_path):
                                         for i in range(batch)])
                 got = base[f"{m}_{k}_{n}_{batch}_{ta:d}{tb:d}_float32"]
                 assert ora.rel_frobenius(got, exact) <= 1e-2, (m, k, n, batch, ta, tb)
-    for tile in ("T", "U", "H", "S", "S2", "R"):
+    for tile in ("T", "U", "H", "S", "S2", "R", "P"):
         other = _run(tile, tmp_path / f"{tile}.npz")
         for key in base.files:
             assert np.array_equal(base[key], other[key]), (tile, key)
