@@ -207,27 +207,29 @@ __global__ void __launch_bounds__(THREADS) row_sum_kernel(const T* __restrict__ 
                                                           int64_t width, int64_t parts, int64_t span) {
   typedef typename Acc<T>::R R;
   const int lane = threadIdx.x & 63;
-  const int64_t item = (int64_t)blockIdx.x * (THREADS / 64) + (threadIdx.x >> 6);
-  if (item >= rows * parts) return;
-  const int64_t row = item / parts, part = item - row * parts;
-  const int64_t lo = part * span, hi = lo + span < width ? lo + span : width;
-  const T* p = x + row * width;
-  R s = R(0);
-  // eight loads in flight, added in the same order as one at a time
-  int64_t c = lo + lane;
-  for (; c + 7 * 64 < hi; c += 8 * 64) {
-    T v[8];
+  // waves stride over the items, so any number of rows fits the capped grid
+  for (int64_t item = (int64_t)blockIdx.x * (THREADS / 64) + (threadIdx.x >> 6); item < rows * parts;
+       item += (int64_t)gridDim.x * (THREADS / 64)) {
+    const int64_t row = item / parts, part = item - row * parts;
+    const int64_t lo = part * span, hi = lo + span < width ? lo + span : width;
+    const T* p = x + row * width;
+    R s = R(0);
+    // eight loads in flight, added in the same order as one at a time
+    int64_t c = lo + lane;
+    for (; c + 7 * 64 < hi; c += 8 * 64) {
+      T v[8];
 #pragma unroll
-    for (int u = 0; u < 8; u++) v[u] = p[c + u * 64];
+      for (int u = 0; u < 8; u++) v[u] = p[c + u * 64];
 #pragma unroll
-    for (int u = 0; u < 8; u++) s += widen(v[u]);
-  }
-  for (; c < hi; c += 64) s += widen(p[c]);
+      for (int u = 0; u < 8; u++) s += widen(v[u]);
+    }
+    for (; c < hi; c += 64) s += widen(p[c]);
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
-  if (lane == 0) {
-    if (parts == 1) out[row] = narrow<T>(s);
-    else partial[item] = s;
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+    if (lane == 0) {
+      if (parts == 1) out[row] = narrow<T>(s);
+      else partial[item] = s;
+    }
   }
 }
 
@@ -237,13 +239,14 @@ __global__ void __launch_bounds__(THREADS) row_partials_kernel(const typename Ac
                                                                T* __restrict__ out, int64_t rows, int64_t parts) {
   typedef typename Acc<T>::R R;
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * (THREADS / 64) + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  R s = R(0);
-  for (int64_t q = lane; q < parts; q += 64) s += partial[row * parts + q];
+  for (int64_t row = (int64_t)blockIdx.x * (THREADS / 64) + (threadIdx.x >> 6); row < rows;
+       row += (int64_t)gridDim.x * (THREADS / 64)) {
+    R s = R(0);
+    for (int64_t q = lane; q < parts; q += 64) s += partial[row * parts + q];
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
-  if (lane == 0) out[row] = narrow<T>(s);
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+    if (lane == 0) out[row] = narrow<T>(s);
+  }
 }
 
 // inner > 1: one lane per (o, part, j) column segment, consecutive lanes on

@@ -206,6 +206,20 @@ def test_sum_large(amd, dtype, shape, axis):
 
 
 @pytest.mark.parametrize("dtype", ["float32", "bfloat16", "float64"])
+def test_sum_many_short_rows(amd, dtype):
+    """Row sums over more rows than one grid of the capped launch holds
+    (300000 rows of 4: the waves stride over the rows) against numpy float64."""
+    shape = (300000, 4)
+    x = normal(21, shape)
+    got = download(amd.sum(upload(x, dtype), shape, 1))
+    values = stored(x, dtype).reshape(shape).astype(np.float64)
+    expected = values.sum(axis=1)
+    accumulate = 1.2e-16 if dtype == "float64" else 6e-8
+    rounding = {"float32": 6e-8, "float64": 1.2e-16, "bfloat16": 3.9e-3}[dtype]
+    assert np.all(np.abs(got - expected) <= 4 * accumulate * np.abs(values).sum(axis=1) + rounding * np.abs(expected))
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16", "float64"])
 @pytest.mark.parametrize("shape,axis", [((3, 4, 5), 0), ((3, 4, 5), 1), ((3, 4, 5), 2), ((2, 300, 7), 1),
                                         ((16, 2048), 1), ((5, 3), 0)])
 def test_softmax_any_axis(amd, dtype, shape, axis):
