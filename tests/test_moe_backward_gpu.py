@@ -159,14 +159,18 @@ def test_sparse_moe_layer_forward_and_all_gradients(lm):
     ry, raux, rdx, rdwr, rdwg, rdwu, rdwd = moe_reference(xv.reshape(tokens, width).astype(np.float64), wr, wg, wu,
                                                           wd, top_k, G.reshape(tokens, width).astype(np.float64),
                                                           float(np.float32(c)))
-    tol = 1e-4  # fp32 storage, fp32 MFMA products, many chained ops
-    assert ora.rel_frobenius(f64(y, (tokens, width)), ry) <= tol
+    # fp32 storage, true fp32 MFMA products: the reference's own GPU pin
+    # for the MoE layer (tests/test_lm_moe.py:105-138) is 2e-5
+    tol = 2e-5
+    errors = dict(y=ora.rel_frobenius(f64(y, (tokens, width)), ry),
+                  x=ora.rel_frobenius(f64(x.grad, (tokens, width)), rdx),
+                  router=ora.rel_frobenius(f64(layer.router.weight.grad, (experts, width)), rdwr),
+                  w_gate=ora.rel_frobenius(f64(layer.w_gate.grad, wg.shape), rdwg),
+                  w_up=ora.rel_frobenius(f64(layer.w_up.grad, wu.shape), rdwu),
+                  w_down=ora.rel_frobenius(f64(layer.w_down.grad, wd.shape), rdwd))
+    print({k: f"{v:.2e}" for k, v in errors.items()})
     assert abs(download(aux.storage)[0] - raux) <= 1e-5 * max(1, abs(raux))
-    assert ora.rel_frobenius(f64(x.grad, (tokens, width)), rdx) <= tol
-    assert ora.rel_frobenius(f64(layer.router.weight.grad, (experts, width)), rdwr) <= tol
-    assert ora.rel_frobenius(f64(layer.w_gate.grad, wg.shape), rdwg) <= tol
-    assert ora.rel_frobenius(f64(layer.w_up.grad, wu.shape), rdwu) <= tol
-    assert ora.rel_frobenius(f64(layer.w_down.grad, wd.shape), rdwd) <= tol
+    assert max(errors.values()) <= tol, errors
     assert sum(layer.last_counts) == tokens * top_k
 
 

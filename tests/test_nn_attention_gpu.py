@@ -6,8 +6,9 @@ and parameter gradient against a float64 composition of the oracle's
 attention forms (oracle/reference.py attention_np / attention_backward_np)
 and the Linear rules, for the fused (bf16, 64 per head), general (fp32, any
 head width <= 256) and product (head width > 256) paths, causal and not.
-fp32 within 1e-5 relative Frobenius error, bf16 within 2e-2 (gradients pass
-through several bf16 roundings)."""
+fp32 within 1e-5 relative Frobenius error; bf16 within 1e-2 of a float64
+reference that rounds to bf16 wherever the layer stores a tensor (the
+reference's own bf16 semantics: every stored result is a bf16 tensor)."""
 import math
 
 import numpy as np
@@ -85,11 +86,15 @@ def test_sequence_linear_shared_weight_gradients(amd):
     assert inputs.grad.storage.tolist() == [2.0, 3.0] * 4
 
 
-def _reference(x, params, heads, causal, with_output):
-    """float64 forward and gradients of loss = sum(y * dy) for the layer."""
+def _reference(x, params, heads, causal, with_output, rnd=lambda a: a):
+    """float64 forward and gradients of loss = sum(y * dy) for the layer.
+    ``rnd`` is applied wherever the device stores a tensor (every product,
+    bias add, attention output and gradient), so that for bf16 storage the
+    reference carries the same roundings as the layer and only the fp32
+    accumulation inside each kernel differs."""
     wq, bq, wk, bk, wv, bv = params[:6]
     batch, time, _ = x.shape
-    q, k, v = x @ wq + bq, x @ wk + bk, x @ wv + bv
+    q, k, v = (rnd(rnd(x @ w) + b) for w, b in ((wq, bq), (wk, bk), (wv, bv)))
     features = q.shape[-1]
     dim = features // heads
     split = lambda t: t.reshape(batch, time, heads, dim)
@@ -99,15 +104,16 @@ def _reference(x, params, heads, causal, with_output):
     for b in range(batch):
         for h in range(heads):
             mixed[b, :, h], lses[b, h] = ora.attention_np(qs[b, :, h], ks[b, :, h], vs[b, :, h], causal=causal)
-    mixed = mixed.reshape(batch, time, features)
-    y = mixed @ params[6] + params[7] if with_output else mixed
+    mixed = rnd(mixed.reshape(batch, time, features))
+    y = rnd(rnd(mixed @ params[6]) + params[7]) if with_output else mixed
 
     def grads(dy):
         out = {}
         dmixed = dy
         if with_output:
-            out["wo"], out["bo"] = mixed.reshape(-1, features).T @ dy.reshape(-1, features), dy.sum(axis=(0, 1))
-            dmixed = dy @ params[6].T
+            out["wo"] = rnd(mixed.reshape(-1, features).T @ dy.reshape(-1, features))
+            out["bo"] = rnd(dy.sum(axis=(0, 1)))
+            dmixed = rnd(dy @ params[6].T)
         dm = dmixed.reshape(batch, time, heads, dim)
         dq, dk, dv = (np.zeros((batch, time, heads, dim)) for _ in range(3))
         for b in range(batch):
@@ -116,11 +122,12 @@ def _reference(x, params, heads, causal, with_output):
                     dm[b, :, h], qs[b, :, h], ks[b, :, h], vs[b, :, h], mixed.reshape(batch, time, heads, dim)[b, :, h],
                     lses[b, h], causal=causal)
         flat = x.reshape(-1, x.shape[-1])
-        dx = 0
+        dx = None
         for name, d, w in (("q", dq, wq), ("k", dk, wk), ("v", dv, wv)):
-            d = d.reshape(-1, features)
-            out["w" + name], out["b" + name] = flat.T @ d, d.sum(axis=0)
-            dx = dx + d @ w.T
+            d = rnd(d.reshape(-1, features))
+            out["w" + name], out["b" + name] = rnd(flat.T @ d), rnd(d.sum(axis=0))
+            part = rnd(d @ w.T)
+            dx = part if dx is None else rnd(dx + part)
         out["x"] = dx.reshape(x.shape)
         return out
 
@@ -158,9 +165,11 @@ def test_forward_and_all_gradients_match_float64(amd, features, heads, causal, d
     xs = stored(x, dtype)
     inputs = Tensor(upload(x, dtype), shape=x.shape, requires_grad=True)
     y = layer(inputs)
-    y_ref, grads = _reference(xs, host, heads, causal, with_output)
-    tol = 1e-5 if dtype == "float32" else 2e-2
-    assert ora.rel_frobenius(download(y.storage), y_ref.ravel()) <= tol
+    rnd = (lambda a: stored(a, "bfloat16")) if dtype == "bfloat16" else (lambda a: a)
+    y_ref, grads = _reference(xs, host, heads, causal, with_output, rnd)
+    tol = 1e-5 if dtype == "float32" else 1e-2
+    errors = {}
+    errors["y"] = ora.rel_frobenius(download(y.storage), y_ref.ravel())
     dy = rng.standard_normal(y_ref.shape)
     y.backward(Tensor(upload(dy, dtype), shape=y.shape))
     ref = grads(stored(dy, dtype))
@@ -172,5 +181,7 @@ def test_forward_and_all_gradients_match_float64(amd, features, heads, causal, d
             # softmax ignores it; the device value is rounding noise
             assert np.linalg.norm(got) <= tol * np.linalg.norm(ref["wk"]), name
             continue
-        assert ora.rel_frobenius(got, ref[name].ravel()) <= tol, name
-    assert ora.rel_frobenius(download(inputs.grad.storage), ref["x"].ravel()) <= tol
+        errors[name] = ora.rel_frobenius(got, ref[name].ravel())
+    errors["x"] = ora.rel_frobenius(download(inputs.grad.storage), ref["x"].ravel())
+    print({k: f"{v:.2e}" for k, v in errors.items()})
+    assert max(errors.values()) <= tol, errors
