@@ -497,6 +497,24 @@ def gather(values: AMDStorage, positions) -> AMDStorage:
     return result
 
 
+def _group_by_target(index, size: int):
+    """CSR grouping of source positions by target, in one counting pass:
+    ``start`` (size + 1 offsets) and ``order`` (the source indices of each
+    target in input order, target by target).  O(n + size); stable, so
+    repeated positions add up in input order."""
+    start = array("q", bytes(8 * (size + 1)))
+    for position in index:
+        start[position + 1] += 1
+    for t in range(size):
+        start[t + 1] += start[t]
+    cursor = start[:size]
+    order = array("q", bytes(8 * len(index)))
+    for i, position in enumerate(index):
+        order[cursor[position]] = i
+        cursor[position] += 1
+    return start, order
+
+
 def scatter(values: AMDStorage, positions, size: int) -> AMDStorage:
     """Zeros of ``size`` with values[i] added at positions[i]
     (src/qutai/backends/cuda.py:218-226).  Repeated positions add up in
@@ -509,14 +527,9 @@ def scatter(values: AMDStorage, positions, size: int) -> AMDStorage:
         raise ValueError("scatter needs one position per value")
     if index and (min(index) < 0 or max(index) >= size):
         raise IndexError("position outside the storage")
-    counts = [0] * (size + 1)
-    for position in index:
-        counts[position + 1] += 1
-    for t in range(size):
-        counts[t + 1] += counts[t]
-    order = sorted(range(len(index)), key=index.__getitem__)
-    start = storage(array("q", counts), dtype="int64")
-    sources = storage(array("q", order), dtype="int64") if order else None
+    counts, order = _group_by_target(index, size)
+    start = storage(counts, dtype="int64")
+    sources = storage(order, dtype="int64") if order else None
     result = AMDStorage(size, values.dtype)
     if size:
         result.runtime.call("qutai_amd_scatter", values.ptr, start.ptr, _p(sources), result.ptr, size,

@@ -289,6 +289,15 @@ def _pad8(n):
     return (n + 7) // 8 * 8
 
 
+def _rows_through_order(token_bytes, *, save, dtype):
+    """Whether the expert forward reads the routed token rows through the
+    route's ``order`` inside the grouped GEMMs instead of copying them: the
+    forward alone (the backward's weight gradients need the gathered block
+    itself), bf16 or fp32 tokens, and a token matrix below 2 GiB (the GEMM
+    addresses it with 32-bit byte offsets of one buffer descriptor)."""
+    return not save and dtype in ("bfloat16", "float32") and token_bytes < (1 << 31)
+
+
 def moe_experts_forward(x, route, w_gate, w_up, w_down, width, hidden, *, save=False):
     """Expert SwiGLU for every routed (token, slot): gather, grouped gate/up
     and silu(gate) * up (one fused grouped GEMM for bf16, same roundings),
@@ -302,9 +311,7 @@ def moe_experts_forward(x, route, w_gate, w_up, w_down, width, hidden, *, save=F
     wp, hp = _pad8(width), _pad8(hidden)
     experts = route["experts"]
     wg, wu, wd = (_as_dtype(w, x.dtype) for w in (w_gate, w_up, w_down))
-    # the forward alone reads the routed rows through `order` inside the
-    # GEMM; the backward's weight gradients need the gathered block itself
-    fused = not save and x.dtype in ("bfloat16", "float32")
+    fused = _rows_through_order(x.nbytes, save=save, dtype=x.dtype)
     rows = x if fused else route_gather_all(x, route, width)
     if (wp, hp) != (width, hidden):
         wg, wu = (repitch(w, experts, hidden, width, hp, wp) for w in (wg, wu))

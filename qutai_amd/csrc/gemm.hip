@@ -84,19 +84,22 @@ __global__ void __launch_bounds__(256) gemm_f64(const double* a, const double* b
 // operand feeds the bf16 MFMA path (mixed inputs, autocast) or when the
 // operand's rows are not 16-byte aligned.  One thread per 16-byte chunk of
 // the destination (E = 8 bf16 or 4 fp32 values; pitch is a multiple of E),
-// 32-bit index arithmetic (the host checks the sizes), element loads that
-// are contiguous across a wavefront and one 16-byte store.
+// element loads that are contiguous across a wavefront and one 16-byte
+// store.  One launch covers the rows [row_base, row_base + rows) with
+// 32-bit chunk indices (rows * pitch / E < 2^31; the host splits larger
+// operands into several launches), the row's (batch, row) pair in 64 bits.
 template <bool SRC_BF16, bool DST_BF16>
-__global__ void __launch_bounds__(256) prepare_operand(const void* src, void* dst, uint32_t rows, uint32_t outer,
-                                                       uint32_t inner, uint32_t pitch, int64_t stride) {
+__global__ void __launch_bounds__(256) prepare_operand(const void* src, void* dst, int64_t row_base, uint32_t rows,
+                                                       int64_t outer, uint32_t inner, uint32_t pitch,
+                                                       int64_t stride) {
   constexpr int E = DST_BF16 ? 8 : 4;
   const uint32_t per_row = pitch / E;
   const uint32_t i = blockIdx.x * 256u + threadIdx.x;
   if (i >= rows * per_row) return;
   const uint32_t r = i / per_row, c0 = (i - r * per_row) * E;
-  const uint32_t z = r / outer, o = r - z * outer;
-  const int64_t at = (int64_t)z * stride + (int64_t)o * inner + c0;
-  char* d = (char*)dst + (int64_t)i * 16;
+  const int64_t row = row_base + r, z = row / outer, o = row - z * outer;
+  const int64_t at = z * stride + o * inner + c0;
+  char* d = (char*)dst + (row_base * per_row + i) * 16;
   if constexpr (SRC_BF16 && DST_BF16) {
     if (c0 + E <= inner) {
       // a whole chunk inside the row: one 16-byte load at the element's own
@@ -564,25 +567,30 @@ void plan(int64_t rows, int64_t inner, int64_t cols, int64_t batch, int64_t left
            : plan_operand(b, b_dtype, bf16, inner, cols, batch, right_stride);
 }
 
-// The re-layout's chunk count must fit the kernel's 32-bit indices.
-bool prepare_fits(const Operand& o) { return o.batches * o.outer * o.pitch < (1ll << 31); }
+// A re-laid-out row must fit the kernel's 32-bit chunk indices (any row of
+// a valid operand does); larger operands take several launches.
+bool prepare_fits(const Operand& o) { return o.pitch < (1ll << 31) && o.inner < (1ll << 32); }
 
 void launch_prepare(Operand& o, int src_dtype, bool bf16, char* ws, hipStream_t stream) {
-  const int64_t rows = o.batches * o.outer, chunks = rows * o.pitch / (bf16 ? 8 : 4);
-  const dim3 grid((unsigned)((chunks + 255) / 256));
-  const uint32_t r = (uint32_t)rows, ou = (uint32_t)o.outer, in = (uint32_t)o.inner, pi = (uint32_t)o.pitch;
-  if (src_dtype == QA_BF16 && bf16)
-    hipLaunchKernelGGL((prepare_operand<true, true>), grid, dim3(256), 0, stream, o.ptr, (void*)ws, r, ou, in, pi,
-                       o.src_stride);
-  else if (bf16)
-    hipLaunchKernelGGL((prepare_operand<false, true>), grid, dim3(256), 0, stream, o.ptr, (void*)ws, r, ou, in, pi,
-                       o.src_stride);
-  else if (src_dtype == QA_BF16)
-    hipLaunchKernelGGL((prepare_operand<true, false>), grid, dim3(256), 0, stream, o.ptr, (void*)ws, r, ou, in, pi,
-                       o.src_stride);
-  else
-    hipLaunchKernelGGL((prepare_operand<false, false>), grid, dim3(256), 0, stream, o.ptr, (void*)ws, r, ou, in, pi,
-                       o.src_stride);
+  const int64_t rows = o.batches * o.outer, per_row = o.pitch / (bf16 ? 8 : 4);
+  const int64_t step = std::max<int64_t>(1, ((1ll << 31) - 1) / per_row);  // rows per launch
+  const uint32_t in = (uint32_t)o.inner, pi = (uint32_t)o.pitch;
+  for (int64_t base = 0; base < rows; base += step) {
+    const uint32_t r = (uint32_t)std::min<int64_t>(step, rows - base);
+    const dim3 grid((unsigned)(((int64_t)r * per_row + 255) / 256));
+    if (src_dtype == QA_BF16 && bf16)
+      hipLaunchKernelGGL((prepare_operand<true, true>), grid, dim3(256), 0, stream, o.ptr, (void*)ws, base, r, o.outer,
+                         in, pi, o.src_stride);
+    else if (bf16)
+      hipLaunchKernelGGL((prepare_operand<false, true>), grid, dim3(256), 0, stream, o.ptr, (void*)ws, base, r,
+                         o.outer, in, pi, o.src_stride);
+    else if (src_dtype == QA_BF16)
+      hipLaunchKernelGGL((prepare_operand<true, false>), grid, dim3(256), 0, stream, o.ptr, (void*)ws, base, r,
+                         o.outer, in, pi, o.src_stride);
+    else
+      hipLaunchKernelGGL((prepare_operand<false, false>), grid, dim3(256), 0, stream, o.ptr, (void*)ws, base, r,
+                         o.outer, in, pi, o.src_stride);
+  }
   o.ptr = ws;
 }
 

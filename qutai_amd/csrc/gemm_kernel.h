@@ -457,6 +457,8 @@ struct GemmKernel {
       uint32_t oa[JA], ob[JB];
       int ka[JA], kb[JB];  // k coordinate of the chunk (validity per K step)
       bool va[JA], vb[JB];
+      // gathered rows: rows of A in the table's range [0, a_bytes / row bytes)
+      const int64_t a_count = gather ? p.a_bytes / (lda * (int64_t)sizeof(T)) : 0;
 #pragma unroll
       for (int j = 0; j < JA; j++) {
         int q = (j * NW + wave) * 64 + lane, outer, c;
@@ -464,8 +466,11 @@ struct GemmKernel {
         ka[j] = KA ? c * E : outer;
         va[j] = KA ? (row0 + outer < M) : (row0 + c * E < M);
         // gathered rows: the row index comes from the table (read only for
-        // rows inside the group), the descriptor spans all of A
+        // rows inside the group), the descriptor spans all of A; an index
+        // outside A's rows reads zeros (its chunks get the out-of-range
+        // offset; a 32-bit byte offset could otherwise wrap onto a real row)
         const int64_t src_row = KA && gather && va[j] ? gather[row0 + outer] : outer;
+        if (KA && gather && va[j] && (src_row < 0 || src_row >= a_count)) va[j] = false;
         oa[j] = (uint32_t)((src_row * lda + c * E) * (int64_t)sizeof(T));
       }
       // A's descriptor base at k0 is a_tile + k0 (K-major) or + k0 * lda

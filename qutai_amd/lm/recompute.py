@@ -1,11 +1,16 @@
-"""Activation recomputation (src/qutai/lm/recompute.py:11-79).
+"""Activation recomputation (the contract of src/qutai/lm/recompute.py:11-79).
 
-``checkpoint`` runs a side-effect-free function without recording, keeps
-only its output, and in backward runs it again with recording on (under the
-matmul precision of the forward) to get the gradients of its arguments and
-of the parameters it closes over.  The parameters must be passed
-explicitly: a trainable tensor reached by the recomputed graph that is
-neither an argument nor a declared parameter raises ``ValueError``."""
+``checkpoint(function, *arguments, parameters=...)`` evaluates ``function``
+with graph recording off and keeps only its output.  The output's backward
+rule is a ``_Replay``: it evaluates the function again with recording on,
+under the matmul precision that was in force for the forward, on stand-in
+leaves that share the arguments' storage, back-propagates through that
+second graph, and hands every leaf gradient to the input it belongs to.
+Parameters the function closes over must be declared, because they are
+graph inputs of the checkpointed node like the arguments; a recomputed
+graph that reaches any other trainable tensor raises ``ValueError``.  A
+tensor that is both an argument and a declared parameter receives the sum of
+its two parts."""
 from __future__ import annotations
 
 from ..backends.device import get_backend
@@ -15,40 +20,60 @@ from ..core.context import set_recording
 from ..core.tensor import Tensor
 
 
-def checkpoint(function, *arguments, parameters=()):
-    parameters = tuple(dict.fromkeys(parameters))
-    if not all(isinstance(value, Tensor) for value in (*arguments, *parameters)):
-        raise TypeError("checkpoint arguments and parameters must be Tensors")
-    parents = tuple(dict.fromkeys((*arguments, *parameters)))
-    with set_recording(False):
-        output = function(*arguments)
-    if not isinstance(output, Tensor):
+def _unique(tensors):
+    """The tensors in first-seen order, each once (identity, not value)."""
+    seen, result = set(), []
+    for tensor in tensors:
+        if id(tensor) not in seen:
+            seen.add(id(tensor))
+            result.append(tensor)
+    return tuple(result)
+
+
+def _single_tensor(value):
+    if not isinstance(value, Tensor):
         raise TypeError("a checkpointed function must return one Tensor")
-    precision = matmul_precision()
+    return value
 
-    def backward(gradient):
-        # fresh leaves for the arguments: their identity separates argument
-        # gradients from parameter gradients when one tensor is both
-        stand_ins = {value: Tensor(value.storage, shape=value.shape, requires_grad=value.requires_grad)
-                     for value in arguments}
-        with set_recording(True), set_matmul_precision(precision):
-            rerun = function(*(stand_ins[value] for value in arguments))
-            if not isinstance(rerun, Tensor):
-                raise TypeError("a checkpointed function must return one Tensor")
-            leaves = grad.backward(rerun, gradient, retain_graph=False) if rerun.requires_grad else {}
-        declared = set(parameters)
-        known = set(stand_ins.values()) | declared
-        if any(leaf not in known for leaf in leaves):
-            raise ValueError("the recomputed function reached a trainable Tensor not passed as a parameter")
-        results = []
-        for value in parents:
-            if not value.requires_grad:
-                results.append(None)
-                continue
-            part = leaves.get(stand_ins[value]) if value in stand_ins else None
-            if value in declared and value in leaves:
-                part = leaves[value] if part is None else get_backend(value.device).add(part, leaves[value])
-            results.append(part)
-        return tuple(results)
 
-    return grad.record(Tensor(output.storage, shape=output.shape), parents, backward)
+class _Replay:
+    """Backward rule of one checkpointed call (see the module docstring)."""
+
+    def __init__(self, function, arguments, parameters, precision):
+        self.function, self.arguments, self.parameters = function, arguments, parameters
+        self.precision = precision
+        self.inputs = _unique((*arguments, *parameters))  # the graph parents, in this order
+
+    def __call__(self, gradient):
+        position = {id(tensor): i for i, tensor in enumerate(self.inputs)}
+        # one stand-in leaf per argument position, sharing its storage: the
+        # argument part of a tensor's gradient arrives on the stand-in, the
+        # closed-over part on the tensor itself
+        stand_ins = [Tensor(a.storage, shape=a.shape, requires_grad=a.requires_grad) for a in self.arguments]
+        owner = {id(s): position[id(a)] for s, a in zip(stand_ins, self.arguments)}
+        for parameter in self.parameters:
+            owner[id(parameter)] = position[id(parameter)]
+        with set_recording(True), set_matmul_precision(self.precision):
+            rerun = _single_tensor(self.function(*stand_ins))
+            leaf_gradients = grad.backward(rerun, gradient, retain_graph=False) if rerun.requires_grad else {}
+        totals = [None] * len(self.inputs)
+        for leaf, part in leaf_gradients.items():
+            slot = owner.get(id(leaf))
+            if slot is None:
+                raise ValueError("the recomputed function reached a trainable Tensor not passed as a parameter")
+            if totals[slot] is None:
+                totals[slot] = part
+            else:
+                totals[slot] = get_backend(self.inputs[slot].device).add(totals[slot], part)
+        return tuple(total if tensor.requires_grad else None for total, tensor in zip(totals, self.inputs))
+
+
+def checkpoint(function, *arguments, parameters=()):
+    parameters = _unique(parameters)
+    for value in (*arguments, *parameters):
+        if not isinstance(value, Tensor):
+            raise TypeError("checkpoint arguments and parameters must be Tensors")
+    with set_recording(False):
+        output = _single_tensor(function(*arguments))
+    replay = _Replay(function, arguments, parameters, matmul_precision())
+    return grad.record(Tensor(output.storage, shape=output.shape), replay.inputs, replay)

@@ -112,13 +112,16 @@ def _check(what: str, lo: np.ndarray, hi: np.ndarray, alloc_bytes: int):
 
 def operand_loads(cfg: Config, f32: bool, kmajor: bool, rows_tile: int, base_elem: int, row0: int, rows: int,
                   k_len: int, ld: int, alloc: int, what: str, gather: np.ndarray | None = None,
-                  swiglu_up: bool = False):
+                  swiglu_up: bool = False, index_check: bool = True):
     """Every load of one operand over one tile's K loop: base_elem is the
     operand pointer after the mode's adjustments (in elements), row0 the
     tile's first row (A) / column (B), rows the operand's valid extent (M or
     N), k_len the K range.  gather (grouped A, K-major): row i of the tile's
     group is row gather[row0 + i] of the operand, the descriptor spans the
-    whole allocation."""
+    whole allocation, the byte offset is a 32-bit value, and an index
+    outside the operand's rows gets the out-of-range offset (index_check;
+    without it -- a planted mistake -- such an index is issued with its
+    wrapped offset, and one that wraps onto a real row is reported)."""
     e, es = (4, 4) if f32 else (8, 2)
     nt = 64 * cfg.wm * cfg.wn
     chunks = rows_tile * cfg.bk // e
@@ -137,7 +140,12 @@ def operand_loads(cfg: Config, f32: bool, kmajor: bool, rows_tile: int, base_ele
     valid = (row0 + outer < rows) if kmajor else (row0 + c * e < rows)
     if gather is not None:
         src = np.where(valid, gather[np.minimum(row0 + outer, gather.size - 1)], outer)
-        off = (src * ld + c * e) * es
+        outside = valid & ((src < 0) | (src >= alloc // ld))
+        off = ((src * ld + c * e) * es) & 0xFFFFFFFF  # the kernel's uint32 byte offset
+        if index_check:
+            valid = valid & ~outside
+        elif np.any(outside & (off + 16 <= min(alloc * es, RANGE_CAP))):
+            raise Violation(f"{what}: a gathered index outside the operand reads a real row")
     else:
         off = (outer * ld + c * e) * es
     nk = (k_len + cfg.bk - 1) // cfg.bk
@@ -291,7 +299,7 @@ def remainder_rows(f32: bool, m: int, k: int, n: int, c0: int, width: int, tb: b
 
 
 def grouped_gemm(cfg: Config, f32: bool, counts: list[int], inner: int, cols: int, transpose_right: bool,
-                 gather: np.ndarray | None = None, source_rows: int = 0):
+                 gather: np.ndarray | None = None, source_rows: int = 0, index_check: bool = True):
     """qutai_amd_gemm_grouped (and the SwiGLU form with cfg = SWIGLU): group g
     owns rows [offsets[g], offsets[g+1]) of A (or, with gather, the rows
     gather[offsets[g]:...] of a source_rows-row A) and of out; its B is
@@ -318,7 +326,7 @@ def grouped_gemm(cfg: Config, f32: bool, counts: list[int], inner: int, cols: in
             row0 = tm * cfg.bm
             if gather is not None:
                 operand_loads(cfg, f32, True, cfg.bm, 0, row0, rows, inner, inner, a_alloc, "A",
-                              gather=gather[lo:hi])
+                              gather=gather[lo:hi], index_check=index_check)
             else:
                 operand_loads(cfg, f32, True, cfg.bm, lo * inner, row0, rows, inner, inner, a_alloc, "A")
             for tn in range(tiles_n):

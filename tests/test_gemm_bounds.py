@@ -36,16 +36,20 @@ def test_model_reports_the_split_k_fault_class():
 
 
 def test_model_reports_a_gather_index_past_the_source():
-    """A planted mistake: a route order entry equal to the number of token
-    rows.  The kernel's descriptor spans exactly the source, so the chunk
-    reads zeros instead of the row -- reported as a chunk outside its
-    descriptor."""
+    """A route order entry outside the token rows reads zeros: equal to the
+    row count, negative, or so large that its 32-bit byte offset wraps onto
+    row 1 (2^32 / 128 + 1 rows of 64 bf16).  The planted mistake -- the
+    kernel without its index check -- reads that real row, and the model
+    reports it."""
     counts = [3, 0, 5]
     order = np.array([0, 1, 2, 3, 4, 5, 6, 7])
-    gm.grouped_gemm(gm.tile_configs(False)[0], False, counts, 64, 32, True, gather=order, source_rows=8)
-    order[5] = 8
+    cfg = gm.tile_configs(False)[0]
+    gm.grouped_gemm(cfg, False, counts, 64, 32, True, gather=order, source_rows=8)
+    for bad in (8, -1, (1 << 32) // 128 + 1):
+        order[5] = bad
+        gm.grouped_gemm(cfg, False, counts, 64, 32, True, gather=order, source_rows=8)
     with pytest.raises(gm.Violation):
-        gm.grouped_gemm(gm.tile_configs(False)[0], False, counts, 64, 32, True, gather=order, source_rows=8)
+        gm.grouped_gemm(cfg, False, counts, 64, 32, True, gather=order, source_rows=8, index_check=False)
 
 
 @pytest.mark.parametrize("f32", [False, True], ids=["bf16", "fp32"])

@@ -263,3 +263,30 @@ def test_deferred_gradient_adds_in_place_only_into_this_pass_grad(fake_device):
     assert Rows.added_in_place == 1
     assert kept.values.tolist() == [1.0, 6.0, 1.0]
     assert w.grad.storage.values.tolist() == [1.0, 11.0, 1.0]
+
+
+def test_scatter_grouping_is_a_stable_counting_sort():
+    """amd.scatter's host grouping: targets' sources in input order (the
+    stable sort of positions), offsets of every target, empty input."""
+    from array import array
+
+    rng = np.random.default_rng(3)
+    for n, size in ((0, 4), (1, 1), (500, 7), (4000, 300)):
+        index = array("q", rng.integers(0, size, n).tolist())
+        start, order = amd._group_by_target(index, size)
+        assert list(order) == sorted(range(n), key=index.__getitem__)
+        assert list(start) == [0] + np.cumsum(np.bincount(np.asarray(index, dtype=np.int64), minlength=size)).tolist()
+
+
+def test_moe_forward_reads_rows_through_the_order_only_below_2_gib():
+    """The routed-row read inside the grouped GEMM addresses the token
+    matrix with 32-bit offsets (qutai_amd_gemm_grouped / _swiglu refuse a
+    token matrix of 2 GiB or more on that path), so larger inputs, and the
+    training forward, take the gathered copy."""
+    from qutai_amd.backends import amd_lm
+
+    assert amd_lm._rows_through_order(8192 * 2048 * 2, save=False, dtype="bfloat16")
+    assert not amd_lm._rows_through_order(8192 * 2048 * 2, save=True, dtype="bfloat16")
+    assert not amd_lm._rows_through_order(1 << 31, save=False, dtype="bfloat16")
+    assert amd_lm._rows_through_order((1 << 31) - 2, save=False, dtype="bfloat16")
+    assert not amd_lm._rows_through_order(1024, save=False, dtype="float64")

@@ -117,6 +117,31 @@ def test_grouped_gemm_gather_equals_gathered_block(amd, lm, dtype, tokens, width
             lm.grouped_gemm(rows, ws, route, width, cols, gather=True, out_dtype=dtype)
 
 
+def test_grouped_gemm_gather_index_outside_the_tokens_reads_zeros(amd, lm):
+    """Route order entries outside the token rows -- the row count, -1, and
+    an index whose 32-bit byte offset would wrap onto row 1 (64 bf16 values
+    = 128 bytes per row, 2^32 / 128 + 1) -- give zero rows; every other row
+    is unchanged."""
+    from array import array
+
+    tokens, width, cols, experts = 40, 64, 32, 4
+    route = lm.routing(upload(normal(77, tokens * experts), "float32"), tokens, experts, 2)
+    xs = upload(normal(78, tokens * width), "bfloat16")
+    ws = upload(normal(79, experts * cols * width, 0.1), "bfloat16")
+    ref = download(lm.grouped_gemm(xs, ws, route, width, cols, out_dtype="float32", gather=True)).reshape(-1, cols)
+    order = np.frombuffer(route["order"].to_array(), dtype=np.int64).copy()
+    bad = {3: tokens, 10: -1, 17: (1 << 32) // 128 + 1}
+    for position, index in bad.items():
+        order[position] = index
+    broken = dict(route, order=amd.storage(array("q", order.tolist()), dtype="int64"))
+    got = download(lm.grouped_gemm(xs, ws, broken, width, cols, out_dtype="float32", gather=True)).reshape(-1, cols)
+    for position in range(ref.shape[0]):
+        if position in bad:
+            assert np.all(got[position] == 0), position
+        else:
+            assert np.array_equal(got[position], ref[position]), position
+
+
 @pytest.mark.parametrize("dtype,tokens,inner,cols,experts,transpose_right", [
     ("bfloat16", 1500, 128, 200, 8, False), ("bfloat16", 700, 1408, 2048, 8, False),
     ("bfloat16", 600, 64, 96, 4, True), ("float32", 900, 192, 96, 4, False), ("bfloat16", 40, 64, 16, 16, False)])
