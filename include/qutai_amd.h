@@ -403,12 +403,18 @@ int qutai_amd_attention_fwd(const void* q, const void* k, const void* v, void* o
  * dY_e^T act_e.  An empty group writes zeros (or keeps out with accumulate).
  * dtype QA_BF16 / QA_F32 for a and b, out_dtype QA_F32 / QA_BF16; rows and
  * cols multiples of 8 (bf16) / 4 (fp32), 16-byte aligned operands.  total_k
- * = offsets[groups] (only used for tile choice).  Replaces the per-expert
- * weight-gradient GEMMs of the expert SwiGLU backward (`linear` backward,
- * src/qutai/lm/layers.py:57-66, run once per expert by SparseMoE,
- * lm/layers.py:395-397). */
+ * = offsets[groups] (only used for tile choice).  With gather (the route's
+ * order, total_k entries), K row k of b is row gather[k] of b, a
+ * [source_rows][cols] token matrix below 2 GiB: the weight gradients
+ * dW_gate / dW_up = dY_e^T X_e read the routed token rows in place instead
+ * of a gathered copy (src/qutai/backends/cuda_lm.py:471-502 copies them,
+ * lm.cu:394-396); an index outside [0, source_rows) reads a zero row.
+ * Replaces the per-expert weight-gradient GEMMs of the expert SwiGLU
+ * backward (`linear` backward, src/qutai/lm/layers.py:57-66, run once per
+ * expert by SparseMoE, lm/layers.py:395-397). */
 int qutai_amd_gemm_grouped_k(const void* a, const void* b, void* out, const int64_t* offsets, int groups, int64_t rows,
-                             int64_t cols, int64_t total_k, int dtype, int out_dtype, int accumulate, void* stream);
+                             int64_t cols, int64_t total_k, int dtype, int out_dtype, int accumulate,
+                             const int64_t* gather, int64_t source_rows, void* stream);
 
 /* Backward of qutai_amd_combine for every routed (token, slot) pair: the
  * pair's expert-major row of d_expert_out = dy[token] * weight, and

@@ -254,19 +254,22 @@ def swiglu_gemm(rows_block, w_gate, w_up, rows, inner, hidden, *, route=None, sa
     return (act, gate, up) if save else act
 
 
-def grouped_gemm_k(a_block, b_block, route, rows, cols, *, out_dtype="float32"):
+def grouped_gemm_k(a_block, b_block, route, rows, cols, *, out_dtype="float32", gather=False):
     """out[e] = A_e^T B_e for every expert, A_e / B_e the expert-major routed
     rows of a_block ([capacity][rows]) and b_block ([capacity][cols]): the
     per-expert weight gradients in one launch (an expert with no rows gets
-    zeros)."""
+    zeros).  With ``gather`` b_block is the token matrix ([route rows][cols])
+    and B_e's rows are read through the route's ``order`` inside the GEMM."""
     experts = route["experts"]
-    if a_block.dtype != b_block.dtype or a_block.size != route["capacity"] * rows or \
-            b_block.size != route["capacity"] * cols:
-        raise ValueError("grouped_gemm_k needs [capacity][rows] and [capacity][cols] blocks of one dtype")
+    b_rows = route["rows"] if gather else route["capacity"]
+    if a_block.dtype != b_block.dtype or a_block.size != route["capacity"] * rows or b_block.size != b_rows * cols:
+        raise ValueError("grouped_gemm_k needs [capacity][rows] and [capacity][cols] (gathered: [tokens][cols]) "
+                         "blocks of one dtype")
     out = AMDStorage(experts * rows * cols, out_dtype)
     if out.size:
         out.runtime.call("qutai_amd_gemm_grouped_k", a_block.ptr, b_block.ptr, out.ptr, route["offsets"].ptr, experts,
-                         rows, cols, route["capacity"], code(a_block.dtype), code(out_dtype), 0, mfma=True)
+                         rows, cols, route["capacity"], code(a_block.dtype), code(out_dtype), 0,
+                         route["order"].ptr if gather else None, b_rows if gather else 0, mfma=True)
     return out
 
 
@@ -289,13 +292,13 @@ def _pad8(n):
     return (n + 7) // 8 * 8
 
 
-def _rows_through_order(token_bytes, *, save, dtype):
-    """Whether the expert forward reads the routed token rows through the
-    route's ``order`` inside the grouped GEMMs instead of copying them: the
-    forward alone (the backward's weight gradients need the gathered block
-    itself), bf16 or fp32 tokens, and a token matrix below 2 GiB (the GEMM
-    addresses it with 32-bit byte offsets of one buffer descriptor)."""
-    return not save and dtype in ("bfloat16", "float32") and token_bytes < (1 << 31)
+def _rows_through_order(token_bytes, *, dtype):
+    """Whether the expert products read the routed token rows through the
+    route's ``order`` inside the grouped GEMMs (the forward's gate/up and,
+    in training, the backward's dW_gate / dW_up) instead of copying them:
+    bf16 or fp32 tokens and a token matrix below 2 GiB (the GEMMs address it
+    with 32-bit byte offsets of one buffer descriptor)."""
+    return dtype in ("bfloat16", "float32") and token_bytes < (1 << 31)
 
 
 def moe_experts_forward(x, route, w_gate, w_up, w_down, width, hidden, *, save=False):
@@ -311,7 +314,7 @@ def moe_experts_forward(x, route, w_gate, w_up, w_down, width, hidden, *, save=F
     wp, hp = _pad8(width), _pad8(hidden)
     experts = route["experts"]
     wg, wu, wd = (_as_dtype(w, x.dtype) for w in (w_gate, w_up, w_down))
-    fused = _rows_through_order(x.nbytes, save=save, dtype=x.dtype)
+    fused = _rows_through_order(x.nbytes, dtype=x.dtype)
     rows = x if fused else route_gather_all(x, route, width)
     if (wp, hp) != (width, hidden):
         wg, wu = (repitch(w, experts, hidden, width, hp, wp) for w in (wg, wu))
@@ -319,7 +322,7 @@ def moe_experts_forward(x, route, w_gate, w_up, w_down, width, hidden, *, save=F
         rows = repitch(rows, 1, route["rows"] if fused else route["capacity"], width,
                        route["rows"] if fused else route["capacity"], wp)
     if x.dtype == "bfloat16" and save:
-        act, gate, up = swiglu_gemm(rows, wg, wu, 0, wp, hp, route=route, save=True)
+        act, gate, up = swiglu_gemm(rows, wg, wu, 0, wp, hp, route=route, save=True, gather=fused)
     elif x.dtype == "bfloat16":
         act, gate, up = swiglu_gemm(rows, wg, wu, 0, wp, hp, route=route, gather=fused), None, None
     else:
@@ -332,7 +335,9 @@ def moe_experts_forward(x, route, w_gate, w_up, w_down, width, hidden, *, save=F
     y = combine_all(down, route, width)
     if not save:
         return y
-    return y, dict(rows=rows, gate=gate, up=up, act=act, down=down, w_gate=wg, w_up=wu, w_down=wd)
+    # rows: the (padded) token matrix when the products read it through the
+    # route's order (gathered), else the expert-major routed copy
+    return y, dict(rows=rows, gathered=fused, gate=gate, up=up, act=act, down=down, w_gate=wg, w_up=wu, w_down=wd)
 
 
 def combine_backward_all(gradient, expert_rows, route, width):
@@ -419,8 +424,9 @@ def moe_experts_backward(gradient, route, saved, width, hidden, *, x_dtype, weig
         d_rows = grouped_gemm(d_gate, saved["w_gate"], route, hp, wp, out_dtype="float32", transpose_right=False)
         grouped_gemm(d_up, saved["w_up"], route, hp, wp, out_dtype="float32", transpose_right=False, out=d_rows,
                      accumulate=True)
-    dw_gate = grouped_gemm_k(d_gate, saved["rows"], route, hp, wp, out_dtype=weight_dtype)
-    dw_up = grouped_gemm_k(d_up, saved["rows"], route, hp, wp, out_dtype=weight_dtype)
+    gathered = saved.get("gathered", False)
+    dw_gate = grouped_gemm_k(d_gate, saved["rows"], route, hp, wp, out_dtype=weight_dtype, gather=gathered)
+    dw_up = grouped_gemm_k(d_up, saved["rows"], route, hp, wp, out_dtype=weight_dtype, gather=gathered)
     if (wp, hp) != (width, hidden):
         d_rows = repitch(d_rows, 1, capacity, wp, capacity, width)
         dw_gate, dw_up = (repitch(w, experts, hp, wp, hidden, width) for w in (dw_gate, dw_up))

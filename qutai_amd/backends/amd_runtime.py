@@ -60,7 +60,7 @@ SIGNATURES = {
     "qutai_amd_route_workspace_size": [_i64, _i64, _i64],
     "qutai_amd_route_gather": [_p, _p, _p, _i64, _i64, _i32, _i32, _p],
     "qutai_amd_combine": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _p],
-    "qutai_amd_gemm_grouped_k": [_p, _p, _p, _p, _i32, _i64, _i64, _i64, _i32, _i32, _i32, _p],
+    "qutai_amd_gemm_grouped_k": [_p, _p, _p, _p, _i32, _i64, _i64, _i64, _i32, _i32, _i32, _p, _i64, _p],
     "qutai_amd_combine_backward": [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p],
     "qutai_amd_route_backward": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p],
     "qutai_amd_scale": [_p, _p, _i64, _f64, _i32, _p],

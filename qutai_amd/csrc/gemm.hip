@@ -257,9 +257,10 @@ __global__ void __launch_bounds__(64 * RWAVES) remainder_columns(const void* a, 
 enum Tile { TILE_L8D2, TILE_L8R, TILE_L4D2, TILE_S, TILE_N, TILE_W, TILE_H, TILE_T, TILE_U, TILE_S2, TILE_R, TILE_P,
             TILE_COUNT };
 
-template <bool F32, bool TA, bool TB, int BM, int BN, int WM, int WN, int BK, int ST, bool DMA, bool SWIGLU = false>
+template <bool F32, bool TA, bool TB, int BM, int BN, int WM, int WN, int BK, int ST, bool DMA, bool SWIGLU = false,
+          bool GATHER_B = false>
 hipError_t launch_cfg(GemmArgs p, hipStream_t stream) {
-  typedef GemmKernel<F32, TA, TB, BM, BN, WM, WN, BK, ST, DMA, SWIGLU> Kern;
+  typedef GemmKernel<F32, TA, TB, BM, BN, WM, WN, BK, ST, DMA, SWIGLU, GATHER_B> Kern;
   int64_t tiles_n = (p.N + Kern::BNO - 1) / Kern::BNO;
   if (p.groups == 0) p.tiles_m = (int)((p.M + BM - 1) / BM);
   int64_t blocks = (int64_t)p.tiles_m * tiles_n * (p.groups ? 1 : p.batch);
@@ -318,6 +319,18 @@ hipError_t launch_tile(Tile tile, GemmArgs p, hipStream_t stream) {
         if (forced_tile() < 0 && pingpong_fits(p)) return launch_pingpong<TA, TB>(p, stream);
       return launch_cfg<F32, TA, TB, 256, 256, 2, 4, KR, 2, true>(p, stream);
   }
+}
+
+// Grouped-K products whose B K rows are read through GemmArgs::b_rows: the
+// two-stage direct-to-LDS tiles (192x256 and 256x192 for bf16, else 256x256).
+template <bool F32>
+hipError_t launch_gathered_k(Tile tile, const GemmArgs& p, hipStream_t stream) {
+  constexpr int KR = F32 ? 32 : 64;
+  if constexpr (!F32) {
+    if (tile == TILE_T) return launch_cfg<F32, true, false, 192, 256, 2, 4, KR, 2, true, false, true>(p, stream);
+    if (tile == TILE_U) return launch_cfg<F32, true, false, 256, 192, 4, 2, KR, 2, true, false, true>(p, stream);
+  }
+  return launch_cfg<F32, true, false, 256, 256, 2, 4, KR, 2, true, false, true>(p, stream);
 }
 
 template <bool F32>
@@ -986,7 +999,8 @@ int qutai_amd_gemm_swiglu(const void* a, const void* w_gate, const void* w_up, v
 }
 
 int qutai_amd_gemm_grouped_k(const void* a, const void* b, void* out, const int64_t* offsets, int groups, int64_t rows,
-                             int64_t cols, int64_t total_k, int dtype, int out_dtype, int accumulate, void* stream_) {
+                             int64_t cols, int64_t total_k, int dtype, int out_dtype, int accumulate,
+                             const int64_t* gather, int64_t source_rows, void* stream_) {
   hipStream_t stream = (hipStream_t)stream_;
   if (groups <= 0 || rows < 0 || cols < 0 || total_k < 0) return QA_EINVAL;
   if (dtype != QA_BF16 && dtype != QA_F32) return QA_EINVAL;
@@ -1016,6 +1030,14 @@ int qutai_amd_gemm_grouped_k(const void* a, const void* b, void* out, const int6
   int64_t es = dtype == QA_BF16 ? 2 : 4;
   if ((p.lda * 256 * es) >= (1ll << 31) || (p.ldb * 256 * es) >= (1ll << 31)) return QA_EINVAL;
   Tile tile = choose_tile(rows, cols, total_k / groups + 1, groups, dtype == QA_BF16);
+  if (gather) {
+    // row offsets into b are 32-bit byte offsets of one buffer descriptor
+    if (source_rows < 0 || source_rows * cols * es >= (1ll << 31)) return QA_EINVAL;
+    p.b_rows = gather;
+    p.b_bytes = source_rows * cols * es;
+    return (int)(dtype == QA_F32 ? launch_gathered_k<true>(tile, p, stream)
+                                 : launch_gathered_k<false>(tile, p, stream));
+  }
   hipError_t err = dtype == QA_F32 ? launch_mma<true>(tile, true, false, p, stream)
                                    : launch_mma<false>(tile, true, false, p, stream);
   return (int)err;

@@ -80,6 +80,12 @@ struct GemmArgs {
   const void* b2;
   void* gate_out;
   void* up_out;
+  // Gathered K rows (grouped-K mode, MN-major B, kernels built with GATHER_B):
+  // K row k of B is row b_rows[k] of b (b_bytes = b's size in bytes), so the
+  // routed token rows of a weight gradient need no copy of their own; an
+  // index outside b's rows reads zeros.
+  const int64_t* b_rows;
+  int64_t b_bytes;
 };
 
 
@@ -155,8 +161,9 @@ struct OperandTile {
 // blocks) and the up weight (odd blocks) at the same N index, so each wave's
 // two 32-column accumulator blocks hold gate and up of the same outputs and
 // the epilogue writes silu(gate) * up: an output tile is BN / 2 wide.
+// GATHER_B: grouped-K mode with B's K rows read through GemmArgs::b_rows.
 template <bool F32, bool TA, bool TB, int BM, int BN, int WM, int WN, int BK, int STAGES, bool DMA,
-          bool SWIGLU = false>
+          bool SWIGLU = false, bool GATHER_B = false>
 struct GemmKernel {
   typedef MmaTraits<F32> Tr;
   typedef typename Tr::T T;
@@ -167,6 +174,7 @@ struct GemmKernel {
   static constexpr int FM = TM / 32, FN = TN / 32;  // 32x32 blocks per wave
   static constexpr int BNO = SWIGLU ? BN / 2 : BN;  // output columns per tile
   static_assert(!SWIGLU || (!F32 && !TA && TB && DMA && FN == 2), "SwiGLU: bf16 NT, two blocks per wave");
+  static_assert(!GATHER_B || (!TB && DMA && STAGES == 2), "gathered K rows: MN-major B, two-stage DMA ring");
   static constexpr bool KA = !TA;                   // A K-major?
   static constexpr bool KB = TB;                    // B K-major?
   typedef OperandTile<F32, KA, BM, BK> TileA;
@@ -363,13 +371,15 @@ struct GemmKernel {
     const T* B_tail = reinterpret_cast<const T*>(p.b_tail);
     int64_t M = p.M, row0 = 0, K = p.K;
     const int64_t* gather = nullptr;  // grouped mode with a_rows: this group's row indices
+    const int64_t* gather_b = nullptr;  // GATHER_B: this group's K-row indices into b
     char* outp = reinterpret_cast<char*>(p.out);
     const int osize = p.out_bf16 ? 2 : 4;
     if (p.group_k) {
       // per-group K range; an empty group writes zeros (or keeps `out`)
       const int64_t k_lo = p.offsets[bz], k_hi = p.offsets[bz + 1];
       A += k_lo * (KA ? 1 : p.lda);
-      B += k_lo * (KB ? 1 : p.ldb);
+      if constexpr (GATHER_B) gather_b = p.b_rows + k_lo;
+      else B += k_lo * (KB ? 1 : p.ldb);
       outp += bz * p.sc * osize;
       row0 = (int64_t)tile_m * BM;
       K = k_hi - k_lo;
@@ -490,7 +500,20 @@ struct GemmKernel {
         ob[j] = (uint32_t)(((int64_t)outer * ldb + c * E) * (int64_t)sizeof(T));
         kb[j] = KB ? c * E : outer;
         vb[j] = KB ? (col0 + outer < N) : (col0 + c * E < N);
+        if constexpr (GATHER_B) ob[j] = (uint32_t)(c * E * (int)sizeof(T));  // byte offset inside a source row
       }
+      // GATHER_B: the source rows of this lane's chunks for the stage issued
+      // next (rows[]) and the one after (rows_next[], loaded one K step ahead
+      // so that the copies never wait for their index); -1 = no row (past the
+      // group's K range or N), read as zeros like an index outside b.
+      const int64_t b_count = GATHER_B ? p.b_bytes / (ldb * (int64_t)sizeof(T)) : 0;
+      int64_t rows[GATHER_B ? JB : 1], rows_next[GATHER_B ? JB : 1];
+      auto fetch_rows = [&](int64_t (&dst)[GATHER_B ? JB : 1], int64_t k0) {
+        if constexpr (GATHER_B) {
+#pragma unroll
+          for (int j = 0; j < JB; j++) dst[j] = (vb[j] && k0 + kb[j] < K) ? gather_b[k0 + kb[j]] : -1;
+        }
+      };
       char* base = reinterpret_cast<char*>(lds);
       // copies of one stage, optionally only instructions [first, last)
       auto issue_range = [&](int stage, int64_t k0, int first, int last) {
@@ -500,8 +523,9 @@ struct GemmKernel {
         const T* at = tail ? a_tail_tile : a_tile;
         const T* bt = tail ? B_tail : B;
         const u32x4 da = lds_rsrc(KA ? at + kk : at + kk * lda, a_span);
-        const u32x4 db = lds_rsrc(KB ? bt + col0 * ldb + kk : bt + kk * ldb + col0,
-                                  (int64_t)(KB ? BN * ldb : BK * ldb) * (int64_t)sizeof(T));
+        const u32x4 db = GATHER_B ? lds_rsrc(B + col0, p.b_bytes - col0 * (int64_t)sizeof(T))
+                                  : lds_rsrc(KB ? bt + col0 * ldb + kk : bt + kk * ldb + col0,
+                                             (int64_t)(KB ? BN * ldb : BK * ldb) * (int64_t)sizeof(T));
         const u32x4 db2 = SWIGLU ? lds_rsrc(B2 + col0 * ldb + k0, (int64_t)BN * ldb * (int64_t)sizeof(T)) : db;
         const int64_t krem = K - k0;
         char* sa = base + stage * STAGE * (int)sizeof(T);
@@ -512,13 +536,27 @@ struct GemmKernel {
             lds_load16(da, sa + (j * NW + wave) * 1024, (va[j] && ka[j] < krem) ? oa[j] : OOB);
 #pragma unroll
         for (int j = 0; j < JB; j++)
-          if (JA + j >= first && JA + j < last)
-            lds_load16(up[j] ? db2 : db, sb + (j * NW + wave) * 1024, (vb[j] && kb[j] < krem) ? ob[j] : OOB);
+          if (JA + j >= first && JA + j < last) {
+            uint32_t off = (vb[j] && kb[j] < krem) ? ob[j] : OOB;
+            if constexpr (GATHER_B) {
+              // the row's 32-bit byte offset from b + col0 (b is below 2 GiB)
+              const int64_t r = rows[j];
+              off = (r >= 0 && r < b_count) ? (uint32_t)(r * ldb * (int64_t)sizeof(T)) + ob[j] : OOB;
+            }
+            lds_load16(up[j] ? db2 : db, sb + (j * NW + wave) * 1024, off);
+          }
       };
       auto issue = [&](int stage, int64_t k0) { issue_range(stage, k0, 0, L); };
+      if constexpr (GATHER_B) {
+        // two stages: stage 0's rows now, stage 1's ahead of the loop
+        fetch_rows(rows, 0);
+        if (nk > 0) issue(0, 0);
+        fetch_rows(rows_next, BK);
+      } else {
 #pragma unroll
-      for (int st = 0; st < STAGES - 1; st++)
-        if (st < nk) issue(st, (int64_t)st * BK);
+        for (int st = 0; st < STAGES - 1; st++)
+          if (st < nk) issue(st, (int64_t)st * BK);
+      }
       for (int kt = 0; kt < nk; kt++) {
         // this wave's copies of stage kt are done when at most the copies of
         // the (up to STAGES-2) younger stages are still outstanding
@@ -528,6 +566,13 @@ struct GemmKernel {
         else if (younger == 1) wait_vm<L>();
         else wait_vm<0>();
         barrier();  // every wave's copies of stage kt are in LDS; stage kt-1 is free
+        if constexpr (GATHER_B) {
+          // rows_next (loaded during the previous step, complete after the
+          // vmcnt wait above) belong to stage kt + 1, issued in this step
+#pragma unroll
+          for (int j = 0; j < JB; j++) rows[j] = rows_next[j];
+          fetch_rows(rows_next, (int64_t)(kt + 2) * BK);
+        }
         const T* sa = lds + (kt % STAGES) * STAGE;
         const bool more = kt + STAGES - 1 < nk;
         const int next = (kt + STAGES - 1) % STAGES;

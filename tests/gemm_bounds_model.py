@@ -353,10 +353,52 @@ def grouped_pair_gemm(cfg: Config, f32: bool, counts: list[int], inner: int, col
         grouped_gemm(cfg, f32, counts, inner, cols, transpose_right)
 
 
-def grouped_k_gemm(cfg: Config, f32: bool, counts: list[int], rows: int, cols: int):
+def gathered_k_loads(cfg: Config, f32: bool, col0: int, cols: int, k_lo: int, k_len: int, gather: np.ndarray,
+                     source_rows: int, index_check: bool = True):
+    """Every load of an MN-major B whose K rows are gathered (GATHER_B): the
+    chunk of k row `outer` in the step at k0 reads row gather[k_lo + k0 +
+    outer] of the [source_rows][cols] matrix -- the index is read only for
+    k0 + outer < k_len and a column inside N, so the table is never read past
+    the group -- through a descriptor based at column col0 that spans the
+    rest of the matrix, with a 32-bit byte offset; an index outside the rows
+    gets the out-of-range offset (without index_check -- a planted mistake --
+    it is issued with its wrapped offset, and one that lands on a real row is
+    reported)."""
+    e, es = (4, 4) if f32 else (8, 2)
+    if cfg.stages != 2 or not cfg.dma:
+        raise ValueError("gathered K rows run on the two-stage direct-to-LDS tiles only")
+    alloc = source_rows * cols
+    q = np.arange(cfg.bn * cfg.bk // e)
+    outer, c = chunk_coords(f32, False, cfg.bn, cfg.bk, q)
+    valid = col0 + c * e < cols
+    span = min(alloc * es - col0 * es, RANGE_CAP)
+    for kt in range((k_len + cfg.bk - 1) // cfg.bk):
+        k = kt * cfg.bk + outer
+        read = valid & (k < k_len)
+        at = k_lo + k[read]
+        if at.size and (at.min() < 0 or at.max() >= gather.size):
+            raise Violation("B: an index read outside the route order")
+        src = np.full(q.size, -1, dtype=np.int64)
+        src[read] = gather[at]
+        inside = read & (src >= 0) & (src < source_rows)
+        wrapped = ((src * cols) * es + c * e * es) & 0xFFFFFFFF
+        issued = inside if index_check else read
+        offs = np.where(issued, wrapped, OOB)
+        hit = offs + 16 <= span
+        if np.any(inside & ~hit):
+            raise Violation("B (gathered): an in-matrix chunk falls outside the descriptor range")
+        if not index_check and np.any(read & ~inside & hit):
+            raise Violation("B (gathered): an index outside the source reads a real row")
+        lo = col0 * es + offs[hit]
+        _check("B (gathered) load", lo, lo + 16, alloc * es)
+
+
+def grouped_k_gemm(cfg: Config, f32: bool, counts: list[int], rows: int, cols: int,
+                   gather: np.ndarray | None = None, source_rows: int = 0, index_check: bool = True):
     """qutai_amd_gemm_grouped_k: out[g] = A_g^T B_g over the K rows
     [offsets[g], offsets[g+1]) of a [capacity][rows] and b [capacity][cols]
-    (A and B MN-major, ta = 1, tb = 0)."""
+    (A and B MN-major, ta = 1, tb = 0); with gather, K row k of B is row
+    gather[k] of a [source_rows][cols] token matrix (gathered_k_loads)."""
     offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
     capacity = int(offsets[-1])
     pa = plan_operand(rows, capacity, 1, 0, f32)
@@ -369,8 +411,12 @@ def grouped_k_gemm(cfg: Config, f32: bool, counts: list[int], rows: int, cols: i
             for tn in range(tiles_n):
                 operand_loads(cfg, f32, False, cfg.bm, k_lo * pa.ld, tm * cfg.bm, rows, k_hi - k_lo, pa.ld,
                               pa.alloc, "A")
-                operand_loads(cfg, f32, False, cfg.bn, k_lo * pb.ld, tn * cfg.bn, cols, k_hi - k_lo, pb.ld,
-                              pb.alloc, "B")
+                if gather is not None:
+                    gathered_k_loads(cfg, f32, tn * cfg.bn, cols, k_lo, k_hi - k_lo, gather, source_rows,
+                                     index_check)
+                else:
+                    operand_loads(cfg, f32, False, cfg.bn, k_lo * pb.ld, tn * cfg.bn, cols, k_hi - k_lo, pb.ld,
+                                  pb.alloc, "B")
                 output_stores(cfg, True, g * rows * cols, tm * cfg.bm, tn * cfg.bn, rows, cols, cols,
                               len(counts) * rows * cols, vec)
 

@@ -163,6 +163,37 @@ def test_grouped_k_products_stay_in_bounds(f32):
         gm.grouped_k_gemm(cfg, f32, counts, rows, cols)
 
 
+@pytest.mark.parametrize("f32", [False, True], ids=["bf16", "fp32"])
+def test_grouped_k_gathered_rows_stay_in_bounds(f32):
+    """The weight gradients reading the token rows through the route order
+    (GATHER_B, on the two-stage tiles the host maps every choice to): ragged
+    groups, empty groups, column counts that are not a multiple of the tile
+    and order entries outside the token matrix."""
+    rng = np.random.default_rng(SEED + 19 + f32)
+    for cfg in [c for c in gm.tile_configs(f32) if c.name in ("L8D2", "T", "U")]:
+        counts = _counts(rng, 6, int(rng.integers(1, 900)))
+        rows, cols = (int(v) * (4 if f32 else 8) for v in rng.integers(1, 40, size=2))
+        tokens = int(sum(counts)) + 5
+        order = rng.integers(0, tokens, size=sum(counts))
+        gm.grouped_k_gemm(cfg, f32, counts, rows, cols, gather=order, source_rows=tokens)
+        if order.size > 3:
+            order[:3] = [tokens, -1, (1 << 32) // (cols * (4 if f32 else 2)) + 1]
+            gm.grouped_k_gemm(cfg, f32, counts, rows, cols, gather=order, source_rows=tokens)
+
+
+def test_model_reports_a_gathered_k_index_past_the_source():
+    """A planted mistake: the gathered-K kernel without its index check
+    issues an order entry past the token rows with its wrapped 32-bit
+    offset, which lands on row 1 (2^32 / 128 + 1 rows of 64 bf16)."""
+    cfg = gm.tile_configs(False)[0]
+    order = np.arange(8)
+    gm.grouped_k_gemm(cfg, False, [3, 0, 5], 16, 64, gather=order, source_rows=8)
+    order[4] = (1 << 32) // 128 + 1
+    gm.grouped_k_gemm(cfg, False, [3, 0, 5], 16, 64, gather=order, source_rows=8)
+    with pytest.raises(gm.Violation):
+        gm.grouped_k_gemm(cfg, False, [3, 0, 5], 16, 64, gather=order, source_rows=8, index_check=False)
+
+
 def test_short_k_strips_stay_in_bounds():
     rng = np.random.default_rng(SEED + 17)
     for m, k, n, batch in [(700, 64, 1040, 2), (129, 24, 144, 3), (64, 8, 2064, 1), (2048, 64, 256, 1)]:

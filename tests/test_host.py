@@ -279,14 +279,14 @@ def test_scatter_grouping_is_a_stable_counting_sort():
 
 
 def test_moe_forward_reads_rows_through_the_order_only_below_2_gib():
-    """The routed-row read inside the grouped GEMM addresses the token
-    matrix with 32-bit offsets (qutai_amd_gemm_grouped / _swiglu refuse a
-    token matrix of 2 GiB or more on that path), so larger inputs, and the
-    training forward, take the gathered copy."""
+    """The routed-row read inside the grouped GEMMs addresses the token
+    matrix with 32-bit offsets (qutai_amd_gemm_grouped / _swiglu / _grouped_k
+    refuse a token matrix of 2 GiB or more on that path), so larger inputs
+    take the gathered copy, in the forward alone and in training."""
     from qutai_amd.backends import amd_lm
 
-    assert amd_lm._rows_through_order(8192 * 2048 * 2, save=False, dtype="bfloat16")
-    assert not amd_lm._rows_through_order(8192 * 2048 * 2, save=True, dtype="bfloat16")
-    assert not amd_lm._rows_through_order(1 << 31, save=False, dtype="bfloat16")
-    assert amd_lm._rows_through_order((1 << 31) - 2, save=False, dtype="bfloat16")
-    assert not amd_lm._rows_through_order(1024, save=False, dtype="float64")
+    assert amd_lm._rows_through_order(8192 * 2048 * 2, dtype="bfloat16")
+    assert amd_lm._rows_through_order(8192 * 2048 * 4, dtype="float32")
+    assert not amd_lm._rows_through_order(1 << 31, dtype="bfloat16")
+    assert amd_lm._rows_through_order((1 << 31) - 2, dtype="bfloat16")
+    assert not amd_lm._rows_through_order(1024, dtype="float64")

@@ -62,12 +62,16 @@ def step():
         wd=stored(wd, "bfloat16").reshape(EXPERTS, WIDTH, HIDDEN),
         order=_i64(route["order"]), offsets=_i64(route["offsets"]), locations=_i64(route["locations"]),
         indices=_i64(route["indices"]), weights=download(route["weights"]).astype(np.float64),
-        rows=download(saved["rows"]).reshape(-1, WIDTH), gate=download(saved["gate"]).reshape(-1, HIDDEN),
+        saved_rows=download(saved["rows"]).reshape(-1, WIDTH), gathered=saved["gathered"],
+        gate=download(saved["gate"]).reshape(-1, HIDDEN),
         up=download(saved["up"]).reshape(-1, HIDDEN), act=download(saved["act"]).reshape(-1, HIDDEN),
         down=download(saved["down"]).reshape(-1, WIDTH), y=download(y).reshape(TOKENS, WIDTH),
         dx=download(dx).reshape(TOKENS, WIDTH), d_weights=download(d_weights).astype(np.float64),
         dwg=download(dwg).reshape(EXPERTS, HIDDEN, WIDTH), dwu=download(dwu).reshape(EXPERTS, HIDDEN, WIDTH),
         dwd=download(dwd).reshape(EXPERTS, WIDTH, HIDDEN), d_logits=download(d_logits).astype(np.float64))
+    # the expert-major routed rows every product reads (through the order
+    # inside the GEMMs, or from the saved copy)
+    host["rows"] = host["x"][host["order"]] if host["gathered"] else host["saved_rows"]
     host["expert_of"] = np.searchsorted(host["offsets"], np.arange(TOKENS * TOP_K), side="right") - 1
     # row of (token, slot) in the expert-major block: the expert's offset
     # plus the slot's location within the expert's rows
@@ -82,13 +86,16 @@ def _sample_tokens(count=24):
 
 def test_routing_matches_the_oracle_and_rows_are_gathered(step):
     """Routing indices, weights and the expert-major order against
-    cpu_lm.routing; the saved block is the token rows in that order."""
+    cpu_lm.routing; the token matrix (32 MiB) is read through that order by
+    the forward's gate/up GEMM and the backward's dW_gate / dW_up, so the
+    saved rows are the token matrix itself, not a routed copy."""
     ref = ora.routing(step["logits"].astype(np.float64).tolist(), TOKENS, EXPERTS, TOP_K)
     assert step["indices"].tolist() == list(ref["indices"])
     assert np.max(np.abs(step["weights"] - np.array(ref["weights"]))) <= 1e-6
     order = np.concatenate([np.array(ids, dtype=np.int64) for ids in ref["ids"]])
     assert step["order"].tolist() == order.tolist()
-    assert np.array_equal(step["rows"], step["x"][step["order"]])
+    assert step["gathered"]
+    assert np.array_equal(step["saved_rows"], step["x"])
 
 
 def test_expert_forward_rows(step):

@@ -79,9 +79,13 @@ def test_grouped_swiglu_matches_unfused_bit_for_bit(amd, lm, tokens, width, hidd
     assert np.array_equal(words(gate)[:used], words(gate_ref)[:used])
     assert np.array_equal(words(up)[:used], words(up_ref)[:used])
     assert np.array_equal(words(act)[:used], words(act_ref)[:used])
-    # rows read through the route's order inside the GEMM: the same values
+    # rows read through the route's order inside the GEMM: the same values,
+    # with and without the saved products (the training forward)
     act_g = lm.swiglu_gemm(xs, gs, us, 0, width, hidden, route=route, gather=True)
     assert np.array_equal(words(act_g)[:used], words(act)[:used])
+    act_gs, gate_gs, up_gs = lm.swiglu_gemm(xs, gs, us, 0, width, hidden, route=route, gather=True, save=True)
+    for got, ref in ((act_gs, act), (gate_gs, gate), (up_gs, up)):
+        assert np.array_equal(words(got)[:used], words(ref)[:used])
     # float64 check on every expert's first and last row
     offsets = download(route["offsets"]).astype(int).tolist()
     xr = stored(download(rows), "bfloat16").reshape(-1, width)
@@ -115,6 +119,51 @@ def test_grouped_gemm_gather_equals_gathered_block(amd, lm, dtype, tokens, width
     if top_k > 1:
         with pytest.raises(ValueError):  # the gathered form takes the token matrix
             lm.grouped_gemm(rows, ws, route, width, cols, gather=True, out_dtype=dtype)
+
+
+@pytest.mark.parametrize("dtype,tokens,rows,cols,experts,top_k", [
+    ("bfloat16", 1500, 200, 256, 8, 2), ("bfloat16", 8192, 1408, 2048, 8, 2), ("bfloat16", 700, 2048, 1408, 8, 2),
+    ("float32", 900, 96, 132, 4, 2), ("bfloat16", 40, 64, 8, 16, 1)])
+def test_grouped_k_gather_equals_gathered_block(amd, lm, dtype, tokens, rows, cols, experts, top_k):
+    """The grouped-K weight-gradient GEMM reading B's K rows (the token rows)
+    through `order` is bit-identical to the GEMM over the gathered block:
+    config 5's dW_gate shape, uneven experts, empty experts (16 experts over
+    40 tokens), K ranges that end inside a K step, ragged column tiles."""
+    logits = normal(tokens + 5, tokens * experts)
+    route = lm.routing(upload(logits, "float32"), tokens, experts, top_k)
+    xs = upload(normal(tokens + 6, tokens * cols), dtype)
+    a = upload(normal(tokens + 7, route["capacity"] * rows), dtype)
+    block = lm.route_gather_all(xs, route, cols)
+    for out_dtype in ("float32", dtype):
+        ref = download(lm.grouped_gemm_k(a, block, route, rows, cols, out_dtype=out_dtype))
+        got = download(lm.grouped_gemm_k(a, xs, route, rows, cols, out_dtype=out_dtype, gather=True))
+        assert np.array_equal(got, ref), out_dtype
+    if top_k > 1:
+        with pytest.raises(ValueError):  # the gathered form takes the token matrix
+            lm.grouped_gemm_k(a, block, route, rows, cols, gather=True)
+
+
+def test_grouped_k_gather_index_outside_the_tokens_reads_zeros(amd, lm):
+    """Order entries outside the token rows (the row count, -1, and an index
+    whose 32-bit byte offset would wrap onto row 1: 2^32 / 128 + 1 rows of
+    64 bf16) contribute zero rows to the weight gradients."""
+    from array import array
+
+    tokens, rows, cols, experts = 40, 16, 64, 4
+    route = lm.routing(upload(normal(80, tokens * experts), "float32"), tokens, experts, 2)
+    xs = upload(normal(81, tokens * cols), "bfloat16")
+    a = upload(normal(82, route["capacity"] * rows), "bfloat16")
+    order = np.frombuffer(route["order"].to_array(), dtype=np.int64).copy()
+    bad = {3: tokens, 10: -1, 17: (1 << 32) // 128 + 1}
+    for position, index in bad.items():
+        order[position] = index
+    broken = dict(route, order=amd.storage(array("q", order.tolist()), dtype="int64"))
+    got = download(lm.grouped_gemm_k(a, xs, broken, rows, cols, gather=True))
+    # the reference block: the gathered rows with the broken positions zeroed
+    block = stored(download(xs), "bfloat16").reshape(tokens, cols)[np.clip(order, 0, tokens - 1)]
+    block[list(bad)] = 0
+    ref = download(lm.grouped_gemm_k(a, upload(block.ravel(), "bfloat16"), route, rows, cols))
+    assert np.array_equal(got, ref)
 
 
 def test_grouped_gemm_gather_index_outside_the_tokens_reads_zeros(amd, lm):
