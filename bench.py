@@ -93,15 +93,21 @@ def gemm_square(dtype, n=4096, seed=1, out_dtype=None):
             {**config, "out": out_dtype, "call": "gemm"})
 
 
-def gemm_ragged(dtype, seed=1):
+def gemm_ragged(dtype, seed=1, order="MNK"):
+    """BASELINE's ragged edge shape 4095x4097x1000 in both axis orders: "MNK"
+    reads it as M x N x K (A 4095x1000, B 1000x4097, a 4095x4097 output),
+    "MKN" as the reference's (rows, inner, cols) convention (A 4095x4097,
+    B 4097x1000, a 4095x1000 output).  fp32 output through ``amd.gemm``
+    (the reference gemm's default)."""
     from qutai_amd.backends import amd
 
-    m, n, k = 4095, 4097, 1000
+    m, n, k = (4095, 4097, 1000) if order == "MNK" else (4095, 1000, 4097)
     rng = np.random.default_rng(seed)
     a = upload(rng.standard_normal(m * k) * k ** -0.5, dtype)
     b = upload(rng.standard_normal(k * n) * k ** -0.5, dtype)
     out = amd.full(m * n, 0.0, dtype="float32")
-    return (lambda: amd.gemm(a, b, m, k, n, out=out)), 2.0 * m * n * k, {"M": m, "N": n, "K": k, "storage": dtype}
+    return ((lambda: amd.gemm(a, b, m, k, n, out=out)), 2.0 * m * n * k,
+            {"M": m, "N": n, "K": k, "storage": dtype, "axis_order": order})
 
 
 def attention_bmm(seed=2):
@@ -300,6 +306,8 @@ WORKLOADS = {
     "gemm_fp32_4096": (lambda: gemm_square("float32"), "fp32"),
     "gemm_bf16_ragged": (lambda: gemm_ragged("bfloat16"), "bf16"),
     "gemm_fp32_ragged": (lambda: gemm_ragged("float32"), "fp32"),
+    "gemm_bf16_ragged_mkn": (lambda: gemm_ragged("bfloat16", order="MKN"), "bf16"),
+    "gemm_fp32_ragged_mkn": (lambda: gemm_ragged("float32", order="MKN"), "fp32"),
     "attention_bmm": (attention_bmm, "bf16"),
     "attention_fused": (attention_fused, "bf16"),
     "attention_fused_causal": (lambda: attention_fused(causal=True), "bf16"),

@@ -82,46 +82,74 @@ __global__ void __launch_bounds__(256) gemm_f64(const double* a, const double* b
 // for i < inner (converted to the compute type; fp32 -> bf16 rounds to
 // nearest even) and 0 in the padding up to `pitch`.  Used when an fp32
 // operand feeds the bf16 MFMA path (mixed inputs, autocast) or when the
-// operand's rows are not 16-byte aligned.  One thread per 16-byte chunk of
-// the destination (E = 8 bf16 or 4 fp32 values; pitch is a multiple of E),
-// element loads that are contiguous across a wavefront and one 16-byte
-// store.  One launch covers the rows [row_base, row_base + rows) with
+// operand's rows are not 16-byte aligned.  Each thread fills PREP_CHUNKS
+// 16-byte chunks of the destination (E = 8 bf16 or 4 fp32 values; pitch is
+// a multiple of E) with loads that are contiguous across a wavefront, all in
+// flight before the 16-byte stores (one per thread measured fastest: the
+// grid then keeps every CU's wave slots busy).  One launch covers the rows [row_base, row_base + rows) with
 // 32-bit chunk indices (rows * pitch / E < 2^31; the host splits larger
 // operands into several launches), the row's (batch, row) pair in 64 bits.
+struct PrepareArgs {
+  const void* src;
+  void* dst;
+  int64_t row_base, outer, stride;
+  uint32_t rows, inner, pitch;
+};
+
+// One destination chunk i (16 bytes) of the re-layout, loaded and packed.
 template <bool SRC_BF16, bool DST_BF16>
-__global__ void __launch_bounds__(256) prepare_operand(const void* src, void* dst, int64_t row_base, uint32_t rows,
-                                                       int64_t outer, uint32_t inner, uint32_t pitch,
-                                                       int64_t stride) {
+__device__ __forceinline__ u32x4 prepare_load(const PrepareArgs& a, uint32_t i) {
   constexpr int E = DST_BF16 ? 8 : 4;
-  const uint32_t per_row = pitch / E;
-  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
-  if (i >= rows * per_row) return;
+  const uint32_t per_row = a.pitch / E;
   const uint32_t r = i / per_row, c0 = (i - r * per_row) * E;
-  const int64_t row = row_base + r, z = row / outer, o = row - z * outer;
-  const int64_t at = z * stride + o * inner + c0;
-  char* d = (char*)dst + (row_base * per_row + i) * 16;
+  const int64_t row = a.row_base + r, z = row / a.outer, o = row - z * a.outer;
+  const int64_t at = z * a.stride + o * a.inner + c0;
   if constexpr (SRC_BF16 && DST_BF16) {
-    if (c0 + E <= inner) {
+    if (c0 + E <= a.inner) {
       // a whole chunk inside the row: one 16-byte load at the element's own
       // (2-byte) alignment -- unaligned global loads are enabled on this
       // platform, and the compiler emits the same for an unaligned memcpy
       u32x4 w;
-      __builtin_memcpy(&w, (const char*)src + at * 2, 16);
-      global_store(d, w);
-      return;
+      __builtin_memcpy(&w, (const char*)a.src + at * 2, 16);
+      return w;
     }
   }
   float v[E];
 #pragma unroll
   for (int t = 0; t < E; t++) {
     v[t] = 0.f;
-    if (c0 + t < inner) v[t] = SRC_BF16 ? bf16_to_f32(((const bf16_t*)src)[at + t]) : ((const float*)src)[at + t];
+    if (c0 + t < a.inner)
+      v[t] = SRC_BF16 ? bf16_to_f32(((const bf16_t*)a.src)[at + t]) : ((const float*)a.src)[at + t];
   }
   if constexpr (DST_BF16)
-    global_store(d, u32x4{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
-                          pack_bf16x2(v[6], v[7])});
+    return u32x4{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
   else
-    global_store(d, f32x4{v[0], v[1], v[2], v[3]});
+    return u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
+}
+
+// PREP_CHUNKS chunks per thread, 256 apart (a wavefront's loads stay
+// contiguous).
+constexpr int PREP_CHUNKS = 1;
+template <bool SRC_BF16, bool DST_BF16>
+__device__ __forceinline__ void prepare_chunks(const PrepareArgs& a, uint32_t block) {
+  constexpr int E = DST_BF16 ? 8 : 4;
+  const uint32_t total = a.rows * (a.pitch / E);
+  u32x4 w[PREP_CHUNKS];
+#pragma unroll
+  for (int q = 0; q < PREP_CHUNKS; q++) {
+    const uint32_t i = (block * PREP_CHUNKS + q) * 256u + threadIdx.x;
+    if (i < total) w[q] = prepare_load<SRC_BF16, DST_BF16>(a, i);
+  }
+#pragma unroll
+  for (int q = 0; q < PREP_CHUNKS; q++) {
+    const uint32_t i = (block * PREP_CHUNKS + q) * 256u + threadIdx.x;
+    if (i < total) global_store((char*)a.dst + (a.row_base * (a.pitch / E) + i) * 16, w[q]);
+  }
+}
+
+template <bool SRC_BF16, bool DST_BF16>
+__global__ void __launch_bounds__(256) prepare_operand(PrepareArgs a) {
+  prepare_chunks<SRC_BF16, DST_BF16>(a, blockIdx.x);
 }
 
 // Split-K reduction: out[b][e] = sum over s of part[b * splits + s][e] in
@@ -143,81 +171,114 @@ __global__ void splitk_reduce(const float* part, void* out, int64_t n, int64_t t
 }
 
 // Column remainder of at most 8 columns with a K-major A (the last r
-// columns of a 256 q + r wide product), in two small launches:
-// gather_columns copies B's r columns once into a compact fp32 block
-// [r][pitch] (zero beyond K; every workgroup of the second launch would
-// otherwise fetch the same scattered elements, one cache line each, at the
-// same time), then remainder_columns computes one output row per wave:
-// 16-byte A loads and the matching column values spread over the lanes,
-// fp32 sums per lane in K order and a fixed xor tree over the lanes, then
-// the GEMM epilogue's accumulate and rounding.  Planned operands only: A's
-// rows are 16-byte aligned and zero-padded to its pitch, so no 16-byte chunk
-// crosses the allocation; `pitch` is K rounded up to 8.
-template <bool BF16, bool KB>
-__global__ void __launch_bounds__(256) gather_columns(const void* b, float* cols, int64_t K, int64_t ldb, int r,
-                                                      int64_t pitch) {
-  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (t >= r * pitch) return;
-  const int64_t j = t / pitch, k = t - j * pitch;
-  float v = 0.f;
-  if (k < K) {
-    const int64_t at = KB ? j * ldb + k : k * ldb + j;
-    v = BF16 ? bf16_to_f32(((const bf16_t*)b)[at]) : ((const float*)b)[at];
-  }
-  cols[t] = v;
-}
+// columns of a 256 q + r wide product): a workgroup of RWAVES waves computes
+// RWAVES * RROWS output rows.  It stages B's r columns for KC values of k at
+// a time in LDS as fp32 (zero beyond K; each element rounded to the compute
+// type first, so an fp32 B read in place gives what its re-laid-out bf16
+// copy would), while every wave's 16-byte loads of its rows of A for the
+// same KC values are in flight:
+// lane l sums the 16-byte chunks l, l + 64, ... of its row in K order
+// (KC is a multiple of 64 chunks, so the staging does not change that
+// order), then a fixed xor tree over the lanes, then the GEMM epilogue's
+// accumulate and rounding.  A is a planned operand: rows 16-byte aligned and
+// zero-padded to its pitch, so no 16-byte chunk crosses the allocation.  B is
+// read at its source dtype and pitch (b_bf16, kb: K-major), r columns from
+// column `col`.
+constexpr int RWAVES = 4, RROWS = 4, RBLOCK = RWAVES * RROWS, RKC = 1024;
+struct RemainderArgs {
+  const void* a;
+  const void* b;
+  void* out;
+  int64_t M, K, lda, ldb, ldc, col;
+  int r, out_bf16, accumulate;
+};
 
-constexpr int RWAVES = 4, RROWS = 4;  // waves per workgroup, rows per wave
-template <bool BF16>
-__global__ void __launch_bounds__(64 * RWAVES) remainder_columns(const void* a, const float* cols, void* out,
-                                                                 int64_t M, int64_t K, int64_t lda, int64_t pitch,
-                                                                 int64_t ldc, int r, int out_bf16, int accumulate) {
+template <bool BF16, bool B_BF16, bool KB>
+__device__ __forceinline__ void remainder_block(const RemainderArgs& p, int64_t block, float* cols) {
   constexpr int E = BF16 ? 8 : 4;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t row0 = ((int64_t)blockIdx.x * RWAVES + wave) * RROWS;
+  constexpr int NC = RKC / E / 64;  // 16-byte chunks per lane and row in one staged block
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t row0 = block * RBLOCK + wave * RROWS;
+  const int r = p.r;
   float acc[RROWS][8];
 #pragma unroll
   for (int i = 0; i < RROWS; i++)
 #pragma unroll
     for (int j = 0; j < 8; j++) acc[i][j] = 0.f;
-  for (int64_t c = lane; c * E < K; c += 64) {
-    u32x4 w[RROWS];
+  for (int64_t kc = 0; kc < p.K; kc += RKC) {
+    // this block's A chunks first (in flight while B's columns are staged)
+    const int64_t chunks = (std::min<int64_t>(p.K - kc, RKC) + E - 1) / E;
+    u32x4 w[RROWS][NC];
 #pragma unroll
-    for (int i = 0; i < RROWS; i++) {
-      const int64_t m = row0 + i;
-      w[i] = u32x4{0u, 0u, 0u, 0u};
-      if (m < M) w[i] = *(const u32x4*)((const char*)a + (m * lda + c * E) * (BF16 ? 2 : 4));
-    }
-    float bv[8][E];
+    for (int i = 0; i < RROWS; i++)
 #pragma unroll
-    for (int j = 0; j < 8; j++)
-#pragma unroll
-      for (int e = 0; e < E; e += 4) {
-        f32x4 v = {0.f, 0.f, 0.f, 0.f};
-        if (j < r) v = *(const f32x4*)(cols + j * pitch + c * E + e);
-        bv[j][e] = v[0];
-        bv[j][e + 1] = v[1];
-        bv[j][e + 2] = v[2];
-        bv[j][e + 3] = v[3];
+      for (int q = 0; q < NC; q++) {
+        const int64_t m = row0 + i, c = lane + 64 * q;
+        w[i][q] = u32x4{0u, 0u, 0u, 0u};
+        if (m < p.M && c < chunks) w[i][q] = *(const u32x4*)((const char*)p.a + (m * p.lda + kc + c * E) * (BF16 ? 2 : 4));
       }
+    __syncthreads();  // the previous block's columns are no longer read
+    // cols[j][k - kc] = B(k, col + j) in the compute type; MN-major B: the
+    // r columns of one k are neighbours, so a wave reads whole row segments
+    // (four loads in flight per thread: the elements of an MN-major B sit
+    // in as many rows, one cache line each)
+    for (int t0 = 0; t0 < r * RKC; t0 += 4 * 64 * RWAVES) {
+      float v[4];
 #pragma unroll
-    for (int i = 0; i < RROWS; i++) {
-      float x[E];
-      if constexpr (BF16) {
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-          x[2 * q] = __uint_as_float(w[i][q] << 16);
-          x[2 * q + 1] = __uint_as_float(w[i][q] & 0xffff0000u);
+      for (int u = 0; u < 4; u++) {
+        const int t = t0 + u * 64 * RWAVES + tid;
+        const int j = KB ? t / RKC : t % r, kk = KB ? t % RKC : t / r;
+        const int64_t k = kc + kk;
+        v[u] = 0.f;
+        if (t < r * RKC && k < p.K) {
+          const int64_t at = KB ? (p.col + j) * p.ldb + k : k * p.ldb + p.col + j;
+          v[u] = B_BF16 ? bf16_to_f32(((const bf16_t*)p.b)[at]) : ((const float*)p.b)[at];
+          if (BF16 && !B_BF16) v[u] = bf16_to_f32(f32_to_bf16(v[u]));
         }
-      } else {
-#pragma unroll
-        for (int q = 0; q < 4; q++) x[q] = __uint_as_float(w[i][q]);
       }
 #pragma unroll
-      for (int e = 0; e < E; e++)
+      for (int u = 0; u < 4; u++) {
+        const int t = t0 + u * 64 * RWAVES + tid;
+        const int j = KB ? t / RKC : t % r, kk = KB ? t % RKC : t / r;
+        if (t < r * RKC) cols[j * RKC + kk] = v[u];
+      }
+    }
+    __syncthreads();
 #pragma unroll
-        for (int j = 0; j < 8; j++)
-          if (j < r) acc[i][j] = __builtin_fmaf(x[e], bv[j][e], acc[i][j]);
+    for (int q = 0; q < NC; q++) {
+      const int64_t c = lane + 64 * q;
+      if (c >= chunks) break;
+      float bv[8][E];
+#pragma unroll
+      for (int j = 0; j < 8; j++)
+#pragma unroll
+        for (int e = 0; e < E; e += 4) {
+          f32x4 v = {0.f, 0.f, 0.f, 0.f};
+          if (j < r) v = *(const f32x4*)(cols + j * RKC + c * E + e);
+          bv[j][e] = v[0];
+          bv[j][e + 1] = v[1];
+          bv[j][e + 2] = v[2];
+          bv[j][e + 3] = v[3];
+        }
+#pragma unroll
+      for (int i = 0; i < RROWS; i++) {
+        float x[E];
+        if constexpr (BF16) {
+#pragma unroll
+          for (int h = 0; h < 4; h++) {
+            x[2 * h] = __uint_as_float(w[i][q][h] << 16);
+            x[2 * h + 1] = __uint_as_float(w[i][q][h] & 0xffff0000u);
+          }
+        } else {
+#pragma unroll
+          for (int h = 0; h < 4; h++) x[h] = __uint_as_float(w[i][q][h]);
+        }
+#pragma unroll
+        for (int e = 0; e < E; e++)
+#pragma unroll
+          for (int j = 0; j < 8; j++)
+            if (j < r) acc[i][j] = __builtin_fmaf(x[e], bv[j][e], acc[i][j]);
+      }
     }
   }
 #pragma unroll
@@ -228,14 +289,31 @@ __global__ void __launch_bounds__(64 * RWAVES) remainder_columns(const void* a, 
       if (j >= r) break;
       float v = acc[i][j];
       for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-      if (lane == j && m < M) {
-        const int64_t at = m * ldc + j;
-        if (accumulate) v += out_bf16 ? bf16_to_f32(((const bf16_t*)out)[at]) : ((const float*)out)[at];
-        if (out_bf16) ((bf16_t*)out)[at] = f32_to_bf16(v);
-        else ((float*)out)[at] = v;
+      if (lane == j && m < p.M) {
+        const int64_t at = m * p.ldc + j;
+        if (p.accumulate) v += p.out_bf16 ? bf16_to_f32(((const bf16_t*)p.out)[at]) : ((const float*)p.out)[at];
+        if (p.out_bf16) ((bf16_t*)p.out)[at] = f32_to_bf16(v);
+        else ((float*)p.out)[at] = v;
       }
     }
   }
+}
+
+template <bool BF16, bool B_BF16, bool KB>
+__global__ void __launch_bounds__(64 * RWAVES) remainder_columns(RemainderArgs p) {
+  __shared__ __attribute__((aligned(16))) float cols[8 * RKC];
+  remainder_block<BF16, B_BF16, KB>(p, blockIdx.x, cols);
+}
+
+// B's re-layout and the column remainder in one launch: they are
+// independent (the remainder reads B at its source pitch), so the first
+// `rem_blocks` workgroups compute remainder rows while the others copy B;
+// the large-tile launch that reads the re-laid-out B follows on the stream.
+template <bool SRC_BF16, bool BF16, bool KB>
+__global__ void __launch_bounds__(256) prepare_remainder(PrepareArgs a, RemainderArgs p, unsigned rem_blocks) {
+  __shared__ __attribute__((aligned(16))) float cols[8 * RKC];
+  if (blockIdx.x < rem_blocks) remainder_block<BF16, SRC_BF16, KB>(p, blockIdx.x, cols);
+  else prepare_chunks<SRC_BF16, BF16>(a, blockIdx.x - rem_blocks);
 }
 
 // Kernel configurations: (BM x BN, WM x WN waves, BK, LDS stages, staging).
@@ -584,26 +662,69 @@ void plan(int64_t rows, int64_t inner, int64_t cols, int64_t batch, int64_t left
 // a valid operand does); larger operands take several launches.
 bool prepare_fits(const Operand& o) { return o.pitch < (1ll << 31) && o.inner < (1ll << 32); }
 
+// The re-layout launches of one operand: rows [base, base + r) per launch,
+// r * pitch / E below 2^31 chunks.
+int prepare_launches(const Operand& o, bool bf16) {
+  const int64_t rows = o.batches * o.outer, per_row = o.pitch / (bf16 ? 8 : 4);
+  const int64_t step = std::max<int64_t>(1, ((1ll << 31) - 1) / per_row);
+  return (int)((rows + step - 1) / step);
+}
+
+PrepareArgs prepare_args(const Operand& o, bool bf16, char* ws, int64_t base, uint32_t rows) {
+  PrepareArgs a;
+  a.src = o.ptr;
+  a.dst = ws;
+  a.row_base = base;
+  a.outer = o.outer;
+  a.stride = o.src_stride;
+  a.rows = rows;
+  a.inner = (uint32_t)o.inner;
+  a.pitch = (uint32_t)o.pitch;
+  (void)bf16;
+  return a;
+}
+
 void launch_prepare(Operand& o, int src_dtype, bool bf16, char* ws, hipStream_t stream) {
   const int64_t rows = o.batches * o.outer, per_row = o.pitch / (bf16 ? 8 : 4);
   const int64_t step = std::max<int64_t>(1, ((1ll << 31) - 1) / per_row);  // rows per launch
-  const uint32_t in = (uint32_t)o.inner, pi = (uint32_t)o.pitch;
   for (int64_t base = 0; base < rows; base += step) {
     const uint32_t r = (uint32_t)std::min<int64_t>(step, rows - base);
-    const dim3 grid((unsigned)(((int64_t)r * per_row + 255) / 256));
-    if (src_dtype == QA_BF16 && bf16)
-      hipLaunchKernelGGL((prepare_operand<true, true>), grid, dim3(256), 0, stream, o.ptr, (void*)ws, base, r, o.outer,
-                         in, pi, o.src_stride);
-    else if (bf16)
-      hipLaunchKernelGGL((prepare_operand<false, true>), grid, dim3(256), 0, stream, o.ptr, (void*)ws, base, r,
-                         o.outer, in, pi, o.src_stride);
-    else if (src_dtype == QA_BF16)
-      hipLaunchKernelGGL((prepare_operand<true, false>), grid, dim3(256), 0, stream, o.ptr, (void*)ws, base, r,
-                         o.outer, in, pi, o.src_stride);
-    else
-      hipLaunchKernelGGL((prepare_operand<false, false>), grid, dim3(256), 0, stream, o.ptr, (void*)ws, base, r,
-                         o.outer, in, pi, o.src_stride);
+    const dim3 grid((unsigned)(((int64_t)r * per_row + 256 * PREP_CHUNKS - 1) / (256 * PREP_CHUNKS)));
+    const PrepareArgs a = prepare_args(o, bf16, ws, base, r);
+    if (src_dtype == QA_BF16 && bf16) hipLaunchKernelGGL((prepare_operand<true, true>), grid, dim3(256), 0, stream, a);
+    else if (bf16) hipLaunchKernelGGL((prepare_operand<false, true>), grid, dim3(256), 0, stream, a);
+    else if (src_dtype == QA_BF16) hipLaunchKernelGGL((prepare_operand<true, false>), grid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((prepare_operand<false, false>), grid, dim3(256), 0, stream, a);
   }
+  o.ptr = ws;
+}
+
+// The column remainder alone (B used in place: its source dtype is the
+// compute type).
+void launch_remainder(const RemainderArgs& r, bool bf16, bool kb, hipStream_t stream) {
+  const dim3 grid((unsigned)((r.M + RBLOCK - 1) / RBLOCK)), block(64 * RWAVES);
+  if (bf16 && kb) hipLaunchKernelGGL((remainder_columns<true, true, true>), grid, block, 0, stream, r);
+  else if (bf16) hipLaunchKernelGGL((remainder_columns<true, true, false>), grid, block, 0, stream, r);
+  else if (kb) hipLaunchKernelGGL((remainder_columns<false, false, true>), grid, block, 0, stream, r);
+  else hipLaunchKernelGGL((remainder_columns<false, false, false>), grid, block, 0, stream, r);
+}
+
+// B's re-layout (one launch) with the column remainder in the same grid.
+void launch_prepare_remainder(Operand& o, int src_dtype, bool bf16, bool kb, char* ws, const RemainderArgs& r,
+                              hipStream_t stream) {
+  const int64_t rows = o.batches * o.outer, per_row = o.pitch / (bf16 ? 8 : 4);
+  const unsigned rem = (unsigned)((r.M + RBLOCK - 1) / RBLOCK);
+  const dim3 grid((unsigned)(rem + (rows * per_row + 256 * PREP_CHUNKS - 1) / (256 * PREP_CHUNKS)));
+  const PrepareArgs a = prepare_args(o, bf16, ws, 0, (uint32_t)rows);
+  const bool sb = src_dtype == QA_BF16;
+  if (sb && bf16 && kb) hipLaunchKernelGGL((prepare_remainder<true, true, true>), grid, dim3(256), 0, stream, a, r, rem);
+  else if (sb && bf16) hipLaunchKernelGGL((prepare_remainder<true, true, false>), grid, dim3(256), 0, stream, a, r, rem);
+  else if (bf16 && kb) hipLaunchKernelGGL((prepare_remainder<false, true, true>), grid, dim3(256), 0, stream, a, r, rem);
+  else if (bf16) hipLaunchKernelGGL((prepare_remainder<false, true, false>), grid, dim3(256), 0, stream, a, r, rem);
+  else if (sb && kb) hipLaunchKernelGGL((prepare_remainder<true, false, true>), grid, dim3(256), 0, stream, a, r, rem);
+  else if (sb) hipLaunchKernelGGL((prepare_remainder<true, false, false>), grid, dim3(256), 0, stream, a, r, rem);
+  else if (kb) hipLaunchKernelGGL((prepare_remainder<false, false, true>), grid, dim3(256), 0, stream, a, r, rem);
+  else hipLaunchKernelGGL((prepare_remainder<false, false, false>), grid, dim3(256), 0, stream, a, r, rem);
   o.ptr = ws;
 }
 
@@ -686,7 +807,7 @@ int plan_windows(int64_t rows, int64_t inner, int64_t cols, int64_t batch, bool 
     x.chunk = 0;
     x.splits = inner > 0 && !x.rows_kernel ? choose_split(rows, x.n, inner, batch, &x.tile, bf16, &x.chunk) : 1;
     x.partial = x.splits > 1 ? split_bytes(rows, x.n, batch, x.splits) : 0;
-    if (x.rows_kernel) x.partial = ((size_t)x.n * ((inner + 7) / 8 * 8) * 4 + 255) / 256 * 256;  // compact columns
+
   }
   return count;
 }
@@ -745,6 +866,26 @@ int qutai_amd_gemm(const void* a, const void* b, void* out, int64_t rows, int64_
   size_t partial = 0;
   for (int i = 0; i < count; i++) partial += w[i].partial;
   char* part = nullptr;
+  // the column remainder's arguments: A as planned (re-laid out before it
+  // runs), B's r columns from column c0 of `b_ptr` (row pitch ldb_src)
+  const int osize_ = out_dtype == QA_BF16 ? 2 : 4;
+  auto remainder_args = [&](const void* a_ptr, const void* b_ptr, const Window& x, int64_t ldb_src) {
+    RemainderArgs r = {};
+    r.a = a_ptr;
+    r.b = b_ptr;
+    r.out = (char*)out + x.c0 * osize_;
+    r.M = rows;
+    r.K = inner;
+    r.lda = pa.ld;
+    r.ldb = ldb_src;
+    r.ldc = cols;
+    r.col = x.c0;
+    r.r = (int)x.n;
+    r.out_bf16 = out_dtype == QA_BF16 ? 1 : 0;
+    r.accumulate = accumulate ? 1 : 0;
+    return r;
+  };
+  bool fused_remainder = false;
   if (inner > 0 && ((pa.copy && !prepare_fits(pa)) || (pb.copy && !prepare_fits(pb)))) return QA_EINVAL;
   if (inner > 0 && (pa.copy || pb.copy || partial)) {
     size_t need = (pa.copy ? pa.bytes : 0) + (pb.copy ? pb.bytes : 0) + partial + 256;
@@ -755,7 +896,15 @@ int qutai_amd_gemm(const void* a, const void* b, void* out, int64_t rows, int64_
       ws += pa.bytes;
     }
     if (pb.copy) {
-      launch_prepare(pb, b_dtype, bf16, ws, stream);
+      // B's re-layout shares its launch with a column remainder (which reads
+      // B at its source pitch and dtype) when it takes one launch
+      if (count == 2 && w[1].rows_kernel && prepare_launches(pb, bf16) == 1) {
+        fused_remainder = true;
+        launch_prepare_remainder(pb, b_dtype, bf16, transpose_right, ws,
+                                 remainder_args(pa.ptr, b, w[1], transpose_right ? inner : cols), stream);
+      } else {
+        launch_prepare(pb, b_dtype, bf16, ws, stream);
+      }
       ws += pb.bytes;
     }
     if (partial) part = ws;
@@ -808,33 +957,12 @@ int qutai_amd_gemm(const void* a, const void* b, void* out, int64_t rows, int64_
       q.vec_c = vec_out(window_part, q.ldc, q.sc);
     }
     if (x.rows_kernel) {
-      // B's columns into the compact block (the window's workspace), then rows
-      float* cols_ws = (float*)part;
-      part += x.partial;
-      const int64_t pitch = (inner + 7) / 8 * 8;
-      const unsigned gblocks = (unsigned)((x.n * pitch + 255) / 256);
-      if (bf16 && transpose_right)
-        hipLaunchKernelGGL((gather_columns<true, true>), dim3(gblocks), dim3(256), 0, stream, q.b, cols_ws, inner,
-                           q.ldb, (int)x.n, pitch);
-      else if (bf16)
-        hipLaunchKernelGGL((gather_columns<true, false>), dim3(gblocks), dim3(256), 0, stream, q.b, cols_ws, inner,
-                           q.ldb, (int)x.n, pitch);
-      else if (transpose_right)
-        hipLaunchKernelGGL((gather_columns<false, true>), dim3(gblocks), dim3(256), 0, stream, q.b, cols_ws, inner,
-                           q.ldb, (int)x.n, pitch);
-      else
-        hipLaunchKernelGGL((gather_columns<false, false>), dim3(gblocks), dim3(256), 0, stream, q.b, cols_ws, inner,
-                           q.ldb, (int)x.n, pitch);
-      const unsigned blocks = (unsigned)((rows + RWAVES * RROWS - 1) / (RWAVES * RROWS));
-      const int bf = out_dtype == QA_BF16 ? 1 : 0, acc = accumulate ? 1 : 0;
-      if (bf16)
-        hipLaunchKernelGGL((remainder_columns<true>), dim3(blocks), dim3(64 * RWAVES), 0, stream, q.a, cols_ws,
-                           (void*)window_out, rows, inner, q.lda, pitch, q.ldc, (int)x.n, bf, acc);
-      else
-        hipLaunchKernelGGL((remainder_columns<false>), dim3(blocks), dim3(64 * RWAVES), 0, stream, q.a, cols_ws,
-                           (void*)window_out, rows, inner, q.lda, pitch, q.ldc, (int)x.n, bf, acc);
-      const hipError_t err = hipGetLastError();
-      if (err != hipSuccess) return (int)err;
+      // the last r columns: done with B's re-layout, or one launch of their own
+      if (!fused_remainder) {
+        launch_remainder(remainder_args(q.a, pb.ptr, x, pb.ld), bf16, transpose_right, stream);
+        const hipError_t err = hipGetLastError();
+        if (err != hipSuccess) return (int)err;
+      }
       continue;
     }
     if (!window_part && count == 1 && ((x.tile == TILE_S2 && forced_tile() < 0) || x.tile == TILE_R) &&

@@ -274,26 +274,35 @@ def window_gemm(cfg: Config, f32: bool, m: int, k: int, n: int, c0: int, width: 
                     output_stores(cfg, out_f32, c0, tm * cfg.bm, tn * cfg.bn, m, width, n, m * n, vec)
 
 
-def remainder_rows(f32: bool, m: int, k: int, n: int, c0: int, width: int, tb: bool):
-    """gather_columns + remainder_columns (gemm.hip): the last `width` <= 8
-    columns of a plain product with a K-major A.  The gather reads B's
-    elements (k, c0 + j) for k < K, j < width into a [width][pitch] block
-    (pitch = K rounded up to 8); each wave row m < M reads A's row in 16-byte
-    chunks c * E < K and the block's matching values; out's (m, c0 + j) at
-    pitch n."""
+def remainder_rows(f32: bool, m: int, k: int, n: int, c0: int, width: int, tb: bool, b_source: bool = False,
+                   b_f32: bool | None = None):
+    """remainder_columns / prepare_remainder (gemm.hip): the last `width` <= 8
+    columns of a plain product with a K-major A.  Each workgroup stages B's
+    elements (k, c0 + j), k < K, j < width, KC values of k at a time
+    into an LDS block [8][KC] (KC = 1024); B is the planned operand, or with b_source the
+    caller's own B (source pitch and dtype b_f32) that the fused re-layout
+    launch reads.  Each wave row m < M reads A's row in 16-byte chunks
+    c * E < K (KC / E chunks per staged block) and the block's matching
+    values; out's (m, c0 + j) at pitch n."""
     e, es = (4, 4) if f32 else (8, 2)
+    kc = 1024
     pa = plan_operand(k, m, 1, m * k, f32)
-    pb = plan_operand(k if tb else n, n if tb else k, 1, k * n, f32)
-    pitch = (k + 7) // 8 * 8
+    if b_source:
+        b_f32 = f32 if b_f32 is None else b_f32
+        ld, alloc, bes = (k if tb else n), k * n, (4 if b_f32 else 2)
+    else:
+        pb = plan_operand(k if tb else n, n if tb else k, 1, k * n, f32)
+        ld, alloc, bes = pb.ld, pb.alloc, es
     kk = np.arange(k)[:, None]
     j = np.arange(width)[None, :]
-    at = ((c0 + j) * pb.ld + kk) if tb else (kk * pb.ld + c0 + j)
-    _check("remainder B load", at.ravel() * es, at.ravel() * es + es, pb.alloc * es)
-    chunks = np.arange((k + e - 1) // e)
-    lo = ((np.arange(m)[:, None] * pa.ld + chunks[None, :] * e) * es).ravel()
-    _check("remainder A load", lo, lo + 16, pa.alloc * es)
-    lo = ((np.arange(width)[:, None] * pitch + chunks[None, :] * e) * 4).ravel()
-    _check("remainder column load", lo, lo + e * 4, width * pitch * 4)
+    at = ((c0 + j) * ld + kk) if tb else (kk * ld + c0 + j)
+    _check("remainder B load", at.ravel() * bes, at.ravel() * bes + bes, alloc * bes)
+    for k0 in range(0, k, kc):
+        chunks = np.arange((min(k - k0, kc) + e - 1) // e)
+        if chunks.size * e > kc:
+            raise Violation("remainder: a chunk past the staged LDS block")
+        lo = ((np.arange(m)[:, None] * pa.ld + k0 + chunks[None, :] * e) * es).ravel()
+        _check("remainder A load", lo, lo + 16, pa.alloc * es)
     at = (np.arange(m)[:, None] * n + c0 + j).ravel()
     _check("remainder store", at * 4, at * 4 + 4, m * n * 4)
 

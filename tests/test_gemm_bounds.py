@@ -101,6 +101,10 @@ def test_column_windows_stay_in_bounds():
                             gm.window_gemm(cfg, f32, m, k, n, n - r, r, ta, tb, splits=splits)
                     if not ta and r <= 8:
                         gm.remainder_rows(f32, m, k, n, n - r, r, tb)
+                        # fused with B's re-layout: B read at its source pitch
+                        # and dtype (bf16 compute of an fp32 B: autocast)
+                        gm.remainder_rows(f32, m, k, n, n - r, r, tb, b_source=True, b_f32=True)
+                        gm.remainder_rows(f32, m, k, n, n - r, r, tb, b_source=True, b_f32=f32)
 
 def _counts(rng, groups, total):
     cuts = np.sort(rng.integers(0, total + 1, size=groups - 1))
