@@ -66,13 +66,11 @@ struct PingPong {
   // s_waitcnt lgkmcnt(0) with vmcnt / expcnt left at their maxima
   __device__ static __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
-  // buffer_load_dwordx4 ... lds of 16 bytes per lane: descriptor base `base`
-  // (uniform), `range` bytes valid from it (beyond: zeros), LDS destination
-  // `m0` (lane l at m0 + 16 l).  Same contract as lds_load16.
-  __device__ static __forceinline__ void copy16(uint64_t base, uint32_t range, uint32_t m0, uint32_t voffset) {
-    const u32x4 d = {(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)base),
-                     (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(base >> 32) & 0xffffu),
-                     (uint32_t)__builtin_amdgcn_readfirstlane(range), 0x00020000u};
+  // buffer_load_dwordx4 ... lds of 16 bytes per lane through descriptor d
+  // (beyond its range: zeros) to LDS byte address m0 (lane l at m0 + 16 l).
+  // Same contract as lds_load16, with the LDS address as a plain 32-bit
+  // value (address 0 is a valid LDS address, not a null pointer).
+  __device__ static __forceinline__ void copy16(u32x4 d, uint32_t m0, uint32_t voffset) {
     asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(voffset), "s"(d)
                  : "memory", "m0");
   }
@@ -230,11 +228,16 @@ struct PingPong {
       const uint64_t base = (uint64_t)(uintptr_t)tile + (uint64_t)kk * 2;
       const uint32_t range = uniform32(r64 <= 0 ? 0u : r64 > 0x7ffffff0 ? 0x7ffffff0u : (uint32_t)r64);
       const uint32_t dst = uniform32((xa ? a_slot(k) : b_slot(k)) + w4 * 1024);
+      // one descriptor for the step's eight copies, instruction j's rows at
+      // + j * step_bytes in the lane offset: lane bytes at or past `range`
+      // read zeros exactly as with a descriptor based at the instruction's
+      // own rows (range - j * step_bytes left), and the offsets stay below
+      // 256 rows of the operand (< 2^31 bytes, the host's check)
+      const u32x4 d = {(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)base),
+                       (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(base >> 32) & 0xffffu),
+                       (uint32_t)__builtin_amdgcn_readfirstlane(range), 0x00020000u};
 #pragma unroll
-      for (int j = 0; j < 8; j++) {
-        const uint32_t off = j * step_bytes;
-        copy16(base + off, range > off ? range - off : 0u, dst + j * 4096, vo[j & 1]);
-      }
+      for (int j = 0; j < 8; j++) copy16(d, dst + j * 4096, vo[j & 1] + j * step_bytes);
     };
 
     // ---- fragment reads and products --------------------------------------------
