@@ -430,7 +430,8 @@ def main():
     if value is not None:
         line["roofline"] = {"bound": "mfma", "achieved": value, "peak": PEAK["bf16"], "unit": "TFLOP/s",
                             "frac": round(value / PEAK["bf16"], 4), "traffic": traffic,
-                            "kernel": "gemm_entry<GemmKernel<bf16 NN, 256x256 tile, 8 waves, BK 64, direct-to-LDS>>",
+                            "kernel": "pingpong_entry<PingPong<bf16 NN>> (256x256 tile, 8 waves in two phase "
+                                      "groups, BK 64, direct-to-LDS A/B rings)",
                             "algorithmic_flops_per_launch": 2 * 4096 ** 3}
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
