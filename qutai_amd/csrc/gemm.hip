@@ -30,7 +30,7 @@ __global__ void __launch_bounds__(Kern::NT) pingpong_entry(GemmArgs p) {
 }
 
 template <class Kern>
-__global__ void __launch_bounds__(Kern::NT) short_entry(ShortArgs p) {
+__global__ void __launch_bounds__(Kern::NT, Kern::MIN_BLOCKS) short_entry(ShortArgs p) {
   __shared__ __attribute__((aligned(16))) char smem[Kern::LDS_BYTES];
   Kern::run(p, smem);
 }
@@ -736,6 +736,9 @@ void launch_prepare_remainder(Operand& o, int src_dtype, bool bf16, bool kb, cha
 // holds at least 16 rounds of the two workgroups a CU runs at once.  Config
 // 3's score product (128 x 2048 x 2048, K 64): 208 us with one chunk per
 // workgroup, 181-185 us with 2, 4 or 8 (the rule gives 4), 200 us with 16.
+// The two-slot ring (50 KiB of LDS) under a 168-register cap fits three
+// workgroups per CU instead of two: 179-183 -> 166-170 us alone, the bmm
+// sequence 789 -> 772 us, bit-identical.
 bool short_fits(const GemmArgs& p, bool bf16, bool ta, bool tb) {
   return bf16 && !ta && tb && p.out_bf16 && !p.accumulate && p.K > 0 && p.K <= 64 && p.N % 16 == 0 &&
          p.vec_c == 2 && p.ldc * 128 * 2 < (1ll << 31);
@@ -759,12 +762,12 @@ hipError_t launch_short(const GemmArgs& p, hipStream_t stream) {
   s.tiles_m = (int)((p.M + 127) / 128);
   s.chunks = (int)((p.N + 127) / 128);
   int strip = s.chunks;
-  const int64_t slots = 2 * cu_count();
+  typedef ShortKernel<2> Kern;
+  const int64_t slots = Kern::MIN_BLOCKS * cu_count();
   while (strip > 1 && p.batch * s.tiles_m * ((s.chunks + strip - 1) / strip) < 16 * slots) strip = (strip + 1) / 2;
   s.strip_chunks = strip;
   s.strips = (s.chunks + strip - 1) / strip;
   if (p.batch * s.tiles_m * s.strips > 0x7fffffff) return hipErrorInvalidValue;
-  typedef ShortKernel<3> Kern;
   hipLaunchKernelGGL(short_entry<Kern>, dim3((unsigned)(p.batch * s.tiles_m * s.strips)), dim3(Kern::NT), 0, stream,
                      s);
   return hipGetLastError();

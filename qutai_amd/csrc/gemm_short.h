@@ -10,7 +10,8 @@
 // workgroups of a row block write neighbouring chunks of the same rows at
 // the same time:
 //  * the B chunks move HBM/L2 -> LDS with direct-to-LDS buffer loads into a
-//    SLOTS-deep ring, SLOTS - 1 chunks ahead of the MFMAs;
+//    SLOTS-deep ring, SLOTS - 1 chunks ahead of the MFMAs (two slots: three
+//    workgroups fit per CU, which keeps more stores in flight);
 //  * the MFMAs compute the transposed block (B rows as the first operand), so
 //    a lane's accumulators hold four consecutive columns of one row; one
 //    gfx950 lane-half swap (v_permlane32_swap) gives every lane eight
@@ -55,6 +56,9 @@ struct ShortKernel {
   static constexpr int OPS = 8;                    // stores per wave and chunk
   static constexpr uint32_t OOB = 0x80000000u;
   static_assert(J == 4 && SLOTS >= 2 && SLOTS <= 3, "shape");
+  // workgroups per CU the launch bounds ask for: with two slots the LDS
+  // (50 KiB) and a 168-register cap fit three (12 waves per CU)
+  static constexpr int MIN_BLOCKS = SLOTS == 2 ? 3 : 2;
 
   template <int N>
   __device__ static __forceinline__ void wait_vm() {

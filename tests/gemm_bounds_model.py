@@ -438,7 +438,7 @@ def short_strip(m: int, k: int, n: int, batch: int, strip: int):
     assert k <= 64 and n % 16 == 0
     pa = plan_operand(k, m, batch, m * k, False)
     pb = plan_operand(k, n, batch, n * k, False)
-    cfg = Config("R", 128, 128, 2, 2, 64, 3)
+    cfg = Config("R", 128, 128, 2, 2, 64, 2)
     tiles_m, chunks = (m + 127) // 128, (n + 127) // 128
     # strip s sweeps chunks s, s + strips, ... (strips = ceil(chunks / strip)):
     # every chunk belongs to exactly one strip
