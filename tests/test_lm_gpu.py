@@ -179,8 +179,8 @@ def test_config5_grouped_expert_gemm_and_moe_forward(amd, lm):
         assert ora.rel_frobenius(gate[sample], exact) <= FP32_TOL
     # full expert SwiGLU + combine against a float64 composition on sampled tokens
     y = download(lm.moe_experts_forward(xs, route, gs, us, ds, width, hidden)).reshape(rows, width)
-    # the forward alone gathers inside the GEMM, the training forward copies
-    # the routed rows first: the same output bits
+    # the forward alone and the training forward (which also writes the gate
+    # and up products for the backward) give the same output bits
     y_saved, _ = lm.moe_experts_forward(xs, route, gs, us, ds, width, hidden, save=True)
     assert np.array_equal(download(y_saved).reshape(rows, width), y)
     ur = stored(w_up, "bfloat16").reshape(experts, hidden, width)

@@ -174,13 +174,15 @@ def test_sparse_moe_layer_forward_and_all_gradients(lm):
     assert sum(layer.last_counts) == tokens * top_k
 
 
-@pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
-def test_backward_through_the_order_equals_the_gathered_copy(lm, dtype):
+@pytest.mark.parametrize("dtype,width,hidden", [("bfloat16", 256, 200), ("float32", 256, 200),
+                                                ("bfloat16", 36, 20)])
+def test_backward_through_the_order_equals_the_gathered_copy(lm, dtype, width, hidden):
     """The training forward reads the token rows through the route's order
     (no routed copy), and the backward's dW_gate / dW_up read them the same
     way: every output and gradient is bit-identical to the backward over the
-    gathered block (uneven experts, one with no rows)."""
-    tokens, width, hidden, experts, top_k = 700, 256, 200, 8, 2
+    gathered block (uneven experts, one with no rows; widths that are not a
+    multiple of 8 run on the zero-padded token matrix)."""
+    tokens, experts, top_k = 700, 8, 2
     logits = normal(95, tokens * experts)
     logits[1::experts] -= 50.0  # expert 1 gets no tokens
     route = lm.routing(upload(logits, "float32"), tokens, experts, top_k)
@@ -188,8 +190,9 @@ def test_backward_through_the_order_equals_the_gathered_copy(lm, dtype):
     ws = [upload(normal(97 + i, experts * hidden * width, 0.05), dtype) for i in range(3)]
     g = upload(normal(100, tokens * width), dtype)
     y, saved = lm.moe_experts_forward(xs, route, *ws, width, hidden, save=True)
-    assert saved["gathered"] and saved["rows"] is xs
-    copy = dict(saved, rows=lm.route_gather_all(xs, route, width), gathered=False)
+    assert saved["gathered"] and (saved["rows"] is xs) == (width % 8 == 0)
+    padded = (width + 7) // 8 * 8
+    copy = dict(saved, rows=lm.route_gather_all(saved["rows"], route, padded), gathered=False)
     through = lm.moe_experts_backward(g, route, saved, width, hidden, x_dtype=dtype, weight_dtype=dtype)
     copied = lm.moe_experts_backward(g, route, copy, width, hidden, x_dtype=dtype, weight_dtype=dtype)
     for a, b in zip(through, copied):
