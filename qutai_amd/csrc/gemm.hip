@@ -248,36 +248,30 @@ __device__ __forceinline__ void remainder_block(const RemainderArgs& p, int64_t 
     for (int q = 0; q < NC; q++) {
       const int64_t c = lane + 64 * q;
       if (c >= chunks) break;
-      float bv[8][E];
+      // one column's values at a time (few registers, so the re-layout
+      // workgroups that share this kernel keep their occupancy); every
+      // (row, column) sum still runs over its chunk's elements in order
 #pragma unroll
-      for (int j = 0; j < 8; j++)
+      for (int j = 0; j < 8; j++) {
+        if (j >= r) break;
+        float bv[E];
 #pragma unroll
         for (int e = 0; e < E; e += 4) {
-          f32x4 v = {0.f, 0.f, 0.f, 0.f};
-          if (j < r) v = *(const f32x4*)(cols + j * RKC + c * E + e);
-          bv[j][e] = v[0];
-          bv[j][e + 1] = v[1];
-          bv[j][e + 2] = v[2];
-          bv[j][e + 3] = v[3];
+          const f32x4 v = *(const f32x4*)(cols + j * RKC + c * E + e);
+          bv[e] = v[0];
+          bv[e + 1] = v[1];
+          bv[e + 2] = v[2];
+          bv[e + 3] = v[3];
         }
 #pragma unroll
-      for (int i = 0; i < RROWS; i++) {
-        float x[E];
-        if constexpr (BF16) {
+        for (int i = 0; i < RROWS; i++) {
 #pragma unroll
-          for (int h = 0; h < 4; h++) {
-            x[2 * h] = __uint_as_float(w[i][q][h] << 16);
-            x[2 * h + 1] = __uint_as_float(w[i][q][h] & 0xffff0000u);
+          for (int e = 0; e < E; e++) {
+            const uint32_t h = w[i][q][BF16 ? e >> 1 : e];
+            const float x = BF16 ? __uint_as_float((e & 1) ? (h & 0xffff0000u) : (h << 16)) : __uint_as_float(h);
+            acc[i][j] = __builtin_fmaf(x, bv[e], acc[i][j]);
           }
-        } else {
-#pragma unroll
-          for (int h = 0; h < 4; h++) x[h] = __uint_as_float(w[i][q][h]);
         }
-#pragma unroll
-        for (int e = 0; e < E; e++)
-#pragma unroll
-          for (int j = 0; j < 8; j++)
-            if (j < r) acc[i][j] = __builtin_fmaf(x[e], bv[j][e], acc[i][j]);
       }
     }
   }
@@ -300,7 +294,7 @@ __device__ __forceinline__ void remainder_block(const RemainderArgs& p, int64_t 
 }
 
 template <bool BF16, bool B_BF16, bool KB>
-__global__ void __launch_bounds__(64 * RWAVES) remainder_columns(RemainderArgs p) {
+__global__ void __launch_bounds__(64 * RWAVES, 3) remainder_columns(RemainderArgs p) {
   __shared__ __attribute__((aligned(16))) float cols[8 * RKC];
   remainder_block<BF16, B_BF16, KB>(p, blockIdx.x, cols);
 }
@@ -310,7 +304,7 @@ __global__ void __launch_bounds__(64 * RWAVES) remainder_columns(RemainderArgs p
 // `rem_blocks` workgroups compute remainder rows while the others copy B;
 // the large-tile launch that reads the re-laid-out B follows on the stream.
 template <bool SRC_BF16, bool BF16, bool KB>
-__global__ void __launch_bounds__(256) prepare_remainder(PrepareArgs a, RemainderArgs p, unsigned rem_blocks) {
+__global__ void __launch_bounds__(256, 3) prepare_remainder(PrepareArgs a, RemainderArgs p, unsigned rem_blocks) {
   __shared__ __attribute__((aligned(16))) float cols[8 * RKC];
   if (blockIdx.x < rem_blocks) remainder_block<BF16, SRC_BF16, KB>(p, blockIdx.x, cols);
   else prepare_chunks<SRC_BF16, BF16>(a, blockIdx.x - rem_blocks);
