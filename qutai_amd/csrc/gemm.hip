@@ -317,7 +317,9 @@ __global__ void __launch_bounds__(256, 3) prepare_remainder(PrepareArgs a, Remai
 //   L4D2: 256x256, 4 waves (one per SIMD, 128x128 per wave), two-stage ring
 //   S   : 128x128, 4 waves, BK 32 / 16, four-stage ring (small grids, short K)
 //   S2  : 128x128, 4 waves, BK 32 / 16, two-stage ring (bf16, K <= 64: four per CU)
-//   N   : 256x64, 4 waves (N <= 64), W : 64x256, 4 waves (M <= 64)
+//   N   : 256x64, 4 waves (N <= 64), BK 64 / 32, two-stage ring, A's copies
+//         streamed (nontemporal: one column tile reads every A row once)
+//   W   : 64x256, 4 waves (M <= 64), BK 32 / 16, four-stage ring
 //   H   : 256x128, 8 waves 4x2 (64x64 per wave), BK 64, three-stage ring
 //         (grids of 256x256 tiles that would leave half the CUs idle)
 //   T, U: 192x256 (8 waves 2x4, 96x64 per wave) and 256x192 (4x2, 64x96),
@@ -325,14 +327,14 @@ __global__ void __launch_bounds__(256, 3) prepare_remainder(PrepareArgs a, Remai
 //         short of the CU count, e.g. 5632 x 2048: 176 tiles -> 240)
 //   R   : short-K row strips (gemm_short.h): bf16 NT with K <= 64, a 128-row
 //         block of A held in registers, 128-column chunks of B through a
-//         three-slot LDS ring, stores straight from the accumulators
+//         two-slot LDS ring, 128-byte row segments staged through LDS
 enum Tile { TILE_L8D2, TILE_L8R, TILE_L4D2, TILE_S, TILE_N, TILE_W, TILE_H, TILE_T, TILE_U, TILE_S2, TILE_R, TILE_P,
             TILE_COUNT };
 
 template <bool F32, bool TA, bool TB, int BM, int BN, int WM, int WN, int BK, int ST, bool DMA, bool SWIGLU = false,
-          bool GATHER_B = false>
+          bool GATHER_B = false, bool STREAM_A = false>
 hipError_t launch_cfg(GemmArgs p, hipStream_t stream) {
-  typedef GemmKernel<F32, TA, TB, BM, BN, WM, WN, BK, ST, DMA, SWIGLU, GATHER_B> Kern;
+  typedef GemmKernel<F32, TA, TB, BM, BN, WM, WN, BK, ST, DMA, SWIGLU, GATHER_B, STREAM_A> Kern;
   int64_t tiles_n = (p.N + Kern::BNO - 1) / Kern::BNO;
   if (p.groups == 0) p.tiles_m = (int)((p.M + BM - 1) / BM);
   int64_t blocks = (int64_t)p.tiles_m * tiles_n * (p.groups ? 1 : p.batch);
@@ -376,7 +378,10 @@ hipError_t launch_tile(Tile tile, GemmArgs p, hipStream_t stream) {
     case TILE_L4D2: return launch_cfg<F32, TA, TB, 256, 256, 2, 2, KR, 2, true>(p, stream);
     case TILE_S: return launch_cfg<F32, TA, TB, 128, 128, 2, 2, KB, 4, true>(p, stream);
     case TILE_S2: return launch_cfg<F32, TA, TB, 128, 128, 2, 2, KB, 2, true>(p, stream);
-    case TILE_N: return launch_cfg<F32, TA, TB, 256, 64, 4, 1, KB, 4, true>(p, stream);
+    case TILE_N:
+      // one column tile: every A row is read by one workgroup, streamed
+      // (nontemporal copies of whole lines, K per stage 64 bf16 / 32 fp32)
+      return launch_cfg<F32, TA, TB, 256, 64, 4, 1, KR, 2, true, false, false, true>(p, stream);
     case TILE_W: return launch_cfg<F32, TA, TB, 64, 256, 1, 4, KB, 4, true>(p, stream);
     case TILE_H: return launch_cfg<F32, TA, TB, 256, 128, 4, 2, KR, 3, true>(p, stream);
     case TILE_T:

@@ -162,8 +162,11 @@ struct OperandTile {
 // two 32-column accumulator blocks hold gate and up of the same outputs and
 // the epilogue writes silu(gate) * up: an output tile is BN / 2 wide.
 // GATHER_B: grouped-K mode with B's K rows read through GemmArgs::b_rows.
+// STREAM_A: A's copies carry the nontemporal hint (lds_load16_nt), for tiles
+// that read every A element once (one column tile: the 256x64 tile of
+// outputs at most 64 wide) in whole 128-byte row segments per K step.
 template <bool F32, bool TA, bool TB, int BM, int BN, int WM, int WN, int BK, int STAGES, bool DMA,
-          bool SWIGLU = false, bool GATHER_B = false>
+          bool SWIGLU = false, bool GATHER_B = false, bool STREAM_A = false>
 struct GemmKernel {
   typedef MmaTraits<F32> Tr;
   typedef typename Tr::T T;
@@ -175,6 +178,8 @@ struct GemmKernel {
   static constexpr int BNO = SWIGLU ? BN / 2 : BN;  // output columns per tile
   static_assert(!SWIGLU || (!F32 && !TA && TB && DMA && FN == 2), "SwiGLU: bf16 NT, two blocks per wave");
   static_assert(!GATHER_B || (!TB && DMA && STAGES == 2), "gathered K rows: MN-major B, two-stage DMA ring");
+  static_assert(!STREAM_A || (DMA && (TA ? BM : BK) * (int)sizeof(typename MmaTraits<F32>::T) % 128 == 0),
+                "streamed A: direct-to-LDS copies of whole 128-byte row segments");
   static constexpr bool KA = !TA;                   // A K-major?
   static constexpr bool KB = TB;                    // B K-major?
   typedef OperandTile<F32, KA, BM, BK> TileA;
@@ -533,7 +538,11 @@ struct GemmKernel {
 #pragma unroll
         for (int j = 0; j < JA; j++)
           if (j >= first && j < last)
-            lds_load16(da, sa + (j * NW + wave) * 1024, (va[j] && ka[j] < krem) ? oa[j] : OOB);
+          {
+            const uint32_t off = (va[j] && ka[j] < krem) ? oa[j] : OOB;
+            if constexpr (STREAM_A) lds_load16_nt(da, sa + (j * NW + wave) * 1024, off);
+            else lds_load16(da, sa + (j * NW + wave) * 1024, off);
+          }
 #pragma unroll
         for (int j = 0; j < JB; j++)
           if (JA + j >= first && JA + j < last) {

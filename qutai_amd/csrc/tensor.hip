@@ -313,7 +313,10 @@ __global__ void __launch_bounds__(THREADS) softmax_rows_kernel(const T* x, T* ou
 // Row softmax, one wavefront per row (4 rows per 256-thread workgroup):
 // 16-byte loads (8 bf16 or 4 fp32 per lane), the row kept in registers for
 // up to 64 * V * CH elements, max and sum reduced inside the wavefront (no
-// LDS, no barrier).  HBM sees one read and one write of every row.
+// LDS, no barrier).  HBM sees one read and one write of every row; the
+// register-held part is read with the nontemporal hint and every store
+// carries it (config 3's 1 GiB of score rows: 365 -> 345 us); chunks beyond
+// it are read three times and keep plain loads.
 template <class T, int CH>  // CH 16-byte chunks per lane held in registers
 __global__ void __launch_bounds__(256) softmax_rows_wave(const T* x, T* out, int64_t rows, int64_t width,
                                                          float scale) {
@@ -353,7 +356,7 @@ __global__ void __launch_bounds__(256) softmax_rows_wave(const T* x, T* out, int
   for (int c = 0; c < CH; c++) {
     int at = lane + 64 * c;
     if (at < chunks) {
-      unpack(xr[at], v[c]);
+      unpack(global_load_nt<u32x4>(xr + at), v[c]);
 #pragma unroll
       for (int e = 0; e < V; e++) peak = fmaxf(peak, v[c][e]);
     }

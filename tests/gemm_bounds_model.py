@@ -51,7 +51,7 @@ def tile_configs(f32: bool) -> list[Config]:
     kb, kr = (16, 32) if f32 else (32, 64)
     table = [Config("L8D2", 256, 256, 2, 4, kr, 2), Config("L8R", 256, 256, 2, 4, kr, 2, dma=False),
              Config("L4D2", 256, 256, 2, 2, kr, 2), Config("S", 128, 128, 2, 2, kb, 4),
-             Config("S2", 128, 128, 2, 2, kb, 2), Config("N", 256, 64, 4, 1, kb, 4),
+             Config("S2", 128, 128, 2, 2, kb, 2), Config("N", 256, 64, 4, 1, kr, 2),
              Config("W", 64, 256, 1, 4, kb, 4), Config("H", 256, 128, 4, 2, kr, 3)]
     if f32:
         table += [Config("T", 256, 256, 2, 4, kr, 2), Config("U", 256, 256, 2, 4, kr, 2)]
