@@ -433,6 +433,7 @@ __global__ void combine_kernel(const T* eo, const float* w, const int64_t* idx, 
 // the expert rows, 4 chunks per lane and slot in flight at once): the
 // routing metadata is read once per row instead of once per chunk, and the
 // row's loads overlap instead of forming one dependent chain per chunk.
+// Every expert row is read once, in whole lines: streamed loads.
 // Same sums in the same order as combine_kernel.
 template <class T, class U>
 __global__ void __launch_bounds__(256) combine_rows_wave(const T* eo, const float* w, const int64_t* idx,
@@ -458,7 +459,7 @@ __global__ void __launch_bounds__(256) combine_rows_wave(const T* eo, const floa
 #pragma unroll
       for (int i = 0; i < R; i++) {
         const int64_t c = c0 + i * 64 + lane;
-        q[i] = c < chunks ? global_load<u32x4>(src + c * V) : u32x4{0, 0, 0, 0};
+        q[i] = c < chunks ? global_load_nt<u32x4>(src + c * V) : u32x4{0, 0, 0, 0};
       }
 #pragma unroll
       for (int i = 0; i < R; i++) {
