@@ -1,7 +1,7 @@
 """Every bf16 GEMM tile shape (256x256, 192x256, 256x192, 256x128, 128x128 with
-a four- or two-stage ring, the 256x256 ping-pong kernel for K a multiple of
-64, and the short-K row strips of NT products with K <= 64 and N a multiple
-of 16)
+a four- or two-stage ring, the thin 256x64 and 64x256 tiles, the 256x256
+ping-pong kernel for K a multiple of 64, and the short-K row strips of NT
+products with K <= 64 and N a multiple of 16), and every fp32 tile,
 sums K in the same order, in chunks of 64 through the same MFMA chain, so a
 tile forced with QUTAI_AMD_GEMM_TILE gives bit-identical output to any other
 for the same call: whole and ragged tiles, the four transpose forms, fp32 and
@@ -79,8 +79,30 @@ def test_forced_tiles_are_bit_identical(tmp_path):
                                         for i in range(batch)])
                 got = base[f"{m}_{k}_{n}_{batch}_{ta:d}{tb:d}_float32"]
                 assert ora.rel_frobenius(got, exact) <= 1e-2, (m, k, n, batch, ta, tb)
-    for tile in ("T", "U", "H", "S", "S2", "R", "P"):
+    for tile in ("T", "U", "H", "S", "S2", "N", "W", "R", "P"):
         other = _run(tile, tmp_path / f"{tile}.npz")
+        for key in base.files:
+            assert np.array_equal(base[key], other[key]), (tile, key)
+
+
+def test_forced_fp32_tiles_are_bit_identical(tmp_path):
+    """fp32 storage: every tile chains v_mfma_f32_32x32x2_f32 over k from 0,
+    so forcing any of them (the thin 256x64 tile with its streamed A copies
+    included) gives the same bits; the 256x256 result is checked against the
+    float64 oracle at the fp32 bar (1e-5)."""
+    cases = [(200, 130, 70, 3), (129, 40, 257, 1), (320, 64, 1040, 2), (129, 24, 144, 2), (64, 8, 600, 1)]
+    base = _run("L8D2", tmp_path / "L8D2_f32.npz", cases, "float32")
+    for m, k, n, batch in cases:
+        a, b = normal(10 + m, batch * m * k), normal(20 + n, batch * k * n)
+        for ta in (False, True):
+            for tb in (False, True):
+                exact = np.concatenate([ora.gemm_f64(a[i * m * k:(i + 1) * m * k], b[i * k * n:(i + 1) * k * n],
+                                                     m, k, n, transpose_left=ta, transpose_right=tb).ravel()
+                                        for i in range(batch)])
+                got = base[f"{m}_{k}_{n}_{batch}_{ta:d}{tb:d}_float32"]
+                assert ora.rel_frobenius(got, exact) <= 1e-5, (m, k, n, batch, ta, tb)
+    for tile in ("H", "S", "S2", "N", "W"):
+        other = _run(tile, tmp_path / f"{tile}_f32.npz", cases, "float32")
         for key in base.files:
             assert np.array_equal(base[key], other[key]), (tile, key)
 
