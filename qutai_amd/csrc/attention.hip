@@ -6,17 +6,19 @@
 // in one pass over K and V.
 //
 // Layout of the work (gfx950, 64-wide wavefronts):
-//  * a workgroup of 4 waves owns 256 consecutive queries of one (batch,
-//    head); each wave owns 64 queries as two blocks of 32 and keeps their Q
-//    fragments in registers for the whole kernel;
+//  * a workgroup owns 256 consecutive queries of one (batch, head): 8 waves
+//    of 32 queries (the default), or 4 waves of two 32-query blocks; each
+//    wave keeps its Q fragments in registers for the whole kernel; two
+//    workgroups run per CU (8-wave shape: four waves per SIMD);
 //  * K and V advance in blocks of 64 keys, copied HBM -> LDS with
 //    buffer_load ... lds into a two-stage ring (8 KiB + 8 KiB per stage); the
-//    copy of block j+1 overlaps the MFMAs of block j;
+//    copy of block j+1 overlaps the MFMAs of block j; the softmax and the
+//    value product run per 32-key half of a block;
 //  * scores are computed transposed, S^T = K Q^T, with
 //    v_mfma_f32_32x32x16_bf16: in the MFMA result layout lane l then holds
 //    query l % 32 of its block and 16 keys of each 32-key block, so the
 //    running max / sum of a query live in one lane (plus its partner lane
-//    l ^ 32, exchanged once per key block);
+//    l ^ 32, exchanged once per 32-key half);
 //  * the probabilities, rounded to bf16, are already in the B-operand layout
 //    of the value product O^T += V^T P^T (the MFMA's k index runs over the keys
 //    in the order the score layout holds them; V is read with the gfx950
@@ -77,79 +79,52 @@ __device__ __forceinline__ float pair_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// One 64-key block for the wave's NQB query blocks.  MASK: some key of the
-// block is past T or (causal) after a query; lim[qb] is then the number of
-// leading keys of the block the lane's query may see, minus 4 * half.
+// The 32 keys 32 mb + [0, 32) of a 64-key block for the wave's NQB query
+// blocks (a block is processed as two such halves: fewer live registers, so
+// that four waves fit per SIMD).  MASK: some key of the block is past T or
+// (causal) after a query; lim[qb] is then the number of leading keys of the
+// block the lane's query may see, minus 4 * half.
 template <int NQB, bool MASK>
-__device__ __forceinline__ void attend_block(const bf16_t* sk, const bf16_t* sv, const bf16x8 (&qf)[NQB][4],
-                                             f32x16 (&o)[NQB][2], float (&m)[NQB], float (&l)[NQB],
-                                             const int (&lim)[NQB], float c, int lane) {
+__device__ __forceinline__ void attend_half(const bf16_t* sk, const bf16_t* sv, const bf16x8 (&qf)[NQB][4],
+                                            f32x16 (&o)[NQB][2], float (&m)[NQB], float (&l)[NQB],
+                                            const int (&lim)[NQB], float c, int lane, int mb) {
   const int half = lane >> 5, col = lane & 31;
   // K fragments (A operand): key row 32 mb + col, d = 16 s + 8 half + [0, 8)
-  bf16x8 kf[2][4];
+  bf16x8 kf[4];
 #pragma unroll
-  for (int mb = 0; mb < 2; mb++)
-#pragma unroll
-    for (int s = 0; s < 4; s++) {
-      int r = 32 * mb + col, ch = 2 * s + half;
-      kf[mb][s] = *reinterpret_cast<const bf16x8*>(sk + r * D + ((ch ^ swz_row8(r)) * 8));
-    }
+  for (int s = 0; s < 4; s++) {
+    int r = 32 * mb + col, ch = 2 * s + half;
+    kf[s] = *reinterpret_cast<const bf16x8*>(sk + r * D + ((ch ^ swz_row8(r)) * 8));
+  }
   // S^T blocks for every query block first, so the value products of one
   // query block overlap the exponentials of the next.
-  f32x16 sc[NQB][2];
+  f32x16 sc[NQB];
 #pragma unroll
-  for (int qb = 0; qb < NQB; qb++)
+  for (int qb = 0; qb < NQB; qb++) {
+    f32x16 acc = {};
 #pragma unroll
-    for (int mb = 0; mb < 2; mb++) {
-      f32x16 acc = {};
-#pragma unroll
-      for (int st = 0; st < 4; st++) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[mb][st], qf[qb][st], acc, 0, 0, 0);
-      sc[qb][mb] = acc;
-    }
-  // V^T fragments (A operand of O^T): lane = d column 32 db + col; keys in
-  // the score layout order: for k-step (mb, st) the 8 keys
-  // 32 mb + 16 st + 4 half + {0..3} and + 8 + {0..3}.
-  bf16x8 vf[2][2][2];  // [db][mb][st]
-  const int g = lane >> 4, i = lane & 15;
-#pragma unroll
-  for (int db = 0; db < 2; db++)
-#pragma unroll
-    for (int mb = 0; mb < 2; mb++)
-#pragma unroll
-      for (int st = 0; st < 2; st++) {
-        int cb = 32 * db + (g & 1) * 16 + 4 * (i & 3);
-        int kb0 = 32 * mb + 16 * st + 4 * (g >> 1) + (i >> 2);
-        int kb1 = kb0 + 8;
-        const bf16_t* p0 = sv + kb0 * D + (((cb >> 3) ^ swz_v(kb0)) * 8) + (cb & 7);
-        const bf16_t* p1 = sv + kb1 * D + (((cb >> 3) ^ swz_v(kb1)) * 8) + (cb & 7);
-        i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4)p0);
-        i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4)p1);
-        i16x8 w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        vf[db][mb][st] = __builtin_bit_cast(bf16x8, w);
-      }
+    for (int st = 0; st < 4; st++) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[st], qf[qb][st], acc, 0, 0, 0);
+    sc[qb] = acc;
+  }
 
   // ---- running max (scaled log2 domain; scale > 0, so max(s) c = max(s c)).
-  // The reference point m only moves when the block's max exceeds it by more
+  // The reference point m only moves when the keys' max exceeds it by more
   // than 8 (a factor 256), so the rescaling of l and O is skipped for most
-  // blocks; the probabilities exp2(s c - m) then stay below 256 and the
+  // halves; the probabilities exp2(s c - m) then stay below 256 and the
   // result is the same softmax (the normaliser uses the same m).
   bool grow_any = false;
   float m_new[NQB];
 #pragma unroll
   for (int qb = 0; qb < NQB; qb++) {
-    // key of element e in block mb: 32 mb + 8 (e / 4) + 4 half + e % 4
+    // key of element e: 32 mb + 8 (e / 4) + 4 half + e % 4
     if (MASK) {
 #pragma unroll
-      for (int mb = 0; mb < 2; mb++)
-#pragma unroll
-        for (int e = 0; e < 16; e++)
-          if (32 * mb + 8 * (e >> 2) + (e & 3) >= lim[qb]) sc[qb][mb][e] = -INFINITY;
+      for (int e = 0; e < 16; e++)
+        if (32 * mb + 8 * (e >> 2) + (e & 3) >= lim[qb]) sc[qb][e] = -INFINITY;
     }
     float peak = -INFINITY;
 #pragma unroll
-    for (int mb = 0; mb < 2; mb++)
-#pragma unroll
-      for (int e = 0; e < 16; e++) peak = fmaxf(peak, sc[qb][mb][e]);
+    for (int e = 0; e < 16; e++) peak = fmaxf(peak, sc[qb][e]);
     const float cand = pair_max(peak) * c;
     const bool grow = cand > m[qb] + 8.f;  // -inf + 8 = -inf: the first visible key always moves m
     m_new[qb] = grow ? cand : m[qb];
@@ -173,41 +148,70 @@ __device__ __forceinline__ void attend_block(const bf16_t* sk, const bf16_t* sv,
       }
     }
   }
+  const int g = lane >> 4, i = lane & 15;
 #pragma unroll
   for (int qb = 0; qb < NQB; qb++) {
     // exp2(-inf - 0) = 0 for a query with no visible key yet
     const float ref = m[qb] == -INFINITY ? 0.f : m[qb];
     float sum = 0.f;
-    bf16x8 pf[2][2];
+    bf16x8 pf[2];
 #pragma unroll
-    for (int mb = 0; mb < 2; mb++)
+    for (int st = 0; st < 2; st++) {
+      // the normaliser sums the fp32 probabilities; the value product takes
+      // them rounded to bf16 (lm.cu:131-134)
+      float pv[8];
 #pragma unroll
-      for (int st = 0; st < 2; st++) {
-        // the normaliser sums the fp32 probabilities; the value product takes
-        // them rounded to bf16 (lm.cu:131-134)
-        float pv[8];
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-          pv[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[qb][mb][8 * st + e], c, -ref));
-          sum += pv[e];
-        }
-        u32x4 w = {pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3]), pack_bf16x2(pv[4], pv[5]),
-                   pack_bf16x2(pv[6], pv[7])};
-        pf[mb][st] = __builtin_bit_cast(bf16x8, w);
+      for (int e = 0; e < 8; e++) {
+        pv[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[qb][8 * st + e], c, -ref));
+        sum += pv[e];
       }
+      u32x4 w = {pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3]), pack_bf16x2(pv[4], pv[5]),
+                 pack_bf16x2(pv[6], pv[7])};
+      pf[st] = __builtin_bit_cast(bf16x8, w);
+    }
     l[qb] += sum;
+    // V^T fragments (A operand of O^T), read just before their products so
+    // they are not live across the softmax: lane = d column 32 db + col;
+    // keys in the score layout order: for k-step st the 8 keys
+    // 32 mb + 16 st + 4 half + {0..3} and + 8 + {0..3}.
+    bf16x8 vf[2][2];  // [db][st]
 #pragma unroll
     for (int db = 0; db < 2; db++)
 #pragma unroll
-      for (int mb = 0; mb < 2; mb++)
+      for (int st = 0; st < 2; st++) {
+        int cb = 32 * db + (g & 1) * 16 + 4 * (i & 3);
+        int kb0 = 32 * mb + 16 * st + 4 * (g >> 1) + (i >> 2);
+        int kb1 = kb0 + 8;
+        const bf16_t* p0 = sv + kb0 * D + (((cb >> 3) ^ swz_v(kb0)) * 8) + (cb & 7);
+        const bf16_t* p1 = sv + kb1 * D + (((cb >> 3) ^ swz_v(kb1)) * 8) + (cb & 7);
+        i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4)p0);
+        i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4)p1);
+        i16x8 w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        vf[db][st] = __builtin_bit_cast(bf16x8, w);
+      }
 #pragma unroll
-        for (int st = 0; st < 2; st++)
-          o[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[db][mb][st], pf[mb][st], o[qb][db], 0, 0, 0);
+    for (int db = 0; db < 2; db++)
+#pragma unroll
+      for (int st = 0; st < 2; st++)
+        o[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[db][st], pf[st], o[qb][db], 0, 0, 0);
   }
 }
 
+// One 64-key block: its two 32-key halves in key order.
+template <int NQB, bool MASK>
+__device__ __forceinline__ void attend_block(const bf16_t* sk, const bf16_t* sv, const bf16x8 (&qf)[NQB][4],
+                                             f32x16 (&o)[NQB][2], float (&m)[NQB], float (&l)[NQB],
+                                             const int (&lim)[NQB], float c, int lane) {
+  attend_half<NQB, MASK>(sk, sv, qf, o, m, l, lim, c, lane, 0);
+  attend_half<NQB, MASK>(sk, sv, qf, o, m, l, lim, c, lane, 1);
+}
+
+// Launch bounds of two workgroups per CU: with 8 waves (the default shape)
+// that is four waves per SIMD, 128 registers, and the waves of the two
+// workgroups, which pass their barriers independently, overlap one's
+// exponentials with the other's MFMAs.
 template <int NW, int NQB>
-__global__ void __launch_bounds__(NW * 64) attention_fwd_d64(AttnArgs p) {
+__global__ void __launch_bounds__(NW * 64, 2) attention_fwd_d64(AttnArgs p) {
   constexpr int QW = 32 * NQB, QPB = NW * QW, CP = 8 / NW;  // copies per wave and tile
   static_assert(CP * NW == 8 && QPB == 256, "a tile is 8 copies of 1 KiB; 256 queries per workgroup");
   __shared__ __attribute__((aligned(16))) bf16_t lds[2][2][TILE];  // [stage][K,V][64 x 64]
