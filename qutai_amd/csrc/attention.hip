@@ -440,64 +440,57 @@ __device__ __forceinline__ void copy_tile(bf16_t* dst, const bf16_t* src, int64_
   }
 }
 
+// One 64-key block for the wave's NQB query blocks, as two 32-key halves
+// in a loop that is not unrolled (so the second half's fragment reads are
+// not hoisted over the first half's products): 127 registers, four waves
+// per SIMD with two 8-wave workgroups per CU.  Every dQ accumulator still
+// takes its products in the order (half 0: k-steps 0, 1), (half 1: 0, 1).
 template <int NQB, bool MASK>
 __device__ __forceinline__ void dq_block(const bf16_t* sk, const bf16_t* sv, const bf16x8 (&qf)[NQB][4],
                                          const bf16x8 (&gf)[NQB][4], const float (&lse2)[NQB], const float (&dl)[NQB],
                                          f32x16 (&dqt)[NQB][2], const int (&lim)[NQB], float c, float scale, int lane) {
   const int half = lane >> 5, col = lane & 31;
-  bf16x8 kf[2][4], vf[2][4];
+#pragma unroll 1
+  for (int mb = 0; mb < 2; mb++) {
 #pragma unroll
-  for (int mb = 0; mb < 2; mb++)
-#pragma unroll
-    for (int s = 0; s < 4; s++) {
-      kf[mb][s] = row_frag(sk, 32 * mb + col, s, half);
-      vf[mb][s] = row_frag(sv, 32 * mb + col, s, half);
-    }
-  bf16x8 ktf[2][2][2];  // K^T fragments [db][mb][st]
-#pragma unroll
-  for (int db = 0; db < 2; db++)
-#pragma unroll
-    for (int mb = 0; mb < 2; mb++)
-#pragma unroll
-      for (int st = 0; st < 2; st++) ktf[db][mb][st] = tr_frag(sk, db, 32 * mb + 16 * st, lane);
-#pragma unroll
-  for (int qb = 0; qb < NQB; qb++) {
-    bf16x8 dsf[2][2];
-#pragma unroll
-    for (int mb = 0; mb < 2; mb++) {
+    for (int qb = 0; qb < NQB; qb++) {
       f32x16 st_ = {}, dp = {};
 #pragma unroll
       for (int s = 0; s < 4; s++) {
-        st_ = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[mb][s], qf[qb][s], st_, 0, 0, 0);
-        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[mb][s], gf[qb][s], dp, 0, 0, 0);
+        const bf16x8 kf = row_frag(sk, 32 * mb + col, s, half), vf = row_frag(sv, 32 * mb + col, s, half);
+        st_ = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[qb][s], st_, 0, 0, 0);
+        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, gf[qb][s], dp, 0, 0, 0);
       }
-      float ds[16];
+      bf16x8 dsf[2];
+      {
+        float ds[16];
 #pragma unroll
-      for (int e = 0; e < 16; e++) {
-        float x = st_[e];
-        if (MASK && 32 * mb + 8 * (e >> 2) + (e & 3) >= lim[qb]) x = -INFINITY;
-        const float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(x, c, -lse2[qb]));
-        ds[e] = pr * (dp[e] - dl[qb]);  // the softmax scale multiplies dQ once, at the end
+        for (int e = 0; e < 16; e++) {
+          float x = st_[e];
+          if (MASK && 32 * mb + 8 * (e >> 2) + (e & 3) >= lim[qb]) x = -INFINITY;
+          const float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(x, c, -lse2[qb]));
+          ds[e] = pr * (dp[e] - dl[qb]);  // the softmax scale multiplies dQ once, at the end
+        }
+#pragma unroll
+        for (int st = 0; st < 2; st++) {
+          u32x4 w = {pack_bf16x2(ds[8 * st], ds[8 * st + 1]), pack_bf16x2(ds[8 * st + 2], ds[8 * st + 3]),
+                     pack_bf16x2(ds[8 * st + 4], ds[8 * st + 5]), pack_bf16x2(ds[8 * st + 6], ds[8 * st + 7])};
+          dsf[st] = __builtin_bit_cast(bf16x8, w);
+        }
       }
+      // dQ^T += K^T dS^T with the K^T fragments (transpose reads) of this half
 #pragma unroll
-      for (int st = 0; st < 2; st++) {
-        u32x4 w = {pack_bf16x2(ds[8 * st], ds[8 * st + 1]), pack_bf16x2(ds[8 * st + 2], ds[8 * st + 3]),
-                   pack_bf16x2(ds[8 * st + 4], ds[8 * st + 5]), pack_bf16x2(ds[8 * st + 6], ds[8 * st + 7])};
-        dsf[mb][st] = __builtin_bit_cast(bf16x8, w);
-      }
-    }
-#pragma unroll
-    for (int db = 0; db < 2; db++)
-#pragma unroll
-      for (int mb = 0; mb < 2; mb++)
+      for (int db = 0; db < 2; db++)
 #pragma unroll
         for (int st = 0; st < 2; st++)
-          dqt[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ktf[db][mb][st], dsf[mb][st], dqt[qb][db], 0, 0, 0);
+          dqt[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_frag(sk, db, 32 * mb + 16 * st, lane), dsf[st],
+                                                                dqt[qb][db], 0, 0, 0);
+    }
   }
 }
 
 template <int NW, int NQB>
-__global__ void __launch_bounds__(NW * 64) attention_bwd_dq_d64(AttnBwdArgs p) {
+__global__ void __launch_bounds__(NW * 64, 2) attention_bwd_dq_d64(AttnBwdArgs p) {
   constexpr int QW = 32 * NQB, QPB = NW * QW, CP = 8 / NW;
   static_assert(CP * NW == 8 && QPB == 256, "a tile is 8 copies of 1 KiB; 256 queries per workgroup");
   __shared__ __attribute__((aligned(16))) bf16_t lds[2][2][TILE];  // [stage][K,V][64 x 64]
