@@ -319,6 +319,7 @@ __global__ void __launch_bounds__(256, 3) prepare_remainder(PrepareArgs a, Remai
 //   S2  : 128x128, 4 waves, BK 32 / 16, two-stage ring (bf16, K <= 64: four per CU)
 //   N   : 256x64, 4 waves (N <= 64), BK 64 / 32, two-stage ring, A's copies
 //         streamed (nontemporal: one column tile reads every A row once)
+//         when A's rows start on 128-byte lines
 //   W   : 64x256, 4 waves (M <= 64), BK 32 / 16, four-stage ring
 //   H   : 256x128, 8 waves 4x2 (64x64 per wave), BK 64, three-stage ring
 //         (grids of 256x256 tiles that would leave half the CUs idle)
@@ -365,6 +366,14 @@ hipError_t launch_pingpong(GemmArgs p, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// A's rows (K-major) or k-rows (MN-major), in every batch entry and second
+// K segment, start on 128-byte lines.
+bool a_lines_aligned(const GemmArgs& p, int64_t es) {
+  auto line = [](int64_t bytes) { return bytes % 128 == 0; };
+  return (uintptr_t)p.a % 128 == 0 && line(p.lda * es) && line(p.sa * es) &&
+         (p.k_head == 0 || (uintptr_t)p.a_tail % 128 == 0);
+}
+
 template <bool F32, bool TA, bool TB>
 hipError_t launch_tile(Tile tile, GemmArgs p, hipStream_t stream) {
   constexpr int KB = F32 ? 16 : 32;  // K per stage of the four-stage rings
@@ -380,8 +389,12 @@ hipError_t launch_tile(Tile tile, GemmArgs p, hipStream_t stream) {
     case TILE_S2: return launch_cfg<F32, TA, TB, 128, 128, 2, 2, KB, 2, true>(p, stream);
     case TILE_N:
       // one column tile: every A row is read by one workgroup, streamed
-      // (nontemporal copies of whole lines, K per stage 64 bf16 / 32 fp32)
-      return launch_cfg<F32, TA, TB, 256, 64, 4, 1, KR, 2, true, false, false, true>(p, stream);
+      // (nontemporal copies, K per stage 64 bf16 / 32 fp32 = 128 bytes of a
+      // K-major row) where A's rows start on 128-byte lines, so that every
+      // copy reads whole lines; otherwise the same tile with plain copies
+      if (a_lines_aligned(p, F32 ? 4 : 2))
+        return launch_cfg<F32, TA, TB, 256, 64, 4, 1, KR, 2, true, false, false, true>(p, stream);
+      return launch_cfg<F32, TA, TB, 256, 64, 4, 1, KR, 2, true>(p, stream);
     case TILE_W: return launch_cfg<F32, TA, TB, 64, 256, 1, 4, KB, 4, true>(p, stream);
     case TILE_H: return launch_cfg<F32, TA, TB, 256, 128, 4, 2, KR, 3, true>(p, stream);
     case TILE_T:
