@@ -401,3 +401,56 @@ def test_backward_query_head_split_matches_one_block_per_kv_head(lm):
         a, b = download(a), download(b)
         assert np.abs(a - b).max() <= 2 ** -7 * np.abs(b).max()
         assert ora.rel_frobenius(a, b) <= 1e-3
+
+
+FOUR_WAVES_CHILD = r"""
+import sys
+import numpy as np
+sys.path.insert(0, sys.argv[2])
+from qutai_amd.backends import amd_lm
+from tests.helpers import download, normal, upload
+outs = {}
+for i, (dims, causal, layout) in enumerate(eval(sys.argv[3])):
+    batch, time, heads, kv_heads, dim = dims
+    q, k, v, g = (upload(normal(90 + 4 * i + j, n), "bfloat16") for j, n in enumerate(
+        (batch * time * heads * dim, batch * time * kv_heads * dim, batch * time * kv_heads * dim,
+         batch * time * heads * dim)))
+    out, lse = amd_lm.attention(q, k, v, *dims, causal=causal, layout=layout)
+    grads = amd_lm.attention_backward(g, q, k, v, out, lse, *dims, causal=causal, layout=layout)
+    for name, x in zip(("out", "lse", "dq", "dk", "dv"), (out, lse, *grads)):
+        outs[f"{i}_{name}"] = download(x)
+np.savez(sys.argv[1], **outs)
+print("done", len(outs))
+"""
+
+
+def test_four_wave_workgroups_match_the_default_shape(lm, tmp_path):
+    """QUTAI_AMD_ATTN_WAVES=4 runs the d64 kernels as 4 waves of two 32-row
+    blocks (forward, dQ) or two 32-key blocks (dK/dV) instead of 8 waves of
+    one: every query's and key's arithmetic is the same, so forward, LSE and
+    all three gradients are bit-identical to the default shape (causal and
+    not, grouped-query heads, ragged lengths, both layouts)."""
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    cases = [((1, 300, 4, 2, 64), True, 1), ((2, 257, 2, 2, 64), False, 0), ((1, 1024, 8, 2, 64), True, 1)]
+    root = Path(__file__).resolve().parent.parent
+    env = dict(os.environ, QUTAI_AMD_ATTN_WAVES="4")
+    path = tmp_path / "four.npz"
+    run = subprocess.run([sys.executable, "-c", FOUR_WAVES_CHILD, str(path), str(root), repr(cases)], env=env,
+                         capture_output=True, text=True, timeout=110)
+    assert run.returncode == 0 and "done" in run.stdout, run.stderr[-2000:]
+    four = np.load(path)
+    for i, (dims, causal, layout) in enumerate(cases):
+        batch, time, heads, kv_heads, dim = dims
+        q, k, v, g = (upload(normal(90 + 4 * i + j, n), "bfloat16") for j, n in enumerate(
+            (batch * time * heads * dim, batch * time * kv_heads * dim, batch * time * kv_heads * dim,
+             batch * time * heads * dim)))
+        out, lse = lm.attention(q, k, v, *dims, causal=causal, layout=layout)
+        grads = lm.attention_backward(g, q, k, v, out, lse, *dims, causal=causal, layout=layout)
+        for name, x in zip(("out", "lse", "dq", "dk", "dv"), (out, lse, *grads)):
+            assert np.array_equal(download(x), four[f"{i}_{name}"]), (i, name)
+        check_heads(download(out), download(lse), download(q), download(k), download(v), dims, causal=causal,
+                    layout=layout, heads_to_check=[(0, 0)])
