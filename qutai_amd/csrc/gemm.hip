@@ -319,7 +319,7 @@ __global__ void __launch_bounds__(256, 3) prepare_remainder(PrepareArgs a, Remai
 //   S2  : 128x128, 4 waves, BK 32 / 16, two-stage ring (bf16, K <= 64: four per CU)
 //   N   : 256x64, 4 waves (N <= 64), BK 64 / 32, two-stage ring, A's copies
 //         streamed (nontemporal: one column tile reads every A row once)
-//         when A's rows start on 128-byte lines
+//         when A's rows start on 128-byte lines and A exceeds 256 MiB
 //   W   : 64x256, 4 waves (M <= 64), BK 32 / 16, four-stage ring
 //   H   : 256x128, 8 waves 4x2 (64x64 per wave), BK 64, three-stage ring
 //         (grids of 256x256 tiles that would leave half the CUs idle)
@@ -366,11 +366,17 @@ hipError_t launch_pingpong(GemmArgs p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// A's rows (K-major) or k-rows (MN-major), in every batch entry and second
-// K segment, start on 128-byte lines.
-bool a_lines_aligned(const GemmArgs& p, int64_t es) {
+// Streamed A copies for the thin tile: A's rows (K-major) or k-rows
+// (MN-major), in every batch entry and second K segment, start on 128-byte
+// lines, and A spans at least the 256 MiB of the memory-side cache (an
+// operand that fits there is cheaper to read with plain loads, which find
+// the lines a previous kernel or call left there: a 16384 x 1408 A of a
+// 32-column product ran 19.5 us plain against 21.6 us streamed).
+bool stream_a(const GemmArgs& p, int64_t es) {
   auto line = [](int64_t bytes) { return bytes % 128 == 0; };
-  return (uintptr_t)p.a % 128 == 0 && line(p.lda * es) && line(p.sa * es) &&
+  const int64_t span = p.a_bytes > 0 ? p.a_bytes
+                       : (p.batch > 1 && p.sa > 0 ? p.batch * p.sa : (p.groups ? 0 : p.M * p.lda)) * es;
+  return span >= (int64_t(256) << 20) && (uintptr_t)p.a % 128 == 0 && line(p.lda * es) && line(p.sa * es) &&
          (p.k_head == 0 || (uintptr_t)p.a_tail % 128 == 0);
 }
 
@@ -391,8 +397,9 @@ hipError_t launch_tile(Tile tile, GemmArgs p, hipStream_t stream) {
       // one column tile: every A row is read by one workgroup, streamed
       // (nontemporal copies, K per stage 64 bf16 / 32 fp32 = 128 bytes of a
       // K-major row) where A's rows start on 128-byte lines, so that every
-      // copy reads whole lines; otherwise the same tile with plain copies
-      if (a_lines_aligned(p, F32 ? 4 : 2))
+      // copy reads whole lines, and A is larger than the memory-side cache;
+      // otherwise the same tile with plain copies
+      if (stream_a(p, F32 ? 4 : 2))
         return launch_cfg<F32, TA, TB, 256, 64, 4, 1, KR, 2, true, false, false, true>(p, stream);
       return launch_cfg<F32, TA, TB, 256, 64, 4, 1, KR, 2, true>(p, stream);
     case TILE_W: return launch_cfg<F32, TA, TB, 64, 256, 1, 4, KB, 4, true>(p, stream);

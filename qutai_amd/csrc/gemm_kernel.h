@@ -165,7 +165,8 @@ struct OperandTile {
 // STREAM_A: A's copies carry the nontemporal hint (lds_load16_nt), for tiles
 // that read every A element once (one column tile: the 256x64 tile of
 // outputs at most 64 wide) in whole 128-byte row segments per K step (the
-// host checks that A's rows start on 128-byte lines).
+// host checks that A's rows start on 128-byte lines and that A is larger
+// than the 256 MiB memory-side cache).
 template <bool F32, bool TA, bool TB, int BM, int BN, int WM, int WN, int BK, int STAGES, bool DMA,
           bool SWIGLU = false, bool GATHER_B = false, bool STREAM_A = false>
 struct GemmKernel {
